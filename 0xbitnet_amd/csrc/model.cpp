@@ -1,0 +1,706 @@
+// Model engine: GGUF load -> device weights, decode step (hipGraph), prefill.
+//
+// Reference call structure this mirrors (packages/rust/crates/oxbitnet/src):
+//   load:    model/loader.rs:75-173 (tensor walk, I2_S scale trailer,
+//            F16 -> F32 norms, F16 embedding kept), :185-291 (names, config),
+//            nn/model.rs:42-190 (layer assembly, tied head detection).
+//   forward: nn/model.rs:193-266 -> nn/transformer.rs:51-75 ->
+//            nn/attention.rs:85-124, nn/ffn.rs:60-80, nn/bitlinear.rs:52-97.
+// Differences by design: q|k|v and gate|up are fused into one matrix each
+// (one quantization of the shared input instead of three / two), weights are
+// repacked to the tiled layout, the KV cache is f16, the decode step is one
+// hipGraph whose kernels read the position from device memory, and the
+// greedy token is reduced on the device.
+#include "model.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+
+#include "oxb_common.h"
+
+using namespace oxb;
+
+#define M_CHECK(call)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess) {                                                         \
+            set_error("%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return -1;                                                                  \
+        }                                                                               \
+    } while (0)
+
+oxb_model::~oxb_model() {
+    if (stream) hipStreamSynchronize(stream);
+    if (graph) hipGraphExecDestroy(graph);
+    for (void *p : allocations) hipFree(p);
+    if (pinned) hipHostFree(pinned);
+    if (stream) hipStreamDestroy(stream);
+    delete gguf;
+}
+
+void *oxb_model::dalloc(size_t bytes) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) {
+        set_error("hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    allocations.push_back(p);
+    return p;
+}
+
+namespace {
+
+// GGUF name of a tensor given its reference (HF) name: the inverse of
+// remap_gguf_name (model/loader.rs:185-219).  Both spellings are accepted.
+std::string gguf_layer_name(int i, const char *component) {
+    return "blk." + std::to_string(i) + "." + component;
+}
+
+struct NameMap {
+    const char *gguf;
+    const char *hf;
+};
+const NameMap kLayerNames[] = {
+    {"attn_q.weight", "self_attn.q_proj.weight"},
+    {"attn_k.weight", "self_attn.k_proj.weight"},
+    {"attn_v.weight", "self_attn.v_proj.weight"},
+    {"attn_output.weight", "self_attn.o_proj.weight"},
+    {"attn_norm.weight", "input_layernorm.weight"},
+    {"ffn_norm.weight", "post_attention_layernorm.weight"},
+    {"attn_sub_norm.weight", "self_attn.sub_norm.weight"},
+    {"ffn_sub_norm.weight", "mlp.sub_norm.weight"},
+    {"ffn_up.weight", "mlp.up_proj.weight"},
+    {"ffn_down.weight", "mlp.down_proj.weight"},
+    {"ffn_gate.weight", "mlp.gate_proj.weight"},
+};
+
+const GgufTensor *find_layer(const GgufFile &g, int i, const char *gguf_comp) {
+    if (auto *t = g.find(gguf_layer_name(i, gguf_comp))) return t;
+    for (auto &nm : kLayerNames)
+        if (!strcmp(nm.gguf, gguf_comp))
+            return g.find("model.layers." + std::to_string(i) + "." + nm.hf);
+    return nullptr;
+}
+
+std::string hf_layer_name(int i, const char *gguf_comp) {
+    for (auto &nm : kLayerNames)
+        if (!strcmp(nm.gguf, gguf_comp))
+            return "model.layers." + std::to_string(i) + "." + nm.hf;
+    return gguf_layer_name(i, gguf_comp);
+}
+
+const GgufTensor *find_global(const GgufFile &g, const char *gguf_name, const char *hf_name) {
+    if (auto *t = g.find(gguf_name)) return t;
+    return g.find(hf_name);
+}
+
+float f16_to_f32_host(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            int k = -1;
+            do { m <<= 1; k++; } while (!(m & 0x400));
+            bits = sign | ((uint32_t)(127 - 15 - k) << 23) | ((m & 0x3ff) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Norm / small vectors: F32 as is, F16 converted (model/loader.rs:150-153).
+bool tensor_to_f32(const GgufFile &g, const GgufTensor &t, std::vector<float> &out) {
+    const uint8_t *src = g.base + g.data_offset + t.offset;
+    const uint64_t n = t.n_elements();
+    out.resize(n);
+    if (t.type == GGML_F32) {
+        memcpy(out.data(), src, n * 4);
+        return true;
+    }
+    if (t.type == GGML_F16) {
+        for (uint64_t i = 0; i < n; ++i) {
+            uint16_t h;
+            memcpy(&h, src + 2 * i, 2);
+            out[i] = f16_to_f32_host(h);
+        }
+        return true;
+    }
+    set_error("tensor %s: norm weights must be F32 or F16 (type %u)", t.name.c_str(), t.type);
+    return false;
+}
+
+struct I2S {
+    const uint8_t *rows;  // natural [N][K/4]
+    int N, K;
+    float scale;
+};
+
+bool get_i2s(const GgufFile &g, const GgufTensor *t, const std::string &hf, int K, int N, I2S &out) {
+    if (!t) {
+        set_error("Missing weight tensor: \"%s\"", hf.c_str());
+        return false;
+    }
+    if (t->type != GGML_I2_S) {
+        set_error("tensor %s: ternary linears must be I2_S (GGML type 36), got type %u",
+                  t->name.c_str(), t->type);
+        return false;
+    }
+    // GGUF shape is [in, out] (ne0 = K): model/loader.rs:131-133
+    if (t->shape.size() < 2 || (int)t->shape[0] != K || (int)t->shape[1] != N) {
+        set_error("tensor %s: shape [%llu, %llu] does not match [%d, %d]", t->name.c_str(),
+                  (unsigned long long)(t->shape.size() > 0 ? t->shape[0] : 0),
+                  (unsigned long long)(t->shape.size() > 1 ? t->shape[1] : 0), K, N);
+        return false;
+    }
+    const uint8_t *p = g.base + g.data_offset + t->offset;
+    const size_t packed = (t->n_elements() + 3) / 4;
+    out.rows = p;
+    out.N = N;
+    out.K = K;
+    memcpy(&out.scale, p + packed, 4);  // first f32 of the 32-byte trailer (:134-136)
+    return true;
+}
+
+uint32_t meta_u32(const GgufFile &g, const std::string &arch, const char *suffix, uint32_t dflt,
+                  bool *found = nullptr) {
+    for (const std::string &pre : {arch, std::string("llama"), std::string("bitnet"),
+                                   std::string("bitnet-25")}) {
+        if (auto *v = g.get(pre + "." + suffix)) {
+            if (v->is_int()) {
+                if (found) *found = true;
+                return (uint32_t)v->u;
+            }
+        }
+    }
+    if (found) *found = false;
+    return dflt;
+}
+
+float meta_f32(const GgufFile &g, const std::string &arch, const char *suffix, float dflt) {
+    for (const std::string &pre : {arch, std::string("llama"), std::string("bitnet"),
+                                   std::string("bitnet-25")}) {
+        if (auto *v = g.get(pre + "." + suffix))
+            if (v->kind == GgufValue::F64) return (float)v->f;
+    }
+    return dflt;
+}
+
+}  // namespace
+
+namespace oxb {
+
+static void (*g_log_fn)(int, const char *, size_t, void *) = nullptr;
+static void *g_log_ud = nullptr;
+static int g_log_min = 2;
+
+void set_log_sink(void (*fn)(int, const char *, size_t, void *), void *ud, int min_level) {
+    g_log_fn = fn;
+    g_log_ud = ud;
+    g_log_min = min_level;
+}
+
+void log_msg(int level, const char *fmt, ...) {
+    if (!g_log_fn || level < g_log_min) return;
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    int n = vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (n < 0) return;
+    g_log_fn(level, buf, (size_t)(n < (int)sizeof buf ? n : (int)sizeof buf - 1), g_log_ud);
+}
+
+static int upload_f32(oxb_model *m, const std::vector<float> &v, float **dst) {
+    *dst = (float *)m->dalloc(v.size() * 4);
+    if (!*dst) return -1;
+    M_CHECK(hipMemcpy(*dst, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+// Concatenate row blocks (natural I2_S) into one fused matrix, upload and
+// repack it to the tiled layout.  interleave: rows alternate between the two
+// parts (gate|up), else parts are stacked (q|k|v).
+static int upload_fused(oxb_model *m, const std::vector<I2S> &parts, bool interleave,
+                        void *staging, void **out, float **scales) {
+    const int K = parts[0].K;
+    const size_t rb = (size_t)K / 4;
+    int N = 0;
+    for (auto &p : parts) N += p.N;
+    std::vector<uint8_t> host((size_t)N * rb);
+    std::vector<float> sc(N);
+    if (interleave) {
+        for (int i = 0; i < parts[0].N; ++i)
+            for (size_t j = 0; j < parts.size(); ++j) {
+                const size_t row = (size_t)i * parts.size() + j;
+                memcpy(host.data() + row * rb, parts[j].rows + (size_t)i * rb, rb);
+                sc[row] = parts[j].scale;
+            }
+    } else {
+        size_t row = 0;
+        for (auto &p : parts) {
+            memcpy(host.data() + row * rb, p.rows, (size_t)p.N * rb);
+            for (int i = 0; i < p.N; ++i) sc[row + i] = p.scale;
+            row += p.N;
+        }
+    }
+    *out = m->dalloc(host.size());
+    if (!*out) return -1;
+    M_CHECK(hipMemcpy(staging, host.data(), host.size(), hipMemcpyHostToDevice));
+    if (oxb_repack_i2s_tiled(staging, *out, N, K, nullptr)) return -1;
+    M_CHECK(hipDeviceSynchronize());
+    m->weight_bytes += host.size();
+    return upload_f32(m, sc, scales);
+}
+
+oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
+    std::unique_ptr<oxb_model> m(new oxb_model());
+    GgufFile *g = gguf_open(path);
+    if (!g) return nullptr;
+    m->gguf = g;
+
+    // config_from_gguf_metadata (model/loader.rs:221-291)
+    m->arch = "bitnet";
+    if (auto *a = g->get("general.architecture"))
+        if (a->kind == GgufValue::STR) m->arch = a->s;
+    const std::string &arch = m->arch;
+    const bool is_b25 = arch == "bitnet-25";
+    m->D = (int)meta_u32(*g, arch, "embedding_length", 2560);
+    m->n_layers = (int)meta_u32(*g, arch, "block_count", 30);
+    m->H = (int)meta_u32(*g, arch, "attention.head_count", 20);
+    m->Hkv = (int)meta_u32(*g, arch, "attention.head_count_kv", (uint32_t)m->H);
+    bool vfound = false;
+    m->V = (int)meta_u32(*g, arch, "vocab_size", 128256, &vfound);
+    if (!vfound) {
+        if (auto *t = g->get("tokenizer.ggml.tokens"))
+            if (t->kind == GgufValue::ARR) m->V = (int)t->arr.size();
+    }
+    m->F = (int)meta_u32(*g, arch, "feed_forward_length", 6912);
+    m->eps = meta_f32(*g, arch, "attention.layer_norm_rms_epsilon", 1e-5f);
+    m->rope_theta = meta_f32(*g, arch, "rope.freq_base", is_b25 ? 500000.0f : 10000.0f);
+    m->relu2 = is_b25;
+    m->hd = m->D / m->H;
+    m->max_seq = max_seq > 0 ? max_seq : 4096;  // lib.rs:93
+    const int D = m->D, F = m->F, H = m->H, Hkv = m->Hkv, hd = m->hd;
+    const int Dq = H * hd, Dkv = Hkv * hd;
+    log_msg(1, "config: arch=%s layers=%d hidden=%d ffn=%d heads=%d kv_heads=%d head_dim=%d vocab=%d",
+            arch.c_str(), m->n_layers, D, F, H, Hkv, hd, m->V);
+    if (hd != 128 || D % H != 0) {
+        set_error("unsupported shape: head_dim %d (hidden %d / heads %d); the kernels need 128", hd, D, H);
+        return nullptr;
+    }
+    if (D % 512 != 0 || F % 256 != 0 || (H % Hkv) != 0) {
+        set_error("unsupported shape: hidden %d must be a multiple of 512, ffn %d of 256, heads %d of kv heads %d",
+                  D, F, H, Hkv);
+        return nullptr;
+    }
+    if (find_global(*g, "output.weight", "lm_head.weight")) {
+        set_error("unsupported: untied LM head (output.weight); only the tied f16 head is implemented");
+        return nullptr;
+    }
+
+    // Validate every tensor on the host before touching the device.
+    struct LayerSrc {
+        I2S q, k, v, o, gt, up, dn;
+        const GgufTensor *norm[4];
+    };
+    static const char *kNormNames[4] = {"attn_norm.weight", "ffn_norm.weight",
+                                        "attn_sub_norm.weight", "ffn_sub_norm.weight"};
+    const int norm_dim[4] = {D, D, Dq, F};
+    std::vector<LayerSrc> src(m->n_layers);
+    for (int i = 0; i < m->n_layers; ++i) {
+        LayerSrc &ls = src[i];
+        if (!get_i2s(*g, find_layer(*g, i, "attn_q.weight"), hf_layer_name(i, "attn_q.weight"), D, Dq, ls.q) ||
+            !get_i2s(*g, find_layer(*g, i, "attn_k.weight"), hf_layer_name(i, "attn_k.weight"), D, Dkv, ls.k) ||
+            !get_i2s(*g, find_layer(*g, i, "attn_v.weight"), hf_layer_name(i, "attn_v.weight"), D, Dkv, ls.v) ||
+            !get_i2s(*g, find_layer(*g, i, "attn_output.weight"), hf_layer_name(i, "attn_output.weight"), Dq, D, ls.o) ||
+            !get_i2s(*g, find_layer(*g, i, "ffn_up.weight"), hf_layer_name(i, "ffn_up.weight"), D, F, ls.up) ||
+            !get_i2s(*g, find_layer(*g, i, "ffn_down.weight"), hf_layer_name(i, "ffn_down.weight"), F, D, ls.dn) ||
+            !get_i2s(*g, find_layer(*g, i, "ffn_gate.weight"), hf_layer_name(i, "ffn_gate.weight"), D, F, ls.gt))
+            return nullptr;
+        for (int k = 0; k < 4; ++k) {
+            ls.norm[k] = find_layer(*g, i, kNormNames[k]);
+            if (!ls.norm[k]) {
+                if (k < 2) {
+                    set_error("Missing weight tensor: \"%s\"", hf_layer_name(i, kNormNames[k]).c_str());
+                    return nullptr;
+                }
+                continue;
+            }
+            if ((int)ls.norm[k]->n_elements() != norm_dim[k] ||
+                (ls.norm[k]->type != GGML_F32 && ls.norm[k]->type != GGML_F16)) {
+                set_error("tensor %s: expected %d F32/F16 elements", ls.norm[k]->name.c_str(), norm_dim[k]);
+                return nullptr;
+            }
+        }
+    }
+    const GgufTensor *te = find_global(*g, "token_embd.weight", "model.embed_tokens.weight");
+    if (!te) {
+        set_error("Missing weight tensor: \"model.embed_tokens.weight\"");
+        return nullptr;
+    }
+    if (te->type != GGML_F16 || te->n_elements() != (uint64_t)m->V * D) {
+        set_error("token_embd.weight must be F16 [%d, %d]", D, m->V);
+        return nullptr;
+    }
+    const GgufTensor *tn = find_global(*g, "output_norm.weight", "model.norm.weight");
+    if (!tn) {
+        set_error("Missing weight tensor: \"model.norm.weight\"");
+        return nullptr;
+    }
+
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+        set_error("hipStreamCreate failed (no usable GPU?)");
+        return nullptr;
+    }
+    if (hipHostMalloc((void **)&m->pinned, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        set_error("hipHostMalloc failed");
+        return nullptr;
+    }
+
+    const size_t staging_bytes = (size_t)std::max(Dq + 2 * Dkv, 2 * F) * std::max(D, F) / 4;
+    void *staging = m->dalloc(staging_bytes);
+    if (!staging) return nullptr;
+
+    const uint64_t total = (uint64_t)m->n_layers + 2;
+    m->layers.resize(m->n_layers);
+    for (int i = 0; i < m->n_layers; ++i) {
+        auto &L = m->layers[i];
+        LayerSrc &ls = src[i];
+        if (upload_fused(m.get(), {ls.q, ls.k, ls.v}, false, staging, &L.wqkv, &L.sqkv) ||
+            upload_fused(m.get(), {ls.o}, false, staging, &L.wo, &L.so) ||
+            upload_fused(m.get(), {ls.gt, ls.up}, true, staging, &L.wgu, &L.sgu) ||
+            upload_fused(m.get(), {ls.dn}, false, staging, &L.wd, &L.sd))
+            return nullptr;
+        float **dst[4] = {&L.attn_norm, &L.ffn_norm, &L.attn_sub, &L.ffn_sub};
+        for (int k = 0; k < 4; ++k) {
+            if (!ls.norm[k]) continue;
+            std::vector<float> w;
+            if (!tensor_to_f32(*g, *ls.norm[k], w) || upload_f32(m.get(), w, dst[k])) return nullptr;
+        }
+        if (hook) hook(2, (uint64_t)i + 1, total, ud);
+    }
+    // embedding (kept f16, model/loader.rs:139-141) and final norm
+    m->embed = (uint16_t *)m->dalloc((size_t)m->V * D * 2);
+    if (!m->embed) return nullptr;
+    if (hipMemcpy(m->embed, g->base + g->data_offset + te->offset, (size_t)m->V * D * 2,
+                  hipMemcpyHostToDevice) != hipSuccess) {
+        set_error("embedding upload failed");
+        return nullptr;
+    }
+    m->weight_bytes += (size_t)m->V * D * 2;
+    {
+        std::vector<float> w;
+        if (!tensor_to_f32(*g, *tn, w) || upload_f32(m.get(), w, &m->final_norm)) return nullptr;
+    }
+    if (hook) hook(2, total, total, ud);
+
+    {
+        std::vector<float> cs((size_t)m->max_seq * (hd / 2) * 2);
+        if (oxb_rope_table(cs.data(), m->max_seq, hd, m->rope_theta) ||
+            upload_f32(m.get(), cs, &m->rope))
+            return nullptr;
+    }
+
+    // KV cache and decode buffers
+    const size_t kv_elems = (size_t)m->n_layers * Hkv * m->max_seq * hd;
+    m->kcache = (uint16_t *)m->dalloc(kv_elems * 2);
+    m->vcache = (uint16_t *)m->dalloc(kv_elems * 2);
+    m->x = (float *)m->dalloc((size_t)D * 4);
+    m->q = (float *)m->dalloc((size_t)Dq * 4);
+    m->attn = (float *)m->dalloc((size_t)Dq * 4);
+    m->h = (float *)m->dalloc((size_t)F * 4);
+    const int max_split = (m->max_seq + 63) / 64;
+    m->part_o = (float *)m->dalloc((size_t)H * max_split * hd * 4);
+    m->part_ml = (float *)m->dalloc((size_t)H * max_split * 2 * 4);
+    m->attn_counters = (int *)m->dalloc((size_t)Hkv * 4);
+    m->logits = (float *)m->dalloc((size_t)m->V * 4);
+    m->lm_part = (float *)m->dalloc((size_t)oxb_lm_head_partials() * 2 * 4);
+    m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
+    m->hist_cap = m->max_seq + 16;
+    m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->part_o ||
+        !m->part_ml || !m->attn_counters || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
+        return nullptr;
+    if (hipMemset(m->kcache, 0, kv_elems * 2) != hipSuccess ||
+        hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess ||
+        hipMemset(m->attn_counters, 0, (size_t)Hkv * 4) != hipSuccess) {
+        set_error("hipMemset failed");
+        return nullptr;
+    }
+    {
+        int st[OXB_STATE_INTS] = {0};
+        st[OXB_ST_HIST_CAP] = m->hist_cap;
+        if (hipMemcpy(m->state, st, sizeof st, hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("state init failed");
+            return nullptr;
+        }
+    }
+    if (hipDeviceSynchronize() != hipSuccess) {
+        set_error("load: device synchronize failed");
+        return nullptr;
+    }
+    log_msg(2, "%d tensors loaded (%.1f MB of device weights)", (int)g->tensors.size(),
+            m->weight_bytes / 1e6);
+    return m.release();
+}
+
+}  // namespace oxb
+
+// One decode step: embedding of state.token at state.pos -> layers -> LM
+// head + argmax (state.token, state.pos += 1).  Every kernel reads the
+// position from device memory, so the same launch sequence replays as a graph.
+int oxb_model::enqueue_decode_step() {
+    void *s = (void *)stream;
+    const int Dq = H * hd, Dkv = Hkv * hd;
+    int *posp = state + OXB_ST_POS;
+    if (oxb_embedding(embed, V, D, nullptr, 1, state, x, s)) return -1;
+    const size_t kv_layer = (size_t)Hkv * max_seq * hd;
+    for (int l = 0; l < n_layers; ++l) {
+        const Layer &L = layers[l];
+        uint16_t *kc = kcache + l * kv_layer, *vc = vcache + l * kv_layer;
+        if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
+                              max_seq, rope, posp, s))
+            return -1;
+        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, part_o, part_ml,
+                            attn_counters, attn, s))
+            return -1;
+        // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
+        if (oxb_bitlinear_gemv(L.wo, attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr, nullptr,
+                               nullptr, s))
+            return -1;
+        if (relu2) {
+            if (oxb_bitlinear_gateup(L.wgu, x, L.ffn_norm, eps, L.sgu, 2 * F, D, h, s)) return -1;
+        } else {
+            set_error("unsupported activation: SiLU gate (arch %s)", arch.c_str());
+            return -1;
+        }
+        if (oxb_bitlinear_gemv(L.wd, h, L.ffn_sub, 1e-5f, L.sd, D, F, x, 1, nullptr, nullptr,
+                               nullptr, s))
+            return -1;
+    }
+    return oxb_lm_head_argmax(x, final_norm, eps, embed, V, D, logits, lm_part, state, tok_hist,
+                              1, s);
+}
+
+int oxb_model::capture_graph() {
+    if (graph) return 0;
+    hipGraph_t g = nullptr;
+    M_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_decode_step();
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (rc) {
+        if (g) hipGraphDestroy(g);
+        return -1;
+    }
+    if (e != hipSuccess) {
+        set_error("hipStreamEndCapture: %s", hipGetErrorString(e));
+        return -1;
+    }
+    e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        graph = nullptr;
+        set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+int oxb_model::ensure_prefill(int n) {
+    if (n <= pf_cap) return 0;
+    const int cap = ((n + 63) / 64) * 64;
+    const int Dq = H * hd;
+    const int Kmax = std::max(D, F);
+    float *nx = (float *)dalloc((size_t)cap * D * 4);
+    float *nq = (float *)dalloc((size_t)cap * Dq * 4);
+    float *na = (float *)dalloc((size_t)cap * Dq * 4);
+    float *nh = (float *)dalloc((size_t)cap * F * 4);
+    float *ns = (float *)dalloc((size_t)cap * 4);
+    void *nX = dalloc((size_t)cap * Kmax);
+    int *nsum = (int *)dalloc((size_t)cap * 4);
+    int *nids = (int *)dalloc((size_t)cap * 4);
+    if (!nx || !nq || !na || !nh || !ns || !nX || !nsum || !nids) return -1;
+    px = nx; pq = nq; pattn = na; ph = nh; pscale = ns; pX = nX; psum = nsum; pids = nids;
+    pf_cap = cap;
+    return 0;
+}
+
+// Prefill n tokens (nn/model.rs:193-266 with n > 1): per-row norm+quantize,
+// MFMA GEMMs with fused epilogues, causal attention, then the LM head on the
+// last row (advance = n).
+int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
+    if (ensure_prefill(n)) return -1;
+    void *s = (void *)stream;
+    const int Dq = H * hd, Dkv = Hkv * hd;
+    M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
+    if (oxb_embedding(embed, V, D, pids, n, state, px, s)) return -1;
+    const size_t kv_layer = (size_t)Hkv * max_seq * hd;
+    for (int l = 0; l < n_layers; ++l) {
+        const Layer &L = layers[l];
+        uint16_t *kc = kcache + l * kv_layer, *vc = vcache + l * kv_layer;
+        if (oxb_quantize_rows_tiled(px, L.attn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
+        if (oxb_gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n, pos,
+                         pq, kc, vc, max_seq, rope, s))
+            return -1;
+        if (oxb_attn_prefill(pq, kc, vc, n, pos, H, Hkv, hd, max_seq, pattn, s)) return -1;
+        if (oxb_quantize_rows_tiled(pattn, L.attn_sub, 1e-5f, n, Dq, pX, pscale, psum, s)) return -1;
+        if (oxb_gemm_i8(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1, s))
+            return -1;
+        if (oxb_quantize_rows_tiled(px, L.ffn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
+        if (!relu2) {
+            set_error("unsupported activation: SiLU gate (arch %s)", arch.c_str());
+            return -1;
+        }
+        if (oxb_gemm_i8(L.wgu, (const int8_t *)pX, pscale, psum, L.sgu, 2 * F, D, n, ph, nullptr, 2, s))
+            return -1;
+        if (oxb_quantize_rows_tiled(ph, L.ffn_sub, 1e-5f, n, F, pX, pscale, psum, s)) return -1;
+        if (oxb_gemm_i8(L.wd, (const int8_t *)pX, pscale, psum, L.sd, D, F, n, px, nullptr, 1, s))
+            return -1;
+    }
+    return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed, V, D, logits,
+                              lm_part, state, tok_hist, n, s);
+}
+
+// ---------------------------------------------------------------------------
+// extern "C" model API (include/oxbitnet_ops.h)
+// ---------------------------------------------------------------------------
+// RoPE table, computed exactly as shaders/rope.wgsl:43-48 evaluates it:
+// theta = f32(pos) * pow(base, (-2 * i) / hd), then cos/sin in f32.
+extern "C" int oxb_rope_table(float *cs, int max_seq, int hd, float theta_base) {
+    OXB_REQUIRE(cs && max_seq > 0 && hd > 0 && hd % 2 == 0, "rope_table: bad arguments");
+    const int half = hd / 2;
+    for (int p = 0; p < max_seq; ++p)
+        for (int i = 0; i < half; ++i) {
+            float fe = -2.0f * (float)i;
+            fe = fe / (float)hd;
+            const float th = (float)p * powf(theta_base, fe);
+            cs[((size_t)p * half + i) * 2] = cosf(th);
+            cs[((size_t)p * half + i) * 2 + 1] = sinf(th);
+        }
+    return 0;
+}
+
+extern "C" oxb_model *oxb_model_load(const char *path, int max_seq) {
+    clear_error();
+    if (!path) {
+        set_error("source is NULL");
+        return nullptr;
+    }
+    return model_load(path, max_seq, nullptr, nullptr);
+}
+
+extern "C" void oxb_model_free(oxb_model *m) { delete m; }
+
+extern "C" int oxb_model_get_info(const oxb_model *m, oxb_model_info *o) {
+    OXB_REQUIRE(m && o, "model is NULL");
+    o->n_layers = m->n_layers;
+    o->hidden = m->D;
+    o->ffn = m->F;
+    o->heads = m->H;
+    o->kv_heads = m->Hkv;
+    o->head_dim = m->hd;
+    o->vocab = m->V;
+    o->max_seq = m->max_seq;
+    o->rms_eps = m->eps;
+    o->rope_theta = m->rope_theta;
+    o->relu2 = m->relu2 ? 1 : 0;
+    o->weight_bytes = m->weight_bytes;
+    return 0;
+}
+
+static int write_state(oxb_model *m) {
+    int *st = m->pinned;
+    st[OXB_ST_POS] = m->pos;
+    st[OXB_ST_TOKEN] = m->pinned[OXB_ST_TOKEN];
+    st[OXB_ST_NGEN] = m->ngen;
+    st[OXB_ST_LM_COUNTER] = 0;
+    st[OXB_ST_HIST_CAP] = m->hist_cap;
+    M_CHECK(hipMemcpyAsync(m->state, st, OXB_STATE_INTS * 4, hipMemcpyHostToDevice, m->stream));
+    M_CHECK(hipStreamSynchronize(m->stream));
+    return 0;
+}
+
+extern "C" int oxb_model_reset(oxb_model *m) {
+    OXB_REQUIRE(m, "model is NULL");
+    m->pos = 0;
+    m->ngen = 0;
+    m->pinned[OXB_ST_TOKEN] = 0;
+    return write_state(m);
+}
+
+extern "C" int oxb_model_position(const oxb_model *m) { return m ? m->pos : -1; }
+
+extern "C" int oxb_model_set_token(oxb_model *m, int32_t tok) {
+    OXB_REQUIRE(m, "model is NULL");
+    m->pinned[8] = tok;
+    M_CHECK(hipMemcpyAsync(m->state + OXB_ST_TOKEN, m->pinned + 8, 4, hipMemcpyHostToDevice,
+                           m->stream));
+    M_CHECK(hipStreamSynchronize(m->stream));
+    return 0;
+}
+
+static int read_token(oxb_model *m, float *logits_host) {
+    M_CHECK(hipMemcpyAsync(m->pinned + 16, m->state, OXB_STATE_INTS * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+    if (logits_host)
+        M_CHECK(hipMemcpyAsync(logits_host, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
+                               m->stream));
+    M_CHECK(hipStreamSynchronize(m->stream));
+    return m->pinned[16 + OXB_ST_TOKEN];
+}
+
+extern "C" int oxb_model_step(oxb_model *m, float *logits_host) {
+    clear_error();
+    OXB_REQUIRE(m, "model is NULL");
+    OXB_REQUIRE(m->pos + 1 <= m->max_seq, "KV cache full: position %d of %d", m->pos, m->max_seq);
+    if (!m->graph && m->capture_graph()) return -1;
+    M_CHECK(hipGraphLaunch(m->graph, m->stream));
+    m->pos += 1;
+    m->ngen += 1;
+    return read_token(m, logits_host);
+}
+
+extern "C" int oxb_model_forward(oxb_model *m, const int32_t *ids, int n, float *logits_host) {
+    clear_error();
+    OXB_REQUIRE(m && ids, "model or ids is NULL");
+    OXB_REQUIRE(n > 0, "forward: empty input");
+    OXB_REQUIRE(m->pos + n <= m->max_seq, "KV cache overflow: %d + %d > %d", m->pos, n, m->max_seq);
+    if (n == 1) {
+        if (oxb_model_set_token(m, ids[0])) return -1;
+        return oxb_model_step(m, logits_host);
+    }
+    if (m->enqueue_prefill(ids, n)) return -1;
+    m->pos += n;
+    m->ngen += 1;
+    return read_token(m, logits_host);
+}
+
+extern "C" int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *tokens_out) {
+    clear_error();
+    OXB_REQUIRE(m && tokens_out, "model or output is NULL");
+    OXB_REQUIRE(n_steps >= 0, "n_steps %d", n_steps);
+    OXB_REQUIRE(m->pos + n_steps <= m->max_seq, "KV cache overflow: %d + %d > %d", m->pos,
+                n_steps, m->max_seq);
+    OXB_REQUIRE(m->ngen + n_steps <= m->hist_cap, "token history full");
+    if (!m->graph && m->capture_graph()) return -1;
+    const int first = m->ngen;
+    for (int i = 0; i < n_steps; ++i) M_CHECK(hipGraphLaunch(m->graph, m->stream));
+    m->pos += n_steps;
+    m->ngen += n_steps;
+    if (n_steps)
+        M_CHECK(hipMemcpyAsync(tokens_out, m->tok_hist + first, (size_t)n_steps * 4,
+                               hipMemcpyDeviceToHost, m->stream));
+    M_CHECK(hipStreamSynchronize(m->stream));
+    return 0;
+}

@@ -1,0 +1,70 @@
+// Model engine (host side): owns the device weights, caches and the decode
+// hipGraph.  Reference: nn/model.rs:42-310, model/loader.rs:75-349.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "oxb_kernels.h"
+
+struct oxb_model {
+    // configuration (model/config.rs:3-48, model/loader.rs:221-291)
+    std::string arch;
+    int n_layers = 0, D = 0, F = 0, H = 0, Hkv = 0, hd = 0, V = 0, max_seq = 0;
+    float eps = 1e-5f, rope_theta = 10000.0f;
+    bool relu2 = true;
+    size_t weight_bytes = 0;
+
+    struct Layer {
+        void *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;  // tiled I2_S
+        float *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sd = nullptr; // per-row scales
+        float *attn_norm = nullptr, *ffn_norm = nullptr;
+        float *attn_sub = nullptr, *ffn_sub = nullptr;  // may be null
+    };
+    std::vector<Layer> layers;
+    uint16_t *embed = nullptr;   // [V][D] f16 (tied LM head)
+    float *final_norm = nullptr;
+    float *rope = nullptr;       // [max_seq][hd/2] (cos, sin)
+    uint16_t *kcache = nullptr, *vcache = nullptr;  // [L][Hkv][max_seq][hd]
+
+    // decode buffers
+    float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;
+    int *attn_counters = nullptr;
+    float *logits = nullptr, *lm_part = nullptr;
+    int *state = nullptr, *tok_hist = nullptr;
+    int hist_cap = 0;
+
+    // prefill buffers (grown on demand)
+    int pf_cap = 0;
+    float *px = nullptr, *pq = nullptr, *pattn = nullptr, *ph = nullptr, *pscale = nullptr;
+    void *pX = nullptr;
+    int *psum = nullptr, *pids = nullptr;
+
+    hipStream_t stream = nullptr;
+    hipGraphExec_t graph = nullptr;
+    int *pinned = nullptr;      // host-pinned scratch for small readbacks
+    int pos = 0;                // host mirror of state[OXB_ST_POS]
+    int ngen = 0;               // host mirror of state[OXB_ST_NGEN]
+
+    std::vector<void *> allocations;
+    oxb::GgufFile *gguf = nullptr;  // kept for the tokenizer metadata
+
+    ~oxb_model();
+    void *dalloc(size_t bytes);
+    int enqueue_decode_step();
+    int ensure_prefill(int n);
+    int enqueue_prefill(const int32_t *ids, int n);
+    int capture_graph();
+};
+
+namespace oxb {
+// Load progress hook used by the C ABI (phase 2 = upload, per tensor).
+typedef void (*LoadHook)(int phase, uint64_t loaded, uint64_t total, void *ud);
+oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud);
+void log_msg(int level, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+}  // namespace oxb

@@ -1,0 +1,153 @@
+// Shared definitions for the MI355X (gfx950) ternary inference kernels.
+//
+// Device-side conventions:
+//  - wave64; every workgroup reduction that must be bit-identical to the
+//    reference shaders uses their order: 256 strided partials, then the
+//    halving tree s[t] += s[t + stride] (stride 128 .. 1).
+//  - all f32 arithmetic is compiled with -ffp-contract=off; explicit fmaf()
+//    is used only where the result is compared within a tolerance.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace oxb {
+
+// Thread-local last-error plumbing shared by every extern "C" entry point.
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+const char *last_error();
+
+}  // namespace oxb
+
+#define OXB_CHECK_HIP(call)                                                   \
+    do {                                                                      \
+        hipError_t oxb_e_ = (call);                                           \
+        if (oxb_e_ != hipSuccess) {                                           \
+            oxb::set_error("%s: %s (%s:%d)", #call, hipGetErrorString(oxb_e_), \
+                           __FILE__, __LINE__);                               \
+            return -1;                                                        \
+        }                                                                     \
+    } while (0)
+
+#define OXB_REQUIRE(cond, ...)            \
+    do {                                  \
+        if (!(cond)) {                    \
+            oxb::set_error(__VA_ARGS__);  \
+            return -1;                    \
+        }                                 \
+    } while (0)
+
+namespace oxb {
+
+constexpr int kWave = 64;
+constexpr int kTileRows = 16;   // rows per tile of the repacked ternary layout
+constexpr int kChunkBytes = 16; // one lane load: 64 ternary weights
+
+// Repacked ternary matrix ("tile-chunk" order, built once at load time):
+//   tile t = rows [16t, 16t+16); inside a tile the 16-byte chunks are stored
+//   chunk-major: offset(t, kc, r) = (t*KC + kc)*16 + r  [in 16-byte units],
+//   KC = K/64.  Chunk (r, kc) is bytes [16kc, 16kc+16) of the row's natural
+//   I2_S encoding, i.e. 4 bit-planes x 16 consecutive weights
+//   k = (kc/2)*128 + g*32 + (kc%2)*16 + j, g = 0..3, j = 0..15.
+// A wave load of lane l -> (r = l%16, kc = kc0 + l/16) reads 1 KiB contiguous.
+__host__ __device__ inline size_t tiled_offset16(int row, int kc, int KC) {
+    return ((size_t)(row >> 4) * KC + kc) * 16 + (row & 15);
+}
+
+}  // namespace oxb
+
+#ifdef __HIPCC__
+namespace oxb {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal: weights are read once per step).
+__device__ inline uint4 load_nt(const uint4 *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// f32 workgroup sum in the shaders' tree order for a 256-thread block.
+// Every thread passes its strided partial; the result is returned to all.
+// red must hold >= 256 floats of LDS.
+__device__ inline float block256_tree_sum(float part, float *red) {
+    const int t = threadIdx.x;
+    red[t] = part;
+    __syncthreads();
+    if (t < 128) red[t] = red[t] + red[t + 128];
+    __syncthreads();
+    if (t < 64) red[t] = red[t] + red[t + 64];
+    __syncthreads();
+    if (t < 64) {
+        float v = red[t];
+#pragma unroll
+        for (int s = 32; s > 0; s >>= 1) v = v + __shfl_down(v, s, 64);
+        if (t == 0) red[0] = v;
+    }
+    __syncthreads();
+    float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__device__ inline float block256_max(float v, float *red) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    if ((t & 63) == 0) red[t >> 6] = v;
+    __syncthreads();
+    float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+__device__ inline int block256_isum(int v, int *red) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+    if ((t & 63) == 0) red[t >> 6] = v;
+    __syncthreads();
+    int r = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return r;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    return v;
+}
+
+// sh/quantize.wgsl:59,68,71 for one value given the row absmax.
+__device__ inline int quant_one(float v, float inv) {
+    int q = (int)rintf(v * inv);
+    return q < -127 ? -127 : (q > 127 ? 127 : q);
+}
+
+// Dot of four 2-bit planes of one packed dword against four int8 activation
+// dwords (one per plane).  Codes c in {0,1,2} are used unshifted where the
+// masked field still fits a signed byte: plane 3 (bits 1:0) x1, plane 2
+// (bits 3:2) x4, planes 1 (bits 5:4) and 0 (bits 7:6, moved down by 2) x16.
+// The true dot is acc1 + acc4/4 + acc16/16 - sum(x) (w = c - 1).
+struct CodeAcc {
+    int a1 = 0, a4 = 0, a16 = 0;
+    __device__ inline void add(uint32_t w, int x0, int x1, int x2, int x3) {
+        a1 = __builtin_amdgcn_sdot4((int)(w & 0x03030303u), x3, a1, false);
+        a4 = __builtin_amdgcn_sdot4((int)(w & 0x0c0c0c0cu), x2, a4, false);
+        a16 = __builtin_amdgcn_sdot4((int)(w & 0x30303030u), x1, a16, false);
+        a16 = __builtin_amdgcn_sdot4((int)((w >> 2) & 0x30303030u), x0, a16, false);
+    }
+    __device__ inline int codes() const { return a1 + (a4 >> 2) + (a16 >> 4); }
+};
+
+}  // namespace oxb
+#endif

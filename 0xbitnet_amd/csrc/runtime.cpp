@@ -1,0 +1,154 @@
+// Host runtime plumbing for liboxbitnet: thread-local errors, device memory,
+// streams, events and device information, exported over the plain C ABI in
+// include/oxbitnet_ops.h.  The reference's equivalent layer is wgpu
+// (gpu/device.rs:11-54, gpu/buffer_pool.rs:12-41); here it is the HIP
+// runtime directly, one process per GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "oxb_common.h"
+#include "oxb_kernels.h"
+
+namespace oxb {
+
+static thread_local std::string g_error;
+static thread_local bool g_has_error = false;
+
+void set_error(const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    g_has_error = true;
+}
+
+void clear_error() {
+    g_error.clear();
+    g_has_error = false;
+}
+
+const char *last_error() { return g_has_error ? g_error.c_str() : nullptr; }
+
+}  // namespace oxb
+
+using namespace oxb;
+
+extern "C" const char *oxb_last_error(void) { return last_error(); }
+
+extern "C" void *oxb_device_malloc(size_t bytes) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        set_error("hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" int oxb_device_free(void *p) {
+    if (!p) return 0;
+    OXB_CHECK_HIP(hipFree(p));
+    return 0;
+}
+
+extern "C" int oxb_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
+    OXB_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    OXB_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
+    OXB_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    OXB_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream) {
+    OXB_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_memset_d(void *dst, int value, size_t bytes, void *stream) {
+    OXB_CHECK_HIP(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return 0;
+}
+
+extern "C" void *oxb_stream_create(void) {
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        set_error("hipStreamCreate: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    return (void *)s;
+}
+
+extern "C" int oxb_stream_destroy(void *stream) {
+    if (stream) OXB_CHECK_HIP(hipStreamDestroy((hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_stream_sync(void *stream) {
+    OXB_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_device_sync(void) {
+    OXB_CHECK_HIP(hipDeviceSynchronize());
+    return 0;
+}
+
+extern "C" void *oxb_event_create(void) {
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) {
+        set_error("hipEventCreate: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    return (void *)ev;
+}
+
+extern "C" int oxb_event_destroy(void *ev) {
+    if (ev) OXB_CHECK_HIP(hipEventDestroy((hipEvent_t)ev));
+    return 0;
+}
+
+extern "C" int oxb_event_record(void *ev, void *stream) {
+    OXB_CHECK_HIP(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_event_sync(void *ev) {
+    OXB_CHECK_HIP(hipEventSynchronize((hipEvent_t)ev));
+    return 0;
+}
+
+extern "C" float oxb_event_elapsed_ms(void *start, void *stop) {
+    float ms = -1.0f;
+    hipError_t e = hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop);
+    if (e != hipSuccess) {
+        set_error("hipEventElapsedTime: %s", hipGetErrorString(e));
+        return -1.0f;
+    }
+    return ms;
+}
+
+extern "C" int oxb_device_info(char *name, int len, int *cus, int *clock_khz, size_t *hbm_bytes) {
+    int dev = 0;
+    OXB_CHECK_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    OXB_CHECK_HIP(hipGetDeviceProperties(&prop, dev));
+    if (name && len > 0) {
+        snprintf(name, (size_t)len, "%s (%s)", prop.name, prop.gcnArchName);
+    }
+    if (cus) *cus = prop.multiProcessorCount;
+    if (clock_khz) *clock_khz = prop.clockRate;
+    if (hbm_bytes) *hbm_bytes = prop.totalGlobalMem;
+    return 0;
+}

@@ -1,0 +1,262 @@
+// Prefill ternary GEMM on int8 MFMA for gfx950.
+//
+// Reference: shaders/ternary_gemm.wgsl:40-136 (64x64 tile, scalar i32 MACs,
+// Y[n*M+m] = f32(acc) * (scales[m] * input_scales[n])), dispatched by
+// nn/bitlinear.rs:207-247; epilogues fuse nn/ffn.rs:60-80 (ReLU^2 gate),
+// nn/transformer.rs:157 (residual), nn/attention.rs:97-107,127-184 (RoPE +
+// cache append).
+//
+// MFMA mapping (v_mfma_i32_16x16x64_i8, A = 16x64, B = 64x16, C = 16x16):
+//   A = weight codes of a 16-row tile: lane l supplies row l%16; its 16
+//       bytes are one bit plane g of the chunk (row, kc = 4s + l/16), i.e.
+//       weights k = (kc/2)*128 + g*32 + (kc%2)*16 + 0..15 as codes 0..2.
+//   B = int8 activations: lane l supplies token l%16, the same 16 k values,
+//       read from the token-tiled activation layout (below).
+//   C: lane l holds rows 4*(l/16) .. +3 (features) of column l%16 (token).
+// Integer accumulation is exact, so any consistent k order gives the
+// reference's int32 accumulator: acc = C(codes) - sum_k x[t][k].
+//
+// Token-tiled activation layout (written by oxb_quantize_rows_tiled):
+//   [n_tok/16 tiles][KC][16 tokens][64 B], 64 B = planes g = 0..3 x 16 B of
+//   x[t][(kc/2)*128 + g*32 + (kc%2)*16 + 0..15].
+#include "oxb_common.h"
+#include "oxb_kernels.h"
+
+namespace oxb {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+enum GemmEpi { GE_STORE = 0, GE_RESID = 1, GE_GATEUP = 2, GE_QKV = 3 };
+
+struct GemmParams {
+    const uint4 *W;        // tiled weights
+    const uint4 *X;        // token-tiled int8 activations
+    const float *xscale;   // [n_tok]
+    const int *xsum;       // [n_tok]
+    const float *wscale;   // [N]
+    int N, K, n_tok;
+    float *Y;              // [n_tok][N] (GATEUP: [n_tok][N/2])
+    int32_t *acc_out;      // optional [n_tok][N]
+    // QKV
+    float *q_out;          // [n_tok][Dq]
+    uint16_t *kcache, *vcache;
+    const float2 *rope;
+    int Dq, Dkv, hd, max_seq, pos0;
+};
+
+__device__ inline v4i plane(uint4 w, int g) {
+    const int sh = 6 - 2 * g;
+    v4i a;
+    a.x = (int)((w.x >> sh) & 0x03030303u);
+    a.y = (int)((w.y >> sh) & 0x03030303u);
+    a.z = (int)((w.z >> sh) & 0x03030303u);
+    a.w = (int)((w.w >> sh) & 0x03030303u);
+    return a;
+}
+
+__device__ inline v4i as_v4i(uint4 u) {
+    v4i a;
+    a.x = (int)u.x; a.y = (int)u.y; a.z = (int)u.z; a.w = (int)u.w;
+    return a;
+}
+
+// Workgroup tile: 64 features x 64 tokens; 4 waves in a 2x2 grid, each wave
+// 2 feature tiles x 2 token tiles of 16x16.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, q = lane >> 4;
+    const int KC = p.K >> 6;
+    const int f0 = blockIdx.x * 64 + (w & 1) * 32;
+    const int tt0 = blockIdx.y * 4 + (w >> 1) * 2;   // first token tile of this wave
+    const int ntt = (p.n_tok + 15) >> 4;
+    if (f0 >= p.N || tt0 >= ntt) return;
+    const bool t1ok = tt0 + 1 < ntt;
+    const bool f1ok = f0 + 16 < p.N;
+
+    v4i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const uint4 *Wt0 = p.W + (size_t)(f0 >> 4) * KC * 16;
+    const uint4 *Wt1 = p.W + (size_t)((f1ok ? f0 + 16 : f0) >> 4) * KC * 16;
+    const uint4 *Xt0 = p.X + ((size_t)tt0 * KC * 16) * 4;
+    const uint4 *Xt1 = p.X + ((size_t)(t1ok ? tt0 + 1 : tt0) * KC * 16) * 4;
+
+    const int steps = KC >> 2;
+    uint4 wa[2], xa[2][4];
+    auto load = [&](int s, uint4 (&wv)[2], uint4 (&xv)[2][4]) {
+        const int kc = 4 * s + q;
+        wv[0] = load_nt(Wt0 + (size_t)kc * 16 + r);
+        wv[1] = load_nt(Wt1 + (size_t)kc * 16 + r);
+        const uint4 *x0 = Xt0 + ((size_t)kc * 16 + r) * 4;
+        const uint4 *x1 = Xt1 + ((size_t)kc * 16 + r) * 4;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            xv[0][g] = x0[g];
+            xv[1][g] = x1[g];
+        }
+    };
+    load(0, wa, xa);
+    for (int s = 0; s < steps; ++s) {
+        uint4 wb[2], xb[2][4];
+        if (s + 1 < steps) load(s + 1, wb, xb);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const v4i a0 = plane(wa[0], g), a1 = plane(wa[1], g);
+            const v4i b0 = as_v4i(xa[0][g]), b1 = as_v4i(xa[1][g]);
+            acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (s + 1 < steps) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                wa[i] = wb[i];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) xa[i][g] = xb[i][g];
+            }
+        }
+    }
+
+    // epilogue: lane holds features n = f0 + ft*16 + 4q + v of token t
+#pragma unroll
+    for (int ft = 0; ft < 2; ++ft) {
+        if (ft == 1 && !f1ok) continue;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            if (tt == 1 && !t1ok) continue;
+            const int t = (tt0 + tt) * 16 + r;
+            if (t >= p.n_tok) continue;
+            const int n0 = f0 + ft * 16 + 4 * q;
+            const int xs = p.xsum[t];
+            const float is = p.xscale[t];
+            float y[4];
+            int32_t a[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                a[v] = acc[ft][tt][v] - xs;
+                // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
+                const float sc = p.wscale[n0 + v] * is;
+                y[v] = (float)a[v] * sc;
+            }
+            if (p.acc_out) {
+                *(int4 *)(p.acc_out + (size_t)t * p.N + n0) = make_int4(a[0], a[1], a[2], a[3]);
+            }
+            if constexpr (EPI == GE_STORE) {
+                *(float4 *)(p.Y + (size_t)t * p.N + n0) = make_float4(y[0], y[1], y[2], y[3]);
+            } else if constexpr (EPI == GE_RESID) {
+                float4 *dst = (float4 *)(p.Y + (size_t)t * p.N + n0);
+                float4 o = *dst;
+                o.x = o.x + y[0]; o.y = o.y + y[1]; o.z = o.z + y[2]; o.w = o.w + y[3];
+                *dst = o;
+            } else if constexpr (EPI == GE_GATEUP) {
+                float g0 = fmaxf(0.0f, y[0]), g1 = fmaxf(0.0f, y[2]);
+                g0 = g0 * g0;
+                g1 = g1 * g1;
+                *(float2 *)(p.Y + (size_t)t * (p.N >> 1) + (n0 >> 1)) =
+                    make_float2(g0 * y[1], g1 * y[3]);
+            } else {  // GE_QKV
+                const int pos = p.pos0 + t;
+                const int Dk = p.Dq + p.Dkv;
+                float o[4] = {y[0], y[1], y[2], y[3]};
+                if (n0 < Dk) {
+                    const int d0 = (n0 < p.Dq ? n0 : n0 - p.Dq) % p.hd;
+#pragma unroll
+                    for (int pr = 0; pr < 2; ++pr) {
+                        const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d0 >> 1) + pr];
+                        const float x0 = y[2 * pr], x1 = y[2 * pr + 1];
+                        float a0 = x0 * cs.x, a1 = x1 * cs.y;
+                        float b0 = x0 * cs.y, b1 = x1 * cs.x;
+                        o[2 * pr] = a0 - a1;
+                        o[2 * pr + 1] = b0 + b1;
+                    }
+                }
+                if (n0 < p.Dq) {
+                    *(float4 *)(p.q_out + (size_t)t * p.Dq + n0) = make_float4(o[0], o[1], o[2], o[3]);
+                } else {
+                    const int j = n0 < Dk ? n0 - p.Dq : n0 - Dk;
+                    const int head = j / p.hd, d = j % p.hd;
+                    uint16_t *cache = n0 < Dk ? p.kcache : p.vcache;
+                    uint16_t *dst = cache + ((size_t)head * p.max_seq + pos) * p.hd + d;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
+                }
+            }
+        }
+    }
+}
+
+}  // namespace oxb
+
+using namespace oxb;
+
+static int gemm_check(int N, int K, int n_tok) {
+    OXB_REQUIRE(N > 0 && N % 32 == 0, "ternary GEMM: out_dim %d must be a multiple of 32", N);
+    OXB_REQUIRE(K > 0 && K % 256 == 0, "ternary GEMM: in_dim %d must be a multiple of 256", K);
+    OXB_REQUIRE(n_tok > 0, "ternary GEMM: n_tok %d", n_tok);
+    return 0;
+}
+
+template <int EPI>
+static int gemm_launch(const GemmParams &p, void *stream) {
+    dim3 grid((p.N + 63) / 64, (p.n_tok + 63) / 64);
+    hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale,
+                           const int *xsum, const float *wscale, int N, int K, int n_tok,
+                           float *Y, int32_t *acc_out, int epilogue, void *stream) {
+    if (gemm_check(N, K, n_tok)) return -1;
+    GemmParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.X = (const uint4 *)X;
+    p.xscale = xscale;
+    p.xsum = xsum;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.n_tok = n_tok;
+    p.Y = Y;
+    p.acc_out = acc_out;
+    switch (epilogue) {
+        case GE_STORE: return gemm_launch<GE_STORE>(p, stream);
+        case GE_RESID: return gemm_launch<GE_RESID>(p, stream);
+        case GE_GATEUP: return gemm_launch<GE_GATEUP>(p, stream);
+        default: oxb::set_error("ternary GEMM: epilogue %d unsupported here", epilogue); return -1;
+    }
+}
+
+extern "C" int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale,
+                            const int *xsum, const float *wscale, int Dq, int Dkv, int hd, int K,
+                            int n_tok, int pos0, float *q_out, uint16_t *kcache,
+                            uint16_t *vcache, int max_seq, const float *rope_cs, void *stream) {
+    const int N = Dq + 2 * Dkv;
+    if (gemm_check(N, K, n_tok)) return -1;
+    OXB_REQUIRE(Dq % 32 == 0 && Dkv % 32 == 0 && hd % 16 == 0, "gemm qkv: bad head split");
+    OXB_REQUIRE(pos0 >= 0 && pos0 + n_tok <= max_seq, "gemm qkv: positions exceed max_seq");
+    GemmParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.X = (const uint4 *)X;
+    p.xscale = xscale;
+    p.xsum = xsum;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.n_tok = n_tok;
+    p.q_out = q_out;
+    p.kcache = kcache;
+    p.vcache = vcache;
+    p.rope = (const float2 *)rope_cs;
+    p.Dq = Dq;
+    p.Dkv = Dkv;
+    p.hd = hd;
+    p.max_seq = max_seq;
+    p.pos0 = pos0;
+    return gemm_launch<GE_QKV>(p, stream);
+}

@@ -1,0 +1,436 @@
+// Decode ternary GEMV family for gfx950 (one token, int8 activations,
+// 2-bit weights streamed from HBM in the tile-chunk layout).
+//
+// Reference: sh/ternary_gemv.wgsl:39-97 (GEMV), sh/quantize.wgsl:28-74,
+// sh/rmsnorm.wgsl:27-63 (fused prologue), sh/rope.wgsl:25-56 +
+// rs/nn/attention.rs:171-184 (QKV epilogue), sh/activation.wgsl +
+// sh/elementwise.wgsl (gate/up epilogue, residual epilogue).
+//
+// One workgroup (4 waves) owns one 16-row tile.  The 4 waves split the
+// tile's K range; inside a wave lane l streams chunks (row l%16,
+// kc0 + l/16 + 4j), so every wave load is one contiguous KiB.  Before the
+// prologue runs, each lane already has its first 8 chunks (128 B) in flight.
+#include "oxb_common.h"
+#include "oxb_kernels.h"
+
+namespace oxb {
+
+constexpr int kPrefetch = 8;   // 16-byte chunks per lane issued per batch
+constexpr int kMaxNormReg = 28; // f32 values per thread in a norm prologue (D <= 7168)
+
+enum Pro { PRO_INT8 = 0, PRO_QUANT = 1 };           // PRO_QUANT: optional RMSNorm + quantize
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GATEUP = 3 };
+
+struct GemvParams {
+    const uint4 *W;        // tile-chunk layout
+    const float *wscale;   // [N]
+    int N, K;
+    // PRO_INT8
+    const int8_t *xq;
+    const float *xscale;   // [1]
+    const int *xsum;       // [1]
+    // PRO_QUANT
+    const float *x;        // [K]
+    const float *gamma;    // [K] or nullptr (no norm)
+    float eps;
+    // epilogues
+    float *y;              // STORE: [N]; RESID: residual stream [N] (in place)
+    int32_t *acc_out;      // optional raw int32 accumulators [N]
+    int8_t *xq_out;        // optional: the prologue's int8 vector [K] (block 0 writes)
+    float *xscale_out;     // optional
+    // QKV
+    float *q_out;          // [Dq]
+    uint16_t *kcache, *vcache;  // [Hkv][max_seq][hd] f16 bits
+    const float2 *rope;    // [max_seq][hd/2] (cos, sin)
+    const int *pos;        // device position
+    int Dq, Dkv, hd, max_seq;
+};
+
+// ---------------------------------------------------------------------------
+// Prologue: RMSNorm (optional) + per-token absmax int8 quantize of one row of
+// D = K f32 values, computed by all 256 threads with the shaders' thread
+// mapping (thread t owns columns t, t+256, ...).  Writes int8 into LDS.
+// ---------------------------------------------------------------------------
+__device__ inline void norm_quant_to_lds(const float *__restrict__ x,
+                                         const float *__restrict__ gamma, float eps,
+                                         int D, int8_t *xq_lds, float *red, int *ired,
+                                         float &scale, int &sumq) {
+    const int t = threadIdx.x;
+    float v[kMaxNormReg];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxNormReg; ++j) {
+        const int c = t + j * 256;
+        v[j] = c < D ? x[c] : 0.0f;
+        if (gamma && c < D) {
+            float sq = v[j] * v[j];
+            ss = ss + sq;
+        }
+    }
+    if (gamma) {
+        const float sum = block256_tree_sum(ss, red);
+        const float rms = 1.0f / sqrtf(sum / (float)D + eps);
+#pragma unroll
+        for (int j = 0; j < kMaxNormReg; ++j) {
+            const int c = t + j * 256;
+            if (c < D) {
+                float a = v[j] * rms;
+                v[j] = a * gamma[c];
+            }
+        }
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxNormReg; ++j)
+        if (t + j * 256 < D) am = fmaxf(am, fabsf(v[j]));
+    am = block256_max(am, red);
+    scale = am == 0.0f ? 1.0f : am / 127.0f;
+    const float inv = am == 0.0f ? 0.0f : 127.0f / am;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxNormReg; ++j) {
+        const int c = t + j * 256;
+        if (c < D) {
+            const int q = quant_one(v[j], inv);
+            xq_lds[c] = (int8_t)q;
+            s += q;
+        }
+    }
+    sumq = block256_isum(s, ired);
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+template <int PRO, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+    extern __shared__ __align__(16) int8_t smem[];
+    int8_t *xq_lds = smem;                                     // [K]
+    float *red = (float *)(smem + p.K);                        // [256]
+    int *ired = (int *)(red + 256);                            // [4]
+    int *wpart = ired + 4;                                     // [4][16]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, c = lane >> 4;
+    const int KC = p.K >> 6;
+    const int tile = blockIdx.x;
+    const uint4 *tw = p.W + (size_t)tile * KC * 16;
+
+    // Wave w owns chunks [kc0, kc1) of this tile.
+    const int per = (KC + 3) >> 2;
+    const int kc0 = w * per;
+    const int kc1 = min(KC, kc0 + per);
+
+    uint4 buf[kPrefetch];
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u) {
+        const int kc = kc0 + c + 4 * u;
+        buf[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r)
+                          : make_uint4(0, 0, 0, 0);
+    }
+
+    // ---- prologue ---------------------------------------------------------
+    float in_scale;
+    int xsum;
+    if constexpr (PRO == PRO_INT8) {
+        const int nv = p.K >> 4;
+        for (int i = tid; i < nv; i += 256)
+            ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
+        in_scale = p.xscale[0];
+        xsum = p.xsum[0];
+        __syncthreads();
+    } else {
+        norm_quant_to_lds(p.x, p.gamma, p.eps, p.K, xq_lds, red, ired, in_scale, xsum);
+        __syncthreads();
+        if (tile == 0 && p.xq_out) {
+            for (int i = tid; i < (p.K >> 4); i += 256)
+                ((int4 *)p.xq_out)[i] = ((const int4 *)xq_lds)[i];
+            if (tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
+        }
+    }
+
+    // ---- main loop ----------------------------------------------------------
+    CodeAcc acc;
+    for (int base = kc0 + c; base < kc1; base += 4 * kPrefetch) {
+        uint4 nxt[kPrefetch];
+#pragma unroll
+        for (int u = 0; u < kPrefetch; ++u) {
+            const int kc = base + 4 * kPrefetch + 4 * u;
+            nxt[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r)
+                              : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kPrefetch; ++u) {
+            const int kc = base + 4 * u;
+            if (kc < kc1) {
+                const int xo = (kc >> 1) * 128 + (kc & 1) * 16;
+                const int4 x0 = *(const int4 *)(xq_lds + xo);
+                const int4 x1 = *(const int4 *)(xq_lds + xo + 32);
+                const int4 x2 = *(const int4 *)(xq_lds + xo + 64);
+                const int4 x3 = *(const int4 *)(xq_lds + xo + 96);
+                acc.add(buf[u].x, x0.x, x1.x, x2.x, x3.x);
+                acc.add(buf[u].y, x0.y, x1.y, x2.y, x3.y);
+                acc.add(buf[u].z, x0.z, x1.z, x2.z, x3.z);
+                acc.add(buf[u].w, x0.w, x1.w, x2.w, x3.w);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kPrefetch; ++u) buf[u] = nxt[u];
+    }
+
+    // ---- reduction: 4 lanes per row, then 4 waves ---------------------------
+    int v = acc.codes();
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (c == 0) wpart[w * 16 + r] = v;
+    __syncthreads();
+    if (tid >= 16) return;
+    const int32_t a = wpart[r] + wpart[16 + r] + wpart[32 + r] + wpart[48 + r] - xsum;
+    const int n = tile * 16 + r;
+    if (p.acc_out) p.acc_out[n] = a;
+    // sh/ternary_gemv.wgsl:94-95: (f32(acc) * scales[row]) * input_scale
+    float yv = (float)a * p.wscale[n];
+    yv = yv * in_scale;
+
+    if constexpr (EPI == EPI_STORE) {
+        p.y[n] = yv;
+    } else if constexpr (EPI == EPI_RESID) {
+        p.y[n] = p.y[n] + yv;   // rs/nn/transformer.rs:157 add(input, out)
+    } else if constexpr (EPI == EPI_GATEUP) {
+        // fused rows interleave gate (even) and up (odd): rs/nn/ffn.rs:60-80
+        const float other = __shfl_xor(yv, 1, 64);
+        if ((n & 1) == 0) {
+            float g = fmaxf(0.0f, yv);   // sh/activation.wgsl:32-33
+            g = g * g;
+            p.y[n >> 1] = g * other;    // sh/elementwise.wgsl:32
+        }
+    } else {  // EPI_QKV
+        const int pos = *p.pos;
+        if (pos < 0 || pos >= p.max_seq) return;  // host checks too; never write out of range
+        const float other = __shfl_xor(yv, 1, 64);
+        const int Dk = p.Dq + p.Dkv;
+        float outv = yv;
+        if (n < Dk) {  // q or k: RoPE on the interleaved pair (2i, 2i+1)
+            const int d = (n < p.Dq ? n : n - p.Dq) % p.hd;
+            const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d >> 1)];
+            if ((n & 1) == 0) {
+                float a0 = yv * cs.x, a1 = other * cs.y;
+                outv = a0 - a1;
+            } else {
+                float a0 = other * cs.y, a1 = yv * cs.x;
+                outv = a0 + a1;
+            }
+        }
+        if (n < p.Dq) {
+            p.q_out[n] = outv;
+        } else {
+            const int j = n < Dk ? n - p.Dq : n - Dk;
+            const int head = j / p.hd, d = j % p.hd;
+            uint16_t *cache = n < Dk ? p.kcache : p.vcache;
+            cache[((size_t)head * p.max_seq + pos) * p.hd + d] = f32_to_f16_bits(outv);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row-wise (optional RMSNorm) + quantize for several tokens (prefill):
+// one workgroup per token row, writes int8 X, per-row scale and sum(q).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void norm_quant_rows_kernel(
+    const float *__restrict__ x, const float *__restrict__ gamma, float eps, int D,
+    int8_t *__restrict__ xq, float *__restrict__ scales, int *__restrict__ sums) {
+    extern __shared__ __align__(16) int8_t smem[];
+    int8_t *q_lds = smem;
+    float *red = (float *)(smem + ((D + 15) & ~15));
+    int *ired = (int *)(red + 256);
+    const int row = blockIdx.x;
+    float scale;
+    int sumq;
+    norm_quant_to_lds(x + (size_t)row * D, gamma, eps, D, q_lds, red, ired, scale, sumq);
+    __syncthreads();
+    for (int i = threadIdx.x; i < (D >> 4); i += 256)
+        ((int4 *)(xq + (size_t)row * D))[i] = ((const int4 *)q_lds)[i];
+    if (threadIdx.x == 0) {
+        scales[row] = scale;
+        if (sums) sums[row] = sumq;
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Same row transform, writing the token-tiled int8 layout the MFMA GEMM reads:
+// [ceil16(n_tok)/16][K/64][16 tokens][4 planes x 16 B].  Rows past n_tok
+// (padding to 16) are zeros with scale 1 and sum 0.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
+    const float *__restrict__ x, const float *__restrict__ gamma, float eps, int D, int n_tok,
+    uint4 *__restrict__ Xt, float *__restrict__ scales, int *__restrict__ sums) {
+    extern __shared__ __align__(16) int8_t smem[];
+    int8_t *q_lds = smem;
+    float *red = (float *)(smem + ((D + 15) & ~15));
+    int *ired = (int *)(red + 256);
+    const int row = blockIdx.x;
+    float scale = 1.0f;
+    int sumq = 0;
+    if (row < n_tok) {
+        norm_quant_to_lds(x + (size_t)row * D, gamma, eps, D, q_lds, red, ired, scale, sumq);
+    } else {
+        for (int i = threadIdx.x; i < (D >> 4); i += 256) ((int4 *)q_lds)[i] = make_int4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const int KC = D >> 6, tile = row >> 4, c = row & 15;
+    for (int i = threadIdx.x; i < KC * 4; i += 256) {
+        const int kc = i >> 2, g = i & 3;
+        const int src = (kc >> 1) * 128 + g * 32 + (kc & 1) * 16;
+        Xt[(((size_t)tile * KC + kc) * 16 + c) * 4 + g] = *(const uint4 *)(q_lds + src);
+    }
+    if (threadIdx.x == 0) {
+        scales[row] = scale;
+        sums[row] = sumq;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+static size_t gemv_smem(int K) { return (size_t)K + 256 * 4 + 4 * 4 + 64 * 4 + 16; }
+
+template <int PRO, int EPI>
+static int launch(const GemvParams &p, hipStream_t s) {
+    const size_t sm = gemv_smem(p.K);
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI>), dim3(p.N / 16), dim3(256), sm, s, p);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+static int check_shape(int N, int K, bool norm) {
+    OXB_REQUIRE(N > 0 && N % 16 == 0, "ternary GEMV: out_dim %d must be a positive multiple of 16", N);
+    OXB_REQUIRE(K > 0 && K % 128 == 0, "ternary GEMV: in_dim %d must be a positive multiple of 128", K);
+    OXB_REQUIRE(K <= 65536, "ternary GEMV: in_dim %d exceeds 65536", K);
+    OXB_REQUIRE(!norm || K <= 256 * kMaxNormReg,
+                "ternary GEMV: fused norm/quantize supports in_dim <= %d (got %d)",
+                256 * kMaxNormReg, K);
+    return 0;
+}
+
+}  // namespace oxb
+
+using namespace oxb;
+
+#define OXB_STREAM hipStream_t stream = (hipStream_t)stream_
+
+extern "C" int oxb_gemv_i8(const void *W_tiled, const int8_t *xq, const float *xscale,
+                           const int *xsum, const float *wscale, int N, int K, float *y,
+                           int32_t *acc_out, void *stream_) {
+    OXB_STREAM;
+    if (check_shape(N, K, false)) return -1;
+    GemvParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.xq = xq;
+    p.xscale = xscale;
+    p.xsum = xsum;
+    p.y = y;
+    p.acc_out = acc_out;
+    return launch<PRO_INT8, EPI_STORE>(p, stream);
+}
+
+extern "C" int oxb_bitlinear_gemv(const void *W_tiled, const float *x, const float *gamma,
+                                  float eps, const float *wscale, int N, int K, float *y,
+                                  int residual, int32_t *acc_out, int8_t *xq_out,
+                                  float *xscale_out, void *stream_) {
+    OXB_STREAM;
+    if (check_shape(N, K, true)) return -1;
+    GemvParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.x = x;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.y = y;
+    p.acc_out = acc_out;
+    p.xq_out = xq_out;
+    p.xscale_out = xscale_out;
+    return residual ? launch<PRO_QUANT, EPI_RESID>(p, stream)
+                    : launch<PRO_QUANT, EPI_STORE>(p, stream);
+}
+
+extern "C" int oxb_bitlinear_gateup(const void *W_tiled, const float *x, const float *gamma,
+                                    float eps, const float *wscale, int N2, int K, float *h,
+                                    void *stream_) {
+    OXB_STREAM;
+    if (check_shape(N2, K, true)) return -1;
+    GemvParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.wscale = wscale;
+    p.N = N2;
+    p.K = K;
+    p.x = x;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.y = h;
+    return launch<PRO_QUANT, EPI_GATEUP>(p, stream);
+}
+
+extern "C" int oxb_bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma,
+                                 float eps, const float *wscale, int Dq, int Dkv, int hd, int K,
+                                 float *q_out, uint16_t *kcache, uint16_t *vcache, int max_seq,
+                                 const float *rope_cs, const int *pos, void *stream_) {
+    OXB_STREAM;
+    const int N = Dq + 2 * Dkv;
+    if (check_shape(N, K, true)) return -1;
+    OXB_REQUIRE(Dq % hd == 0 && Dkv % hd == 0 && hd % 16 == 0 && Dq % 16 == 0,
+                "qkv: head_dim %d must divide Dq %d and Dkv %d", hd, Dq, Dkv);
+    GemvParams p{};
+    p.W = (const uint4 *)W_tiled;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.x = x;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.q_out = q_out;
+    p.kcache = kcache;
+    p.vcache = vcache;
+    p.rope = (const float2 *)rope_cs;
+    p.pos = pos;
+    p.Dq = Dq;
+    p.Dkv = Dkv;
+    p.hd = hd;
+    p.max_seq = max_seq;
+    return launch<PRO_QUANT, EPI_QKV>(p, stream);
+}
+
+extern "C" int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_rows,
+                                   int D, int8_t *xq, float *scales, int *sums,
+                                   void *stream_) {
+    OXB_STREAM;
+    OXB_REQUIRE(D > 0 && D % 16 == 0 && D <= 256 * kMaxNormReg,
+                "norm_quant_rows: D %d must be a multiple of 16 and <= %d", D, 256 * kMaxNormReg);
+    OXB_REQUIRE(n_rows > 0, "norm_quant_rows: n_rows %d", n_rows);
+    const size_t sm = (size_t)D + 256 * 4 + 16 + 16;
+    hipLaunchKernelGGL(norm_quant_rows_kernel, dim3(n_rows), dim3(256), sm, stream, x, gamma,
+                       eps, D, xq, scales, sums);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float eps, int n_tok,
+                                       int D, void *Xt, float *scales, int *sums, void *stream_) {
+    OXB_STREAM;
+    OXB_REQUIRE(D > 0 && D % 256 == 0 && D <= 256 * kMaxNormReg,
+                "quantize_rows_tiled: D %d must be a multiple of 256 and <= %d", D, 256 * kMaxNormReg);
+    OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
+    const size_t sm = (size_t)D + 256 * 4 + 16 + 16;
+    const int rows = (n_tok + 15) & ~15;
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(rows), dim3(256), sm, stream, x, gamma,
+                       eps, D, n_tok, (uint4 *)Xt, scales, sums);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}

@@ -1,0 +1,188 @@
+/*
+ * oxbitnet_ops.h — MI355X (gfx950) hot-path entry points of liboxbitnet.
+ *
+ * Plain C ABI: device pointers, sizes and an opaque stream (a hipStream_t
+ * passed as void*, NULL = the default stream).  Every function returns 0 on
+ * success and -1 on failure, with the message available from
+ * oxb_last_error() on the calling thread.  Shapes the kernels do not support
+ * are rejected before launch.
+ *
+ * Each entry cites the reference routine it replaces (paths relative to
+ * packages/rust/crates/oxbitnet/src/ in m96-chan/0xBitNet; sh/ = shaders/).
+ *
+ * Data formats
+ *   I2_S natural:  [N][K/4] bytes, 128-element blocks of 32 bytes, element
+ *                  b*128 + g*32 + j at bits (7-2g):(6-2g) of byte b*32 + j,
+ *                  code = w + 1 (model/loader.rs:124-137, shaders/ternary_gemv.wgsl:3-10).
+ *   I2_S tiled:    the same bytes regrouped into 16-row tiles of 16-byte
+ *                  chunks, chunk-major inside a tile (produced once at load
+ *                  by oxb_repack_i2s_tiled; consumed by the GEMV/GEMM).
+ *   KV cache:      [Hkv][max_seq][128] f16 per layer (the reference keeps
+ *                  [max_seq][Hkv][hd] f32, nn/attention.rs:23-48).
+ *   decode state:  int32[8] on the device, indices below.
+ */
+#ifndef OXBITNET_OPS_H
+#define OXBITNET_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXB_ST_POS 0         /* next position (== KV length before the step) */
+#define OXB_ST_TOKEN 1       /* current token id (greedy argmax output)      */
+#define OXB_ST_NGEN 2        /* LM-head invocations since reset              */
+#define OXB_ST_LM_COUNTER 3  /* internal: LM-head last-block ticket          */
+#define OXB_ST_HIST_CAP 4    /* capacity of the token history buffer         */
+#define OXB_STATE_INTS 8
+
+/* ---- errors, device memory, streams, events (plumbing) ----------------- */
+const char *oxb_last_error(void);
+void *oxb_device_malloc(size_t bytes);
+int oxb_device_free(void *p);
+int oxb_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int oxb_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int oxb_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+int oxb_memset_d(void *dst, int value, size_t bytes, void *stream);
+void *oxb_stream_create(void);
+int oxb_stream_destroy(void *stream);
+int oxb_stream_sync(void *stream);
+int oxb_device_sync(void);
+void *oxb_event_create(void);
+int oxb_event_destroy(void *ev);
+int oxb_event_record(void *ev, void *stream);
+int oxb_event_sync(void *ev);
+float oxb_event_elapsed_ms(void *start, void *stop);
+/* name (NUL-terminated, truncated to len), CU count, peak clock kHz, HBM bytes */
+int oxb_device_info(char *name, int len, int *cus, int *clock_khz, size_t *hbm_bytes);
+
+/* ---- load-time layout ---------------------------------------------------- */
+/* Natural I2_S [N][K/4] -> tiled layout.  N % 16 == 0, K % 128 == 0.
+ * Replaces the raw upload of model/weights.rs:23-69 (no repack there). */
+int oxb_repack_i2s_tiled(const void *natural, void *tiled, int N, int K, void *stream);
+
+/* ---- ternary GEMV (decode, one token) ----------------------------------- */
+/* y[n] = ((float)acc[n] * wscale[n]) * xscale[0], acc = sum_k w[n][k]*xq[k]
+ * exactly in int32; xsum[0] = sum_k xq[k].  acc_out optional.
+ * Replaces shaders/ternary_gemv.wgsl:39-97 dispatched by
+ * nn/bitlinear.rs:161-205. */
+int oxb_gemv_i8(const void *W_tiled, const int8_t *xq, const float *xscale, const int *xsum,
+                const float *wscale, int N, int K, float *y, int32_t *acc_out, void *stream);
+
+/* BitLinear for one token: optional RMSNorm (gamma may be NULL) -> absmax int8
+ * quantize -> ternary GEMV; residual != 0 adds into y (y += out).
+ * acc_out / xq_out / xscale_out optional (for parity checks).
+ * Replaces nn/bitlinear.rs:52-97 (n == 1) plus the residual add of
+ * nn/transformer.rs:157 / shaders/elementwise.wgsl. */
+int oxb_bitlinear_gemv(const void *W_tiled, const float *x, const float *gamma, float eps,
+                       const float *wscale, int N, int K, float *y, int residual,
+                       int32_t *acc_out, int8_t *xq_out, float *xscale_out, void *stream);
+
+/* Fused gate|up BitLinear (rows interleaved gate0, up0, gate1, up1, ...):
+ * h[i] = relu(gate_i)^2 * up_i.  Replaces nn/ffn.rs:60-80 (two BitLinears +
+ * shaders/activation.wgsl + shaders/elementwise.wgsl). */
+int oxb_bitlinear_gateup(const void *W_tiled, const float *x, const float *gamma, float eps,
+                         const float *wscale, int N2, int K, float *h, void *stream);
+
+/* Fused q|k|v BitLinear + RoPE on q and k + f16 KV append at *pos.
+ * Replaces nn/attention.rs:97-107,127-184 (three BitLinears, two RoPE
+ * dispatches, two cache copies).  rope_cs: [max_seq][hd/2] (cos, sin) f32. */
+int oxb_bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float eps,
+                      const float *wscale, int Dq, int Dkv, int hd, int K, float *q_out,
+                      uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
+                      const int *pos, void *stream);
+
+/* Host-side RoPE table [max_seq][hd/2] of (cos, sin) f32 with
+ * theta = f32(pos) * pow(base, (-2*i) / hd), as shaders/rope.wgsl:43-48
+ * computes it per element (built once at load instead of per dispatch). */
+int oxb_rope_table(float *cs_host, int max_seq, int hd, float theta_base);
+
+/* ---- prefill ------------------------------------------------------------- */
+/* Per-row optional RMSNorm + absmax int8 quantize of [n_rows][D] f32:
+ * xq int8, scales f32 [n_rows], sums int32 [n_rows] (sum of q, may be NULL).
+ * Replaces shaders/rmsnorm.wgsl + shaders/quantize.wgsl (nn/bitlinear.rs:60-82). */
+int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_rows, int D,
+                        int8_t *xq, float *scales, int *sums, void *stream);
+
+/* Ternary GEMM on int8 MFMA: Y[t][n] = (float)acc[t][n] * (wscale[n] * xscale[t]).
+ * epilogue: 0 store, 1 residual add (Y += ...), 2 gate|up fusion (Y is
+ * [n_tok][N/2]), 3 q|k|v + RoPE + KV append (qkv_* arguments used).
+ * Replaces shaders/ternary_gemm.wgsl:40-136 dispatched by nn/bitlinear.rs:207-247. */
+int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
+                const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,
+                int epilogue, void *stream);
+int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
+                 const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
+                 float *q_out, uint16_t *kcache, uint16_t *vcache, int max_seq,
+                 const float *rope_cs, void *stream);
+
+/* ---- attention ------------------------------------------------------------ */
+/* Decode attention for one token over L = *pos + 1 cached positions.
+ * part_o: [H][ceil(max_seq/64)][128] f32, part_ml: [H][ceil(max_seq/64)][2],
+ * counters: int[Hkv] zeroed once at allocation (the kernel leaves them zero).
+ * out: [H*128] f32.  Replaces nn/attention.rs:109-118 (scores, softmax, P.V). */
+int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                    const int *pos, int H, int Hkv, int hd, int max_seq, float *part_o,
+                    float *part_ml, int *counters, float *out, void *stream);
+
+/* Causal prefill attention for n_tok queries at positions pos0.. (GQA group 4).
+ * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
+int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
+                     int pos0, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
+
+/* ---- embedding / LM head --------------------------------------------------- */
+/* x[t] = E[ids[t]] (f16 -> f32; out-of-range ids give zeros); ids == NULL reads
+ * the decode state's token.  Replaces nn/model.rs:312-352. */
+int oxb_embedding(const uint16_t *E, int V, int D, const int *ids, int n_tok, const int *state,
+                  float *x, void *stream);
+
+/* Final RMSNorm of x -> tied f16 LM head -> logits [V] -> greedy argmax
+ * (lowest index on ties) written to state[OXB_ST_TOKEN], appended to
+ * tok_hist (if state[OXB_ST_HIST_CAP] allows), state[OXB_ST_POS] += advance.
+ * part: float[2 * oxb_lm_head_partials()].  Replaces nn/model.rs:226-262,
+ * 393-448 plus read_logits (:269-298) and sampling.rs with top_k = 1. */
+int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const uint16_t *E, int V,
+                       int D, float *logits, float *part, int *state, int *tok_hist,
+                       int advance, void *stream);
+int oxb_lm_head_partials(void);
+
+/* ---- model (ids level) ------------------------------------------------------
+ * The ids-level seam the parity and benchmark harnesses drive: the
+ * reference's generate_from_ids is private (lib.rs:130) and stops on EOS. */
+typedef struct oxb_model oxb_model;
+
+typedef struct oxb_model_info {
+    int n_layers, hidden, ffn, heads, kv_heads, head_dim, vocab, max_seq;
+    float rms_eps, rope_theta;
+    int relu2;           /* 1: ReLU^2 gate (arch "bitnet-25"), 0: SiLU */
+    size_t weight_bytes; /* device bytes held by weights */
+} oxb_model_info;
+
+/* Parse a GGUF (v2/v3) file, upload and repack.  max_seq <= 0 means 4096
+ * (lib.rs:93).  Replaces BitNet::load's model half (lib.rs:77-94,
+ * model/loader.rs:75-173, nn/model.rs:42-190). */
+oxb_model *oxb_model_load(const char *path, int max_seq);
+void oxb_model_free(oxb_model *m);
+int oxb_model_get_info(const oxb_model *m, oxb_model_info *out);
+/* KV length back to 0 (nn/model.rs:300-310). */
+int oxb_model_reset(oxb_model *m);
+/* forward(ids): prefill n >= 1 tokens at the current position; writes the
+ * last token's logits to logits_host (nullable) and returns the greedy
+ * token (>= 0) or -1.  nn/model.rs:193-298. */
+int oxb_model_forward(oxb_model *m, const int32_t *ids, int n, float *logits_host);
+/* n_steps greedy decode steps from the current token, each one replay of a
+ * captured hipGraph; tokens_out[n_steps] (host).  Returns 0 / -1. */
+int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *tokens_out);
+/* Current KV length. */
+int oxb_model_position(const oxb_model *m);
+/* Overwrite the current token (host sampling between decode steps). */
+int oxb_model_set_token(oxb_model *m, int32_t tok);
+/* One decode step from the current token, logits to host (nullable). */
+int oxb_model_step(oxb_model *m, float *logits_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,132 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every symbol the
+public headers declare, and its host logic (defaults, argument and GGUF
+validation) behaves like the reference's FFI (oxbitnet-ffi/src/lib.rs).
+No GPU compute is called here."""
+import ctypes as C
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, pkg, synth
+
+nat = pkg._native
+
+
+def header_functions():
+    names = set()
+    for h in ("oxbitnet.h", "oxbitnet_ops.h"):
+        src = open(os.path.join(ROOT, "include", h)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b((?:oxbitnet|oxb)_\w+)\s*\(", src, re.M):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    L = nat.lib()
+    names = header_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # and the ctypes table covers them all
+    assert set(names) <= set(nat.SIGNATURES)
+
+
+def test_default_options_match_reference():
+    L = nat.lib()
+    o = L.oxbitnet_default_generate_options()
+    assert (o.max_tokens, o.top_k, o.repeat_last_n) == (256, 50, 64)
+    assert o.temperature == pytest.approx(1.0) and o.repeat_penalty == pytest.approx(1.1)
+    lo = L.oxbitnet_default_load_options()
+    assert not lo.on_progress and not lo.progress_userdata and not lo.cache_dir
+    assert C.sizeof(nat.GenerateOptions) == 40          # LP64 layout of the reference struct
+    assert C.sizeof(nat.LoadProgress) == 32
+    assert C.sizeof(nat.LoadOptions) == 24
+
+
+def _err():
+    m = nat.lib().oxbitnet_error_message()
+    return m.decode() if m else None
+
+
+def test_load_argument_errors():
+    L = nat.lib()
+    assert not L.oxbitnet_load(None, None)
+    assert _err() == "source must not be NULL"
+    assert not L.oxbitnet_load(b"/nonexistent/model.gguf", None)
+    assert _err().startswith("IO error")
+    assert not L.oxbitnet_load(b"https://example.com/model.gguf", None)
+    assert _err().startswith("HTTP error")
+    assert not L.oxbitnet_load(b"\xff\xfe", None)
+    assert _err().startswith("invalid UTF-8")
+    L.oxbitnet_free(None)  # no-op
+    assert L.oxbitnet_generate(None, b"hi", None, nat.TokenFn(), None) == -1
+    assert _err() == "model must not be NULL"
+    assert L.oxbitnet_chat(None, None, 0, None, nat.TokenFn(), None) == -1
+    assert _err() == "model must not be NULL"
+
+
+def _write(tmp_path, name, data: bytes):
+    p = tmp_path / name
+    p.write_bytes(data)
+    return str(p).encode()
+
+
+def test_gguf_parse_errors(tmp_path):
+    L = nat.lib()
+    assert not L.oxbitnet_load(_write(tmp_path, "bad.gguf", b"GGML" + b"\0" * 60), None)
+    assert _err() == "Invalid GGUF magic: 0x4c4d4747 (expected 0x46554747)"
+    assert not L.oxbitnet_load(_write(tmp_path, "v9.gguf", struct.pack("<IIQQ", 0x46554747, 9, 0, 0)), None)
+    assert _err() == "Unsupported GGUF version: 9"
+    assert not L.oxbitnet_load(_write(tmp_path, "short.gguf", struct.pack("<II", 0x46554747, 3)), None)
+    assert _err().startswith("GGUF parse error: Unexpected EOF")
+    kv = synth._s("x") + struct.pack("<I", 77)
+    assert not L.oxbitnet_load(_write(tmp_path, "meta.gguf",
+                                      struct.pack("<IIQQ", 0x46554747, 3, 0, 1) + kv), None)
+    assert _err() == "Unknown GGUF metadata type: 77"
+    t = synth._s("w") + struct.pack("<IQQ", 1, 4, 99) + struct.pack("<Q", 0)
+    assert not L.oxbitnet_load(_write(tmp_path, "type.gguf",
+                                      struct.pack("<IIQQ", 0x46554747, 3, 1, 0) + t), None)
+    assert _err() == "Unsupported GGML type: 99"
+
+
+def test_missing_tensor_error(tmp_path):
+    cfg = synth.small_config(n_layers=1, vocab=300)
+    path = str(tmp_path / "m.gguf")
+    synth.write_gguf(path, cfg, seed=3)
+    # drop blk.0.attn_q.weight by renaming it in the file (same length)
+    data = bytearray(open(path, "rb").read())
+    i = data.find(b"blk.0.attn_q.weight")
+    data[i:i + len(b"blk.0.attn_q.weight")] = b"blk.0.attn_Q.weight"
+    p2 = _write(tmp_path, "m2.gguf", bytes(data))
+    assert not nat.lib().oxbitnet_load(p2, None)
+    assert _err() == 'Missing weight tensor: "model.layers.0.self_attn.q_proj.weight"'
+
+
+def test_synthetic_writer_roundtrip(tmp_path):
+    import oracle as O
+    cfg = synth.small_config(n_layers=1, vocab=300)
+    path = str(tmp_path / "s.gguf")
+    synth.write_gguf(path, cfg, seed=5)
+    meta, t = synth.read_gguf_tensors(path)
+    assert meta["general.architecture"] == "bitnet-25"
+    assert len(meta["tokenizer.ggml.tokens"]) == 300
+    packed, scale = t["blk.0.attn_q.weight"]
+    assert packed.shape == (512, 128) and 0.012 < scale < 0.02
+    w = synth.i2s_unpack(packed, 512)
+    assert set(np.unique(w)) <= {-1, 0, 1}
+    # product packer == oracle packer (ts/i2s-pack.ts restatement)
+    assert np.array_equal(synth.i2s_pack(w), O.i2s_pack(w))
+    assert np.array_equal(O.i2s_unpack(packed, 512), w)
+    frac = np.bincount(w.reshape(-1) + 1) / w.size
+    assert np.all(np.abs(frac - 1 / 3) < 0.01)
+    assert t["token_embd.weight"].shape == (300, 512)
+
+
+def test_i2s_pack_known_bytes():
+    for fill, u32 in ((-1, 0), (1, 0xAAAAAAAA), (0, 0x55555555)):
+        b = synth.i2s_pack(np.full((1, 128), fill, np.int8))
+        assert int(b[0, :4].view("<u4")[0]) == u32

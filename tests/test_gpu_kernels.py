@@ -1,0 +1,304 @@
+"""Parity of each HIP hot-path kernel against the CPU oracle, through the C ABI.
+
+Bars: int8 activations, int32 accumulators and every f32 value the oracle
+computes with the same operation sequence are compared bit for bit; the
+attention and LM-head sums (different reduction order by design, f16 KV) are
+compared with an explicit tolerance, tighter than the 1e-3 relative bound
+the path is held to.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import ops, synth, ternary
+
+pytestmark = pytest.mark.gpu
+
+
+def _scale_config1(seed):
+    # 1 / mean|m| of a seeded N(0, 0.02) master (the single-GEMV workload)
+    m = np.random.default_rng([seed, 99]).standard_normal(1 << 16) * 0.02
+    return float(np.float32(1.0 / np.abs(m).mean()))
+
+
+def _gemv_case(N, K, seed):
+    rng = np.random.default_rng(seed)
+    w = ternary(rng, N, K)
+    Wn = synth.i2s_pack(w)
+    x = rng.standard_normal(K).astype(np.float32)
+    q, s = O.quantize(x)
+    return Wn, q[0], float(s[0])
+
+
+@pytest.mark.parametrize("N,K", [(6912, 2560), (16, 128), (48, 384), (2560, 6912)])
+def test_gemv_i8_bitexact(N, K):
+    Wn, xq, xs = _gemv_case(N, K, seed=N + K)
+    ws = np.full(N, _scale_config1(1), np.float32)
+    acc_o, y_o = O.gemv(Wn, xq, ws, xs, K)
+    Wt = ops.upload_ternary(Wn, K)
+    acc, y = ops.gemv_i8(Wt, xq, xs, ws, N, K)
+    assert np.array_equal(acc, acc_o)
+    assert np.array_equal(y.view(np.uint32), y_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K", [(28672, 8192), (8192, 28672)])
+def test_gemv_i8_sweep_shapes(N, K):
+    Wn, xq, xs = _gemv_case(N, K, seed=7)
+    ws = np.full(N, 0.75, np.float32)
+    acc_o, y_o = O.gemv(Wn, xq, ws, xs, K)
+    Wt = ops.upload_ternary(Wn, K)
+    acc, y = ops.gemv_i8(Wt, xq, xs, ws, N, K)
+    assert np.array_equal(acc, acc_o)
+    assert np.array_equal(y, y_o)
+
+
+def test_gemv_extremes_and_zero():
+    K = 28672
+    N = 32
+    w = np.ones((N, K), np.int8)
+    w[1::2] = -1
+    w[16:] = 0
+    Wt = ops.upload_ternary(synth.i2s_pack(w), K)
+    for xv in (127, -127):
+        xq = np.full(K, xv, np.int8)
+        acc, y = ops.gemv_i8(Wt, xq, 1.0, np.ones(N, np.float32), N, K)
+        exp = np.where(np.arange(N) < 16, np.where(np.arange(N) % 2 == 0, 1, -1), 0) * xv * K
+        assert np.array_equal(acc, exp)
+    # the reference's known answer (ternary-gemv.test.ts:35-53): +-128 at K=128
+    w2 = np.zeros((16, 128), np.int8)
+    w2[0], w2[1] = 1, -1
+    acc, y = ops.gemv_i8(ops.upload_ternary(synth.i2s_pack(w2), 128), np.ones(128, np.int8), 1.0,
+                         np.ones(16, np.float32), 16, 128)
+    assert acc[:2].tolist() == [128, -128] and y[:2].tolist() == [128.0, -128.0]
+    assert not acc[2:].any()
+
+
+def test_gemv_rejects_bad_shapes():
+    Wt = ops.DeviceArray((1024,), np.uint8)
+    with pytest.raises(ops.NativeError, match="multiple of 16"):
+        ops.gemv_i8(Wt, np.zeros(128, np.int8), 1.0, np.ones(8, np.float32), 8, 128)
+    with pytest.raises(ops.NativeError, match="multiple of 128"):
+        ops.gemv_i8(Wt, np.zeros(64, np.int8), 1.0, np.ones(16, np.float32), 16, 64)
+
+
+@pytest.mark.parametrize("K,N,norm,resid", [(2560, 2560, True, True), (6912, 2560, True, True),
+                                            (2560, 6912, False, False), (2560, 640, True, False)])
+def test_bitlinear_gemv_fused_norm_quant(K, N, norm, resid):
+    rng = np.random.default_rng(K * 7 + N)
+    w = ternary(rng, N, K)
+    Wn = synth.i2s_pack(w)
+    x = (rng.standard_normal(K) * 3).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32) if norm else None
+    ws = np.full(N, 0.0163, np.float32)
+    r = rng.standard_normal(N).astype(np.float32) if resid else None
+    # oracle: rs/nn/bitlinear.rs:52-97 (eps 1e-5)
+    h = O.rmsnorm(x, g, 1e-5) if norm else x[None]
+    q, s = O.quantize(h)
+    acc_o, y_o = O.gemv(Wn, q[0], ws, s[0], K)
+    if resid:
+        y_o = O.add(r, y_o)
+    Wt = ops.upload_ternary(Wn, K)
+    acc, y, xq, xs = ops.bitlinear_gemv(Wt, x, g, 1e-5, ws, N, K, residual=r)
+    assert np.array_equal(xq, q[0])
+    assert np.float32(xs) == s[0]
+    assert np.array_equal(acc, acc_o)
+    assert np.array_equal(y, y_o)
+
+
+def test_norm_quant_rows_bitexact():
+    rng = np.random.default_rng(11)
+    for D in (2560, 6912, 16):
+        x = (rng.standard_normal((5, D)) * rng.uniform(0.1, 10, (5, 1))).astype(np.float32)
+        x[2] = 0.0  # all-zero row: scale 1, q 0 (quantize.test.ts:43-52)
+        g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+        q, s, sm = ops.norm_quant_rows(x, g, 1e-5)
+        qo, so = O.quantize(O.rmsnorm(x, g, 1e-5))
+        assert np.array_equal(q, qo) and np.array_equal(s, so)
+        assert np.array_equal(sm, qo.astype(np.int64).sum(1))
+        q2, s2, _ = ops.norm_quant_rows(x, None, 0.0)
+        qo2, so2 = O.quantize(x)
+        assert np.array_equal(q2, qo2) and np.array_equal(s2, so2)
+
+
+def test_gateup_fused_bitexact():
+    rng = np.random.default_rng(12)
+    K, F = 2560, 6912
+    wg, wu = ternary(rng, F, K), ternary(rng, F, K)
+    inter = np.empty((2 * F, K), np.int8)
+    inter[0::2], inter[1::2] = wg, wu
+    ws = np.empty(2 * F, np.float32)
+    ws[0::2], ws[1::2] = 0.0151, 0.0172
+    x = rng.standard_normal(K).astype(np.float32) * 5
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    q, s = O.quantize(O.rmsnorm(x, g, 1e-5))
+    _, yg = O.gemv(synth.i2s_pack(wg), q[0], 0.0151, s[0], K)
+    _, yu = O.gemv(synth.i2s_pack(wu), q[0], 0.0172, s[0], K)
+    h_o = O.mul(O.relu2(yg), yu)  # rs/nn/ffn.rs:60-80
+    h = ops.bitlinear_gateup(ops.upload_ternary(synth.i2s_pack(inter), K), x, g, 1e-5, ws, 2 * F, K)
+    assert np.array_equal(h, h_o)
+
+
+def rope_table(max_seq, hd, theta):
+    cs = np.zeros((max_seq, hd // 2, 2), np.float32)
+    ops.check(ops.lib().oxb_rope_table(cs.ctypes.data, max_seq, hd, theta), "rope")
+    return cs
+
+
+def test_rope_table_matches_oracle():
+    cs = rope_table(300, 128, 500000.0)
+    unit = np.zeros((300, 1, 128), np.float32)
+    unit[:, :, 0::2] = 1.0
+    for p in (0, 1, 17, 299):
+        y = O.rope(unit[p].reshape(-1), 1, 1, 128, p, 500000.0).reshape(64, 2)
+        assert np.array_equal(cs[p], y), p
+
+
+def test_qkv_rope_kv_append():
+    rng = np.random.default_rng(13)
+    K, H, Hkv, hd, S = 2560, 20, 5, 128, 64
+    Dq, Dkv = H * hd, Hkv * hd
+    wq, wk, wv = ternary(rng, Dq, K), ternary(rng, Dkv, K), ternary(rng, Dkv, K)
+    sq, sk, sv = 0.016, 0.017, 0.015
+    x = rng.standard_normal(K).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    pos = 37
+    # oracle: three BitLinears on the same normed input, RoPE at pos
+    h = O.rmsnorm(x, g, 1e-5)
+    q8, s8 = O.quantize(h)
+    _, q = O.gemv(synth.i2s_pack(wq), q8[0], sq, s8[0], K)
+    _, k = O.gemv(synth.i2s_pack(wk), q8[0], sk, s8[0], K)
+    _, v = O.gemv(synth.i2s_pack(wv), q8[0], sv, s8[0], K)
+    qr = O.rope(q, 1, H, hd, pos, 500000.0)
+    kr = O.rope(k, 1, Hkv, hd, pos, 500000.0)
+    fused = np.concatenate([wq, wk, wv])
+    ws = np.concatenate([np.full(Dq, sq), np.full(Dkv, sk), np.full(Dkv, sv)]).astype(np.float32)
+    Wt = ops.upload_ternary(synth.i2s_pack(fused), K)
+    dx = ops.DeviceArray.from_host(x)
+    dg = ops.DeviceArray.from_host(g)
+    dws = ops.DeviceArray.from_host(ws)
+    dq = ops.DeviceArray((Dq,), np.float32)
+    kc = ops.DeviceArray((Hkv * S * hd,), np.uint16, zero=True)
+    vc = ops.DeviceArray((Hkv * S * hd,), np.uint16, zero=True)
+    rope = ops.DeviceArray.from_host(rope_table(S, hd, 500000.0))
+    dpos = ops.DeviceArray.from_host(np.array([pos], np.int32))
+    ops.check(ops.lib().oxb_bitlinear_qkv(Wt.ptr, dx.ptr, dg.ptr, 1e-5, dws.ptr, Dq, Dkv, hd, K,
+                                          dq.ptr, kc.ptr, vc.ptr, S, rope.ptr, dpos.ptr, None), "qkv")
+    ops.sync()
+    assert np.array_equal(dq.download(), qr)
+    kh = kc.download().view(np.float16).reshape(Hkv, S, hd)
+    vh = vc.download().view(np.float16).reshape(Hkv, S, hd)
+    assert np.array_equal(kh[:, pos].reshape(-1), kr.astype(np.float16))
+    assert np.array_equal(vh[:, pos].reshape(-1), v.astype(np.float16))
+    mask = np.ones(S, bool)
+    mask[pos] = False
+    assert not kh[:, mask].any() and not vh[:, mask].any()
+
+
+def _oracle_attn(q, kc16, vc16, n, S, H, Hkv, hd):
+    # caches [Hkv][S][hd] f16 -> the reference layout [S][Hkv][hd] f32
+    k = kc16[:, :S].astype(np.float32).transpose(1, 0, 2).copy()
+    v = vc16[:, :S].astype(np.float32).transpose(1, 0, 2).copy()
+    return O.attention(q, k, v, n, S, H, Hkv, hd)
+
+
+@pytest.mark.parametrize("pos", [0, 63, 64, 200, 511])
+def test_attn_decode(pos):
+    rng = np.random.default_rng(pos + 1)
+    H, Hkv, hd, S = 20, 5, 128, 512
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
+    out, cnt = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S)
+    ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+    assert not cnt.any()  # counters left at zero for the next launch / graph replay
+
+
+def test_attn_prefill_causal():
+    rng = np.random.default_rng(21)
+    H, Hkv, hd, S = 20, 5, 128, 256
+    pos0, n = 30, 100
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
+    out = ops.attn_prefill(q, kc, vc, n, pos0, H, Hkv, hd, S)
+    ref = _oracle_attn(q.reshape(-1), kc, vc, n, pos0 + n, H, Hkv, hd).reshape(n, H * hd)
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
+                                   (32, 256, 65)])
+def test_gemm_mfma_bitexact(N, K, n):
+    rng = np.random.default_rng(N + n)
+    w = ternary(rng, N, K)
+    Wn = synth.i2s_pack(w)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    ws = np.full(N, 0.0158, np.float32)
+    q, s = O.quantize(O.rmsnorm(x, g, 1e-5))
+    acc_o, Y_o = O.gemm(Wn, q, ws, s, K)
+    Wt = ops.upload_ternary(Wn, K)
+    acc, Y, sc = ops.gemm(Wt, x, g, 1e-5, ws, N, K)
+    assert np.array_equal(sc, s)
+    assert np.array_equal(acc, acc_o)
+    assert np.array_equal(Y, Y_o)
+
+
+def test_gemm_epilogues():
+    rng = np.random.default_rng(31)
+    K, F, n = 2560, 6912, 40
+    wg, wu = ternary(rng, F, K), ternary(rng, F, K)
+    inter = np.empty((2 * F, K), np.int8)
+    inter[0::2], inter[1::2] = wg, wu
+    ws = np.empty(2 * F, np.float32)
+    ws[0::2], ws[1::2] = 0.0151, 0.0172
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    q, s = O.quantize(x)
+    _, yg = O.gemm(synth.i2s_pack(wg), q, 0.0151, s, K)
+    _, yu = O.gemm(synth.i2s_pack(wu), q, 0.0172, s, K)
+    _, H, _ = ops.gemm(ops.upload_ternary(synth.i2s_pack(inter), K), x, None, 0.0, ws, 2 * F, K,
+                    epilogue=2)
+    assert np.array_equal(H, O.mul(O.relu2(yg), yu))
+    # residual
+    wd = ternary(rng, K, F)
+    h = rng.standard_normal((n, F)).astype(np.float32)
+    r = rng.standard_normal((n, K)).astype(np.float32)
+    qh, sh = O.quantize(h)
+    _, yd = O.gemm(synth.i2s_pack(wd), qh, 0.02, sh, F)
+    _, R, _ = ops.gemm(ops.upload_ternary(synth.i2s_pack(wd), F), h, None, 0.0,
+                    np.full(K, 0.02, np.float32), K, F, epilogue=1, Y0=r)
+    assert np.array_equal(R, O.add(r, yd))
+
+
+def test_lm_head_argmax():
+    rng = np.random.default_rng(41)
+    V, D = 5003, 2560
+    E = (rng.standard_normal((V, D)) * 0.02).astype(np.float16)
+    x = rng.standard_normal(D).astype(np.float32) * 4
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    logits, tok, st, hist = ops.lm_head_argmax(x, g, 1e-5, E)
+    h = O.rmsnorm(x, g, 1e-5)[0]
+    ref = O.lm_head(h, E.view(np.uint16))
+    np.testing.assert_allclose(logits, ref, rtol=1e-4, atol=1e-5)
+    assert tok == int(np.argmax(logits)) == O.argmax(ref)
+    assert st[ops.STATE_POS] == 1 and st[ops.STATE_NGEN] == 1 and st[ops.STATE_LM_COUNTER] == 0
+    assert hist[0] == tok
+
+
+def test_lm_head_tie_lowest_index():
+    D, V = 512, 4000
+    E = np.zeros((V, D), np.float16)
+    E[[17, 2500, 3999], :] = 1.0  # three identical best rows
+    logits, tok, _, _ = ops.lm_head_argmax(np.ones(D, np.float32), np.ones(D, np.float32), 1e-5, E)
+    assert tok == 17
+
+
+def test_embedding_gather():
+    rng = np.random.default_rng(51)
+    E = rng.standard_normal((300, 512)).astype(np.float16)
+    ids = np.array([0, 299, 300, 5, -1], np.int32)
+    x = ops.embedding(E, ids)
+    assert np.array_equal(x[0], E[0].astype(np.float32))
+    assert np.array_equal(x[1], E[299].astype(np.float32))
+    assert not x[2].any() and not x[4].any()  # out of vocab -> zeros (embedding.wgsl:38-45)
+    assert np.array_equal(x[3], E[5].astype(np.float32))
