@@ -90,7 +90,7 @@ SIGNATURES = {
     "oxb_gemm_i8": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, vp]),
     "oxb_gemm_qkv": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32,
                                vp, vp]),
-    "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
+    "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "oxb_attn_prefill": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "oxb_embedding": (C.c_int, [vp, i32, i32, vp, i32, vp, vp, vp]),
     "oxb_lm_head_argmax": (C.c_int, [vp, vp, f32, vp, i32, i32, vp, vp, vp, vp, i32, vp]),

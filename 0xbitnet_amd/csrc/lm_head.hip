@@ -67,6 +67,10 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) hv[j][i] = h_lds[(j * 64 + lane) * 8 + i];
 
+    // One wave per row, reproducing sh/f32_matmul.wgsl:51-68 exactly: shader
+    // thread t accumulates pairs dh = t, t+256, ... as acc += h*e0; acc += h*e1,
+    // then the halving tree.  Lane l plays threads 4l .. 4l+3, so its 16-byte
+    // load j holds the pairs dh = 256j + 4l + i of those four threads.
     float best = -INFINITY;
     int besti = 0x7fffffff;
     const int rowstride = D >> 3;   // uint4 per row
@@ -81,18 +85,31 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
         }
 #pragma unroll
         for (int q = 0; q < kLmRowsInFlight; ++q) {
-            float acc = 0.0f;
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
                 const __half2 *hh = (const __half2 *)&e[q][j];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float2 f = __half22float2(hh[i]);
-                    acc = fmaf(hv[j][2 * i], f.x, acc);
-                    acc = fmaf(hv[j][2 * i + 1], f.y, acc);
+                    const float2 f = __half22float2(hh[i]);
+                    float m0 = hv[j][2 * i] * f.x;
+                    a[i] = a[i] + m0;
+                    float m1 = hv[j][2 * i + 1] * f.y;
+                    a[i] = a[i] + m1;
                 }
             }
-            acc = wave_sum(acc);
+            // tree: strides 128..4 pair lane l with lane l + stride/4
+#pragma unroll
+            for (int sl = 32; sl >= 1; sl >>= 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float o = __shfl_down(a[i], sl, 64);
+                    a[i] = a[i] + o;
+                }
+            }
+            a[0] = a[0] + a[2];   // stride 2
+            a[1] = a[1] + a[3];
+            const float acc = __shfl(a[0] + a[1], 0, 64);  // stride 1, broadcast
             const int row = rb + q;
             if (row < r1) {
                 if (lane == 0) p.logits[row] = acc;

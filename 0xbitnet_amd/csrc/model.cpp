@@ -420,21 +420,15 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->q = (float *)m->dalloc((size_t)Dq * 4);
     m->attn = (float *)m->dalloc((size_t)Dq * 4);
     m->h = (float *)m->dalloc((size_t)F * 4);
-    const int max_split = (m->max_seq + 63) / 64;
-    m->part_o = (float *)m->dalloc((size_t)H * max_split * hd * 4);
-    m->part_ml = (float *)m->dalloc((size_t)H * max_split * 2 * 4);
-    m->attn_counters = (int *)m->dalloc((size_t)Hkv * 4);
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->lm_part = (float *)m->dalloc((size_t)oxb_lm_head_partials() * 2 * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->part_o ||
-        !m->part_ml || !m->attn_counters || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_elems * 2) != hipSuccess ||
-        hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess ||
-        hipMemset(m->attn_counters, 0, (size_t)Hkv * 4) != hipSuccess) {
+        hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess) {
         set_error("hipMemset failed");
         return nullptr;
     }
@@ -472,8 +466,7 @@ int oxb_model::enqueue_decode_step() {
         if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
                               max_seq, rope, posp, s))
             return -1;
-        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, part_o, part_ml,
-                            attn_counters, attn, s))
+        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, attn, s))
             return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
         if (oxb_bitlinear_gemv(L.wo, attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr, nullptr,

@@ -33,8 +33,6 @@ struct oxb_model {
 
     // decode buffers
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
-    float *part_o = nullptr, *part_ml = nullptr;
-    int *attn_counters = nullptr;
     float *logits = nullptr, *lm_part = nullptr;
     int *state = nullptr, *tok_hist = nullptr;
     int hist_cap = 0;

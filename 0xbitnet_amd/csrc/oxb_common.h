@@ -127,6 +127,28 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
+// exp(x) for the softmax, fixed so that host and device give the same bits:
+// Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2, so k*head is exact,
+// plus the tail), degree-7 Taylor polynomial of e^r by Horner, ldexp by k.
+// Every step is a separately rounded f32 op (no contraction); ~2 ulp.
+__device__ inline float oxb_expf(float x) {
+    if (x != x) return x;
+    if (x < -103.972084f) return 0.0f;
+    if (x > 88.7228394f) return __builtin_inff();
+    const float kf = rintf(x * 1.44269502f);
+    float r = x - kf * 0.693145751953125f;
+    r = r - kf * 1.42860677e-06f;
+    float p = 1.98412701e-04f;
+    p = p * r + 1.38888892e-03f;
+    p = p * r + 8.33333377e-03f;
+    p = p * r + 4.16666679e-02f;
+    p = p * r + 1.66666672e-01f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)kf);
+}
+
 // sh/quantize.wgsl:59,68,71 for one value given the row absmax.
 __device__ inline int quant_one(float v, float inv) {
     int q = (int)rintf(v * inv);

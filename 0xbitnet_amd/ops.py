@@ -198,15 +198,11 @@ def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int,
     dk = DeviceArray.from_host(np.ascontiguousarray(kcache, np.float16).view(np.uint16))
     dv = DeviceArray.from_host(np.ascontiguousarray(vcache, np.float16).view(np.uint16))
     dpos = DeviceArray.from_host(np.array([pos], np.int32))
-    ms = (max_seq + 63) // 64
-    po = DeviceArray((H * ms * hd,), np.float32)
-    pm = DeviceArray((H * ms * 2,), np.float32)
-    cnt = DeviceArray((Hkv,), np.int32, zero=True)
     out = DeviceArray((H * hd,), np.float32)
-    check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, po.ptr, pm.ptr,
-                                cnt.ptr, out.ptr, None), "attn_decode")
+    check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, out.ptr,
+                                None), "attn_decode")
     sync()
-    return out.download(), cnt.download()
+    return out.download()
 
 
 def attn_prefill(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, n_tok: int, pos0: int,

@@ -119,15 +119,15 @@ int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, cons
                  const float *rope_cs, void *stream);
 
 /* ---- attention ------------------------------------------------------------ */
-/* Decode attention for one token over L = *pos + 1 cached positions.
- * part_o: [H][ceil(max_seq/64)][128] f32, part_ml: [H][ceil(max_seq/64)][2],
- * counters: int[Hkv] zeroed once at allocation (the kernel leaves them zero).
- * out: [H*128] f32.  Replaces nn/attention.rs:109-118 (scores, softmax, P.V). */
+/* Decode attention for one token over L = *pos + 1 cached positions, in the
+ * reference's order (f32 result identical to the shaders' arithmetic on the
+ * f16-rounded cache).  q, out: [H*128] f32.  Replaces nn/attention.rs:109-118
+ * (scores, softmax, P.V dispatches). */
 int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                    const int *pos, int H, int Hkv, int hd, int max_seq, float *part_o,
-                    float *part_ml, int *counters, float *out, void *stream);
+                    const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
+                    void *stream);
 
-/* Causal prefill attention for n_tok queries at positions pos0.. (GQA group 4).
+/* Causal prefill attention for n_tok queries at positions pos0.., same order.
  * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
                      int pos0, int H, int Hkv, int hd, int max_seq, float *out, void *stream);

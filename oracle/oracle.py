@@ -60,6 +60,8 @@ def _declare(L):
     L.oxo_f16_to_f32.restype = C.c_float
     L.oxo_f32_to_f16.argtypes = [C.c_float]
     L.oxo_f32_to_f16.restype = C.c_uint16
+    L.oxo_expf.argtypes = [C.c_float]
+    L.oxo_expf.restype = C.c_float
     L.oxo_i2s_pack_row.argtypes = [_i8p, C.c_int, _u8p]
     L.oxo_i2s_get.argtypes = [_u8p, C.c_int]
     L.oxo_i2s_get.restype = C.c_int
@@ -101,6 +103,10 @@ def f16_to_f32(h: int) -> float:
 
 def f32_to_f16(f: float) -> int:
     return lib().oxo_f32_to_f16(f)
+
+
+def expf(x: float) -> float:
+    return lib().oxo_expf(x)
 
 
 # ---- I2_S -----------------------------------------------------------------

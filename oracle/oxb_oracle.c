@@ -73,6 +73,29 @@ uint16_t oxo_f32_to_f16(float f) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* exp: Cody-Waite range reduction + degree-7 Taylor polynomial.  Every op is */
+/* a separately rounded f32 op, so the same steps give the same bits on any  */
+/* IEEE machine without FMA contraction.                                     */
+/* ------------------------------------------------------------------------ */
+float oxo_expf(float x) {
+    if (x != x) return x;
+    if (x < -103.972084f) return 0.0f;
+    if (x > 88.7228394f) return INFINITY;
+    const float kf = rintf(x * 1.44269502f);   /* round(x / ln2) */
+    float r = x - kf * 0.693145751953125f;     /* ln2 head: k*head is exact */
+    r = r - kf * 1.42860677e-06f;              /* ln2 tail */
+    float p = 1.98412701e-04f;                 /* 1/7! */
+    p = p * r + 1.38888892e-03f;               /* 1/6! */
+    p = p * r + 8.33333377e-03f;               /* 1/5! */
+    p = p * r + 4.16666679e-02f;               /* 1/4! */
+    p = p * r + 1.66666672e-01f;               /* 1/3! */
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)kf);
+}
+
+/* ------------------------------------------------------------------------ */
 /* The shaders' workgroup reduction: 256 strided partials, then a halving    */
 /* tree (sh/rmsnorm.wgsl:41-55, sh/softmax.wgsl:58-71, sh/f32_matmul.wgsl). */
 /* ------------------------------------------------------------------------ */
@@ -245,7 +268,7 @@ void oxo_relu2(const float *x, size_t n, float *y) {
 }
 
 void oxo_silu(const float *x, size_t n, float *y) {
-    for (size_t i = 0; i < n; i++) y[i] = x[i] / (1.0f + expf(-x[i])); /* :36 */
+    for (size_t i = 0; i < n; i++) y[i] = x[i] / (1.0f + oxo_expf(-x[i])); /* :36 */
 }
 
 void oxo_add(const float *a, const float *b, size_t n, float *y) {
@@ -294,11 +317,11 @@ static void softmax_row(const float *in, int D, float *out) {
     float row_max = tree_max(p);
     for (int tid = 0; tid < WG; tid++) {
         float s = 0.0f;
-        for (int c = tid; c < D; c += WG) s = s + expf(in[c] - row_max);
+        for (int c = tid; c < D; c += WG) s = s + oxo_expf(in[c] - row_max);
         p[tid] = s;
     }
     float inv_sum = 1.0f / tree_sum(p);
-    for (int c = 0; c < D; c++) out[c] = expf(in[c] - row_max) * inv_sum;
+    for (int c = 0; c < D; c++) out[c] = oxo_expf(in[c] - row_max) * inv_sum;
 }
 
 void oxo_softmax(const float *x, int rows, int D, float *y) {

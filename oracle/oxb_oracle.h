@@ -16,6 +16,10 @@
  *   - every f32 op is a separately rounded IEEE op: no FMA contraction
  *     (built with -ffp-contract=off);
  *   - WGSL inverseSqrt(v) is restated as 1.0f / sqrtf(v);
+ *   - WGSL exp() (implementation-defined) is restated as oxo_expf: Cody-Waite
+ *     reduction x = k*ln2 + r (ln2 split into a 15-bit head and a tail),
+ *     degree-7 Taylor polynomial of e^r by Horner, then ldexp(p, k); max
+ *     error ~2 ulp, pinned against double-precision exp in the tests;
  *   - WGSL round() is round-half-to-even (rintf), NOT the TS spec's
  *     Math.round (ts/reference.ts:70), which differs on .5 ties;
  *   - workgroup reductions follow the shaders' order exactly: 256 strided
@@ -35,6 +39,9 @@ extern "C" {
 /* ---- f16 <-> f32 (IEEE binary16, round-to-nearest-even) ---------------- */
 float    oxo_f16_to_f32(uint16_t h);
 uint16_t oxo_f32_to_f16(float f);
+
+/* ---- exp used wherever the shaders call exp() (softmax, SiLU) ---------- */
+float oxo_expf(float x);
 
 /* ---- I2_S packing ------------------------------------------------------ */
 /* Pack K ternary values {-1,0,+1} of one row into I2_S bytes (K padded to a

@@ -114,7 +114,7 @@ def test_c_abi_generate_and_chat_greedy():
     assert h, L.oxbitnet_error_message()
     assert progress[0][0] == 0 and progress[-1] == (2, 1.0)
     got = []
-    tf = nat.TokenFn(lambda t, n, ud: (got.append(C.string_at(t, n).decode()), 0)[1])
+    tf = nat.TokenFn(lambda t, n, ud: (got.append(C.string_at(t, n)), 0)[1])
     g = L.oxbitnet_default_generate_options()
     g.max_tokens, g.top_k, g.repeat_penalty = 12, 1, 1.0
     assert L.oxbitnet_generate(h, b"hello world", C.byref(g), tf, None) == 0

@@ -52,6 +52,21 @@ def test_f32_to_f16_matches_numpy_rne():
     assert np.array_equal(got, ref)
 
 
+def test_expf_within_2ulp_of_double():
+    rng = np.random.default_rng(9)
+    xs = np.concatenate([rng.uniform(-103, 88, 20000), rng.uniform(-10, 0, 20000),
+                         np.array([0.0, -0.0, 1.0, -1.0, 88.7, -87.3, -100.0, 1e-8, -1e-8])])
+    xs = xs.astype(np.float32)
+    got = np.array([O.expf(float(x)) for x in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    ulp = np.maximum(ulp, np.float64(2.0 ** -149))
+    err = np.abs(got.astype(np.float64) - ref) / ulp
+    assert err.max() <= 2.0, err.max()
+    assert O.expf(0.0) == 1.0 and O.expf(-200.0) == 0.0 and O.expf(-3.4e38) == 0.0
+    assert O.expf(100.0) == float("inf")
+
+
 # ---------------------------------------------------------------- I2_S -----
 @pytest.mark.parametrize("case", GOLD["i2s_fill_u32"]["cases"])
 def test_i2s_known_bytes(case):
