@@ -90,11 +90,13 @@ SIGNATURES = {
     "oxb_gemm_i8": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, vp]),
     "oxb_gemm_qkv": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32,
                                vp, vp]),
-    "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]),
     "oxb_attn_prefill": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "oxb_embedding": (C.c_int, [vp, i32, i32, vp, i32, vp, vp, vp]),
     "oxb_lm_head_argmax": (C.c_int, [vp, vp, f32, vp, i32, i32, vp, vp, vp, vp, i32, vp]),
     "oxb_lm_head_partials": (C.c_int, []),
+    "oxb_repack_lm": (C.c_int, [vp, vp, i32, i32, vp]),
+    "oxb_lm_bytes": (C.c_size_t, [i32, i32]),
     # model
     "oxb_model_load": (vp, [C.c_char_p, C.c_int]),
     "oxb_model_free": (None, [vp]),

@@ -122,6 +122,123 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
     for (int c = 0; c < NC; ++c) orow[gg[c] * kHd + d] = acc[c];
 }
 
+// ---------------------------------------------------------------------------
+// Decode (one query at position *pos, S = pos + 1), two kernels:
+//  A  scores: grid (position blocks, Hkv); 256 threads = G heads x (256/G)
+//     positions, one 128-term dot chain each; scores[h][s] to global.
+//  B  softmax + P.V: grid (Hkv, slices); each workgroup takes the G heads of
+//     one KV head and 64/G of the 128 dims, i.e. exactly one wave of 64
+//     sequential sums.  The other waves load the scores, run the softmax
+//     reductions and stage the V slice (as f32, transposed) in LDS, so the
+//     summing wave reads 4 steps per LDS load.
+// ---------------------------------------------------------------------------
+template <int G>
+__global__ __launch_bounds__(256) void attn_scores_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const int *__restrict__ pos_ptr,
+    int max_seq, float scale, float *__restrict__ scores) {
+    constexpr int P = 256 / G;
+    __shared__ float qs[G * kHd];
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1;
+    const int b = blockIdx.x, hk = blockIdx.y;
+    if (b * P >= S) return;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < G * kHd; i += 256) qs[i] = q[(size_t)hk * G * kHd + i];
+    __syncthreads();
+    const int g = tid / P, s = b * P + tid % P;
+    if (s >= S) return;
+    const uint4 *kr = (const uint4 *)(kc + ((size_t)hk * max_seq + s) * kHd);
+    uint4 k[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) k[i] = kr[i];
+    const float *qg = qs + g * kHd;
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const __half2 *hh = (const __half2 *)&k[i];
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) {
+            const float2 kf = __half22float2(hh[k2]);
+            float m0 = qg[i * 8 + 2 * k2] * kf.x;
+            dot = dot + m0;
+            float m1 = qg[i * 8 + 2 * k2 + 1] * kf.y;
+            dot = dot + m1;
+        }
+    }
+    scores[(size_t)(hk * G + g) * max_seq + s] = dot * scale;
+}
+
+constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB)
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_pv_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out) {
+    constexpr int DW = 64 / G;               // dims per workgroup
+    constexpr int kVChunk = kVFloats / DW;   // positions staged per pass
+    extern __shared__ __align__(16) float smem[];
+    float *pr = smem;                         // [G][Spad] scores, then probabilities
+    __shared__ float red[324];
+    __shared__ __align__(16) float vt[kVFloats];   // V slice, [d][s] f32
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1;
+    const int Spad = (S + 3) & ~3;
+    const int hk = blockIdx.x, d0 = blockIdx.y * DW;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < G * S; i += 256) {
+        const int g = i / S, s = i % S;
+        pr[g * Spad + s] = scores[(size_t)(hk * G + g) * max_seq + s];
+    }
+    __syncthreads();
+    // sh/softmax.wgsl:25-80 per head: max, strided exp sums + tree, normalise
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+        float* row = pr + g * Spad;
+        float m = -3.402823e+38f;
+        for (int s = tid; s < S; s += 256) m = fmaxf(m, row[s]);
+        m = block256_max(m, red);
+        float part = 0.0f;
+        for (int s = tid; s < S; s += 256) part = part + oxb_expf(row[s] - m);
+        const float inv = 1.0f / block256_tree_sum_fast(part, red);
+        for (int s = tid; s < S; s += 256) row[s] = oxb_expf(row[s] - m) * inv;
+        for (int s = S + tid; s < Spad; s += 256) row[s] = 0.0f;
+    }
+    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s
+    const int lane = tid & 63;
+    const int g = lane / DW, dd = lane % DW;
+    float acc = 0.0f;
+    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
+    for (int c0 = 0; c0 < S; c0 += kVChunk) {
+        const int n = min(kVChunk, S - c0);
+        __syncthreads();  // previous chunk consumed (and softmax done)
+        for (int i = tid; i < n * DW; i += 256) {
+            const int s = i / DW, e = i % DW;
+            vt[e * kVChunk + s] = __half2float(__ushort_as_half(Vh[(size_t)(c0 + s) * kHd + e]));
+        }
+        __syncthreads();
+        if (tid < 64) {
+            const float *prow = pr + g * Spad + c0;
+            const float *vrow = vt + dd * kVChunk;
+            int s = 0;
+            for (; s + 4 <= n; s += 4) {
+                const float4 p4 = *(const float4 *)(prow + s);
+                const float4 v4 = *(const float4 *)(vrow + s);
+                float m0 = p4.x * v4.x; acc = acc + m0;
+                float m1 = p4.y * v4.y; acc = acc + m1;
+                float m2 = p4.z * v4.z; acc = acc + m2;
+                float m3 = p4.w * v4.w; acc = acc + m3;
+            }
+            for (; s < n; ++s) {
+                float m = prow[s] * vrow[s];
+                acc = acc + m;
+            }
+        }
+    }
+    if (tid < 64) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
+}
+
 template <int G>
 static int launch_exact(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                         int pos0, int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
@@ -164,11 +281,46 @@ static int dispatch(const float *q, const uint16_t *kc, const uint16_t *vc, cons
 
 using namespace oxb;
 
+template <int G>
+static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
+                         int Hkv, int max_seq, float *scores, float *out, hipStream_t s) {
+    const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    constexpr int P = 256 / G;
+    hipLaunchKernelGGL(attn_scores_kernel<G>, dim3((max_seq + P - 1) / P, Hkv), dim3(256), 0, s, q,
+                       kc, pos, max_seq, scale, scores);
+    OXB_CHECK_HIP(hipGetLastError());
+    const size_t smem = (size_t)G * ((max_seq + 3) & ~3) * sizeof(float);
+    static size_t configured = 0;
+    if (smem > 32 * 1024 && smem > configured) {
+        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_pv_kernel<G>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        configured = smem;
+    }
+    hipLaunchKernelGGL(attn_pv_kernel<G>, dim3(Hkv, G * kHd / 64), dim3(256), smem, s, scores, vc,
+                       pos, max_seq, out);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
 extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                               const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
-                               void *stream) {
-    OXB_REQUIRE(pos, "attention: pos is NULL");
-    return dispatch(q, kcache, vcache, pos, 0, 1, H, Hkv, hd, max_seq, max_seq, out, stream);
+                               const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
+                               float *out, void *stream) {
+    OXB_REQUIRE(pos && scores, "attention: pos or scores is NULL");
+    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    const int G = H / Hkv;
+    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
+                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    switch (G) {
+        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        default:
+            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
+            return -1;
+    }
 }
 
 extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache,

@@ -13,7 +13,6 @@
 namespace oxb {
 
 constexpr int kLmBlocks = 1024;  // persistent-style grid: 4 workgroups per CU
-constexpr int kLmRowsInFlight = 4;
 constexpr int kLmMaxLoads = 8;   // 16-byte loads per row per lane: D <= 8*64*8 = 4096
 
 struct LmParams {
@@ -33,89 +32,109 @@ __device__ inline bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-template <int NL>  // 16-byte loads per row per lane: D = 512 * NL
+// Row-per-lane layout of the tied embedding for the LM head ("lm-tiled"):
+// 64-row tiles; each lane (row) streams the pairs (E[2dh], E[2dh+1]) of its
+// row in the order the shader's reduction consumes them: shader thread
+// t = bitrev8(i) for i = 0..255, and for each t its pairs dh = t + 256 j,
+// j = 0..NJ-1 (NJ = D/512).  Dword u = i*NJ + j of row r of tile T sits at
+// uint4 ((T*NQ + u/4)*64 + r), component u%4 (NQ = 64*NJ uint4 per lane).
+// The halving tree of sh/f32_matmul.wgsl:59-68 is the balanced pairwise
+// tree over the 256 thread sums taken in bit-reversed order, so a lane can
+// fold it left to right: 16-leaf subtrees in registers, then the 16 subtree
+// sums.  Result: the shader's exact f32 value, no cross-lane traffic.
+__host__ __device__ inline int bitrev4(int x) {
+    return ((x & 1) << 3) | ((x & 2) << 1) | ((x & 4) >> 1) | ((x & 8) >> 3);
+}
+
+template <int NJ>  // D = 512 * NJ
 __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
-    __shared__ float red[256];
-    __shared__ __align__(16) float h_lds[kLmMaxLoads * 64 * 8];
+    __shared__ float red[324];
+    __shared__ __align__(16) float h_lds[kLmMaxLoads * 512];
+    __shared__ __align__(16) float2 hp[256 * NJ];   // h pairs in consumption order
     __shared__ float bval[4];
     __shared__ int bidx[4];
     __shared__ int ticket_s;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = p.D;
+    constexpr int NQ = 64 * NJ;   // uint4 per lane per tile
 
-    // rows of this block
-    const int per = (p.V + gridDim.x - 1) / gridDim.x;
-    const int r0 = blockIdx.x * per, r1 = min(p.V, r0 + per);
-
-    // final RMSNorm in the shader's order (strided partials + tree)
+    // final RMSNorm (sh/rmsnorm.wgsl order), h to LDS
     float ss = 0.0f;
     for (int c = tid; c < D; c += 256) {
         float v = p.x[c];
         float sq = v * v;
         ss = ss + sq;
     }
-    const float sum = block256_tree_sum(ss, red);
+    const float sum = block256_tree_sum_fast(ss, red);
     const float rms = 1.0f / sqrtf(sum / (float)D + p.eps);
     for (int c = tid; c < D; c += 256) {
         float a = p.x[c] * rms;
         h_lds[c] = a * p.gamma[c];
     }
     __syncthreads();
-    float hv[NL][8];
-#pragma unroll
-    for (int j = 0; j < NL; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hv[j][i] = h_lds[(j * 64 + lane) * 8 + i];
+    for (int u = tid; u < 256 * NJ; u += 256) {
+        const int i = u / NJ, j = u % NJ;
+        const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
+        const int dh = t + 256 * j;
+        hp[u] = make_float2(h_lds[2 * dh], h_lds[2 * dh + 1]);
+    }
+    __syncthreads();
 
-    // One wave per row, reproducing sh/f32_matmul.wgsl:51-68 exactly: shader
-    // thread t accumulates pairs dh = t, t+256, ... as acc += h*e0; acc += h*e1,
-    // then the halving tree.  Lane l plays threads 4l .. 4l+3, so its 16-byte
-    // load j holds the pairs dh = 256j + 4l + i of those four threads.
+    const int ntiles = (p.V + 63) >> 6;
     float best = -INFINITY;
     int besti = 0x7fffffff;
-    const int rowstride = D >> 3;   // uint4 per row
-    for (int rb = r0 + w * kLmRowsInFlight; rb < r1; rb += 4 * kLmRowsInFlight) {
-        uint4 e[kLmRowsInFlight][NL];
+    __shared__ float Tl[4][16][64];   // per-lane 16-leaf subtree sums
+    for (int tile = blockIdx.x * 4 + w; tile < ntiles; tile += gridDim.x * 4) {
+        const uint4 *src = p.E + (size_t)tile * NQ * 64 + lane;
+#pragma unroll 1
+        for (int k = 0; k < 16; ++k) {
+            // 16 leaves i = 16k + m, m = 0..15: 16*NJ dwords = 4*NJ uint4
+            uint4 e[4 * NJ];
 #pragma unroll
-        for (int q = 0; q < kLmRowsInFlight; ++q) {
-            const int row = min(rb + q, r1 - 1);
+            for (int qq = 0; qq < 4 * NJ; ++qq) e[qq] = load_nt(src + (size_t)(k * 4 * NJ + qq) * 64);
+            const float2 *hk = hp + k * 16 * NJ;
+            float L[16];
 #pragma unroll
-            for (int j = 0; j < NL; ++j)
-                e[q][j] = load_nt(p.E + (size_t)row * rowstride + j * 64 + lane);
-        }
+            for (int m = 0; m < 16; ++m) {
+                float acc = 0.0f;
 #pragma unroll
-        for (int q = 0; q < kLmRowsInFlight; ++q) {
-            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < NL; ++j) {
-                const __half2 *hh = (const __half2 *)&e[q][j];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float2 f = __half22float2(hh[i]);
-                    float m0 = hv[j][2 * i] * f.x;
-                    a[i] = a[i] + m0;
-                    float m1 = hv[j][2 * i + 1] * f.y;
-                    a[i] = a[i] + m1;
+                for (int j = 0; j < NJ; ++j) {
+                    const int u = m * NJ + j;
+                    const uint32_t word = (&e[u >> 2].x)[u & 3];
+                    const float2 hh = hk[u];
+                    const float e0 = __half2float(__ushort_as_half((uint16_t)(word & 0xffffu)));
+                    const float e1 = __half2float(__ushort_as_half((uint16_t)(word >> 16)));
+                    float m0 = hh.x * e0;
+                    acc = acc + m0;
+                    float m1 = hh.y * e1;
+                    acc = acc + m1;
                 }
+                L[m] = acc;
             }
-            // tree: strides 128..4 pair lane l with lane l + stride/4
 #pragma unroll
-            for (int sl = 32; sl >= 1; sl >>= 1) {
+            for (int st = 1; st < 16; st <<= 1)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float o = __shfl_down(a[i], sl, 64);
-                    a[i] = a[i] + o;
-                }
-            }
-            a[0] = a[0] + a[2];   // stride 2
-            a[1] = a[1] + a[3];
-            const float acc = __shfl(a[0] + a[1], 0, 64);  // stride 1, broadcast
-            const int row = rb + q;
-            if (row < r1) {
-                if (lane == 0) p.logits[row] = acc;
-                if (better(acc, row, best, besti)) { best = acc; besti = row; }
-            }
+                for (int m = 0; m < 16; m += 2 * st) L[m] = L[m] + L[m + st];
+            Tl[w][k][lane] = L[0];
         }
+        float T[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) T[k] = Tl[w][k][lane];
+#pragma unroll
+        for (int st = 1; st < 16; st <<= 1)
+#pragma unroll
+            for (int m = 0; m < 16; m += 2 * st) T[m] = T[m] + T[m + st];
+        const int row = tile * 64 + lane;
+        if (row < p.V) {
+            p.logits[row] = T[0];
+            if (better(T[0], row, best, besti)) { best = T[0]; besti = row; }
+        }
+    }
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) {
+        const float ov = __shfl_xor(best, s, 64);
+        const int oi = __shfl_xor(besti, s, 64);
+        if (better(ov, oi, best, besti)) { best = ov; besti = oi; }
     }
     if (lane == 0) { bval[w] = best; bidx[w] = besti; }
     __syncthreads();
@@ -177,6 +196,31 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t *__restri
             (id >= 0 && id < V) ? __half2float(__ushort_as_half(E[(size_t)id * D + d])) : 0.0f;
 }
 
+// Natural f16 embedding [V][D] -> the LM head's lm-tiled layout (above).
+__global__ void repack_lm_kernel(const uint32_t *__restrict__ E, uint4 *__restrict__ dst, int V,
+                                 int D) {
+    const int NJ = D / 512, NQ = 64 * NJ;
+    const int ntiles = (V + 63) / 64;
+    const size_t total = (size_t)ntiles * NQ * 64;
+    for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(idx % 64);
+        const size_t rest = idx / 64;
+        const int qq = (int)(rest % NQ);
+        const int tile = (int)(rest / NQ);
+        const int row = tile * 64 + r;
+        uint32_t wv[4];
+        for (int c = 0; c < 4; ++c) {
+            const int u = qq * 4 + c;
+            const int i = u / NJ, j = u % NJ;
+            const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
+            const int dh = t + 256 * j;
+            wv[c] = row < V ? E[(size_t)row * (D / 2) + dh] : 0u;
+        }
+        dst[idx] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    }
+}
+
 // Natural I2_S rows [N][K/4] -> tile-chunk layout (see oxb_common.h).
 __global__ void repack_tiled_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
                                     int N, int KC) {
@@ -193,10 +237,10 @@ __global__ void repack_tiled_kernel(const uint4 *__restrict__ src, uint4 *__rest
 using namespace oxb;
 
 extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
-                                  const uint16_t *E, int V, int D, float *logits, float *part,
+                                  const void *E, int V, int D, float *logits, float *part,
                                   int *state, int *tok_hist, int advance, void *stream) {
-    OXB_REQUIRE(D % 512 == 0 && D <= kLmMaxLoads * 512,
-                "lm_head: hidden %d must be a multiple of 512 and <= %d", D, kLmMaxLoads * 512);
+    OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512,
+                "lm_head: hidden %d must be a multiple of 512 and <= 2560", D);
     OXB_REQUIRE(V > 0, "lm_head: vocab %d", V);
     LmParams p{x, gamma, eps, (const uint4 *)E, V, D, logits, (float2 *)part, state, tok_hist,
                advance};
@@ -206,14 +250,27 @@ extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
     case n:                                                                             \
         hipLaunchKernelGGL(lm_head_kernel<n>, dim3(kLmBlocks), dim3(256), 0, s, p);     \
         break;
-        OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5) OXB_NL(6) OXB_NL(7) OXB_NL(8)
+        OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5)
 #undef OXB_NL
+        default:
+            oxb::set_error("lm_head: hidden %d unsupported (512 .. 2560)", D);
+            return -1;
     }
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
 extern "C" int oxb_lm_head_partials(void) { return kLmBlocks; }
+
+extern "C" int oxb_repack_lm(const uint16_t *E, void *E_lm, int V, int D, void *stream) {
+    OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512 && V > 0, "repack_lm: bad shape V %d D %d", V, D);
+    hipLaunchKernelGGL(repack_lm_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream,
+                       (const uint32_t *)E, (uint4 *)E_lm, V, D);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" size_t oxb_lm_bytes(int V, int D) { return (size_t)((V + 63) / 64) * 64 * D * 2; }
 
 extern "C" int oxb_embedding(const uint16_t *E, int V, int D, const int *ids, int n_tok,
                              const int *state, float *x, void *stream) {

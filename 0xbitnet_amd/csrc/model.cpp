@@ -399,6 +399,8 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
         return nullptr;
     }
     m->weight_bytes += (size_t)m->V * D * 2;
+    m->embed_lm = m->dalloc(oxb_lm_bytes(m->V, D));
+    if (!m->embed_lm || oxb_repack_lm(m->embed, m->embed_lm, m->V, D, nullptr)) return nullptr;
     {
         std::vector<float> w;
         if (!tensor_to_f32(*g, *tn, w) || upload_f32(m.get(), w, &m->final_norm)) return nullptr;
@@ -420,12 +422,13 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->q = (float *)m->dalloc((size_t)Dq * 4);
     m->attn = (float *)m->dalloc((size_t)Dq * 4);
     m->h = (float *)m->dalloc((size_t)F * 4);
+    m->scores = (float *)m->dalloc((size_t)H * m->max_seq * 4);
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->lm_part = (float *)m->dalloc((size_t)oxb_lm_head_partials() * 2 * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_elems * 2) != hipSuccess ||
         hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess) {
@@ -466,7 +469,7 @@ int oxb_model::enqueue_decode_step() {
         if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
                               max_seq, rope, posp, s))
             return -1;
-        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, attn, s))
+        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, attn, s))
             return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
         if (oxb_bitlinear_gemv(L.wo, attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr, nullptr,
@@ -482,7 +485,7 @@ int oxb_model::enqueue_decode_step() {
                                nullptr, s))
             return -1;
     }
-    return oxb_lm_head_argmax(x, final_norm, eps, embed, V, D, logits, lm_part, state, tok_hist,
+    return oxb_lm_head_argmax(x, final_norm, eps, embed_lm, V, D, logits, lm_part, state, tok_hist,
                               1, s);
 }
 
@@ -561,7 +564,7 @@ int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
         if (oxb_gemm_i8(L.wd, (const int8_t *)pX, pscale, psum, L.sd, D, F, n, px, nullptr, 1, s))
             return -1;
     }
-    return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed, V, D, logits,
+    return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed_lm, V, D, logits,
                               lm_part, state, tok_hist, n, s);
 }
 

@@ -26,13 +26,14 @@ struct oxb_model {
         float *attn_sub = nullptr, *ffn_sub = nullptr;  // may be null
     };
     std::vector<Layer> layers;
-    uint16_t *embed = nullptr;   // [V][D] f16 (tied LM head)
+    uint16_t *embed = nullptr;   // [V][D] f16 (token embedding)
+    void *embed_lm = nullptr;    // the same table in the LM head's layout
     float *final_norm = nullptr;
     float *rope = nullptr;       // [max_seq][hd/2] (cos, sin)
     uint16_t *kcache = nullptr, *vcache = nullptr;  // [L][Hkv][max_seq][hd]
 
     // decode buffers
-    float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
+    float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr, *scores = nullptr;
     float *logits = nullptr, *lm_part = nullptr;
     int *state = nullptr, *tok_hist = nullptr;
     int hist_cap = 0;

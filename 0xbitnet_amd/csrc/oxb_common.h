@@ -115,6 +115,59 @@ __device__ inline int block256_isum(int v, int *red) {
     return r;
 }
 
+// Order-free wave reductions over DPP (row_shr 1/2/4/8, row_bcast 15/31);
+// the identity of the inactive sources is 0, so these are for integer sums
+// and maxima of non-negative floats.  The result is lane 63's, returned
+// to every lane.
+template <int CTRL, int ROWMASK>
+__device__ inline int dpp0(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWMASK, 0xf, false);
+}
+
+__device__ inline int wave_isum_dpp(int v) {
+    v += dpp0<0x111, 0xf>(v);
+    v += dpp0<0x112, 0xf>(v);
+    v += dpp0<0x114, 0xf>(v);
+    v += dpp0<0x118, 0xf>(v);
+    v += dpp0<0x142, 0xa>(v);
+    v += dpp0<0x143, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ inline float wave_nonneg_max_dpp(float f) {
+    int v = __float_as_int(f);
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x111, 0xf>(v))));
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x112, 0xf>(v))));
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x114, 0xf>(v))));
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x118, 0xf>(v))));
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x142, 0xa>(v))));
+    v = __float_as_int(fmaxf(__int_as_float(v), __int_as_float(dpp0<0x143, 0xc>(v))));
+    return __int_as_float(__builtin_amdgcn_readlane(v, 63));
+}
+
+// The shaders' 256-thread halving tree (s[t] += s[t+stride], stride 128..1)
+// with one LDS pass: wave 0 folds strides 128 and 64 in registers, then
+// every thread evaluates strides 32..1 of the 64 survivors locally.  red
+// holds >= 320 floats; all 256 threads must call; result to all threads.
+__device__ inline float block256_tree_sum_fast(float part, float *red) {
+    const int t = threadIdx.x;
+    red[t] = part;
+    __syncthreads();
+    if (t < 64) red[256 + t] = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
+    __syncthreads();
+    float a[64];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 f = *(const float4 *)(red + 256 + 4 * i);
+        a[4 * i] = f.x; a[4 * i + 1] = f.y; a[4 * i + 2] = f.z; a[4 * i + 3] = f.w;
+    }
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1)
+#pragma unroll
+        for (int i = 0; i < st; ++i) a[i] = a[i] + a[i + st];
+    return a[0];
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);

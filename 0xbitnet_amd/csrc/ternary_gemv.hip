@@ -48,47 +48,59 @@ struct GemvParams {
 
 // ---------------------------------------------------------------------------
 // Prologue: RMSNorm (optional) + per-token absmax int8 quantize of one row of
-// D = K f32 values, computed by all 256 threads with the shaders' thread
-// mapping (thread t owns columns t, t+256, ...).  Writes int8 into LDS.
+// D f32 values by all 256 threads with the shaders' thread mapping (thread t
+// owns columns t, t+256, ...: sh/rmsnorm.wgsl:41-45, sh/quantize.wgsl:42-45).
+// The caller issues the loads (load_row) before its weight prefetch so both
+// round trips overlap.  Writes int8 into LDS, returns the scale and this
+// wave's share of sum(q) in wq[w] (summed after the caller's next barrier).
+// LDS: red >= 324 floats, wq >= 4 ints.
 // ---------------------------------------------------------------------------
-__device__ inline void norm_quant_to_lds(const float *__restrict__ x,
-                                         const float *__restrict__ gamma, float eps,
-                                         int D, int8_t *xq_lds, float *red, int *ired,
-                                         float &scale, int &sumq) {
+template <int NREG>
+__device__ inline void load_row(const float *__restrict__ x, const float *__restrict__ gamma,
+                                int D, float (&v)[NREG], float (&g)[NREG]) {
     const int t = threadIdx.x;
-    float v[kMaxNormReg];
-    float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxNormReg; ++j) {
+    for (int j = 0; j < NREG; ++j) {
         const int c = t + j * 256;
         v[j] = c < D ? x[c] : 0.0f;
-        if (gamma && c < D) {
-            float sq = v[j] * v[j];
-            ss = ss + sq;
-        }
+        g[j] = (gamma && c < D) ? gamma[c] : 0.0f;
     }
-    if (gamma) {
-        const float sum = block256_tree_sum(ss, red);
-        const float rms = 1.0f / sqrtf(sum / (float)D + eps);
+}
+
+template <int NREG>
+__device__ inline float norm_quant_regs(float (&v)[NREG], const float (&g)[NREG], bool norm,
+                                        float eps, int D, int8_t *xq_lds, float *red, int *wq) {
+    const int t = threadIdx.x;
+    if (norm) {
+        float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMaxNormReg; ++j) {
-            const int c = t + j * 256;
-            if (c < D) {
-                float a = v[j] * rms;
-                v[j] = a * gamma[c];
+        for (int j = 0; j < NREG; ++j) {
+            if (t + j * 256 < D) {
+                float sq = v[j] * v[j];
+                ss = ss + sq;
             }
+        }
+        const float sum = block256_tree_sum_fast(ss, red);
+        const float rms = 1.0f / sqrtf(sum / (float)D + eps);  // inverseSqrt
+#pragma unroll
+        for (int j = 0; j < NREG; ++j) {
+            float a = v[j] * rms;
+            v[j] = a * g[j];
         }
     }
     float am = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxNormReg; ++j)
+    for (int j = 0; j < NREG; ++j)
         if (t + j * 256 < D) am = fmaxf(am, fabsf(v[j]));
-    am = block256_max(am, red);
-    scale = am == 0.0f ? 1.0f : am / 127.0f;
-    const float inv = am == 0.0f ? 0.0f : 127.0f / am;
+    am = wave_nonneg_max_dpp(am);
+    if ((t & 63) == 0) red[320 + (t >> 6)] = am;
+    __syncthreads();
+    am = fmaxf(fmaxf(red[320], red[321]), fmaxf(red[322], red[323]));
+    const float scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
+    const float inv = am == 0.0f ? 0.0f : 127.0f / am;     // :68
     int s = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxNormReg; ++j) {
+    for (int j = 0; j < NREG; ++j) {
         const int c = t + j * 256;
         if (c < D) {
             const int q = quant_one(v[j], inv);
@@ -96,20 +108,22 @@ __device__ inline void norm_quant_to_lds(const float *__restrict__ x,
             s += q;
         }
     }
-    sumq = block256_isum(s, ired);
+    s = wave_isum_dpp(s);
+    if ((t & 63) == 0) wq[t >> 6] = s;
+    return scale;
 }
 
 __device__ inline uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-template <int PRO, int EPI>
+template <int PRO, int EPI, int NREG>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) int8_t smem[];
-    int8_t *xq_lds = smem;                                     // [K]
-    float *red = (float *)(smem + p.K);                        // [256]
-    int *ired = (int *)(red + 256);                            // [4]
-    int *wpart = ired + 4;                                     // [4][16]
+    int8_t *xq_lds = smem;                       // [K]
+    float *red = (float *)(smem + p.K);          // [324]
+    int *wq = (int *)(red + 324);                // [4]
+    int *wpart = wq + 4;                         // [256]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -118,17 +132,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int tile = blockIdx.x;
     const uint4 *tw = p.W + (size_t)tile * KC * 16;
 
+    // ---- loads: activations first, then this lane's first weight chunks ----
+    float v[NREG], g[NREG];
+    if constexpr (PRO == PRO_QUANT) load_row<NREG>(p.x, p.gamma, p.K, v, g);
+    float resid = 0.0f;
+    if constexpr (EPI == EPI_RESID) {
+        if (tid < 16) resid = p.y[tile * 16 + tid];
+    }
     // Wave w owns chunks [kc0, kc1) of this tile.
     const int per = (KC + 3) >> 2;
     const int kc0 = w * per;
     const int kc1 = min(KC, kc0 + per);
-
     uint4 buf[kPrefetch];
 #pragma unroll
     for (int u = 0; u < kPrefetch; ++u) {
         const int kc = kc0 + c + 4 * u;
-        buf[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r)
-                          : make_uint4(0, 0, 0, 0);
+        buf[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r) : make_uint4(0, 0, 0, 0);
     }
 
     // ---- prologue ---------------------------------------------------------
@@ -142,8 +161,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         xsum = p.xsum[0];
         __syncthreads();
     } else {
-        norm_quant_to_lds(p.x, p.gamma, p.eps, p.K, xq_lds, red, ired, in_scale, xsum);
+        in_scale = norm_quant_regs<NREG>(v, g, p.gamma != nullptr, p.eps, p.K, xq_lds, red, wq);
         __syncthreads();
+        xsum = wq[0] + wq[1] + wq[2] + wq[3];
         if (tile == 0 && p.xq_out) {
             for (int i = tid; i < (p.K >> 4); i += 256)
                 ((int4 *)p.xq_out)[i] = ((const int4 *)xq_lds)[i];
@@ -158,8 +178,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int u = 0; u < kPrefetch; ++u) {
             const int kc = base + 4 * kPrefetch + 4 * u;
-            nxt[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r)
-                              : make_uint4(0, 0, 0, 0);
+            nxt[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < kPrefetch; ++u) {
@@ -180,14 +199,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         for (int u = 0; u < kPrefetch; ++u) buf[u] = nxt[u];
     }
 
-    // ---- reduction: 4 lanes per row, then 4 waves ---------------------------
-    int v = acc.codes();
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (c == 0) wpart[w * 16 + r] = v;
+    // ---- reduction: 16 partials per row (4 lanes x 4 waves) through LDS ----
+    wpart[tid] = acc.codes();
     __syncthreads();
     if (tid >= 16) return;
-    const int32_t a = wpart[r] + wpart[16 + r] + wpart[32 + r] + wpart[48 + r] - xsum;
+    int a = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a += wpart[k * 16 + r];
+    a -= xsum;
     const int n = tile * 16 + r;
     if (p.acc_out) p.acc_out[n] = a;
     // sh/ternary_gemv.wgsl:94-95: (f32(acc) * scales[row]) * input_scale
@@ -197,14 +216,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     if constexpr (EPI == EPI_STORE) {
         p.y[n] = yv;
     } else if constexpr (EPI == EPI_RESID) {
-        p.y[n] = p.y[n] + yv;   // rs/nn/transformer.rs:157 add(input, out)
+        p.y[n] = resid + yv;   // rs/nn/transformer.rs:157 add(input, out)
     } else if constexpr (EPI == EPI_GATEUP) {
         // fused rows interleave gate (even) and up (odd): rs/nn/ffn.rs:60-80
         const float other = __shfl_xor(yv, 1, 64);
         if ((n & 1) == 0) {
-            float g = fmaxf(0.0f, yv);   // sh/activation.wgsl:32-33
-            g = g * g;
-            p.y[n >> 1] = g * other;    // sh/elementwise.wgsl:32
+            float gt = fmaxf(0.0f, yv);   // sh/activation.wgsl:32-33
+            gt = gt * gt;
+            p.y[n >> 1] = gt * other;     // sh/elementwise.wgsl:32
         }
     } else {  // EPI_QKV
         const int pos = *p.pos;
@@ -244,20 +263,19 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
     extern __shared__ __align__(16) int8_t smem[];
     int8_t *q_lds = smem;
     float *red = (float *)(smem + ((D + 15) & ~15));
-    int *ired = (int *)(red + 256);
+    int *wq = (int *)(red + 324);
     const int row = blockIdx.x;
-    float scale;
-    int sumq;
-    norm_quant_to_lds(x + (size_t)row * D, gamma, eps, D, q_lds, red, ired, scale, sumq);
+    float v[kMaxNormReg], g[kMaxNormReg];
+    load_row<kMaxNormReg>(x + (size_t)row * D, gamma, D, v, g);
+    const float scale = norm_quant_regs<kMaxNormReg>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
     __syncthreads();
     for (int i = threadIdx.x; i < (D >> 4); i += 256)
         ((int4 *)(xq + (size_t)row * D))[i] = ((const int4 *)q_lds)[i];
     if (threadIdx.x == 0) {
         scales[row] = scale;
-        if (sums) sums[row] = sumq;
+        if (sums) sums[row] = wq[0] + wq[1] + wq[2] + wq[3];
     }
 }
-
 
 // ---------------------------------------------------------------------------
 // Same row transform, writing the token-tiled int8 layout the MFMA GEMM reads:
@@ -270,14 +288,17 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
     extern __shared__ __align__(16) int8_t smem[];
     int8_t *q_lds = smem;
     float *red = (float *)(smem + ((D + 15) & ~15));
-    int *ired = (int *)(red + 256);
+    int *wq = (int *)(red + 324);
     const int row = blockIdx.x;
     float scale = 1.0f;
     int sumq = 0;
     if (row < n_tok) {
-        norm_quant_to_lds(x + (size_t)row * D, gamma, eps, D, q_lds, red, ired, scale, sumq);
+        float v[kMaxNormReg], g[kMaxNormReg];
+        load_row<kMaxNormReg>(x + (size_t)row * D, gamma, D, v, g);
+        scale = norm_quant_regs<kMaxNormReg>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
     } else {
         for (int i = threadIdx.x; i < (D >> 4); i += 256) ((int4 *)q_lds)[i] = make_int4(0, 0, 0, 0);
+        if (threadIdx.x < 4) wq[threadIdx.x] = 0;
     }
     __syncthreads();
     const int KC = D >> 6, tile = row >> 4, c = row & 15;
@@ -288,21 +309,30 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
     }
     if (threadIdx.x == 0) {
         scales[row] = scale;
-        sums[row] = sumq;
+        sums[row] = sumq + wq[0] + wq[1] + wq[2] + wq[3];
     }
 }
 
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-static size_t gemv_smem(int K) { return (size_t)K + 256 * 4 + 4 * 4 + 64 * 4 + 16; }
+static size_t gemv_smem(int K) { return (size_t)K + 324 * 4 + 4 * 4 + 256 * 4 + 16; }
 
-template <int PRO, int EPI>
-static int launch(const GemvParams &p, hipStream_t s) {
+template <int PRO, int EPI, int NREG>
+static int launch_n(const GemvParams &p, hipStream_t s) {
     const size_t sm = gemv_smem(p.K);
-    hipLaunchKernelGGL((gemv_kernel<PRO, EPI>), dim3(p.N / 16), dim3(256), sm, s, p);
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG>), dim3(p.N / 16), dim3(256), sm, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
+}
+
+// NREG = f32 values per thread in the norm prologue (ceil(K / 256)).
+template <int PRO, int EPI>
+static int launch(const GemvParams &p, hipStream_t s) {
+    if (PRO == PRO_INT8) return launch_n<PRO, EPI, 1>(p, s);
+    if (p.K <= 1024) return launch_n<PRO, EPI, 4>(p, s);
+    if (p.K <= 2560) return launch_n<PRO, EPI, 10>(p, s);
+    return launch_n<PRO, EPI, kMaxNormReg>(p, s);
 }
 
 static int check_shape(int N, int K, bool norm) {
@@ -414,7 +444,7 @@ extern "C" int oxb_norm_quant_rows(const float *x, const float *gamma, float eps
     OXB_REQUIRE(D > 0 && D % 16 == 0 && D <= 256 * kMaxNormReg,
                 "norm_quant_rows: D %d must be a multiple of 16 and <= %d", D, 256 * kMaxNormReg);
     OXB_REQUIRE(n_rows > 0, "norm_quant_rows: n_rows %d", n_rows);
-    const size_t sm = (size_t)D + 256 * 4 + 16 + 16;
+    const size_t sm = (size_t)((D + 15) & ~15) + 324 * 4 + 16 + 16;
     hipLaunchKernelGGL(norm_quant_rows_kernel, dim3(n_rows), dim3(256), sm, stream, x, gamma,
                        eps, D, xq, scales, sums);
     OXB_CHECK_HIP(hipGetLastError());
@@ -427,7 +457,7 @@ extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float
     OXB_REQUIRE(D > 0 && D % 256 == 0 && D <= 256 * kMaxNormReg,
                 "quantize_rows_tiled: D %d must be a multiple of 256 and <= %d", D, 256 * kMaxNormReg);
     OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
-    const size_t sm = (size_t)D + 256 * 4 + 16 + 16;
+    const size_t sm = (size_t)((D + 15) & ~15) + 324 * 4 + 16 + 16;
     const int rows = (n_tok + 15) & ~15;
     hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(rows), dim3(256), sm, stream, x, gamma,
                        eps, D, n_tok, (uint4 *)Xt, scales, sums);

@@ -199,8 +199,9 @@ def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int,
     dv = DeviceArray.from_host(np.ascontiguousarray(vcache, np.float16).view(np.uint16))
     dpos = DeviceArray.from_host(np.array([pos], np.int32))
     out = DeviceArray((H * hd,), np.float32)
-    check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, out.ptr,
-                                None), "attn_decode")
+    sc = DeviceArray((H * max_seq,), np.float32)
+    check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, sc.ptr,
+                                out.ptr, None), "attn_decode")
     sync()
     return out.download()
 
@@ -222,7 +223,10 @@ def lm_head_argmax(x: np.ndarray, gamma: np.ndarray, eps: float, E_f16: np.ndarr
     V, D = E_f16.shape
     dx = DeviceArray.from_host(np.ascontiguousarray(x, np.float32))
     dg = DeviceArray.from_host(np.ascontiguousarray(gamma, np.float32))
-    dE = DeviceArray.from_host(np.ascontiguousarray(E_f16).view(np.uint16))
+    dE0 = DeviceArray.from_host(np.ascontiguousarray(E_f16).view(np.uint16))
+    dE = DeviceArray((lib().oxb_lm_bytes(V, D),), np.uint8)
+    check(lib().oxb_repack_lm(dE0.ptr, dE.ptr, V, D, None), "repack_lm")
+    dE0.free()
     logits = DeviceArray((V,), np.float32)
     part = DeviceArray((2 * lib().oxb_lm_head_partials(),), np.float32)
     st = np.zeros(STATE_INTS, np.int32)

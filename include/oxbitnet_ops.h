@@ -121,11 +121,11 @@ int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, cons
 /* ---- attention ------------------------------------------------------------ */
 /* Decode attention for one token over L = *pos + 1 cached positions, in the
  * reference's order (f32 result identical to the shaders' arithmetic on the
- * f16-rounded cache).  q, out: [H*128] f32.  Replaces nn/attention.rs:109-118
+ * f16-rounded cache).  q, out: [H*128] f32; scores: [H][max_seq] f32 scratch.  Replaces nn/attention.rs:109-118
  * (scores, softmax, P.V dispatches). */
 int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                    const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
-                    void *stream);
+                    const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
+                    float *out, void *stream);
 
 /* Causal prefill attention for n_tok queries at positions pos0.., same order.
  * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
@@ -138,12 +138,19 @@ int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vca
 int oxb_embedding(const uint16_t *E, int V, int D, const int *ids, int n_tok, const int *state,
                   float *x, void *stream);
 
-/* Final RMSNorm of x -> tied f16 LM head -> logits [V] -> greedy argmax
+/* Tied embedding [V][D] f16 -> the LM head's row-per-lane layout (64-row
+ * tiles, each row's f16 pairs in the order the shader's reduction consumes
+ * them).  E_lm holds oxb_lm_bytes(V, D) bytes.  D % 512 == 0, D <= 2560. */
+int oxb_repack_lm(const uint16_t *E, void *E_lm, int V, int D, void *stream);
+size_t oxb_lm_bytes(int V, int D);
+
+/* Final RMSNorm of x -> tied f16 LM head (E_lm from oxb_repack_lm) -> logits [V]
+ * (bit-identical to sh/f32_matmul.wgsl's reduction order) -> greedy argmax
  * (lowest index on ties) written to state[OXB_ST_TOKEN], appended to
  * tok_hist (if state[OXB_ST_HIST_CAP] allows), state[OXB_ST_POS] += advance.
  * part: float[2 * oxb_lm_head_partials()].  Replaces nn/model.rs:226-262,
  * 393-448 plus read_logits (:269-298) and sampling.rs with top_k = 1. */
-int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const uint16_t *E, int V,
+int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const void *E_lm, int V,
                        int D, float *logits, float *part, int *state, int *tok_hist,
                        int advance, void *stream);
 int oxb_lm_head_partials(void);

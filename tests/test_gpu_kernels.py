@@ -287,9 +287,9 @@ def test_lm_head_argmax():
 
 
 def test_lm_head_tie_lowest_index():
-    D, V = 512, 4000
+    D, V = 512, 4001
     E = np.zeros((V, D), np.float16)
-    E[[17, 2500, 3999], :] = 1.0  # three identical best rows
+    E[[17, 2500, 3999], :] = 1.0  # three identical best rows (V not a multiple of 64)
     logits, tok, _, _ = ops.lm_head_argmax(np.ones(D, np.float32), np.ones(D, np.float32), 1e-5, E)
     assert tok == 17
 
