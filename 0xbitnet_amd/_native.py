@@ -93,8 +93,7 @@ SIGNATURES = {
     "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]),
     "oxb_attn_prefill": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "oxb_embedding": (C.c_int, [vp, i32, i32, vp, i32, vp, vp, vp]),
-    "oxb_lm_head_argmax": (C.c_int, [vp, vp, f32, vp, i32, i32, vp, vp, vp, vp, i32, vp]),
-    "oxb_lm_head_partials": (C.c_int, []),
+    "oxb_lm_head_argmax": (C.c_int, [vp, vp, f32, vp, i32, i32, vp, vp, vp, i32, vp]),
     "oxb_repack_lm": (C.c_int, [vp, vp, i32, i32, vp]),
     "oxb_lm_bytes": (C.c_size_t, [i32, i32]),
     # model

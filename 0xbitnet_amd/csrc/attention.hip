@@ -136,33 +136,37 @@ template <int G>
 __global__ __launch_bounds__(256) void attn_scores_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const int *__restrict__ pos_ptr,
     int max_seq, float scale, float *__restrict__ scores) {
-    constexpr int P = 256 / G;
-    __shared__ float qs[G * kHd];
+    constexpr int P = 256 / G;   // positions per workgroup; a wave covers 64/P heads
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
     const int b = blockIdx.x, hk = blockIdx.y;
     if (b * P >= S) return;
     const int tid = threadIdx.x;
-    for (int i = tid; i < G * kHd; i += 256) qs[i] = q[(size_t)hk * G * kHd + i];
-    __syncthreads();
     const int g = tid / P, s = b * P + tid % P;
-    if (s >= S) return;
-    const uint4 *kr = (const uint4 *)(kc + ((size_t)hk * max_seq + s) * kHd);
+    // K row (clamped to a valid position) and the head's q row, all in flight
+    // together; q is the same for the lanes of a head (cache broadcast).
+    const uint4 *kr = (const uint4 *)(kc + ((size_t)hk * max_seq + min(s, S - 1)) * kHd);
     uint4 k[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) k[i] = kr[i];
-    const float *qg = qs + g * kHd;
+    const float4 *qg = (const float4 *)(q + (size_t)(hk * G + g) * kHd);
+    float4 qv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qv[i] = qg[i];
+    if (s >= S) return;
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const __half2 *hh = (const __half2 *)&k[i];
+        const float4 qa = qv[2 * i], qb = qv[2 * i + 1];
+        const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
         for (int k2 = 0; k2 < 4; ++k2) {
             const float2 kf = __half22float2(hh[k2]);
-            float m0 = qg[i * 8 + 2 * k2] * kf.x;
+            float m0 = qq[2 * k2] * kf.x;
             dot = dot + m0;
-            float m1 = qg[i * 8 + 2 * k2 + 1] * kf.y;
+            float m1 = qq[2 * k2 + 1] * kf.y;
             dot = dot + m1;
         }
     }
@@ -171,70 +175,149 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
 
 constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB)
 
+// Softmax of one score row by one wave, in the order of sh/softmax.wgsl:25-80
+// for a 256-thread workgroup: lane l plays threads l, l+64, l+128, l+192,
+// each summing its strided positions in order; the halving tree's first two
+// levels pair those four, the remaining six are the xor butterfly (every lane
+// ends with the tree's value: x + y == y + x exactly).  The max is exact in
+// any order.
+__device__ inline void wave_softmax_row(float *row, int S, int Spad, int lane) {
+    float m = -3.402823e+38f;
+    for (int s = lane; s < S; s += 64) m = fmaxf(m, row[s]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 256) {
+        const int s = s0 + lane;
+        if (s < S) p0 = p0 + oxb_expf(row[s] - m);
+        if (s + 64 < S) p1 = p1 + oxb_expf(row[s + 64] - m);
+        if (s + 128 < S) p2 = p2 + oxb_expf(row[s + 128] - m);
+        if (s + 192 < S) p3 = p3 + oxb_expf(row[s + 192] - m);
+    }
+    float c = (p0 + p2) + (p1 + p3);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) c = c + __shfl_xor(c, o, 64);
+    const float inv = 1.0f / c;
+    for (int s = lane; s < S; s += 64) row[s] = oxb_expf(row[s] - m) * inv;
+    for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
+}
+
+// acc + sum_{s < n} p[s] * v[s], one product and one add at a time in order
+// of s.  The LDS operands of the next 16 positions are read while the
+// current 16 are summed (p and v 16-byte aligned).
+__device__ inline float pv_chain(const float *p, const float *v, int n, float acc) {
+    auto ld = [&](float4 (&P)[4], float4 (&V)[4], int at) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            P[j] = *(const float4 *)(p + at + 4 * j);
+            V[j] = *(const float4 *)(v + at + 4 * j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto mac = [&](const float4 (&P)[4], const float4 (&V)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float m0 = P[j].x * V[j].x; acc = acc + m0;
+            float m1 = P[j].y * V[j].y; acc = acc + m1;
+            float m2 = P[j].z * V[j].z; acc = acc + m2;
+            float m3 = P[j].w * V[j].w; acc = acc + m3;
+        }
+    };
+    int s = 0;
+    if (n >= 16) {
+        float4 PA[4], VA[4], PB[4], VB[4];
+        ld(PA, VA, 0);
+        for (; s + 48 <= n; s += 32) {
+            ld(PB, VB, s + 16);
+            mac(PA, VA);
+            ld(PA, VA, s + 32);
+            mac(PB, VB);
+        }
+        if (s + 32 <= n) {
+            ld(PB, VB, s + 16);
+            mac(PA, VA);
+            mac(PB, VB);
+            s += 32;
+        } else {
+            mac(PA, VA);
+            s += 16;
+        }
+    }
+    for (; s + 4 <= n; s += 4) {
+        const float4 p4 = *(const float4 *)(p + s);
+        const float4 v4 = *(const float4 *)(v + s);
+        float m0 = p4.x * v4.x; acc = acc + m0;
+        float m1 = p4.y * v4.y; acc = acc + m1;
+        float m2 = p4.z * v4.z; acc = acc + m2;
+        float m3 = p4.w * v4.w; acc = acc + m3;
+    }
+    for (; s < n; ++s) {
+        float m = p[s] * v[s];
+        acc = acc + m;
+    }
+    return acc;
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void attn_pv_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out) {
     constexpr int DW = 64 / G;               // dims per workgroup
+    constexpr int PPP = DW / 8;              // uint4 (8 f16) per position of the slice
     constexpr int kVChunk = kVFloats / DW;   // positions staged per pass
-    extern __shared__ __align__(16) float smem[];
-    float *pr = smem;                         // [G][Spad] scores, then probabilities
-    __shared__ float red[324];
-    __shared__ __align__(16) float vt[kVFloats];   // V slice, [d][s] f32
+    constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
+    extern __shared__ __align__(16) float pr[];   // [G][Spad] scores, then probabilities
+    __shared__ __align__(16) float vt[kVFloats];  // V slice, [d][s] f32
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
     const int Spad = (S + 3) & ~3;
     const int hk = blockIdx.x, d0 = blockIdx.y * DW;
-    const int tid = threadIdx.x;
-    for (int i = tid; i < G * S; i += 256) {
-        const int g = i / S, s = i % S;
-        pr[g * Spad + s] = scores[(size_t)(hk * G + g) * max_seq + s];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
+
+    // V slice of the first chunk: issued before anything else
+    uint4 r[kLoads];
+    auto load_chunk = [&](int c0) {
+        const int n = min(kVChunk, S - c0);
+#pragma unroll
+        for (int k = 0; k < kLoads; ++k) {
+            const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
+            r[k] = s < n ? *(const uint4 *)(Vh + (size_t)(c0 + s) * kHd + 8 * h)
+                         : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_chunk(0);
+
+    // each wave owns heads w, w+4: load its score rows and run their softmax
+    for (int g = w; g < G; g += 4) {
+        float *row = pr + g * Spad;
+        const float *src = scores + (size_t)(hk * G + g) * max_seq;
+        for (int s = lane; s < S; s += 64) row[s] = src[s];
+        wave_softmax_row(row, S, Spad, lane);
     }
-    __syncthreads();
-    // sh/softmax.wgsl:25-80 per head: max, strided exp sums + tree, normalise
-#pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        float* row = pr + g * Spad;
-        float m = -3.402823e+38f;
-        for (int s = tid; s < S; s += 256) m = fmaxf(m, row[s]);
-        m = block256_max(m, red);
-        float part = 0.0f;
-        for (int s = tid; s < S; s += 256) part = part + oxb_expf(row[s] - m);
-        const float inv = 1.0f / block256_tree_sum_fast(part, red);
-        for (int s = tid; s < S; s += 256) row[s] = oxb_expf(row[s] - m) * inv;
-        for (int s = S + tid; s < Spad; s += 256) row[s] = 0.0f;
-    }
+
     // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s
-    const int lane = tid & 63;
     const int g = lane / DW, dd = lane % DW;
     float acc = 0.0f;
-    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
     for (int c0 = 0; c0 < S; c0 += kVChunk) {
         const int n = min(kVChunk, S - c0);
-        __syncthreads();  // previous chunk consumed (and softmax done)
-        for (int i = tid; i < n * DW; i += 256) {
-            const int s = i / DW, e = i % DW;
-            vt[e * kVChunk + s] = __half2float(__ushort_as_half(Vh[(size_t)(c0 + s) * kHd + e]));
+        __syncthreads();  // probabilities ready / previous chunk consumed
+#pragma unroll
+        for (int k = 0; k < kLoads; ++k) {
+            const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
+            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 f = __half22float2(*(const __half2 *)&wv[e]);
+                vt[(8 * h + 2 * e) * kVChunk + s] = f.x;
+                vt[(8 * h + 2 * e + 1) * kVChunk + s] = f.y;
+            }
         }
         __syncthreads();
-        if (tid < 64) {
-            const float *prow = pr + g * Spad + c0;
-            const float *vrow = vt + dd * kVChunk;
-            int s = 0;
-            for (; s + 4 <= n; s += 4) {
-                const float4 p4 = *(const float4 *)(prow + s);
-                const float4 v4 = *(const float4 *)(vrow + s);
-                float m0 = p4.x * v4.x; acc = acc + m0;
-                float m1 = p4.y * v4.y; acc = acc + m1;
-                float m2 = p4.z * v4.z; acc = acc + m2;
-                float m3 = p4.w * v4.w; acc = acc + m3;
-            }
-            for (; s < n; ++s) {
-                float m = prow[s] * vrow[s];
-                acc = acc + m;
-            }
-        }
+        if (c0 + kVChunk < S) load_chunk(c0 + kVChunk);
+        if (tid < 64) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVChunk, n, acc);
     }
     if (tid < 64) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }

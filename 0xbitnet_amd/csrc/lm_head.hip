@@ -12,25 +12,17 @@
 
 namespace oxb {
 
-constexpr int kLmBlocks = 1024;  // persistent-style grid: 4 workgroups per CU
-constexpr int kLmMaxLoads = 8;   // 16-byte loads per row per lane: D <= 8*64*8 = 4096
-
 struct LmParams {
     const float *x;        // residual stream row [D] (pre final-norm)
     const float *gamma;    // final norm weight [D]
     float eps;
-    const uint4 *E;        // [V][D] f16
+    const uint4 *E;        // lm-tiled embedding (below)
     int V, D;
     float *logits;         // [V]
-    float2 *part;          // [gridDim.x] (max value, index bits)
     int *state;            // decode state (see oxb_kernels.h)
     int *tok_hist;         // [max_gen] generated tokens, may be null
     int advance;           // positions to add to state.pos (tokens in this forward)
 };
-
-__device__ inline bool better(float v, int i, float bv, int bi) {
-    return v > bv || (v == bv && i < bi);
-}
 
 // Row-per-lane layout of the tied embedding for the LM head ("lm-tiled"):
 // 64-row tiles; each lane (row) streams the pairs (E[2dh], E[2dh+1]) of its
@@ -40,147 +32,195 @@ __device__ inline bool better(float v, int i, float bv, int bi) {
 // uint4 ((T*NQ + u/4)*64 + r), component u%4 (NQ = 64*NJ uint4 per lane).
 // The halving tree of sh/f32_matmul.wgsl:59-68 is the balanced pairwise
 // tree over the 256 thread sums taken in bit-reversed order, so a lane can
-// fold it left to right: 16-leaf subtrees in registers, then the 16 subtree
-// sums.  Result: the shader's exact f32 value, no cross-lane traffic.
+// fold it left to right: 8-leaf subtrees in registers, pairs of them into
+// the 16 sums of 16 leaves, then the tree over those 16.  Result: the
+// shader's exact f32 value.
 __host__ __device__ inline int bitrev4(int x) {
     return ((x & 1) << 3) | ((x & 2) << 1) | ((x & 4) >> 1) | ((x & 8) >> 3);
 }
 
+// (value, index) -> u64 whose unsigned maximum is the largest value with the
+// lowest index on ties (rs/sampling.rs argmax semantics); -0 counts as +0,
+// as the comparison v > best does.
+__device__ inline unsigned long long argmax_key(float v, int i) {
+    if (v == 0.0f) v = 0.0f;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xffffffffu - (uint32_t)i);
+}
+
+__device__ inline bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// Barrier that orders LDS only: a plain __syncthreads() would also wait for
+// the weight prefetch in flight.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// 8 leaves (half of a 16-leaf group) of one row: 8*NJ pairs = 2*NJ uint4.
+// Each product is fma(h, e, +0): the same value as h*e except that a -0
+// product becomes +0, which cannot change the running sum (it starts at +0
+// and a round-to-nearest sum is -0 only if both terms are -0).  The fma
+// takes the f16 operand directly (v_fma_mix_f32), one op instead of two.
+template <int NJ>
+__device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk) {
+    float L[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int u = m * NJ + j;
+            const uint32_t word = (&e[u >> 2].x)[u & 3];
+            const float2 hh = hk[u];
+            const float e0 = __half2float(__ushort_as_half((uint16_t)(word & 0xffffu)));
+            const float e1 = __half2float(__ushort_as_half((uint16_t)(word >> 16)));
+            const float m0 = __builtin_fmaf(hh.x, e0, 0.0f);
+            acc = acc + m0;
+            const float m1 = __builtin_fmaf(hh.y, e1, 0.0f);
+            acc = acc + m1;
+        }
+        L[m] = acc;
+    }
+#pragma unroll
+    for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+        for (int m = 0; m < 8; m += 2 * st) L[m] = L[m] + L[m + st];
+    return L[0];
+}
+
+// One workgroup per lm tile at a time (tiles blockIdx.x + i*gridDim.x); its
+// 4 waves split the tile's 32 half-groups (8 leaves each) 8 apiece and
+// stream them double-buffered, so 20 KiB per wave stay in flight.  The 16
+// group sums meet in LDS; one wave per tile folds them, writes the logits and
+// keeps a running argmax.  Block winners meet in one 64-bit atomic max
+// (argmax_key) in the decode state; the last block to take a ticket
+// publishes the token.  Agent-scope atomic RMWs are coherent across the
+// chip's L2s, and each block waits for its max to return before taking its
+// ticket, so the ticket order covers every max.  No cache-wide fences: a
+// release/acquire per block writes back and invalidates the L2 and cost
+// ~0.25 us per block.
 template <int NJ>  // D = 512 * NJ
 __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
     __shared__ float red[324];
-    __shared__ __align__(16) float h_lds[kLmMaxLoads * 512];
     __shared__ __align__(16) float2 hp[256 * NJ];   // h pairs in consumption order
+    __shared__ float Tl[2][16][64];                 // group sums, double-buffered per tile
     __shared__ float bval[4];
     __shared__ int bidx[4];
-    __shared__ int ticket_s;
+    constexpr int NQ = 64 * NJ, HQ = 2 * NJ;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = p.D;
-    constexpr int NQ = 64 * NJ;   // uint4 per lane per tile
+    const int ntiles = (p.V + 63) >> 6;
+    const int my_tiles =
+        (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int nseq = my_tiles * 8;  // half-groups of this wave
+    auto src_of = [&](int s) {
+        const int tile = blockIdx.x + (s >> 3) * gridDim.x;
+        const int hg = 8 * w + (s & 7);
+        return p.E + ((size_t)tile * NQ + (size_t)hg * HQ) * 64 + lane;
+    };
+    auto load_hg = [&](uint4 (&dst)[HQ], int s) {
+        const uint4 *sp = src_of(s);
+        // keep each batch together so the wait for one batch never covers the next
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) dst[q] = load_nt(sp + q * 64);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    uint4 A[HQ], B[HQ];
+    if (nseq > 0) load_hg(A, 0);   // weights do not depend on the norm: start early
 
-    // final RMSNorm (sh/rmsnorm.wgsl order), h to LDS
+    // final RMSNorm (sh/rmsnorm.wgsl order) straight into the pair table
     float ss = 0.0f;
     for (int c = tid; c < D; c += 256) {
-        float v = p.x[c];
-        float sq = v * v;
+        const float v = p.x[c];
+        const float sq = v * v;
         ss = ss + sq;
     }
     const float sum = block256_tree_sum_fast(ss, red);
     const float rms = 1.0f / sqrtf(sum / (float)D + p.eps);
-    for (int c = tid; c < D; c += 256) {
-        float a = p.x[c] * rms;
-        h_lds[c] = a * p.gamma[c];
-    }
-    __syncthreads();
     for (int u = tid; u < 256 * NJ; u += 256) {
         const int i = u / NJ, j = u % NJ;
         const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
-        const int dh = t + 256 * j;
-        hp[u] = make_float2(h_lds[2 * dh], h_lds[2 * dh + 1]);
+        const int d0 = 2 * (t + 256 * j);
+        const float a0 = p.x[d0] * rms, a1 = p.x[d0 + 1] * rms;
+        hp[u] = make_float2(a0 * p.gamma[d0], a1 * p.gamma[d0 + 1]);
     }
     __syncthreads();
 
-    const int ntiles = (p.V + 63) >> 6;
     float best = -INFINITY;
     int besti = 0x7fffffff;
-    __shared__ float Tl[4][16][64];   // per-lane 16-leaf subtree sums
-    for (int tile = blockIdx.x * 4 + w; tile < ntiles; tile += gridDim.x * 4) {
-        const uint4 *src = p.E + (size_t)tile * NQ * 64 + lane;
-#pragma unroll 1
-        for (int k = 0; k < 16; ++k) {
-            // 16 leaves i = 16k + m, m = 0..15: 16*NJ dwords = 4*NJ uint4
-            uint4 e[4 * NJ];
+    auto finish_pair = [&](float g0, float g1, int s) {
+        const int k = (8 * w + (s & 7)) >> 1;   // 16-leaf group
+        const int i = s >> 3;                   // tile ordinal within this block
+        Tl[i & 1][k][lane] = g0 + g1;
+        if ((s & 7) == 6) {                     // this tile's groups are all done
+            lds_barrier();
+            if (w == (i & 3)) {
+                float T[16];
 #pragma unroll
-            for (int qq = 0; qq < 4 * NJ; ++qq) e[qq] = load_nt(src + (size_t)(k * 4 * NJ + qq) * 64);
-            const float2 *hk = hp + k * 16 * NJ;
-            float L[16];
+                for (int kk = 0; kk < 16; ++kk) T[kk] = Tl[i & 1][kk][lane];
 #pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                float acc = 0.0f;
+                for (int st = 1; st < 16; st <<= 1)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    const int u = m * NJ + j;
-                    const uint32_t word = (&e[u >> 2].x)[u & 3];
-                    const float2 hh = hk[u];
-                    const float e0 = __half2float(__ushort_as_half((uint16_t)(word & 0xffffu)));
-                    const float e1 = __half2float(__ushort_as_half((uint16_t)(word >> 16)));
-                    float m0 = hh.x * e0;
-                    acc = acc + m0;
-                    float m1 = hh.y * e1;
-                    acc = acc + m1;
+                    for (int m = 0; m < 16; m += 2 * st) T[m] = T[m] + T[m + st];
+                const int row = (blockIdx.x + i * gridDim.x) * 64 + lane;
+                if (row < p.V) {
+                    p.logits[row] = T[0];
+                    if (better(T[0], row, best, besti)) { best = T[0]; besti = row; }
                 }
-                L[m] = acc;
             }
-#pragma unroll
-            for (int st = 1; st < 16; st <<= 1)
-#pragma unroll
-                for (int m = 0; m < 16; m += 2 * st) L[m] = L[m] + L[m + st];
-            Tl[w][k][lane] = L[0];
         }
-        float T[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) T[k] = Tl[w][k][lane];
-#pragma unroll
-        for (int st = 1; st < 16; st <<= 1)
-#pragma unroll
-            for (int m = 0; m < 16; m += 2 * st) T[m] = T[m] + T[m + st];
-        const int row = tile * 64 + lane;
-        if (row < p.V) {
-            p.logits[row] = T[0];
-            if (better(T[0], row, best, besti)) { best = T[0]; besti = row; }
-        }
+    };
+    int s = 0;
+    for (; s < nseq - 2; s += 2) {
+        load_hg(B, s + 1);
+        const float g0 = lm_half_group<NJ>(A, hp + (8 * w + (s & 7)) * 8 * NJ);
+        load_hg(A, s + 2);
+        const float g1 = lm_half_group<NJ>(B, hp + (8 * w + (s & 7) + 1) * 8 * NJ);
+        finish_pair(g0, g1, s);
     }
+    if (nseq > 0) {   // last pair: nothing left to prefetch
+        load_hg(B, s + 1);
+        const float g0 = lm_half_group<NJ>(A, hp + (8 * w + (s & 7)) * 8 * NJ);
+        const float g1 = lm_half_group<NJ>(B, hp + (8 * w + (s & 7) + 1) * 8 * NJ);
+        finish_pair(g0, g1, s);
+    }
+
 #pragma unroll
-    for (int s = 32; s > 0; s >>= 1) {
-        const float ov = __shfl_xor(best, s, 64);
-        const int oi = __shfl_xor(besti, s, 64);
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(besti, o, 64);
         if (better(ov, oi, best, besti)) { best = ov; besti = oi; }
     }
     if (lane == 0) { bval[w] = best; bidx[w] = besti; }
     __syncthreads();
-    if (tid == 0) {
-        float bv = bval[0];
-        int bi = bidx[0];
-        for (int k = 1; k < 4; ++k)
-            if (better(bval[k], bidx[k], bv, bi)) { bv = bval[k]; bi = bidx[k]; }
-        p.part[blockIdx.x] = make_float2(bv, __int_as_float(bi));
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0)
-        ticket_s = __hip_atomic_fetch_add(&p.state[OXB_ST_LM_COUNTER], 1, __ATOMIC_ACQ_REL,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket_s != (int)gridDim.x - 1) return;
-    __threadfence();
-    // last block: reduce the per-block winners (lowest index on ties)
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int b = tid; b < (int)gridDim.x; b += 256) {
-        const float v = __hip_atomic_load(&p.part[b].x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int i = __float_as_int(
-            __hip_atomic_load(&p.part[b].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if (better(v, i, bv, bi)) { bv = v; bi = i; }
-    }
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) {
-        const float ov = __shfl_xor(bv, s, 64);
-        const int oi = __shfl_xor(bi, s, 64);
-        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { bval[w] = bv; bidx[w] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int k = 1; k < 4; ++k)
-            if (better(bval[k], bidx[k], bval[0], bidx[0])) { bval[0] = bval[k]; bidx[0] = bidx[k]; }
-        const int tok = bidx[0];
-        int *st = p.state;
-        st[OXB_ST_TOKEN] = tok;
-        if (p.tok_hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) p.tok_hist[st[OXB_ST_NGEN]] = tok;
-        st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
-        st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
-        st[OXB_ST_LM_COUNTER] = 0;
-    }
+    if (tid != 0) return;
+    float bv = bval[0];
+    int bi = bidx[0];
+    for (int k = 1; k < 4; ++k)
+        if (better(bval[k], bidx[k], bv, bi)) { bv = bval[k]; bi = bidx[k]; }
+    int *st = p.state;
+    unsigned long long *key = (unsigned long long *)(st + OXB_ST_LM_KEY);
+    const unsigned long long old =
+        __hip_atomic_fetch_max(key, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"((uint32_t)old));   // wait for the max before the ticket
+    const int ticket = __hip_atomic_fetch_add(&st[OXB_ST_LM_COUNTER], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    if (ticket != (int)gridDim.x - 1) return;
+    const unsigned long long k =
+        __hip_atomic_fetch_or(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int tok = (int)(0xffffffffu - (uint32_t)k);
+    st[OXB_ST_TOKEN] = tok;
+    if (p.tok_hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) p.tok_hist[st[OXB_ST_NGEN]] = tok;
+    st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
+    st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&st[OXB_ST_LM_COUNTER], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x[t][d] = E[id_t][d] (f16 -> f32); ids out of range give zeros.
@@ -237,18 +277,20 @@ __global__ void repack_tiled_kernel(const uint4 *__restrict__ src, uint4 *__rest
 using namespace oxb;
 
 extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
-                                  const void *E, int V, int D, float *logits, float *part,
-                                  int *state, int *tok_hist, int advance, void *stream) {
+                                  const void *E, int V, int D, float *logits, int *state,
+                                  int *tok_hist, int advance, void *stream) {
     OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512,
                 "lm_head: hidden %d must be a multiple of 512 and <= 2560", D);
     OXB_REQUIRE(V > 0, "lm_head: vocab %d", V);
-    LmParams p{x, gamma, eps, (const uint4 *)E, V, D, logits, (float2 *)part, state, tok_hist,
-               advance};
+    OXB_REQUIRE(((uintptr_t)state & 7) == 0, "lm_head: state must be 8-byte aligned");
+    LmParams p{x, gamma, eps, (const uint4 *)E, V, D, logits, state, tok_hist, advance};
+    // 4 tiles per workgroup: ~2 workgroups per CU for a 128k vocabulary
+    const int grid = ((V + 63) / 64 + 3) / 4;
     hipStream_t s = (hipStream_t)stream;
     switch (D / 512) {
-#define OXB_NL(n)                                                                       \
-    case n:                                                                             \
-        hipLaunchKernelGGL(lm_head_kernel<n>, dim3(kLmBlocks), dim3(256), 0, s, p);     \
+#define OXB_NL(n)                                                                   \
+    case n:                                                                         \
+        hipLaunchKernelGGL(lm_head_kernel<n>, dim3(grid), dim3(256), 0, s, p);      \
         break;
         OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5)
 #undef OXB_NL
@@ -259,8 +301,6 @@ extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
-
-extern "C" int oxb_lm_head_partials(void) { return kLmBlocks; }
 
 extern "C" int oxb_repack_lm(const uint16_t *E, void *E_lm, int V, int D, void *stream) {
     OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512 && V > 0, "repack_lm: bad shape V %d D %d", V, D);

@@ -424,11 +424,10 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->h = (float *)m->dalloc((size_t)F * 4);
     m->scores = (float *)m->dalloc((size_t)H * m->max_seq * 4);
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
-    m->lm_part = (float *)m->dalloc((size_t)oxb_lm_head_partials() * 2 * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->lm_part || !m->state || !m->tok_hist)
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_elems * 2) != hipSuccess ||
         hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess) {
@@ -485,7 +484,7 @@ int oxb_model::enqueue_decode_step() {
                                nullptr, s))
             return -1;
     }
-    return oxb_lm_head_argmax(x, final_norm, eps, embed_lm, V, D, logits, lm_part, state, tok_hist,
+    return oxb_lm_head_argmax(x, final_norm, eps, embed_lm, V, D, logits, state, tok_hist,
                               1, s);
 }
 
@@ -565,7 +564,7 @@ int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
             return -1;
     }
     return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed_lm, V, D, logits,
-                              lm_part, state, tok_hist, n, s);
+                              state, tok_hist, n, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -622,6 +621,8 @@ static int write_state(oxb_model *m) {
     st[OXB_ST_NGEN] = m->ngen;
     st[OXB_ST_LM_COUNTER] = 0;
     st[OXB_ST_HIST_CAP] = m->hist_cap;
+    st[5] = 0;
+    st[OXB_ST_LM_KEY] = st[OXB_ST_LM_KEY + 1] = 0;
     M_CHECK(hipMemcpyAsync(m->state, st, OXB_STATE_INTS * 4, hipMemcpyHostToDevice, m->stream));
     M_CHECK(hipStreamSynchronize(m->stream));
     return 0;

@@ -34,7 +34,7 @@ struct oxb_model {
 
     // decode buffers
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr, *scores = nullptr;
-    float *logits = nullptr, *lm_part = nullptr;
+    float *logits = nullptr;
     int *state = nullptr, *tok_hist = nullptr;
     int hist_cap = 0;
 

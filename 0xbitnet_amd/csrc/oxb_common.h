@@ -168,6 +168,33 @@ __device__ inline float block256_tree_sum_fast(float part, float *red) {
     return a[0];
 }
 
+// The same 256-thread halving tree with a single barrier.  After the
+// strides 128..32 and 16 the survivor i < 16 is
+//   w[i] = (u[i] + u[i+32]) + (u[i+16] + u[i+48]),
+//   u[j] = (s[j] + s[j+128]) + (s[j+64] + s[j+192]),
+// so lane i of every 16-lane row reads its 16 leaves from LDS and folds them
+// in that order; DPP row_shl:8,4,2,1 (lane l takes lane l+k of its row) does
+// strides 8..1 and lane 0 holds the shader's sum.  red >= 256 floats; all
+// 256 threads must call; result to all threads.
+__device__ inline float block256_tree_sum_1b(float part, float *red) {
+    const int t = threadIdx.x;
+    red[t] = part;
+    __syncthreads();
+    const int i = t & 15;
+    float u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int j = i + 16 * k;
+        u[k] = (red[j] + red[j + 128]) + (red[j + 64] + red[j + 192]);
+    }
+    float s = (u[0] + u[2]) + (u[1] + u[3]);
+    s = s + __int_as_float(dpp0<0x108, 0xf>(__float_as_int(s)));
+    s = s + __int_as_float(dpp0<0x104, 0xf>(__float_as_int(s)));
+    s = s + __int_as_float(dpp0<0x102, 0xf>(__float_as_int(s)));
+    s = s + __int_as_float(dpp0<0x101, 0xf>(__float_as_int(s)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);

@@ -7,15 +7,18 @@
 // sh/elementwise.wgsl (gate/up epilogue, residual epilogue).
 //
 // One workgroup (4 waves) owns one 16-row tile.  The 4 waves split the
-// tile's K range; inside a wave lane l streams chunks (row l%16,
-// kc0 + l/16 + 4j), so every wave load is one contiguous KiB.  Before the
-// prologue runs, each lane already has its first 8 chunks (128 B) in flight.
+// tile's K range into whole 128-blocks; inside a wave lane l streams chunks
+// (row l%16, kc0 + l/16 + 4j), so every wave load is one contiguous KiB.
+// All loads are branch-free (clamped addresses, masked values) so the
+// compiler's memory counters stay exact: the weights are in flight while
+// the prologue runs.  The prologue has two barriers (the RMS sum and the
+// absmax); each wave then quantizes exactly the K range it multiplies, so
+// the main loop starts without a third.
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
 namespace oxb {
 
-constexpr int kPrefetch = 8;   // 16-byte chunks per lane issued per batch
 constexpr int kMaxNormReg = 28; // f32 values per thread in a norm prologue (D <= 7168)
 
 enum Pro { PRO_INT8 = 0, PRO_QUANT = 1 };           // PRO_QUANT: optional RMSNorm + quantize
@@ -47,23 +50,36 @@ struct GemvParams {
 };
 
 // ---------------------------------------------------------------------------
-// Prologue: RMSNorm (optional) + per-token absmax int8 quantize of one row of
-// D f32 values by all 256 threads with the shaders' thread mapping (thread t
-// owns columns t, t+256, ...: sh/rmsnorm.wgsl:41-45, sh/quantize.wgsl:42-45).
-// The caller issues the loads (load_row) before its weight prefetch so both
-// round trips overlap.  Writes int8 into LDS, returns the scale and this
-// wave's share of sum(q) in wq[w] (summed after the caller's next barrier).
-// LDS: red >= 324 floats, wq >= 4 ints.
+// Row prologue for the several-token kernels: RMSNorm (optional) + per-token
+// absmax int8 quantize of one row of D f32 values by all 256 threads with
+// the shaders' thread mapping (thread t owns columns t, t+256, ...:
+// sh/rmsnorm.wgsl:41-45, sh/quantize.wgsl:42-45).  Writes int8 into LDS,
+// returns the scale and this wave's share of sum(q) in wq[w] (summed after
+// the caller's next barrier).  LDS: red >= 324 floats, wq >= 4 ints.
 // ---------------------------------------------------------------------------
+// Issues the loads only (clamped addresses, no use of the values), so a
+// caller can put more loads behind them; mask_row then zeroes columns >= D.
 template <int NREG>
 __device__ inline void load_row(const float *__restrict__ x, const float *__restrict__ gamma,
                                 int D, float (&v)[NREG], float (&g)[NREG]) {
     const int t = threadIdx.x;
+    const float *gp = gamma ? gamma : x;   // loads stay unconditional
 #pragma unroll
     for (int j = 0; j < NREG; ++j) {
-        const int c = t + j * 256;
-        v[j] = c < D ? x[c] : 0.0f;
-        g[j] = (gamma && c < D) ? gamma[c] : 0.0f;
+        const int c = min(t + j * 256, D - 1);
+        v[j] = x[c];
+        g[j] = gp[c];
+    }
+}
+
+template <int NREG>
+__device__ inline void mask_row(int D, float (&v)[NREG], float (&g)[NREG]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) {
+        const bool in = t + j * 256 < D;
+        v[j] = in ? v[j] : 0.0f;
+        g[j] = in ? g[j] : 0.0f;
     }
 }
 
@@ -71,16 +87,15 @@ template <int NREG>
 __device__ inline float norm_quant_regs(float (&v)[NREG], const float (&g)[NREG], bool norm,
                                         float eps, int D, int8_t *xq_lds, float *red, int *wq) {
     const int t = threadIdx.x;
+    mask_row<NREG>(D, v, const_cast<float (&)[NREG]>(g));
     if (norm) {
-        float ss = 0.0f;
+        float ss = 0.0f;   // columns past D hold +0 and add exactly nothing
 #pragma unroll
         for (int j = 0; j < NREG; ++j) {
-            if (t + j * 256 < D) {
-                float sq = v[j] * v[j];
-                ss = ss + sq;
-            }
+            float sq = v[j] * v[j];
+            ss = ss + sq;
         }
-        const float sum = block256_tree_sum_fast(ss, red);
+        const float sum = block256_tree_sum_1b(ss, red);
         const float rms = 1.0f / sqrtf(sum / (float)D + eps);  // inverseSqrt
 #pragma unroll
         for (int j = 0; j < NREG; ++j) {
@@ -90,8 +105,7 @@ __device__ inline float norm_quant_regs(float (&v)[NREG], const float (&g)[NREG]
     }
     float am = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NREG; ++j)
-        if (t + j * 256 < D) am = fmaxf(am, fabsf(v[j]));
+    for (int j = 0; j < NREG; ++j) am = fmaxf(am, fabsf(v[j]));
     am = wave_nonneg_max_dpp(am);
     if ((t & 63) == 0) red[320 + (t >> 6)] = am;
     __syncthreads();
@@ -117,86 +131,143 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-template <int PRO, int EPI, int NREG>
+// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [256]
+// | vf [K] f32 (PRO_QUANT only: the normalised activations).
+__host__ __device__ inline size_t gemv_smem(int K, bool quant) {
+    return (size_t)K + (256 + 4 + 4 + 256) * 4 + (quant ? (size_t)K * 4 : 0);
+}
+
+// NREG: strided f32 values per thread in the prologue (ceil(K/256));
+// PF: 16-byte weight chunks per lane per batch.
+template <int PRO, int EPI, int NREG, int PF>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) int8_t smem[];
-    int8_t *xq_lds = smem;                       // [K]
-    float *red = (float *)(smem + p.K);          // [324]
-    int *wq = (int *)(red + 324);                // [4]
-    int *wpart = wq + 4;                         // [256]
+    const int K = p.K;
+    int8_t *xq_lds = smem;
+    float *red = (float *)(smem + K);
+    float *wmax = red + 256;
+    int *wq = (int *)(wmax + 4);
+    int *wpart = wq + 4;
+    float *vf = (float *)(wpart + 256);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, c = lane >> 4;
-    const int KC = p.K >> 6;
+    const int KC = K >> 6;
+    const int per = (((KC + 3) >> 2) + 1) & ~1;   // chunks per wave: whole 128-blocks
+    const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
+    const int cpl = (per + 3) >> 2;               // chunks per lane
+    const int nb = (cpl + PF - 1) / PF;           // batches (uniform)
     const int tile = blockIdx.x;
     const uint4 *tw = p.W + (size_t)tile * KC * 16;
 
-    // ---- loads: activations first, then this lane's first weight chunks ----
+    // ---- loads: prologue inputs, then the residual, then the weights -------
     float v[NREG], g[NREG];
-    if constexpr (PRO == PRO_QUANT) load_row<NREG>(p.x, p.gamma, p.K, v, g);
+    if constexpr (PRO == PRO_QUANT) load_row<NREG>(p.x, p.gamma, K, v, g);
     float resid = 0.0f;
-    if constexpr (EPI == EPI_RESID) {
-        if (tid < 16) resid = p.y[tile * 16 + tid];
-    }
-    // Wave w owns chunks [kc0, kc1) of this tile.
-    const int per = (KC + 3) >> 2;
-    const int kc0 = w * per;
-    const int kc1 = min(KC, kc0 + per);
-    uint4 buf[kPrefetch];
+    if constexpr (EPI == EPI_RESID) resid = p.y[tile * 16 + (tid & 15)];
+    auto load_batch = [&](uint4 (&dst)[PF], int b) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kPrefetch; ++u) {
-        const int kc = kc0 + c + 4 * u;
-        buf[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r) : make_uint4(0, 0, 0, 0);
-    }
+        for (int u = 0; u < PF; ++u) {
+            const int kc = kc0 + c + 4 * (b * PF + u);
+            dst[u] = load_nt(tw + (size_t)min(kc, kc1 - 1) * 16 + r);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    uint4 A[PF], B[PF];
+    load_batch(A, 0);
 
     // ---- prologue ---------------------------------------------------------
     float in_scale;
-    int xsum;
+    int xsum = 0;
     if constexpr (PRO == PRO_INT8) {
-        const int nv = p.K >> 4;
-        for (int i = tid; i < nv; i += 256)
+        for (int i = tid; i < (K >> 4); i += 256)
             ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
         in_scale = p.xscale[0];
         xsum = p.xsum[0];
         __syncthreads();
     } else {
-        in_scale = norm_quant_regs<NREG>(v, g, p.gamma != nullptr, p.eps, p.K, xq_lds, red, wq);
-        __syncthreads();
-        xsum = wq[0] + wq[1] + wq[2] + wq[3];
-        if (tile == 0 && p.xq_out) {
-            for (int i = tid; i < (p.K >> 4); i += 256)
-                ((int4 *)p.xq_out)[i] = ((const int4 *)xq_lds)[i];
-            if (tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
-        }
-    }
-
-    // ---- main loop ----------------------------------------------------------
-    CodeAcc acc;
-    for (int base = kc0 + c; base < kc1; base += 4 * kPrefetch) {
-        uint4 nxt[kPrefetch];
+        mask_row<NREG>(K, v, g);
+        if (p.gamma) {
+            float ss = 0.0f;   // columns past K hold +0 and add exactly nothing
 #pragma unroll
-        for (int u = 0; u < kPrefetch; ++u) {
-            const int kc = base + 4 * kPrefetch + 4 * u;
-            nxt[u] = kc < kc1 ? load_nt(tw + (size_t)kc * 16 + r) : make_uint4(0, 0, 0, 0);
-        }
+            for (int j = 0; j < NREG; ++j) {
+                float sq = v[j] * v[j];
+                ss = ss + sq;
+            }
+            const float sum = block256_tree_sum_1b(ss, red);
+            const float rms = 1.0f / sqrtf(sum / (float)K + p.eps);  // inverseSqrt
 #pragma unroll
-        for (int u = 0; u < kPrefetch; ++u) {
-            const int kc = base + 4 * u;
-            if (kc < kc1) {
-                const int xo = (kc >> 1) * 128 + (kc & 1) * 16;
-                const int4 x0 = *(const int4 *)(xq_lds + xo);
-                const int4 x1 = *(const int4 *)(xq_lds + xo + 32);
-                const int4 x2 = *(const int4 *)(xq_lds + xo + 64);
-                const int4 x3 = *(const int4 *)(xq_lds + xo + 96);
-                acc.add(buf[u].x, x0.x, x1.x, x2.x, x3.x);
-                acc.add(buf[u].y, x0.y, x1.y, x2.y, x3.y);
-                acc.add(buf[u].z, x0.z, x1.z, x2.z, x3.z);
-                acc.add(buf[u].w, x0.w, x1.w, x2.w, x3.w);
+            for (int j = 0; j < NREG; ++j) {
+                float a = v[j] * rms;
+                v[j] = a * g[j];
             }
         }
+        float am = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kPrefetch; ++u) buf[u] = nxt[u];
+        for (int j = 0; j < NREG; ++j) {
+            const int col = tid + 256 * j;
+            if (col < K) vf[col] = v[j];
+            am = fmaxf(am, fabsf(v[j]));
+        }
+        am = wave_nonneg_max_dpp(am);
+        if (lane == 0) wmax[w] = am;
+        __syncthreads();
+        am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        in_scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
+        const float inv = am == 0.0f ? 0.0f : 127.0f / am;  // :68
+        // this wave's K range [64 kc0, 64 kc1): quantize, keep its sum(q)
+        int sq = 0;
+        const int k0 = kc0 * 64, k1 = kc1 * 64;
+        const bool out = tile == 0 && p.xq_out;
+#pragma unroll
+        for (int i = 0; i < NREG; ++i) {
+            const int k = k0 + lane + 64 * i;
+            if (k < k1) {
+                const int q = quant_one(vf[k], inv);
+                xq_lds[k] = (int8_t)q;
+                sq += q;
+                if (out) p.xq_out[k] = (int8_t)q;
+            }
+        }
+        sq = wave_isum_dpp(sq);
+        if (lane == 0) wq[w] = sq;
+        if (out && tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
+    }
+
+    // ---- main loop: chunks past this wave's range multiply zero codes ------
+    CodeAcc acc;
+    auto mac_batch = [&](const uint4 (&src)[PF], int b) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int kc = kc0 + c + 4 * (b * PF + u);
+            const int kcl = min(kc, kc1 - 1);   // own range (kc1 >= 1)
+            const uint4 wv = kc < kc1 ? src[u] : make_uint4(0, 0, 0, 0);
+            const int xo = (kcl >> 1) * 128 + (kcl & 1) * 16;
+            const int4 x0 = *(const int4 *)(xq_lds + xo);
+            const int4 x1 = *(const int4 *)(xq_lds + xo + 32);
+            const int4 x2 = *(const int4 *)(xq_lds + xo + 64);
+            const int4 x3 = *(const int4 *)(xq_lds + xo + 96);
+            acc.add(wv.x, x0.x, x1.x, x2.x, x3.x);
+            acc.add(wv.y, x0.y, x1.y, x2.y, x3.y);
+            acc.add(wv.z, x0.z, x1.z, x2.z, x3.z);
+            acc.add(wv.w, x0.w, x1.w, x2.w, x3.w);
+        }
+    };
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+        load_batch(B, b + 1);
+        mac_batch(A, b);
+        load_batch(A, b + 2);
+        mac_batch(B, b + 1);
+    }
+    if (b + 1 < nb) {
+        load_batch(B, b + 1);
+        mac_batch(A, b);
+        mac_batch(B, b + 1);
+    } else {
+        mac_batch(A, b);
     }
 
     // ---- reduction: 16 partials per row (4 lanes x 4 waves) through LDS ----
@@ -206,6 +277,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     int a = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) a += wpart[k * 16 + r];
+    if constexpr (PRO == PRO_QUANT) xsum = wq[0] + wq[1] + wq[2] + wq[3];
     a -= xsum;
     const int n = tile * 16 + r;
     if (p.acc_out) p.acc_out[n] = a;
@@ -316,23 +388,38 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-static size_t gemv_smem(int K) { return (size_t)K + 324 * 4 + 4 * 4 + 256 * 4 + 16; }
-
-template <int PRO, int EPI, int NREG>
+template <int PRO, int EPI, int NREG, int PF>
 static int launch_n(const GemvParams &p, hipStream_t s) {
-    const size_t sm = gemv_smem(p.K);
-    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG>), dim3(p.N / 16), dim3(256), sm, s, p);
+    const size_t sm = gemv_smem(p.K, PRO == PRO_QUANT);
+    if (sm > 64 * 1024) {
+        static bool raised = false;   // per instantiation
+        if (!raised) {
+            OXB_CHECK_HIP(hipFuncSetAttribute((const void *)gemv_kernel<PRO, EPI, NREG, PF>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              160 * 1024));
+            raised = true;
+        }
+    }
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF>), dim3(p.N / 16), dim3(256), sm, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-// NREG = f32 values per thread in the norm prologue (ceil(K / 256)).
+// NREG = ceil(K/256) bucket for PRO_QUANT; PF = chunks per lane per batch,
+// at most 4 (two batches in flight keep <= 8 chunks per lane).
 template <int PRO, int EPI>
 static int launch(const GemvParams &p, hipStream_t s) {
-    if (PRO == PRO_INT8) return launch_n<PRO, EPI, 1>(p, s);
-    if (p.K <= 1024) return launch_n<PRO, EPI, 4>(p, s);
-    if (p.K <= 2560) return launch_n<PRO, EPI, 10>(p, s);
-    return launch_n<PRO, EPI, kMaxNormReg>(p, s);
+    const int KC = p.K >> 6;
+    const int cpl = (((((KC + 3) >> 2) + 1) & ~1) + 3) >> 2;
+    if constexpr (PRO == PRO_INT8) {
+        if (cpl <= 1) return launch_n<PRO, EPI, 1, 1>(p, s);
+        if (cpl <= 3) return launch_n<PRO, EPI, 1, 3>(p, s);
+        return launch_n<PRO, EPI, 1, 4>(p, s);
+    } else {
+        if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1>(p, s);
+        if (p.K <= 2560) return launch_n<PRO, EPI, 10, 3>(p, s);
+        return launch_n<PRO, EPI, kMaxNormReg, 4>(p, s);
+    }
 }
 
 static int check_shape(int N, int K, bool norm) {

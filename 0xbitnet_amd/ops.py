@@ -228,12 +228,11 @@ def lm_head_argmax(x: np.ndarray, gamma: np.ndarray, eps: float, E_f16: np.ndarr
     check(lib().oxb_repack_lm(dE0.ptr, dE.ptr, V, D, None), "repack_lm")
     dE0.free()
     logits = DeviceArray((V,), np.float32)
-    part = DeviceArray((2 * lib().oxb_lm_head_partials(),), np.float32)
     st = np.zeros(STATE_INTS, np.int32)
     st[STATE_HIST_CAP] = 4
     dst = DeviceArray.from_host(st)
     hist = DeviceArray((4,), np.int32, zero=True)
-    check(lib().oxb_lm_head_argmax(dx.ptr, dg.ptr, eps, dE.ptr, V, D, logits.ptr, part.ptr, dst.ptr,
+    check(lib().oxb_lm_head_argmax(dx.ptr, dg.ptr, eps, dE.ptr, V, D, logits.ptr, dst.ptr,
                                    hist.ptr, 1, None), "lm_head_argmax")
     sync()
     s = dst.download()

@@ -36,6 +36,7 @@ extern "C" {
 #define OXB_ST_NGEN 2        /* LM-head invocations since reset              */
 #define OXB_ST_LM_COUNTER 3  /* internal: LM-head last-block ticket          */
 #define OXB_ST_HIST_CAP 4    /* capacity of the token history buffer         */
+#define OXB_ST_LM_KEY 6      /* internal: ints 6-7, LM-head argmax key (u64) */
 #define OXB_STATE_INTS 8
 
 /* ---- errors, device memory, streams, events (plumbing) ----------------- */
@@ -148,12 +149,12 @@ size_t oxb_lm_bytes(int V, int D);
  * (bit-identical to sh/f32_matmul.wgsl's reduction order) -> greedy argmax
  * (lowest index on ties) written to state[OXB_ST_TOKEN], appended to
  * tok_hist (if state[OXB_ST_HIST_CAP] allows), state[OXB_ST_POS] += advance.
- * part: float[2 * oxb_lm_head_partials()].  Replaces nn/model.rs:226-262,
+ * state is 8-byte aligned with OXB_ST_LM_COUNTER and OXB_ST_LM_KEY zero
+ * (the kernel leaves them zero).  Replaces nn/model.rs:226-262,
  * 393-448 plus read_logits (:269-298) and sampling.rs with top_k = 1. */
 int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const void *E_lm, int V,
-                       int D, float *logits, float *part, int *state, int *tok_hist,
-                       int advance, void *stream);
-int oxb_lm_head_partials(void);
+                       int D, float *logits, int *state, int *tok_hist, int advance,
+                       void *stream);
 
 /* ---- model (ids level) ------------------------------------------------------
  * The ids-level seam the parity and benchmark harnesses drive: the
