@@ -139,8 +139,11 @@ __host__ __device__ inline size_t gemv_smem(int K, bool quant) {
 
 // NREG: strided f32 values per thread in the prologue (ceil(K/256));
 // PF: 16-byte weight chunks per lane per batch.
+// Waves per SIMD the register budget must allow: 4 (<= 128 VGPRs) for the
+// one-batch shapes, so that e.g. 864 workgroups of a 13824-row GEMV are all
+// resident at once; the 4-chunk batches need more registers.
 template <int PRO, int EPI, int NREG, int PF>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) int8_t smem[];
     const int K = p.K;
     int8_t *xq_lds = smem;
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int per = (((KC + 3) >> 2) + 1) & ~1;   // chunks per wave: whole 128-blocks
     const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
     const int cpl = (per + 3) >> 2;               // chunks per lane
-    const int nb = (cpl + PF - 1) / PF;           // batches (uniform)
+    const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 when PF <= 3)
     const int tile = blockIdx.x;
     const uint4 *tw = p.W + (size_t)tile * KC * 16;
 
@@ -175,7 +178,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    uint4 A[PF], B[PF];
+    uint4 A[PF];
+    [[maybe_unused]] uint4 B[PF];
     load_batch(A, 0);
 
     // ---- prologue ---------------------------------------------------------
@@ -255,19 +259,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             acc.add(wv.w, x0.w, x1.w, x2.w, x3.w);
         }
     };
-    int b = 0;
-    for (; b + 2 < nb; b += 2) {
-        load_batch(B, b + 1);
-        mac_batch(A, b);
-        load_batch(A, b + 2);
-        mac_batch(B, b + 1);
-    }
-    if (b + 1 < nb) {
-        load_batch(B, b + 1);
-        mac_batch(A, b);
-        mac_batch(B, b + 1);
+    if constexpr (PF <= 3) {   // the launcher picks PF <= 3 only when one batch covers the range
+        mac_batch(A, 0);
     } else {
-        mac_batch(A, b);
+        int b = 0;
+        for (; b + 2 < nb; b += 2) {
+            load_batch(B, b + 1);
+            mac_batch(A, b);
+            load_batch(A, b + 2);
+            mac_batch(B, b + 1);
+        }
+        if (b + 1 < nb) {
+            load_batch(B, b + 1);
+            mac_batch(A, b);
+            mac_batch(B, b + 1);
+        } else {
+            mac_batch(A, b);
+        }
     }
 
     // ---- reduction: 16 partials per row (4 lanes x 4 waves) through LDS ----
