@@ -14,9 +14,21 @@ The JSON line also carries
                 N=8192 x K=28672, M=1, timed with HIP events over launches that
                 rotate 16 distinct weight copies (940 MB > the 256 MB MALL);
   gemv_sweep    the same for the other decode/sweep shapes;
+  gemm_sweep    the ternary GEMM on int8 MFMA at M = 8 .. 4096 tokens for
+                both sweep shapes (TOPS, and GB/s of the algorithmic bytes);
+  prefill_block the 512-token prefill block: RMSNorm + quantize, fused
+                gate|up GEMM with relu^2 * up, subln + requantize, down GEMM;
+  long_context  2048-token prefill, then bs=1 greedy decode up to 2560
+                cached positions;
   cpu_baseline  the CPU oracle (C restatement of the reference arithmetic,
                 OpenMP) decoding on the same model: a bounded sample of
                 steps after a short prompt.
+
+    python bench.py --roofline-only [--calib-mib 256]
+
+runs only the 8192 x 28672 GEMV (plus, with --calib-mib, one device copy of
+that many MiB, the calibration kernel for the FETCH_SIZE / WRITE_SIZE
+counters) -- the command the rocprofv3 --pmc runs profile.
 """
 from __future__ import annotations
 
@@ -37,6 +49,19 @@ HBM_PEAK_GBS = 8000.0
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the 8192x28672 GEMV from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (copy-kernel calibrated)."""
+    path = os.path.join(ROOT, "profiles", "gemv_8192x28672_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def gemv_roofline(ops, synth, N: int, K: int, copies: int, iters: int) -> dict:
@@ -80,6 +105,159 @@ def gemv_roofline(ops, synth, N: int, K: int, copies: int, iters: int) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": algo, "copies": copies}
 
 
+MFMA_I8_PEAK_TOPS = 5000.0
+
+
+def _timed(L, stream, fn, iters: int) -> float:
+    """Mean ms per call of fn(i) over iters launches on `stream` (HIP events)."""
+    e0, e1 = L.oxb_event_create(), L.oxb_event_create()
+    fn(0)
+    L.oxb_stream_sync(stream)
+    L.oxb_event_record(e0, stream)
+    for i in range(iters):
+        fn(i)
+    L.oxb_event_record(e1, stream)
+    L.oxb_event_sync(e1)
+    ms = L.oxb_event_elapsed_ms(e0, e1) / iters
+    L.oxb_event_destroy(e0)
+    L.oxb_event_destroy(e1)
+    return ms
+
+
+def _host_tiles(rng, M: int, K: int):
+    """int8 activations of M seeded N(0,1) rows (per-token absmax, RNE, +-127)
+    in the GEMM's token-tiled layout [Mpad/16][K/64][16 tokens][4 planes x 16],
+    plane g of chunk kc holding k = (kc//2)*128 + g*32 + (kc%2)*16 + j;
+    returns (tiles, scales, sums) with rows past M zero (scale 1, sum 0)."""
+    mpad = (M + 63) // 64 * 64
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    am = np.abs(x).max(axis=1, keepdims=True)
+    q = np.clip(np.rint(x * (np.float32(127.0) / am)), -127, 127).astype(np.int8)
+    Q = np.zeros((mpad, K), np.int8)
+    Q[:M] = q
+    t = Q.reshape(mpad // 16, 16, K // 128, 4, 2, 16).transpose(0, 2, 4, 1, 3, 5)
+    sc = np.ones(mpad, np.float32)
+    sc[:M] = (am[:, 0] / np.float32(127.0)).astype(np.float32)
+    sm = np.zeros(mpad, np.int32)
+    sm[:M] = q.astype(np.int64).sum(axis=1)
+    return np.ascontiguousarray(t).reshape(-1), sc, sm
+
+
+def gemm_sweep(ops, synth, N: int, K: int, M: int, copies: int, iters: int) -> dict:
+    """Ternary GEMM (int8 MFMA, int32 accumulate, f32 epilogue) at M tokens."""
+    L = ops.lib()
+    rng = np.random.default_rng([N, K, M])
+    nat = ops.DeviceArray.from_host(synth.random_i2s(rng, N, K).reshape(-1))
+    Ws = [ops.repack_tiled(nat, N, K) for _ in range(copies)]
+    nat.free()
+    stream = L.oxb_stream_create()
+    ht, hs, hm = _host_tiles(rng, M, K)
+    Xt, sc, sm = (ops.DeviceArray.from_host(a) for a in (ht, hs, hm))
+    dw = ops.DeviceArray.from_host(np.full(N, 0.016, np.float32))
+    Y = ops.DeviceArray((M, N), np.float32)
+
+    def run(i):
+        ops.check(L.oxb_gemm_i8(Ws[i % copies].ptr, Xt.ptr, sc.ptr, sm.ptr, dw.ptr, N, K, M,
+                                Y.ptr, None, 0, stream), "gemm")
+    ms = _timed(L, stream, run, iters)
+    L.oxb_stream_destroy(stream)
+    for b in Ws + [Xt, sc, sm, dw, Y]:
+        b.free()
+    ops_n = 2.0 * M * N * K
+    algo = N * K // 4 + M * K + 4 * M * N + 4
+    tops = ops_n / (ms * 1e-3) / 1e12
+    gbs = algo / (ms * 1e-3) / 1e9
+    return {"N": N, "K": K, "M": M, "us": round(ms * 1e3, 2), "TOPS": round(tops, 2),
+            "frac_mfma": round(tops / MFMA_I8_PEAK_TOPS, 4), "GBps": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": algo, "copies": copies}
+
+
+def prefill_block(ops, synth, M: int = 512, iters: int = 20) -> dict:
+    """RMSNorm + quantize -> gate|up GEMM (relu^2 * up fused) -> subln +
+    requantize -> down GEMM, on M tokens of the 2B shape."""
+    L = ops.lib()
+    cfg = synth.BITNET_2B
+    D, F = cfg.hidden, cfg.ffn
+    rng = np.random.default_rng(512)
+    nat = ops.DeviceArray.from_host(synth.random_i2s(rng, 2 * F, D).reshape(-1))
+    Wgu = ops.repack_tiled(nat, 2 * F, D)
+    nat.free()
+    nat = ops.DeviceArray.from_host(synth.random_i2s(rng, D, F).reshape(-1))
+    Wd = ops.repack_tiled(nat, D, F)
+    nat.free()
+    g1 = ops.DeviceArray.from_host(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    g2 = ops.DeviceArray.from_host(rng.uniform(0.5, 1.5, F).astype(np.float32))
+    s1 = ops.DeviceArray.from_host(np.full(2 * F, 0.016, np.float32))
+    s2 = ops.DeviceArray.from_host(np.full(D, 0.016, np.float32))
+    stream = L.oxb_stream_create()
+    mpad = (M + 63) // 64 * 64
+    x = ops.DeviceArray.from_host(rng.standard_normal((M, D)).astype(np.float32))
+    X1 = ops.DeviceArray((mpad * D,), np.int8, zero=True)
+    X2 = ops.DeviceArray((mpad * F,), np.int8, zero=True)
+    sc = ops.DeviceArray((mpad,), np.float32)
+    sm = ops.DeviceArray((mpad,), np.int32)
+    h = ops.DeviceArray((M, F), np.float32)
+    y = ops.DeviceArray((M, D), np.float32)
+
+    def run(_):
+        ops.check(L.oxb_quantize_rows_tiled(x.ptr, g1.ptr, 1e-5, M, D, X1.ptr, sc.ptr, sm.ptr,
+                                            stream), "q1")
+        ops.check(L.oxb_gemm_i8(Wgu.ptr, X1.ptr, sc.ptr, sm.ptr, s1.ptr, 2 * F, D, M, h.ptr,
+                                None, 2, stream), "gateup")
+        ops.check(L.oxb_quantize_rows_tiled(h.ptr, g2.ptr, 1e-5, M, F, X2.ptr, sc.ptr, sm.ptr,
+                                            stream), "q2")
+        ops.check(L.oxb_gemm_i8(Wd.ptr, X2.ptr, sc.ptr, sm.ptr, s2.ptr, D, F, M, y.ptr, None, 0,
+                                stream), "down")
+    ms = _timed(L, stream, run, iters)
+    L.oxb_stream_destroy(stream)
+    for b in (Wgu, Wd, g1, g2, s1, s2, x, X1, X2, sc, sm, h, y):
+        b.free()
+    ops_n = 2.0 * M * (2 * F) * D + 2.0 * M * D * F
+    tops = ops_n / (ms * 1e-3) / 1e12
+    return {"M": M, "ms": round(ms, 4), "ops": int(ops_n), "TOPS": round(tops, 2),
+            "frac_mfma": round(tops / MFMA_I8_PEAK_TOPS, 4),
+            "kernels": "quantize_rows_tiled, gemm gate|up (relu^2*up), quantize_rows_tiled "
+                       "(subln), gemm down"}
+
+
+def long_context(pkg, synth, path: str, prompt_len: int = 2048, steps: int = 512) -> dict:
+    """2048-token prefill, then bs=1 greedy decode to 2560 cached positions."""
+    rng = np.random.default_rng(4096)
+    prompt = rng.integers(0, synth.BITNET_2B.vocab, prompt_len).astype(np.int32)
+    m = pkg.Model(path, max_seq=prompt_len + steps + 8)
+    m.forward(prompt[:64], want_logits=False)   # warm-up (graph capture, code paths)
+    m.decode_greedy(4)
+    m.reset()
+    import importlib as _il
+    ops = _il.import_module("0xbitnet_amd.ops")
+    ops.sync()
+    t0 = time.perf_counter()
+    m.forward(prompt, want_logits=False)
+    ops.sync()
+    pf = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    m.decode_greedy(steps)
+    ops.sync()
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"prompt_tokens": prompt_len, "decode_tokens": steps, "batch": 1,
+            "prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(prompt_len / pf, 1),
+            "decode_tok_s": round(steps / dt, 2), "kv_positions_max": prompt_len + steps}
+
+
+def calib_copy(ops, mib: int) -> None:
+    """One device-to-device copy of `mib` MiB: the reference kernel whose
+    FETCH_SIZE / WRITE_SIZE readings scale the counters to bytes."""
+    L = ops.lib()
+    n = mib << 20
+    a = ops.DeviceArray((n,), np.uint8, zero=True)
+    b = ops.DeviceArray((n,), np.uint8)
+    ops.check(L.oxb_memcpy_d2d(b.ptr, a.ptr, n, None), "calib copy")
+    ops.sync()
+    a.free()
+    b.free()
+
+
 def cpu_baseline(synth, path: str, prompt: np.ndarray, steps: int) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -108,6 +286,10 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the GEMM sweep, prefill block and long-context runs")
+    ap.add_argument("--roofline-only", action="store_true")
+    ap.add_argument("--calib-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
@@ -119,6 +301,12 @@ def main() -> int:
     synth = importlib.import_module("0xbitnet_amd.synth")
     info = ops.device_info()
     log(f"device {info['name']} CUs {info['cus']}")
+    if args.roofline_only:
+        roof = gemv_roofline(ops, synth, 8192, 28672, copies=16, iters=400)
+        if args.calib_mib:
+            calib_copy(ops, args.calib_mib)
+        print(json.dumps({"roofline_gemv": roof, "calib_copy_mib": args.calib_mib}), flush=True)
+        return 0
 
     t = time.time()
     path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
@@ -160,6 +348,23 @@ def main() -> int:
             sweep.append(r)
             log(f"gemv {N}x{K}: {r['us']} us {r['GBps']} GB/s")
 
+    extra = {}
+    if not args.no_extra:
+        gs = []
+        for N, K in ((28672, 8192), (8192, 28672)):
+            for M in (8, 64, 512, 4096):
+                copies = 8 if M <= 64 else 2
+                r = gemm_sweep(ops, synth, N, K, M, copies=copies, iters=40 if M < 4096 else 10)
+                gs.append(r)
+                log(f"gemm {N}x{K} M={M}: {r['us']} us {r['TOPS']} TOPS {r['GBps']} GB/s")
+        extra["gemm_sweep"] = gs
+        pb = prefill_block(ops, synth)
+        log(f"prefill block M=512: {pb['ms']} ms {pb['TOPS']} TOPS")
+        extra["prefill_block"] = pb
+        lc = long_context(pkg, synth, path)
+        log(f"long context: prefill {lc['prefill_ms']} ms, decode {lc['decode_tok_s']} tok/s")
+        extra["long_context"] = lc
+
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -192,10 +397,11 @@ def main() -> int:
         "decode_step_frac": round(step_bytes * tps / 1e9 / HBM_PEAK_GBS, 4),
         "prefill_ms": round(prefill_s * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": roof["GBps"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": roof["frac"], "traffic": None,
+                     "unit": "GB/s", "frac": roof["frac"], "traffic": measured_traffic(),
                      "kernel": "gemv_kernel<PRO_INT8,EPI_STORE> N=8192 K=28672 M=1",
                      "bytes_per_launch": roof["bytes"], "us_per_launch": roof["us"]},
         "gemv_sweep": sweep,
+        **extra,
         "cpu_baseline": cpu,
         "device": info["name"],
     }
