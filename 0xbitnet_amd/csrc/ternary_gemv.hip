@@ -9,11 +9,11 @@
 // One workgroup (4 waves) owns one 16-row tile.  The 4 waves split the
 // tile's K range into whole 128-blocks; inside a wave lane l streams chunks
 // (row l%16, kc0 + l/16 + 4j), so every wave load is one contiguous KiB.
-// All loads are branch-free (clamped addresses, masked values) so the
-// compiler's memory counters stay exact: the weights are in flight while
-// the prologue runs.  The prologue has two barriers (the RMS sum and the
-// absmax); each wave then quantizes exactly the K range it multiplies, so
-// the main loop starts without a third.
+// All loads are branch-free (clamped addresses, masked values; none at all
+// when K is a multiple of 256) so the compiler's memory counters stay exact:
+// the weights are in flight while the prologue runs.  The prologue keeps
+// every activation in registers in the shaders' thread mapping: one barrier
+// for the RMS sum, one for the absmax, one after the int8 values land in LDS.
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
@@ -131,18 +131,30 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [256]
-// | vf [K] f32 (PRO_QUANT only: the normalised activations).
-__host__ __device__ inline size_t gemv_smem(int K, bool quant) {
-    return (size_t)K + (256 + 4 + 4 + 256) * 4 + (quant ? (size_t)K * 4 : 0);
+// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [256].
+__host__ __device__ inline size_t gemv_smem(int K) {
+    return (size_t)K + (256 + 4 + 4 + 256) * 4;
+}
+
+// x[t + 256 j], gamma[t + 256 j] for K == 256 * NREG (no clamps needed).
+template <int NREG>
+__device__ inline void load_row_exact(const float *__restrict__ x, const float *__restrict__ gp,
+                                      float (&v)[NREG], float (&g)[NREG]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NREG; ++j) {
+        v[j] = x[t + j * 256];
+        g[j] = gp[t + j * 256];
+    }
 }
 
 // NREG: strided f32 values per thread in the prologue (ceil(K/256));
 // PF: 16-byte weight chunks per lane per batch.
 // Waves per SIMD the register budget must allow: 4 (<= 128 VGPRs) for the
 // one-batch shapes, so that e.g. 864 workgroups of a 13824-row GEMV are all
-// resident at once; the 4-chunk batches need more registers.
-template <int PRO, int EPI, int NREG, int PF>
+// resident at once; the 4-chunk double-buffered batches need more registers.
+// EXACT: K == 256 * NREG.
+template <int PRO, int EPI, int NREG, int PF, bool EXACT>
 __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) int8_t smem[];
     const int K = p.K;
@@ -151,7 +163,6 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
     float *wmax = red + 256;
     int *wq = (int *)(wmax + 4);
     int *wpart = wq + 4;
-    float *vf = (float *)(wpart + 256);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -160,13 +171,16 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
     const int per = (((KC + 3) >> 2) + 1) & ~1;   // chunks per wave: whole 128-blocks
     const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
     const int cpl = (per + 3) >> 2;               // chunks per lane
-    const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 when PF <= 3)
+    const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless PF == 4)
     const int tile = blockIdx.x;
     const uint4 *tw = p.W + (size_t)tile * KC * 16;
 
     // ---- loads: prologue inputs, then the residual, then the weights -------
     float v[NREG], g[NREG];
-    if constexpr (PRO == PRO_QUANT) load_row<NREG>(p.x, p.gamma, K, v, g);
+    if constexpr (PRO == PRO_QUANT) {
+        if constexpr (EXACT) load_row_exact<NREG>(p.x, p.gamma ? p.gamma : p.x, v, g);
+        else load_row<NREG>(p.x, p.gamma, K, v, g);
+    }
     float resid = 0.0f;
     if constexpr (EPI == EPI_RESID) resid = p.y[tile * 16 + (tid & 15)];
     auto load_batch = [&](uint4 (&dst)[PF], int b) {
@@ -192,7 +206,7 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
         xsum = p.xsum[0];
         __syncthreads();
     } else {
-        mask_row<NREG>(K, v, g);
+        if constexpr (!EXACT) mask_row<NREG>(K, v, g);
         if (p.gamma) {
             float ss = 0.0f;   // columns past K hold +0 and add exactly nothing
 #pragma unroll
@@ -210,34 +224,29 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
         }
         float am = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NREG; ++j) {
-            const int col = tid + 256 * j;
-            if (col < K) vf[col] = v[j];
-            am = fmaxf(am, fabsf(v[j]));
-        }
+        for (int j = 0; j < NREG; ++j) am = fmaxf(am, fabsf(v[j]));
         am = wave_nonneg_max_dpp(am);
         if (lane == 0) wmax[w] = am;
         __syncthreads();
         am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
         in_scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
         const float inv = am == 0.0f ? 0.0f : 127.0f / am;  // :68
-        // this wave's K range [64 kc0, 64 kc1): quantize, keep its sum(q)
         int sq = 0;
-        const int k0 = kc0 * 64, k1 = kc1 * 64;
         const bool out = tile == 0 && p.xq_out;
 #pragma unroll
-        for (int i = 0; i < NREG; ++i) {
-            const int k = k0 + lane + 64 * i;
-            if (k < k1) {
-                const int q = quant_one(vf[k], inv);
-                xq_lds[k] = (int8_t)q;
+        for (int j = 0; j < NREG; ++j) {
+            const int col = tid + 256 * j;
+            if (EXACT || col < K) {
+                const int q = quant_one(v[j], inv);
+                xq_lds[col] = (int8_t)q;
                 sq += q;
-                if (out) p.xq_out[k] = (int8_t)q;
+                if (out) p.xq_out[col] = (int8_t)q;
             }
         }
         sq = wave_isum_dpp(sq);
         if (lane == 0) wq[w] = sq;
         if (out && tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
+        __syncthreads();   // the int8 vector is complete
     }
 
     // ---- main loop: chunks past this wave's range multiply zero codes ------
@@ -259,7 +268,7 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
             acc.add(wv.w, x0.w, x1.w, x2.w, x3.w);
         }
     };
-    if constexpr (PF <= 3) {   // the launcher picks PF <= 3 only when one batch covers the range
+    if constexpr (PF != 4) {   // the launcher picks PF != 4 only when one batch covers the range
         mac_batch(A, 0);
     } else {
         int b = 0;
@@ -396,37 +405,41 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-template <int PRO, int EPI, int NREG, int PF>
+template <int PRO, int EPI, int NREG, int PF, bool EXACT>
 static int launch_n(const GemvParams &p, hipStream_t s) {
-    const size_t sm = gemv_smem(p.K, PRO == PRO_QUANT);
+    const size_t sm = gemv_smem(p.K);
     if (sm > 64 * 1024) {
         static bool raised = false;   // per instantiation
         if (!raised) {
-            OXB_CHECK_HIP(hipFuncSetAttribute((const void *)gemv_kernel<PRO, EPI, NREG, PF>,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              160 * 1024));
+            OXB_CHECK_HIP(hipFuncSetAttribute(
+                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF>), dim3(p.N / 16), dim3(256), sm, s, p);
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT>), dim3(p.N / 16), dim3(256), sm, s,
+                       p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-// NREG = ceil(K/256) bucket for PRO_QUANT; PF = chunks per lane per batch,
-// at most 4 (two batches in flight keep <= 8 chunks per lane).
+// PRO_QUANT: NREG = ceil(K/256) bucket (EXACT when K == 256 * NREG), all of
+// a lane's weight chunks in one batch.  PRO_INT8: PF from the chunks per
+// lane, 4-chunk batches double-buffered when one batch does not cover them.
 template <int PRO, int EPI>
 static int launch(const GemvParams &p, hipStream_t s) {
     const int KC = p.K >> 6;
     const int cpl = (((((KC + 3) >> 2) + 1) & ~1) + 3) >> 2;
     if constexpr (PRO == PRO_INT8) {
-        if (cpl <= 1) return launch_n<PRO, EPI, 1, 1>(p, s);
-        if (cpl <= 3) return launch_n<PRO, EPI, 1, 3>(p, s);
-        return launch_n<PRO, EPI, 1, 4>(p, s);
+        if (cpl <= 1) return launch_n<PRO, EPI, 1, 1, false>(p, s);
+        if (cpl <= 3) return launch_n<PRO, EPI, 1, 3, false>(p, s);
+        return launch_n<PRO, EPI, 1, 4, false>(p, s);
     } else {
-        if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1>(p, s);
-        if (p.K <= 2560) return launch_n<PRO, EPI, 10, 3>(p, s);
-        return launch_n<PRO, EPI, kMaxNormReg, 4>(p, s);
+        if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1, false>(p, s);
+        if (p.K == 2560) return launch_n<PRO, EPI, 10, 3, true>(p, s);
+        if (p.K <= 2560) return launch_n<PRO, EPI, 10, 3, false>(p, s);
+        if (p.K == 6912) return launch_n<PRO, EPI, 27, 7, true>(p, s);
+        return launch_n<PRO, EPI, kMaxNormReg, 7, false>(p, s);
     }
 }
 
