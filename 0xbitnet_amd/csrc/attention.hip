@@ -124,53 +124,78 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 
 // ---------------------------------------------------------------------------
 // Decode (one query at position *pos, S = pos + 1), two kernels:
-//  A  scores: grid (position blocks, Hkv); 256 threads = G heads x (256/G)
-//     positions, one 128-term dot chain each; scores[h][s] to global.
+//  A  scores: grid (64-position blocks, Hkv); the block's K rows are loaded
+//     once, coalesced, into LDS and shared by the G heads (wave w = heads w,
+//     w + 4); one lane per position runs the 128-term chain; scores[h][s]
+//     to global.
 //  B  softmax + P.V: grid (Hkv, slices); each workgroup takes the G heads of
 //     one KV head and 64/G of the 128 dims, i.e. exactly one wave of 64
 //     sequential sums.  The other waves load the scores, run the softmax
 //     reductions and stage the V slice (as f32, transposed) in LDS, so the
 //     summing wave reads 4 steps per LDS load.
 // ---------------------------------------------------------------------------
+constexpr int kScoreP = 64;   // positions per scores workgroup (one per lane)
+
 template <int G>
 __global__ __launch_bounds__(256) void attn_scores_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const int *__restrict__ pos_ptr,
     int max_seq, float scale, float *__restrict__ scores) {
-    constexpr int P = 256 / G;   // positions per workgroup; a wave covers 64/P heads
+    // K rows of this position block, 16 uint4 each, padded to 17 so that the
+    // 64 lanes reading one column hit different banks.
+    __shared__ uint4 ks[kScoreP][17];
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
     const int b = blockIdx.x, hk = blockIdx.y;
-    if (b * P >= S) return;
-    const int tid = threadIdx.x;
-    const int g = tid / P, s = b * P + tid % P;
-    // K row (clamped to a valid position) and the head's q row, all in flight
-    // together; q is the same for the lanes of a head (cache broadcast).
-    const uint4 *kr = (const uint4 *)(kc + ((size_t)hk * max_seq + min(s, S - 1)) * kHd);
-    uint4 k[16];
+    const int s0 = b * kScoreP;
+    if (s0 >= S) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // coalesced tile load: thread i takes uint4 i, i + 256, ... of the rows
+    const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
+    uint4 kt[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) k[i] = kr[i];
-    const float4 *qg = (const float4 *)(q + (size_t)(hk * G + g) * kHd);
-    float4 qv[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) qv[i] = qg[i];
-    if (s >= S) return;
-    float dot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const __half2 *hh = (const __half2 *)&k[i];
-        const float4 qa = qv[2 * i], qb = qv[2 * i + 1];
-        const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) {
-            const float2 kf = __half22float2(hh[k2]);
-            float m0 = qq[2 * k2] * kf.x;
-            dot = dot + m0;
-            float m1 = qq[2 * k2 + 1] * kf.y;
-            dot = dot + m1;
-        }
+    for (int k = 0; k < 4; ++k) {
+        const int i = tid + 256 * k, row = i >> 4;
+        kt[k] = K4[(size_t)min(s0 + row, S - 1) * 16 + (i & 15)];
     }
-    scores[(size_t)(hk * G + g) * max_seq + s] = dot * scale;
+    // this wave's heads (w, w + 4, ...): q rows in registers, one lane per position
+    constexpr int HPW = G > 4 ? G / 4 : 1;
+    float4 qv[HPW][32];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        const int g = min(w + 4 * h, G - 1);
+        const float4 *qg = (const float4 *)(q + (size_t)(hk * G + g) * kHd);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qv[h][i] = qg[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = tid + 256 * k;
+        ks[i >> 4][i & 15] = kt[k];
+    }
+    __syncthreads();
+    const int s = s0 + lane;
+    if (w >= G || s >= S) return;
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint4 kr = ks[lane][i];
+            const __half2 *hh = (const __half2 *)&kr;
+            const float4 qa = qv[h][2 * i], qb = qv[h][2 * i + 1];
+            const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const float2 kf = __half22float2(hh[k2]);
+                float m0 = qq[2 * k2] * kf.x;
+                dot = dot + m0;
+                float m1 = qq[2 * k2 + 1] * kf.y;
+                dot = dot + m1;
+            }
+        }
+        scores[(size_t)(hk * G + w + 4 * h) * max_seq + s] = dot * scale;
+    }
 }
 
 constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB)
@@ -186,19 +211,21 @@ __device__ inline void wave_softmax_row(float *row, int S, int Spad, int lane) {
     for (int s = lane; s < S; s += 64) m = fmaxf(m, row[s]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    // exp(x - max) is kept in the row: the shader evaluates it again for the
+    // normalisation, with the same operands and so the same value
     float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 256) {
         const int s = s0 + lane;
-        if (s < S) p0 = p0 + oxb_expf(row[s] - m);
-        if (s + 64 < S) p1 = p1 + oxb_expf(row[s + 64] - m);
-        if (s + 128 < S) p2 = p2 + oxb_expf(row[s + 128] - m);
-        if (s + 192 < S) p3 = p3 + oxb_expf(row[s + 192] - m);
+        if (s < S) { const float e = oxb_expf(row[s] - m); row[s] = e; p0 = p0 + e; }
+        if (s + 64 < S) { const float e = oxb_expf(row[s + 64] - m); row[s + 64] = e; p1 = p1 + e; }
+        if (s + 128 < S) { const float e = oxb_expf(row[s + 128] - m); row[s + 128] = e; p2 = p2 + e; }
+        if (s + 192 < S) { const float e = oxb_expf(row[s + 192] - m); row[s + 192] = e; p3 = p3 + e; }
     }
     float c = (p0 + p2) + (p1 + p3);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) c = c + __shfl_xor(c, o, 64);
     const float inv = 1.0f / c;
-    for (int s = lane; s < S; s += 64) row[s] = oxb_expf(row[s] - m) * inv;
+    for (int s = lane; s < S; s += 64) row[s] = row[s] * inv;
     for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
 }
 
@@ -368,9 +395,8 @@ template <int G>
 static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                          int Hkv, int max_seq, float *scores, float *out, hipStream_t s) {
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
-    constexpr int P = 256 / G;
-    hipLaunchKernelGGL(attn_scores_kernel<G>, dim3((max_seq + P - 1) / P, Hkv), dim3(256), 0, s, q,
-                       kc, pos, max_seq, scale, scores);
+    hipLaunchKernelGGL(attn_scores_kernel<G>, dim3((max_seq + kScoreP - 1) / kScoreP, Hkv),
+                       dim3(256), 0, s, q, kc, pos, max_seq, scale, scores);
     OXB_CHECK_HIP(hipGetLastError());
     const size_t smem = (size_t)G * ((max_seq + 3) & ~3) * sizeof(float);
     static size_t configured = 0;
