@@ -158,16 +158,9 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         const int i = tid + 256 * k, row = i >> 4;
         kt[k] = K4[(size_t)min(s0 + row, S - 1) * 16 + (i & 15)];
     }
-    // this wave's heads (w, w + 4, ...): q rows in registers, one lane per position
-    constexpr int HPW = G > 4 ? G / 4 : 1;
-    float4 qv[HPW][32];
-#pragma unroll
-    for (int h = 0; h < HPW; ++h) {
-        const int g = min(w + 4 * h, G - 1);
-        const float4 *qg = (const float4 *)(q + (size_t)(hk * G + g) * kHd);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) qv[h][i] = qg[i];
-    }
+    // the G q rows to LDS (one float4 per thread); read back as broadcasts
+    __shared__ __align__(16) float4 qs[G * 32];
+    if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int i = tid + 256 * k;
@@ -176,21 +169,26 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     __syncthreads();
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
+    constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
+        const float4 *qg = qs + (w + 4 * h) * 32;
+        // products as fma(q, k, +0): equal to q*k but for the sign of a zero
+        // product, which cannot change a sum that starts at +0
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint4 kr = ks[lane][i];
-            const __half2 *hh = (const __half2 *)&kr;
-            const float4 qa = qv[h][2 * i], qb = qv[h][2 * i + 1];
+            const float4 qa = qg[2 * i], qb = qg[2 * i + 1];
             const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
-                const float2 kf = __half22float2(hh[k2]);
-                float m0 = qq[2 * k2] * kf.x;
+                const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
+                const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
+                const float m0 = __builtin_fmaf(qq[2 * k2], k0, 0.0f);
                 dot = dot + m0;
-                float m1 = qq[2 * k2 + 1] * kf.y;
+                const float m1 = __builtin_fmaf(qq[2 * k2 + 1], k1, 0.0f);
                 dot = dot + m1;
             }
         }
@@ -198,21 +196,52 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     }
 }
 
-constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB)
+constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB, plus row padding)
 
-// Softmax of one score row by one wave, in the order of sh/softmax.wgsl:25-80
-// for a 256-thread workgroup: lane l plays threads l, l+64, l+128, l+192,
-// each summing its strided positions in order; the halving tree's first two
-// levels pair those four, the remaining six are the xor butterfly (every lane
-// ends with the tree's value: x + y == y + x exactly).  The max is exact in
-// any order.
-__device__ inline void wave_softmax_row(float *row, int S, int Spad, int lane) {
+// Softmax of one score row (global src, S values) by one wave into the LDS
+// row, in the order of sh/softmax.wgsl:25-80 for a 256-thread workgroup:
+// lane l plays threads l, l+64, l+128, l+192, each summing its strided
+// positions in order (out-of-range positions add an exact +0); the tree's
+// first two levels pair those four in the lane, wave_tree_sum does the rest.
+// exp(x - max) is evaluated once: the shader's normalisation pass evaluates
+// it again with the same operands.  The max is exact in any order.
+// Rows of up to 512 positions stay in registers; longer rows go through LDS.
+__device__ inline void wave_softmax_row(float *row, const float *__restrict__ src, int S,
+                                        int Spad, int lane) {
+    if (S <= 512) {
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = src[min(lane + 64 * k, S - 1)];
+        float m = -3.402823e+38f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (lane + 64 * k < S) m = fmaxf(m, x[k]);
+        m = wave_max_dpp(m);
+        float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            x[k] = lane + 64 * k < S ? oxb_expf(x[k] - m) : 0.0f;
+            p[k & 3] = p[k & 3] + x[k];
+        }
+        const float inv = 1.0f / wave_tree_sum((p[0] + p[2]) + (p[1] + p[3]));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int s = lane + 64 * k;
+            if (s < Spad) row[s] = s < S ? x[k] * inv : 0.0f;
+        }
+        return;
+    }
+    for (int base = 0; base < S; base += 512) {   // stage the row, 8 loads in flight
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = src[min(base + lane + 64 * k, S - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (base + lane + 64 * k < S) row[base + lane + 64 * k] = t[k];
+    }
     float m = -3.402823e+38f;
     for (int s = lane; s < S; s += 64) m = fmaxf(m, row[s]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    // exp(x - max) is kept in the row: the shader evaluates it again for the
-    // normalisation, with the same operands and so the same value
+    m = wave_max_dpp(m);
     float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 256) {
         const int s = s0 + lane;
@@ -221,10 +250,7 @@ __device__ inline void wave_softmax_row(float *row, int S, int Spad, int lane) {
         if (s + 128 < S) { const float e = oxb_expf(row[s + 128] - m); row[s + 128] = e; p2 = p2 + e; }
         if (s + 192 < S) { const float e = oxb_expf(row[s + 192] - m); row[s + 192] = e; p3 = p3 + e; }
     }
-    float c = (p0 + p2) + (p1 + p3);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) c = c + __shfl_xor(c, o, 64);
-    const float inv = 1.0f / c;
+    const float inv = 1.0f / wave_tree_sum((p0 + p2) + (p1 + p3));
     for (int s = lane; s < S; s += 64) row[s] = row[s] * inv;
     for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
 }
@@ -293,9 +319,10 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     constexpr int DW = 64 / G;               // dims per workgroup
     constexpr int PPP = DW / 8;              // uint4 (8 f16) per position of the slice
     constexpr int kVChunk = kVFloats / DW;   // positions staged per pass
+    constexpr int kVS = kVChunk + 4;         // padded row: the DW rows start in different banks
     constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
     extern __shared__ __align__(16) float pr[];   // [G][Spad] scores, then probabilities
-    __shared__ __align__(16) float vt[kVFloats];  // V slice, [d][s] f32
+    __shared__ __align__(16) float vt[DW * kVS];  // V slice, [d][s] f32
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
@@ -318,12 +345,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     load_chunk(0);
 
     // each wave owns heads w, w+4: load its score rows and run their softmax
-    for (int g = w; g < G; g += 4) {
-        float *row = pr + g * Spad;
-        const float *src = scores + (size_t)(hk * G + g) * max_seq;
-        for (int s = lane; s < S; s += 64) row[s] = src[s];
-        wave_softmax_row(row, S, Spad, lane);
-    }
+    for (int g = w; g < G; g += 4)
+        wave_softmax_row(pr + g * Spad, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane);
 
     // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s
     const int g = lane / DW, dd = lane % DW;
@@ -338,13 +361,13 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float2 f = __half22float2(*(const __half2 *)&wv[e]);
-                vt[(8 * h + 2 * e) * kVChunk + s] = f.x;
-                vt[(8 * h + 2 * e + 1) * kVChunk + s] = f.y;
+                vt[(8 * h + 2 * e) * kVS + s] = f.x;
+                vt[(8 * h + 2 * e + 1) * kVS + s] = f.y;
             }
         }
         __syncthreads();
         if (c0 + kVChunk < S) load_chunk(c0 + kVChunk);
-        if (tid < 64) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVChunk, n, acc);
+        if (tid < 64) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc);
     }
     if (tid < 64) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }

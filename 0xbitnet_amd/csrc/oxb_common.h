@@ -195,6 +195,36 @@ __device__ inline float block256_tree_sum_1b(float part, float *red) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
 }
 
+// Max over the wave of finite floats (lanes without a DPP source keep their
+// own value), returned to every lane.
+template <int CTRL, int ROWMASK>
+__device__ inline float dpp_keep(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ inline float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_keep<0x111, 0xf>(v));
+    v = fmaxf(v, dpp_keep<0x112, 0xf>(v));
+    v = fmaxf(v, dpp_keep<0x114, 0xf>(v));
+    v = fmaxf(v, dpp_keep<0x118, 0xf>(v));
+    v = fmaxf(v, dpp_keep<0x142, 0xa>(v));
+    v = fmaxf(v, dpp_keep<0x143, 0xc>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Halving tree s[l] += s[l + stride], stride 32..1, over the 64 lanes (the
+// last six levels of the shaders' 256-thread tree); lane 0's value returned
+// to every lane.  Strides 32 and 16 by lane shuffles, 8..1 by DPP row_shl.
+__device__ inline float wave_tree_sum(float c) {
+    c = c + __shfl_down(c, 32, 64);
+    c = c + __shfl_down(c, 16, 64);
+    c = c + __int_as_float(dpp0<0x108, 0xf>(__float_as_int(c)));
+    c = c + __int_as_float(dpp0<0x104, 0xf>(__float_as_int(c)));
+    c = c + __int_as_float(dpp0<0x102, 0xf>(__float_as_int(c)));
+    c = c + __int_as_float(dpp0<0x101, 0xf>(__float_as_int(c)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), 0));
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
