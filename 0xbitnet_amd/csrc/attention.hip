@@ -170,16 +170,25 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
+    // this lane's K row into registers, then each head's q row (LDS broadcast):
+    // the 128-step chain below then waits on nothing
+    uint4 kr16[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kr16[i] = ks[lane][i];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
         const float4 *qg = qs + (w + 4 * h) * 32;
+        float4 qv[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qv[i] = qg[i];
+        __builtin_amdgcn_sched_barrier(0);
         // products as fma(q, k, +0): equal to q*k but for the sign of a zero
         // product, which cannot change a sum that starts at +0
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const uint4 kr = ks[lane][i];
-            const float4 qa = qg[2 * i], qb = qg[2 * i + 1];
+            const uint4 kr = kr16[i];
+            const float4 qa = qv[2 * i], qb = qv[2 * i + 1];
             const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
             const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
 #pragma unroll

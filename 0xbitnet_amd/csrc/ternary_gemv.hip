@@ -232,20 +232,24 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
         in_scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
         const float inv = am == 0.0f ? 0.0f : 127.0f / am;  // :68
         int sq = 0;
-        const bool out = tile == 0 && p.xq_out;
+        int qv[NREG];
 #pragma unroll
         for (int j = 0; j < NREG; ++j) {
             const int col = tid + 256 * j;
+            qv[j] = quant_one(v[j], inv);
             if (EXACT || col < K) {
-                const int q = quant_one(v[j], inv);
-                xq_lds[col] = (int8_t)q;
-                sq += q;
-                if (out) p.xq_out[col] = (int8_t)q;
+                xq_lds[col] = (int8_t)qv[j];
+                sq += qv[j];
             }
         }
         sq = wave_isum_dpp(sq);
         if (lane == 0) wq[w] = sq;
-        if (out && tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
+        if (tile == 0 && p.xq_out) {   // parity checks only
+#pragma unroll
+            for (int j = 0; j < NREG; ++j)
+                if (EXACT || tid + 256 * j < K) p.xq_out[tid + 256 * j] = (int8_t)qv[j];
+            if (tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
+        }
         __syncthreads();   // the int8 vector is complete
     }
 
