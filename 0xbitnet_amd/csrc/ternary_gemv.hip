@@ -131,9 +131,9 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [256].
-__host__ __device__ inline size_t gemv_smem(int K) {
-    return (size_t)K + (256 + 4 + 4 + 256) * 4;
+// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [TT][256].
+__host__ __device__ inline size_t gemv_smem(int K, int TT) {
+    return (size_t)K + (256 + 4 + 4 + 256 * TT) * 4;
 }
 
 // x[t + 256 j], gamma[t + 256 j] for K == 256 * NREG (no clamps needed).
@@ -153,9 +153,13 @@ __device__ inline void load_row_exact(const float *__restrict__ x, const float *
 // Waves per SIMD the register budget must allow: 4 (<= 128 VGPRs) for the
 // one-batch shapes, so that e.g. 864 workgroups of a 13824-row GEMV are all
 // resident at once; the 4-chunk double-buffered batches need more registers.
-// EXACT: K == 256 * NREG.
-template <int PRO, int EPI, int NREG, int PF, bool EXACT>
-__global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
+// EXACT: K == 256 * NREG.  TT: 16-row tiles per workgroup (> 1 amortises the
+// prologue over more rows when the grid would otherwise oversubscribe the
+// CUs, e.g. the 13824-row gate|up GEMV); each chunk's activations are read
+// from LDS once for all TT tiles.
+template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT>
+__global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
+    static_assert(TT == 1 || PF != 4, "multi-batch streaming is single-tile");
     extern __shared__ __align__(16) int8_t smem[];
     const int K = p.K;
     int8_t *xq_lds = smem;
@@ -172,8 +176,7 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
     const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
     const int cpl = (per + 3) >> 2;               // chunks per lane
     const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless PF == 4)
-    const int tile = blockIdx.x;
-    const uint4 *tw = p.W + (size_t)tile * KC * 16;
+    const int tile0 = blockIdx.x * TT;
 
     // ---- loads: prologue inputs, then the residual, then the weights -------
     float v[NREG], g[NREG];
@@ -182,18 +185,22 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
         else load_row<NREG>(p.x, p.gamma, K, v, g);
     }
     float resid = 0.0f;
-    if constexpr (EPI == EPI_RESID) resid = p.y[tile * 16 + (tid & 15)];
-    auto load_batch = [&](uint4 (&dst)[PF], int b) {
+    if constexpr (EPI == EPI_RESID) resid = p.y[tile0 * 16 + (tid & (16 * TT - 1))];
+    auto load_batch = [&](uint4 (&dst)[TT][PF], int b) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const int kc = kc0 + c + 4 * (b * PF + u);
-            dst[u] = load_nt(tw + (size_t)min(kc, kc1 - 1) * 16 + r);
+        for (int t = 0; t < TT; ++t) {
+            const uint4 *tw = p.W + (size_t)(tile0 + t) * KC * 16;
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                const int kc = kc0 + c + 4 * (b * PF + u);
+                dst[t][u] = load_nt(tw + (size_t)min(kc, kc1 - 1) * 16 + r);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    uint4 A[PF];
-    [[maybe_unused]] uint4 B[PF];
+    uint4 A[TT][PF];
+    [[maybe_unused]] uint4 B[TT][PF];
     load_batch(A, 0);
 
     // ---- prologue ---------------------------------------------------------
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
         }
         sq = wave_isum_dpp(sq);
         if (lane == 0) wq[w] = sq;
-        if (tile == 0 && p.xq_out) {   // parity checks only
+        if (tile0 == 0 && p.xq_out) {   // parity checks only
 #pragma unroll
             for (int j = 0; j < NREG; ++j)
                 if (EXACT || tid + 256 * j < K) p.xq_out[tid + 256 * j] = (int8_t)qv[j];
@@ -254,22 +261,25 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
     }
 
     // ---- main loop: chunks past this wave's range multiply zero codes ------
-    CodeAcc acc;
-    auto mac_batch = [&](const uint4 (&src)[PF], int b) {
+    CodeAcc acc[TT];
+    auto mac_batch = [&](const uint4 (&src)[TT][PF], int b) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
             const int kc = kc0 + c + 4 * (b * PF + u);
             const int kcl = min(kc, kc1 - 1);   // own range (kc1 >= 1)
-            const uint4 wv = kc < kc1 ? src[u] : make_uint4(0, 0, 0, 0);
             const int xo = (kcl >> 1) * 128 + (kcl & 1) * 16;
             const int4 x0 = *(const int4 *)(xq_lds + xo);
             const int4 x1 = *(const int4 *)(xq_lds + xo + 32);
             const int4 x2 = *(const int4 *)(xq_lds + xo + 64);
             const int4 x3 = *(const int4 *)(xq_lds + xo + 96);
-            acc.add(wv.x, x0.x, x1.x, x2.x, x3.x);
-            acc.add(wv.y, x0.y, x1.y, x2.y, x3.y);
-            acc.add(wv.z, x0.z, x1.z, x2.z, x3.z);
-            acc.add(wv.w, x0.w, x1.w, x2.w, x3.w);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const uint4 wv = kc < kc1 ? src[t][u] : make_uint4(0, 0, 0, 0);
+                acc[t].add(wv.x, x0.x, x1.x, x2.x, x3.x);
+                acc[t].add(wv.y, x0.y, x1.y, x2.y, x3.y);
+                acc[t].add(wv.z, x0.z, x1.z, x2.z, x3.z);
+                acc[t].add(wv.w, x0.w, x1.w, x2.w, x3.w);
+            }
         }
     };
     if constexpr (PF != 4) {   // the launcher picks PF != 4 only when one batch covers the range
@@ -292,15 +302,16 @@ __global__ __launch_bounds__(256, PF <= 3 ? 4 : 2) void gemv_kernel(GemvParams p
     }
 
     // ---- reduction: 16 partials per row (4 lanes x 4 waves) through LDS ----
-    wpart[tid] = acc.codes();
+#pragma unroll
+    for (int t = 0; t < TT; ++t) wpart[t * 256 + tid] = acc[t].codes();
     __syncthreads();
-    if (tid >= 16) return;
+    if (tid >= 16 * TT) return;
     int a = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) a += wpart[k * 16 + r];
+    for (int k = 0; k < 16; ++k) a += wpart[(tid >> 4) * 256 + k * 16 + r];
     if constexpr (PRO == PRO_QUANT) xsum = wq[0] + wq[1] + wq[2] + wq[3];
     a -= xsum;
-    const int n = tile * 16 + r;
+    const int n = tile0 * 16 + tid;
     if (p.acc_out) p.acc_out[n] = a;
     // sh/ternary_gemv.wgsl:94-95: (f32(acc) * scales[row]) * input_scale
     float yv = (float)a * p.wscale[n];
@@ -409,27 +420,28 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-template <int PRO, int EPI, int NREG, int PF, bool EXACT>
+template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT = 1>
 static int launch_n(const GemvParams &p, hipStream_t s) {
-    const size_t sm = gemv_smem(p.K);
+    const size_t sm = gemv_smem(p.K, TT);
     if (sm > 64 * 1024) {
         static bool raised = false;   // per instantiation
         if (!raised) {
             OXB_CHECK_HIP(hipFuncSetAttribute(
-                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT>,
+                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT>), dim3(p.N / 16), dim3(256), sm, s,
-                       p);
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT>), dim3(p.N / (16 * TT)),
+                       dim3(256), sm, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-// PRO_QUANT: NREG = ceil(K/256) bucket (EXACT when K == 256 * NREG), all of
+// NREG = ceil(K/256) bucket for PRO_QUANT (EXACT when K == 256 * NREG), all of
 // a lane's weight chunks in one batch.  PRO_INT8: PF from the chunks per
 // lane, 4-chunk batches double-buffered when one batch does not cover them.
+// Grids over ~3 workgroups per CU take 4 tiles per workgroup.
 template <int PRO, int EPI>
 static int launch(const GemvParams &p, hipStream_t s) {
     const int KC = p.K >> 6;
@@ -440,7 +452,10 @@ static int launch(const GemvParams &p, hipStream_t s) {
         return launch_n<PRO, EPI, 1, 4, false>(p, s);
     } else {
         if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1, false>(p, s);
-        if (p.K == 2560) return launch_n<PRO, EPI, 10, 3, true>(p, s);
+        if (p.K == 2560) {
+            if (p.N >= 8192 && p.N % 64 == 0) return launch_n<PRO, EPI, 10, 3, true, 4>(p, s);
+            return launch_n<PRO, EPI, 10, 3, true>(p, s);
+        }
         if (p.K <= 2560) return launch_n<PRO, EPI, 10, 3, false>(p, s);
         if (p.K == 6912) return launch_n<PRO, EPI, 27, 7, true>(p, s);
         return launch_n<PRO, EPI, kMaxNormReg, 7, false>(p, s);
