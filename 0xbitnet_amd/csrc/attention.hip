@@ -381,6 +381,151 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     if (tid < 64) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Decode, one kernel: one 1024-thread workgroup per KV head does scores,
+// softmax and P.V for its G <= 4 query heads, so a layer's attention is one
+// launch and the scores never leave LDS.  Same arithmetic as the two-kernel
+// path (and the shaders).  Positions are taken in chunks: 256 K rows (wave
+// w: head w/4, positions (w%4)*64 + lane of the chunk), then 128 V rows
+// staged as f32 [128 dims][128 + 4 pad] (lane = one output (head, dim)).
+// Rows past the cache length are neither loaded nor used.
+// Faster than the two-kernel path only for short caches (each KV head's
+// K/V streams through one CU, ~30 GB/s): ~1 us less per layer at 64-128
+// positions, slower past ~200.  The host picks it by position.
+// LDS (dynamic): buf 69632 B (K chunk [256][17 uint4] | V chunk [128][132] f32)
+// | scores [G][Spad_max] f32 | q [G][128] f32.
+// ---------------------------------------------------------------------------
+constexpr int kFusedKC = 256;               // K rows per chunk
+constexpr int kFusedVC = 128;               // V rows per chunk
+constexpr int kFusedVS = kFusedVC + 4;      // padded V row (floats)
+constexpr size_t kFusedBuf = (size_t)kFusedKC * 17 * 16;   // 69632 B >= 128*132*4
+static_assert((size_t)kHd * kFusedVS * 4 <= kFusedBuf, "V chunk must fit the K chunk buffer");
+
+__host__ __device__ inline size_t attn_fused_smem(int G, int max_seq) {
+    return kFusedBuf + (size_t)G * ((max_seq + 3) & ~3) * 4 + (size_t)G * kHd * 4;
+}
+
+template <int G>
+__global__ __launch_bounds__(1024) void attn_fused_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int max_seq, float scale, float *__restrict__ out) {
+    static_assert(G == 1 || G == 2 || G == 4, "fused decode attention: G <= 4");
+    extern __shared__ __align__(16) int8_t smem_f[];
+    uint4 (*ks)[17] = (uint4 (*)[17])smem_f;
+    float *vt = (float *)smem_f;
+    const int spad_max = (max_seq + 3) & ~3;
+    float *sc = (float *)(smem_f + kFusedBuf);           // [G][spad_max]
+    float4 *qs = (float4 *)(sc + (size_t)G * spad_max);   // [G][32]
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1;
+    const int Spad = (S + 3) & ~3;
+    const int hk = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
+
+    // ---- scores ------------------------------------------------------------
+    auto load_k = [&](uint4 (&kt)[4], int c0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = tid + 1024 * k;   // row i/16, column i%16 of the chunk
+            const int row = c0 + (i >> 4);
+            kt[k] = row < S ? K4[(size_t)row * 16 + (i & 15)] : make_uint4(0, 0, 0, 0);
+        }
+    };
+    uint4 kt[4];
+    load_k(kt, 0);
+    if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
+    const int g = w >> 2, pg = w & 3;   // this wave's head and position group
+    for (int c0 = 0; c0 < S; c0 += kFusedKC) {
+        if (c0) __syncthreads();        // the previous chunk's rows are consumed
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = tid + 1024 * k;
+            ks[i >> 4][i & 15] = kt[k];
+        }
+        __syncthreads();
+        if (c0 + kFusedKC < S) load_k(kt, c0 + kFusedKC);
+        const int s = c0 + pg * 64 + lane;
+        if (g < G && s < S) {
+            // 128-term chain in two halves (q half and K half in registers);
+            // products fma(q, k, +0) = q*k up to the sign of a zero product
+            float dot = 0.0f;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                float4 qv[16];
+                uint4 kr[8];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) qv[i] = qs[g * 32 + half * 16 + i];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kr[i] = ks[pg * 64 + lane][half * 8 + i];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float qq[8] = {qv[2 * i].x, qv[2 * i].y, qv[2 * i].z, qv[2 * i].w,
+                                         qv[2 * i + 1].x, qv[2 * i + 1].y, qv[2 * i + 1].z,
+                                         qv[2 * i + 1].w};
+                    const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+                    for (int k2 = 0; k2 < 4; ++k2) {
+                        const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
+                        const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
+                        const float m0 = __builtin_fmaf(qq[2 * k2], k0, 0.0f);
+                        dot = dot + m0;
+                        const float m1 = __builtin_fmaf(qq[2 * k2 + 1], k1, 0.0f);
+                        dot = dot + m1;
+                    }
+                }
+            }
+            sc[g * spad_max + s] = dot * scale;
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax: wave g < G owns head g's row ------------------------------
+    if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane);
+
+    // ---- P.V: lane = output (head go, dim d), waves < 2G ----------------------
+    // Staging: wave w gathers positions 4w..4w+3 (+64 on the second pass) of
+    // the chunk, lane l the f16 pair of dims 2l, 2l+1: four row-coalesced
+    // 4-byte loads, then one float4 (4 positions) per dim into vt[d][s].
+    const int go = w >> 1, d = ((w & 1) << 6) | lane;
+    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd);
+    auto load_v = [&](uint32_t (&vr)[2][4], int c0) {
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int sr = c0 + pass * 64 + 4 * w + j;
+                vr[pass][j] = sr < S ? V2[(size_t)sr * (kHd / 2) + lane] : 0u;
+            }
+    };
+    uint32_t vr[2][4];
+    load_v(vr, 0);
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < S; c0 += kFusedVC) {
+        const int n = min(kFusedVC, S - c0);
+        __syncthreads();   // softmax done / K rows or the previous V chunk consumed
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            float4 lo, hi;   // dims 2*lane and 2*lane + 1 at 4 positions
+            float2 f0 = __half22float2(*(const __half2 *)&vr[pass][0]);
+            float2 f1 = __half22float2(*(const __half2 *)&vr[pass][1]);
+            float2 f2 = __half22float2(*(const __half2 *)&vr[pass][2]);
+            float2 f3 = __half22float2(*(const __half2 *)&vr[pass][3]);
+            lo = make_float4(f0.x, f1.x, f2.x, f3.x);
+            hi = make_float4(f0.y, f1.y, f2.y, f3.y);
+            const int sr = pass * 64 + 4 * w;
+            *(float4 *)(vt + (2 * lane) * kFusedVS + sr) = lo;
+            *(float4 *)(vt + (2 * lane + 1) * kFusedVS + sr) = hi;
+        }
+        __syncthreads();
+        if (c0 + kFusedVC < S) load_v(vr, c0 + kFusedVC);
+        if (go < G) acc = pv_chain(sc + go * spad_max + c0, vt + d * kFusedVS, n, acc);
+    }
+    if (go < G) out[(size_t)(hk * G + go) * kHd + d] = acc;
+}
+
 template <int G>
 static int launch_exact(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                         int pos0, int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
@@ -461,6 +606,44 @@ extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uin
         default:
             oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
             return -1;
+    }
+}
+
+template <int G>
+static int launch_fused(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
+                        int Hkv, int max_seq, float *out, hipStream_t s) {
+    const size_t smem = attn_fused_smem(G, max_seq);
+    static size_t configured = 0;
+    if (smem > configured) {
+        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_fused_kernel<G>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        configured = smem;
+    }
+    const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    hipLaunchKernelGGL(attn_fused_kernel<G>, dim3(Hkv), dim3(1024), smem, s, q, kc, vc, pos,
+                       max_seq, scale, out);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int oxb_attn_decode_fused_supported(int H, int Hkv, int hd, int max_seq) {
+    if (hd != kHd || Hkv <= 0 || H % Hkv != 0) return 0;
+    const int G = H / Hkv;
+    return (G == 1 || G == 2 || G == 4) && attn_fused_smem(G, max_seq) <= 160 * 1024;
+}
+
+extern "C" int oxb_attn_decode_fused(const float *q, const uint16_t *kcache,
+                                     const uint16_t *vcache, const int *pos, int H, int Hkv,
+                                     int hd, int max_seq, float *out, void *stream) {
+    OXB_REQUIRE(pos, "attention: pos is NULL");
+    OXB_REQUIRE(oxb_attn_decode_fused_supported(H, Hkv, hd, max_seq),
+                "fused decode attention: unsupported shape (H %d, Hkv %d, hd %d, max_seq %d)", H,
+                Hkv, hd, max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    switch (H / Hkv) {
+        case 1: return launch_fused<1>(q, kcache, vcache, pos, Hkv, max_seq, out, s);
+        case 2: return launch_fused<2>(q, kcache, vcache, pos, Hkv, max_seq, out, s);
+        default: return launch_fused<4>(q, kcache, vcache, pos, Hkv, max_seq, out, s);
     }
 }
 

@@ -13,6 +13,8 @@
 // greedy token is reduced on the device.
 #include "model.h"
 
+#include <cstdlib>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
@@ -36,6 +38,7 @@ using namespace oxb;
 oxb_model::~oxb_model() {
     if (stream) hipStreamSynchronize(stream);
     if (graph) hipGraphExecDestroy(graph);
+    if (graph_fused) hipGraphExecDestroy(graph_fused);
     for (void *p : allocations) hipFree(p);
     if (pinned) hipHostFree(pinned);
     if (stream) hipStreamDestroy(stream);
@@ -426,6 +429,13 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
+    // one-kernel decode attention while the cache holds <= 192 positions: it
+    // saves a launch but streams each KV head's cache through one CU, which
+    // loses to the two-kernel path (spread over the chip) beyond ~200
+    // positions (MI355X, 2B shape).  OXB_ATTN_FUSED_MAX_S overrides (0: off).
+    m->fused_max_s = 192;
+    if (const char *env = getenv("OXB_ATTN_FUSED_MAX_S")) m->fused_max_s = atoi(env);
+    if (!oxb_attn_decode_fused_supported(m->H, m->Hkv, m->hd, m->max_seq)) m->fused_max_s = 0;
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
     if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist)
         return nullptr;
@@ -456,7 +466,7 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
 // One decode step: embedding of state.token at state.pos -> layers -> LM
 // head + argmax (state.token, state.pos += 1).  Every kernel reads the
 // position from device memory, so the same launch sequence replays as a graph.
-int oxb_model::enqueue_decode_step() {
+int oxb_model::enqueue_decode_step(bool fused_attn) {
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     int *posp = state + OXB_ST_POS;
@@ -468,7 +478,8 @@ int oxb_model::enqueue_decode_step() {
         if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
                               max_seq, rope, posp, s))
             return -1;
-        if (oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, attn, s))
+        if (fused_attn ? oxb_attn_decode_fused(q, kc, vc, posp, H, Hkv, hd, max_seq, attn, s)
+                       : oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, attn, s))
             return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
         if (oxb_bitlinear_gemv(L.wo, attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr, nullptr,
@@ -488,11 +499,12 @@ int oxb_model::enqueue_decode_step() {
                               1, s);
 }
 
-int oxb_model::capture_graph() {
-    if (graph) return 0;
+int oxb_model::capture_graph(bool fused_attn) {
+    hipGraphExec_t &slot = fused_attn ? graph_fused : graph;
+    if (slot) return 0;
     hipGraph_t g = nullptr;
     M_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_decode_step();
+    int rc = enqueue_decode_step(fused_attn);
     hipError_t e = hipStreamEndCapture(stream, &g);
     if (rc) {
         if (g) hipGraphDestroy(g);
@@ -502,14 +514,20 @@ int oxb_model::capture_graph() {
         set_error("hipStreamEndCapture: %s", hipGetErrorString(e));
         return -1;
     }
-    e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&slot, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e != hipSuccess) {
-        graph = nullptr;
+        slot = nullptr;
         set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
         return -1;
     }
     return 0;
+}
+
+hipGraphExec_t oxb_model::step_graph(int p) {
+    const bool fused = p + 1 <= fused_max_s;
+    if (capture_graph(fused)) return nullptr;
+    return fused ? graph_fused : graph;
 }
 
 int oxb_model::ensure_prefill(int n) {
@@ -661,8 +679,9 @@ extern "C" int oxb_model_step(oxb_model *m, float *logits_host) {
     clear_error();
     OXB_REQUIRE(m, "model is NULL");
     OXB_REQUIRE(m->pos + 1 <= m->max_seq, "KV cache full: position %d of %d", m->pos, m->max_seq);
-    if (!m->graph && m->capture_graph()) return -1;
-    M_CHECK(hipGraphLaunch(m->graph, m->stream));
+    hipGraphExec_t ge = m->step_graph(m->pos);
+    if (!ge) return -1;
+    M_CHECK(hipGraphLaunch(ge, m->stream));
     m->pos += 1;
     m->ngen += 1;
     return read_token(m, logits_host);
@@ -690,9 +709,12 @@ extern "C" int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *token
     OXB_REQUIRE(m->pos + n_steps <= m->max_seq, "KV cache overflow: %d + %d > %d", m->pos,
                 n_steps, m->max_seq);
     OXB_REQUIRE(m->ngen + n_steps <= m->hist_cap, "token history full");
-    if (!m->graph && m->capture_graph()) return -1;
     const int first = m->ngen;
-    for (int i = 0; i < n_steps; ++i) M_CHECK(hipGraphLaunch(m->graph, m->stream));
+    for (int i = 0; i < n_steps; ++i) {
+        hipGraphExec_t ge = m->step_graph(m->pos + i);
+        if (!ge) return -1;
+        M_CHECK(hipGraphLaunch(ge, m->stream));
+    }
     m->pos += n_steps;
     m->ngen += n_steps;
     if (n_steps)

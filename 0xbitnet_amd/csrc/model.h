@@ -45,7 +45,10 @@ struct oxb_model {
     int *psum = nullptr, *pids = nullptr;
 
     hipStream_t stream = nullptr;
-    hipGraphExec_t graph = nullptr;
+    // decode step graphs: two-kernel attention, and one-kernel attention for
+    // caches of up to fused_max_s positions (0: never)
+    hipGraphExec_t graph = nullptr, graph_fused = nullptr;
+    int fused_max_s = 0;
     int *pinned = nullptr;      // host-pinned scratch for small readbacks
     int pos = 0;                // host mirror of state[OXB_ST_POS]
     int ngen = 0;               // host mirror of state[OXB_ST_NGEN]
@@ -55,10 +58,12 @@ struct oxb_model {
 
     ~oxb_model();
     void *dalloc(size_t bytes);
-    int enqueue_decode_step();
+    int enqueue_decode_step(bool fused_attn);
     int ensure_prefill(int n);
     int enqueue_prefill(const int32_t *ids, int n);
-    int capture_graph();
+    int capture_graph(bool fused_attn);
+    // the graph for a step whose token sits at position p (captured on first use)
+    hipGraphExec_t step_graph(int p);
 };
 
 namespace oxb {

@@ -192,16 +192,21 @@ def gemm(Wt, x: np.ndarray, gamma, eps: float, wscale: np.ndarray, N: int, K: in
 
 
 def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, H: int, Hkv: int,
-                hd: int, max_seq: int):
-    """q [H*hd] f32; caches [Hkv][max_seq][hd] f16; attends over pos+1 positions."""
+                hd: int, max_seq: int, fused: bool = False):
+    """q [H*hd] f32; caches [Hkv][max_seq][hd] f16; attends over pos+1 positions.
+    fused: the one-kernel variant (oxb_attn_decode_fused)."""
     dq = DeviceArray.from_host(np.ascontiguousarray(q, np.float32))
     dk = DeviceArray.from_host(np.ascontiguousarray(kcache, np.float16).view(np.uint16))
     dv = DeviceArray.from_host(np.ascontiguousarray(vcache, np.float16).view(np.uint16))
     dpos = DeviceArray.from_host(np.array([pos], np.int32))
     out = DeviceArray((H * hd,), np.float32)
-    sc = DeviceArray((H * max_seq,), np.float32)
-    check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, sc.ptr,
-                                out.ptr, None), "attn_decode")
+    if fused:
+        check(lib().oxb_attn_decode_fused(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq,
+                                          out.ptr, None), "attn_decode_fused")
+    else:
+        sc = DeviceArray((H * max_seq,), np.float32)
+        check(lib().oxb_attn_decode(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq, sc.ptr,
+                                    out.ptr, None), "attn_decode")
     sync()
     return out.download()
 

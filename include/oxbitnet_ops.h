@@ -128,6 +128,15 @@ int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcac
                     const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
                     float *out, void *stream);
 
+/* The same decode attention as one kernel: one 1024-thread workgroup per KV
+ * head computes scores, softmax and P.V in LDS (no scores buffer), same
+ * result bits.  Faster for short caches (one CU per KV head streams the
+ * whole cache); H/Hkv <= 4 and the LDS of oxb_attn_decode_fused_supported. */
+int oxb_attn_decode_fused_supported(int H, int Hkv, int hd, int max_seq);
+int oxb_attn_decode_fused(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                          const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
+                          void *stream);
+
 /* Causal prefill attention for n_tok queries at positions pos0.., same order.
  * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,

@@ -215,6 +215,33 @@ def test_attn_decode_bitexact(pos, H, Hkv, S):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (255, 20, 5, 512),
+                                         (256, 20, 5, 512), (300, 20, 5, 408), (511, 20, 5, 512),
+                                         (700, 8, 4, 1024), (1500, 20, 5, 4096),
+                                         (4095, 20, 5, 4096), (129, 4, 4, 256)])
+def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
+    """One-kernel decode attention: same bits as the oracle (and the split path)."""
+    assert ops.lib().oxb_attn_decode_fused_supported(H, Hkv, 128, S)
+    rng = np.random.default_rng(pos * 7 + H)
+    hd = 128
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
+    out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, fused=True)
+    ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_attn_decode_fused_rejects_unsupported():
+    L = ops.lib()
+    assert not L.oxb_attn_decode_fused_supported(32, 4, 128, 512)     # 8 heads per KV head
+    assert not L.oxb_attn_decode_fused_supported(20, 5, 64, 512)      # head_dim 64
+    assert not L.oxb_attn_decode_fused_supported(20, 5, 128, 1 << 16)  # LDS
+    with pytest.raises(ops.NativeError, match="unsupported shape"):
+        ops.attn_decode(np.zeros(32 * 128, np.float32), np.zeros((4, 8, 128), np.float16),
+                        np.zeros((4, 8, 128), np.float16), 3, 32, 4, 128, 8, fused=True)
+
+
 def test_attn_prefill_causal_bitexact():
     rng = np.random.default_rng(21)
     H, Hkv, hd, S = 20, 5, 128, 256

@@ -82,6 +82,42 @@ def test_graph_decode_matches_stepwise():
     m.close()
 
 
+def _decode_logits(path, prompt, steps, max_seq, fused_max_s):
+    import os
+    old = os.environ.get("OXB_ATTN_FUSED_MAX_S")
+    os.environ["OXB_ATTN_FUSED_MAX_S"] = str(fused_max_s)   # read when the model loads
+    try:
+        m = pkg.Model(path, max_seq=max_seq)
+    finally:
+        if old is None:
+            del os.environ["OXB_ATTN_FUSED_MAX_S"]
+        else:
+            os.environ["OXB_ATTN_FUSED_MAX_S"] = old
+    tok, logits = m.forward(prompt)
+    out = [logits]
+    toks = [tok]
+    for _ in range(steps):
+        tok, logits = m.step()
+        out.append(logits)
+        toks.append(tok)
+    m.close()
+    return toks, np.stack(out)
+
+
+def test_fused_and_split_decode_attention_identical():
+    """The one-kernel attention graph (short caches) and the two-kernel graph
+    give the same bits, including across the switch between them."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab, 500).astype(np.int32)
+    t_split, l_split = _decode_logits(path, prompt, 24, 600, 0)
+    t_mixed, l_mixed = _decode_logits(path, prompt, 24, 600, 512)
+    t_fused, l_fused = _decode_logits(path, prompt, 24, 600, 600)
+    assert t_split == t_mixed == t_fused
+    assert np.array_equal(l_split.view(np.uint32), l_mixed.view(np.uint32))
+    assert np.array_equal(l_split.view(np.uint32), l_fused.view(np.uint32))
+
+
 def test_single_token_forward_is_decode_path():
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
