@@ -42,6 +42,10 @@ struct GemmParams {
     uint16_t *kcache, *vcache;
     const float2 *rope;
     int Dq, Dkv, hd, max_seq, pos0;
+    // optional: token t is at position tok_pos[t] of its own cache, which
+    // starts kv_tok_stride elements after token t-1's (batched decode)
+    const int *tok_pos;
+    size_t kv_tok_stride;
 };
 
 __device__ inline v4i plane(uint4 w, int g) {
@@ -58,6 +62,63 @@ __device__ inline v4i as_v4i(uint4 u) {
     v4i a;
     a.x = (int)u.x; a.y = (int)u.y; a.z = (int)u.z; a.w = (int)u.w;
     return a;
+}
+
+// Epilogue for one lane's 4 accumulators: features n0 .. n0+3 of token t.
+template <int EPI>
+__device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int n0) {
+    const int xs = p.xsum[t];
+    const float is = p.xscale[t];
+    float y[4];
+    int32_t a[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        a[v] = c[v] - xs;
+        // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
+        const float sc = p.wscale[n0 + v] * is;
+        y[v] = (float)a[v] * sc;
+    }
+    if (p.acc_out) *(int4 *)(p.acc_out + (size_t)t * p.N + n0) = make_int4(a[0], a[1], a[2], a[3]);
+    if constexpr (EPI == GE_STORE) {
+        *(float4 *)(p.Y + (size_t)t * p.N + n0) = make_float4(y[0], y[1], y[2], y[3]);
+    } else if constexpr (EPI == GE_RESID) {
+        float4 *dst = (float4 *)(p.Y + (size_t)t * p.N + n0);
+        float4 o = *dst;
+        o.x = o.x + y[0]; o.y = o.y + y[1]; o.z = o.z + y[2]; o.w = o.w + y[3];
+        *dst = o;
+    } else if constexpr (EPI == GE_GATEUP) {
+        float g0 = fmaxf(0.0f, y[0]), g1 = fmaxf(0.0f, y[2]);
+        g0 = g0 * g0;
+        g1 = g1 * g1;
+        *(float2 *)(p.Y + (size_t)t * (p.N >> 1) + (n0 >> 1)) = make_float2(g0 * y[1], g1 * y[3]);
+    } else {  // GE_QKV
+        const int pos = p.tok_pos ? p.tok_pos[t] : p.pos0 + t;
+        if (pos < 0 || pos >= p.max_seq) return;   // host checks too; never write out of range
+        const int Dk = p.Dq + p.Dkv;
+        float o[4] = {y[0], y[1], y[2], y[3]};
+        if (n0 < Dk) {
+            const int d0 = (n0 < p.Dq ? n0 : n0 - p.Dq) % p.hd;
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d0 >> 1) + pr];
+                const float x0 = y[2 * pr], x1 = y[2 * pr + 1];
+                float a0 = x0 * cs.x, a1 = x1 * cs.y;
+                float b0 = x0 * cs.y, b1 = x1 * cs.x;
+                o[2 * pr] = a0 - a1;
+                o[2 * pr + 1] = b0 + b1;
+            }
+        }
+        if (n0 < p.Dq) {
+            *(float4 *)(p.q_out + (size_t)t * p.Dq + n0) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            const int j = n0 < Dk ? n0 - p.Dq : n0 - Dk;
+            const int head = j / p.hd, d = j % p.hd;
+            uint16_t *cache = (n0 < Dk ? p.kcache : p.vcache) + (p.tok_pos ? t * p.kv_tok_stride : 0);
+            uint16_t *dst = cache + ((size_t)head * p.max_seq + pos) * p.hd + d;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
+        }
+    }
 }
 
 // Workgroup tile: 64 features x 64 tokens; 4 waves in a 2x2 grid, each wave
@@ -131,62 +192,92 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             if (tt == 1 && !t1ok) continue;
             const int t = (tt0 + tt) * 16 + r;
             if (t >= p.n_tok) continue;
-            const int n0 = f0 + ft * 16 + 4 * q;
-            const int xs = p.xsum[t];
-            const float is = p.xscale[t];
-            float y[4];
-            int32_t a[4];
+            gemm_store<EPI>(p, acc[ft][tt], t, f0 + ft * 16 + 4 * q);
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM for n_tok <= 64 (batched decode, small-M sweeps): the GEMV's
+// decomposition with MFMA inside.  A workgroup owns TF 16-row feature tiles
+// and all TT = ceil(n_tok/16) token tiles; its 4 waves split K (in 4-chunk
+// MFMA steps) and meet in LDS, where each wave sums a quarter of the tiles
+// (int32, exact) and runs the epilogue.  N/16/TF workgroups keep the chip
+// busy where the 64x64 tiling launches too few.
+// ---------------------------------------------------------------------------
+template <int EPI, int TT, int TF>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
+    constexpr int NT = TF * TT;   // 16x16 tiles per wave
+    __shared__ v4i red[4][NT][64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, q = lane >> 4;
+    const int KC = p.K >> 6, steps = KC >> 2;
+    const int per = (steps + 3) >> 2;
+    const int s0 = min(w * per, steps), s1 = min(steps, s0 + per);
+    const int ftile0 = blockIdx.x * TF;
+
+    v4i acc[TF][TT];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                a[v] = acc[ft][tt][v] - xs;
-                // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
-                const float sc = p.wscale[n0 + v] * is;
-                y[v] = (float)a[v] * sc;
-            }
-            if (p.acc_out) {
-                *(int4 *)(p.acc_out + (size_t)t * p.N + n0) = make_int4(a[0], a[1], a[2], a[3]);
-            }
-            if constexpr (EPI == GE_STORE) {
-                *(float4 *)(p.Y + (size_t)t * p.N + n0) = make_float4(y[0], y[1], y[2], y[3]);
-            } else if constexpr (EPI == GE_RESID) {
-                float4 *dst = (float4 *)(p.Y + (size_t)t * p.N + n0);
-                float4 o = *dst;
-                o.x = o.x + y[0]; o.y = o.y + y[1]; o.z = o.z + y[2]; o.w = o.w + y[3];
-                *dst = o;
-            } else if constexpr (EPI == GE_GATEUP) {
-                float g0 = fmaxf(0.0f, y[0]), g1 = fmaxf(0.0f, y[2]);
-                g0 = g0 * g0;
-                g1 = g1 * g1;
-                *(float2 *)(p.Y + (size_t)t * (p.N >> 1) + (n0 >> 1)) =
-                    make_float2(g0 * y[1], g1 * y[3]);
-            } else {  // GE_QKV
-                const int pos = p.pos0 + t;
-                const int Dk = p.Dq + p.Dkv;
-                float o[4] = {y[0], y[1], y[2], y[3]};
-                if (n0 < Dk) {
-                    const int d0 = (n0 < p.Dq ? n0 : n0 - p.Dq) % p.hd;
+    for (int i = 0; i < TF; ++i)
 #pragma unroll
-                    for (int pr = 0; pr < 2; ++pr) {
-                        const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d0 >> 1) + pr];
-                        const float x0 = y[2 * pr], x1 = y[2 * pr + 1];
-                        float a0 = x0 * cs.x, a1 = x1 * cs.y;
-                        float b0 = x0 * cs.y, b1 = x1 * cs.x;
-                        o[2 * pr] = a0 - a1;
-                        o[2 * pr + 1] = b0 + b1;
-                    }
-                }
-                if (n0 < p.Dq) {
-                    *(float4 *)(p.q_out + (size_t)t * p.Dq + n0) = make_float4(o[0], o[1], o[2], o[3]);
-                } else {
-                    const int j = n0 < Dk ? n0 - p.Dq : n0 - Dk;
-                    const int head = j / p.hd, d = j % p.hd;
-                    uint16_t *cache = n0 < Dk ? p.kcache : p.vcache;
-                    uint16_t *dst = cache + ((size_t)head * p.max_seq + pos) * p.hd + d;
+        for (int j = 0; j < TT; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    auto load = [&](int s, uint4 (&wv)[TF], uint4 (&xv)[TT][4]) {
+        const int kc = 4 * s + q;
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
-                }
+        for (int f = 0; f < TF; ++f)
+            wv[f] = load_nt(p.W + ((size_t)(ftile0 + f) * KC + kc) * 16 + r);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const uint4 *x = p.X + (((size_t)t * KC + kc) * 16 + r) * 4;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) xv[t][g] = x[g];
+        }
+    };
+    auto mac = [&](const uint4 (&wv)[TF], const uint4 (&xv)[TT][4]) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int f = 0; f < TF; ++f) {
+                const v4i a = plane(wv[f], g);
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+                    acc[f][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, as_v4i(xv[t][g]), acc[f][t],
+                                                                      0, 0, 0);
             }
         }
+    };
+    if (s0 < s1) {
+        uint4 wa[TF], xa[TT][4], wb[TF], xb[TT][4];
+        load(s0, wa, xa);
+        int s = s0;
+        for (; s + 2 < s1; s += 2) {
+            load(s + 1, wb, xb);
+            mac(wa, xa);
+            load(s + 2, wa, xa);
+            mac(wb, xb);
+        }
+        if (s + 1 < s1) {
+            load(s + 1, wb, xb);
+            mac(wa, xa);
+            mac(wb, xb);
+        } else {
+            mac(wa, xa);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) red[w][f * TT + t][lane] = acc[f][t];
+    __syncthreads();
+    const int ntok = p.n_tok;
+    for (int i = w; i < NT; i += 4) {
+        v4i c = red[0][i][lane];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) c += red[k][i][lane];
+        const int f = i / TT, t = (i % TT) * 16 + r;
+        if (t < ntok) gemm_store<EPI>(p, c, t, (ftile0 + f) * 16 + 4 * q);
     }
 }
 
@@ -201,10 +292,31 @@ static int gemm_check(int N, int K, int n_tok) {
     return 0;
 }
 
+template <int EPI, int TT, int TF>
+static int skinny_launch(const GemmParams &p, hipStream_t s) {
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, TT, TF>), dim3(p.N / (16 * TF)), dim3(256), 0, s, p);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+// n_tok <= 64: skinny kernel (2 feature tiles per workgroup once there are
+// 3+ token tiles and enough rows, to halve the activation re-reads); else
+// the 64x64 tiled kernel.
 template <int EPI>
 static int gemm_launch(const GemmParams &p, void *stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (p.n_tok <= 64) {
+        const int tt = (p.n_tok + 15) >> 4;
+        const bool two = tt >= 3 && p.N % 32 == 0 && p.N / 32 >= 256;
+        switch (tt) {
+            case 1: return skinny_launch<EPI, 1, 1>(p, s);
+            case 2: return skinny_launch<EPI, 2, 1>(p, s);
+            case 3: return two ? skinny_launch<EPI, 3, 2>(p, s) : skinny_launch<EPI, 3, 1>(p, s);
+            default: return two ? skinny_launch<EPI, 4, 2>(p, s) : skinny_launch<EPI, 4, 1>(p, s);
+        }
+    }
     dim3 grid((p.N + 63) / 64, (p.n_tok + 63) / 64);
-    hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }

@@ -255,7 +255,12 @@ def test_attn_prefill_causal_bitexact():
 
 
 @pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
-                                   (32, 256, 65)])
+                                   (32, 256, 65),
+                                   # n <= 64: the skinny kernel, 1..4 token tiles, 1 or 2
+                                   # feature tiles per workgroup, uneven K splits over waves
+                                   (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
+                                   (8192, 2560, 40), (8192, 512, 64), (256, 1280, 64),
+                                   (96, 256, 1)])
 def test_gemm_mfma_bitexact(N, K, n):
     rng = np.random.default_rng(N + n)
     w = ternary(rng, N, K)
