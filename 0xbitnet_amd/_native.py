@@ -108,6 +108,16 @@ SIGNATURES = {
     "oxb_model_position": (C.c_int, [vp]),
     "oxb_model_set_token": (C.c_int, [vp, i32]),
     "oxb_model_step": (C.c_int, [vp, vp]),
+    "oxb_attn_decode_batch": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
+                                        vp, vp, vp]),
+    "oxb_lm_head_argmax_batch": (C.c_int, [vp, C.c_size_t, vp, f32, vp, i32, i32, vp, vp, i32,
+                                           vp, i32, i32, i32, vp]),
+    "oxb_batch_create": (vp, [vp, i32, i32]),
+    "oxb_batch_free": (None, [vp]),
+    "oxb_batch_prefill": (C.c_int, [vp, i32, vp, i32]),
+    "oxb_batch_decode_greedy": (C.c_int, [vp, i32, vp]),
+    "oxb_batch_position": (C.c_int, [vp, i32]),
+    "oxb_batch_logits": (C.c_int, [vp, vp]),
     # reference C ABI
     "oxbitnet_set_logger": (None, [LogFn, vp, C.c_uint8]),
     "oxbitnet_default_generate_options": (GenerateOptions, []),

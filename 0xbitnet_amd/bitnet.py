@@ -167,3 +167,47 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+class Batch:
+    """Batched greedy decode of independent sequences on a loaded Model
+    (include/oxbitnet_ops.h oxb_batch_*); each slot's tokens and logits are
+    those of a one-sequence Model on the same prompt."""
+
+    def __init__(self, model: Model, batch: int, max_seq: int):
+        self._model = model   # keeps the weights alive
+        self._b = lib().oxb_batch_create(model._m, batch, max_seq)
+        if not self._b:
+            raise NativeError(last_error())
+        self.batch = batch
+
+    def prefill(self, slot: int, ids) -> int:
+        ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
+        tok = lib().oxb_batch_prefill(self._b, slot, ids.ctypes.data, ids.size)
+        if tok < 0:
+            raise NativeError(last_error())
+        return tok
+
+    def decode_greedy(self, n_steps: int) -> np.ndarray:
+        out = np.empty((self.batch, n_steps), np.int32)
+        check(lib().oxb_batch_decode_greedy(self._b, n_steps, out.ctypes.data), "batch decode")
+        return out
+
+    def position(self, slot: int) -> int:
+        return lib().oxb_batch_position(self._b, slot)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty((self.batch, self._model.vocab), np.float32)
+        check(lib().oxb_batch_logits(self._b, out.ctypes.data), "batch logits")
+        return out
+
+    def close(self) -> None:
+        if self._b:
+            lib().oxb_batch_free(self._b)
+            self._b = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

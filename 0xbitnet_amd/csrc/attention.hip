@@ -139,10 +139,17 @@ constexpr int kScoreP = 64;   // positions per scores workgroup (one per lane)
 template <int G>
 __global__ __launch_bounds__(256) void attn_scores_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const int *__restrict__ pos_ptr,
-    int max_seq, float scale, float *__restrict__ scores) {
+    int max_seq, float scale, float *__restrict__ scores, size_t kv_stride, int pos_stride) {
     // K rows of this position block, 16 uint4 each, padded to 17 so that the
     // 64 lanes reading one column hit different banks.
     __shared__ uint4 ks[kScoreP][17];
+    {   // sequence blockIdx.z of a batch: its own q, cache, position, scores
+        const int z = blockIdx.z, H = gridDim.y * G;
+        q += (size_t)z * H * kHd;
+        kc += (size_t)z * kv_stride;
+        pos_ptr += (size_t)z * pos_stride;
+        scores += (size_t)z * H * max_seq;
+    }
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
@@ -324,7 +331,15 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
 template <int G>
 __global__ __launch_bounds__(256) void attn_pv_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out) {
+    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
+    int pos_stride) {
+    {   // sequence blockIdx.z of a batch
+        const int z = blockIdx.z, H = gridDim.x * G;
+        scores += (size_t)z * H * max_seq;
+        vc += (size_t)z * kv_stride;
+        pos_ptr += (size_t)z * pos_stride;
+        out += (size_t)z * H * kHd;
+    }
     constexpr int DW = 64 / G;               // dims per workgroup
     constexpr int PPP = DW / 8;              // uint4 (8 f16) per position of the slice
     constexpr int kVChunk = kVFloats / DW;   // positions staged per pass
@@ -570,10 +585,12 @@ using namespace oxb;
 
 template <int G>
 static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
-                         int Hkv, int max_seq, float *scores, float *out, hipStream_t s) {
+                         int Hkv, int max_seq, float *scores, float *out, hipStream_t s,
+                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0) {
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
-    hipLaunchKernelGGL(attn_scores_kernel<G>, dim3((max_seq + kScoreP - 1) / kScoreP, Hkv),
-                       dim3(256), 0, s, q, kc, pos, max_seq, scale, scores);
+    hipLaunchKernelGGL(attn_scores_kernel<G>,
+                       dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
+                       kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     const size_t smem = (size_t)G * ((max_seq + 3) & ~3) * sizeof(float);
     static size_t configured = 0;
@@ -582,8 +599,8 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
         configured = smem;
     }
-    hipLaunchKernelGGL(attn_pv_kernel<G>, dim3(Hkv, G * kHd / 64), dim3(256), smem, s, scores, vc,
-                       pos, max_seq, out);
+    hipLaunchKernelGGL(attn_pv_kernel<G>, dim3(Hkv, G * kHd / 64, batch), dim3(256), smem, s,
+                       scores, vc, pos, max_seq, out, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -603,6 +620,31 @@ extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uin
         case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        default:
+            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
+            return -1;
+    }
+}
+
+extern "C" int oxb_attn_decode_batch(const float *q, const uint16_t *kcache,
+                                     const uint16_t *vcache, const int *pos, int pos_stride,
+                                     size_t kv_stride, int batch, int H, int Hkv, int hd,
+                                     int max_seq, float *scores, float *out, void *stream) {
+    OXB_REQUIRE(pos && scores, "attention: pos or scores is NULL");
+    OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
+    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
+                "attention: caches of a batch overlap (stride %zu)", kv_stride);
+    const int G = H / Hkv;
+    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
+                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    switch (G) {
+        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
+        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
+        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
+        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
         default:
             oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
             return -1;

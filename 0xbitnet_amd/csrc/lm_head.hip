@@ -18,10 +18,13 @@ struct LmParams {
     float eps;
     const uint4 *E;        // lm-tiled embedding (below)
     int V, D;
-    float *logits;         // [V]
-    int *state;            // decode state (see oxb_kernels.h)
-    int *tok_hist;         // [max_gen] generated tokens, may be null
+    float *logits;         // [NV][V]
+    int *state;            // decode state (see oxb_kernels.h), one block per row
+    int *tok_hist;         // [max_gen] generated tokens per row, may be null
     int advance;           // positions to add to state.pos (tokens in this forward)
+    size_t x_stride;       // floats between rows of x
+    int state_stride;      // ints between the rows' state blocks
+    int hist_stride;       // ints between the rows' token histories
 };
 
 // Row-per-lane layout of the tied embedding for the LM head ("lm-tiled"):
@@ -104,13 +107,13 @@ __device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk
 // ticket, so the ticket order covers every max.  No cache-wide fences: a
 // release/acquire per block writes back and invalidates the L2 and cost
 // ~0.25 us per block.
-template <int NJ>  // D = 512 * NJ
+template <int NJ, int NV>  // D = 512 * NJ; NV rows of x (one pass over E)
 __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
     __shared__ float red[324];
-    __shared__ __align__(16) float2 hp[256 * NJ];   // h pairs in consumption order
-    __shared__ float Tl[2][16][64];                 // group sums, double-buffered per tile
-    __shared__ float bval[4];
-    __shared__ int bidx[4];
+    __shared__ __align__(16) float2 hp[NV][256 * NJ];   // h pairs in consumption order
+    __shared__ float Tl[NV][2][16][64];                  // group sums, double-buffered per tile
+    __shared__ float bval[NV][4];
+    __shared__ int bidx[NV][4];
     constexpr int NQ = 64 * NJ, HQ = 2 * NJ;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = p.D;
@@ -134,103 +137,132 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
     uint4 A[HQ], B[HQ];
     if (nseq > 0) load_hg(A, 0);   // weights do not depend on the norm: start early
 
-    // final RMSNorm (sh/rmsnorm.wgsl order) straight into the pair table
-    float ss = 0.0f;
-    for (int c = tid; c < D; c += 256) {
-        const float v = p.x[c];
-        const float sq = v * v;
-        ss = ss + sq;
-    }
-    const float sum = block256_tree_sum_fast(ss, red);
-    const float rms = 1.0f / sqrtf(sum / (float)D + p.eps);
-    for (int u = tid; u < 256 * NJ; u += 256) {
-        const int i = u / NJ, j = u % NJ;
-        const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
-        const int d0 = 2 * (t + 256 * j);
-        const float a0 = p.x[d0] * rms, a1 = p.x[d0 + 1] * rms;
-        hp[u] = make_float2(a0 * p.gamma[d0], a1 * p.gamma[d0 + 1]);
+    // final RMSNorm (sh/rmsnorm.wgsl order) of each row straight into its pair table
+#pragma unroll 1
+    for (int v = 0; v < NV; ++v) {
+        const float *x = p.x + (size_t)v * p.x_stride;
+        float ss = 0.0f;
+        for (int c = tid; c < D; c += 256) {
+            const float xv = x[c];
+            const float sq = xv * xv;
+            ss = ss + sq;
+        }
+        const float sum = block256_tree_sum_fast(ss, red);
+        const float rms = 1.0f / sqrtf(sum / (float)D + p.eps);
+        for (int u = tid; u < 256 * NJ; u += 256) {
+            const int i = u / NJ, j = u % NJ;
+            const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
+            const int d0 = 2 * (t + 256 * j);
+            const float a0 = x[d0] * rms, a1 = x[d0 + 1] * rms;
+            hp[v][u] = make_float2(a0 * p.gamma[d0], a1 * p.gamma[d0 + 1]);
+        }
     }
     __syncthreads();
 
-    float best = -INFINITY;
-    int besti = 0x7fffffff;
-    auto finish_pair = [&](float g0, float g1, int s) {
+    float best[NV];
+    int besti[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) { best[v] = -INFINITY; besti[v] = 0x7fffffff; }
+    auto finish_pair = [&](const float (&g0)[NV], const float (&g1)[NV], int s) {
         const int k = (8 * w + (s & 7)) >> 1;   // 16-leaf group
         const int i = s >> 3;                   // tile ordinal within this block
-        Tl[i & 1][k][lane] = g0 + g1;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) Tl[v][i & 1][k][lane] = g0[v] + g1[v];
         if ((s & 7) == 6) {                     // this tile's groups are all done
             lds_barrier();
             if (w == (i & 3)) {
-                float T[16];
-#pragma unroll
-                for (int kk = 0; kk < 16; ++kk) T[kk] = Tl[i & 1][kk][lane];
-#pragma unroll
-                for (int st = 1; st < 16; st <<= 1)
-#pragma unroll
-                    for (int m = 0; m < 16; m += 2 * st) T[m] = T[m] + T[m + st];
                 const int row = (blockIdx.x + i * gridDim.x) * 64 + lane;
-                if (row < p.V) {
-                    p.logits[row] = T[0];
-                    if (better(T[0], row, best, besti)) { best = T[0]; besti = row; }
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    float T[16];
+#pragma unroll
+                    for (int kk = 0; kk < 16; ++kk) T[kk] = Tl[v][i & 1][kk][lane];
+#pragma unroll
+                    for (int st = 1; st < 16; st <<= 1)
+#pragma unroll
+                        for (int m = 0; m < 16; m += 2 * st) T[m] = T[m] + T[m + st];
+                    if (row < p.V) {
+                        p.logits[(size_t)v * p.V + row] = T[0];
+                        if (better(T[0], row, best[v], besti[v])) { best[v] = T[0]; besti[v] = row; }
+                    }
                 }
             }
         }
     };
+    auto half_groups = [&](const uint4 (&e)[HQ], int hg, float (&g)[NV]) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) g[v] = lm_half_group<NJ>(e, hp[v] + hg * 8 * NJ);
+    };
     int s = 0;
+    float g0[NV], g1[NV];
     for (; s < nseq - 2; s += 2) {
         load_hg(B, s + 1);
-        const float g0 = lm_half_group<NJ>(A, hp + (8 * w + (s & 7)) * 8 * NJ);
+        half_groups(A, 8 * w + (s & 7), g0);
         load_hg(A, s + 2);
-        const float g1 = lm_half_group<NJ>(B, hp + (8 * w + (s & 7) + 1) * 8 * NJ);
+        half_groups(B, 8 * w + (s & 7) + 1, g1);
         finish_pair(g0, g1, s);
     }
     if (nseq > 0) {   // last pair: nothing left to prefetch
         load_hg(B, s + 1);
-        const float g0 = lm_half_group<NJ>(A, hp + (8 * w + (s & 7)) * 8 * NJ);
-        const float g1 = lm_half_group<NJ>(B, hp + (8 * w + (s & 7) + 1) * 8 * NJ);
+        half_groups(A, 8 * w + (s & 7), g0);
+        half_groups(B, 8 * w + (s & 7) + 1, g1);
         finish_pair(g0, g1, s);
     }
 
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(besti, o, 64);
-        if (better(ov, oi, best, besti)) { best = ov; besti = oi; }
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best[v], o, 64);
+            const int oi = __shfl_xor(besti[v], o, 64);
+            if (better(ov, oi, best[v], besti[v])) { best[v] = ov; besti[v] = oi; }
+        }
+        if (lane == 0) { bval[v][w] = best[v]; bidx[v][w] = besti[v]; }
     }
-    if (lane == 0) { bval[w] = best; bidx[w] = besti; }
     __syncthreads();
     if (tid != 0) return;
-    float bv = bval[0];
-    int bi = bidx[0];
-    for (int k = 1; k < 4; ++k)
-        if (better(bval[k], bidx[k], bv, bi)) { bv = bval[k]; bi = bidx[k]; }
-    int *st = p.state;
-    unsigned long long *key = (unsigned long long *)(st + OXB_ST_LM_KEY);
-    const unsigned long long old =
-        __hip_atomic_fetch_max(key, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("" ::"v"((uint32_t)old));   // wait for the max before the ticket
-    const int ticket = __hip_atomic_fetch_add(&st[OXB_ST_LM_COUNTER], 1, __ATOMIC_RELAXED,
+    uint32_t sink = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        float bv = bval[v][0];
+        int bi = bidx[v][0];
+        for (int k = 1; k < 4; ++k)
+            if (better(bval[v][k], bidx[v][k], bv, bi)) { bv = bval[v][k]; bi = bidx[v][k]; }
+        unsigned long long *key =
+            (unsigned long long *)(p.state + (size_t)v * p.state_stride + OXB_ST_LM_KEY);
+        sink |= (uint32_t)__hip_atomic_fetch_max(key, argmax_key(bv, bi), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("" ::"v"(sink));   // wait for the maxima before the ticket
+    const int ticket = __hip_atomic_fetch_add(&p.state[OXB_ST_LM_COUNTER], 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
     if (ticket != (int)gridDim.x - 1) return;
-    const unsigned long long k =
-        __hip_atomic_fetch_or(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int tok = (int)(0xffffffffu - (uint32_t)k);
-    st[OXB_ST_TOKEN] = tok;
-    if (p.tok_hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) p.tok_hist[st[OXB_ST_NGEN]] = tok;
-    st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
-    st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
-    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&st[OXB_ST_LM_COUNTER], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        int *st = p.state + (size_t)v * p.state_stride;
+        unsigned long long *key = (unsigned long long *)(st + OXB_ST_LM_KEY);
+        const unsigned long long k =
+            __hip_atomic_fetch_or(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int tok = (int)(0xffffffffu - (uint32_t)k);
+        int *hist = p.tok_hist ? p.tok_hist + (size_t)v * p.hist_stride : nullptr;
+        st[OXB_ST_TOKEN] = tok;
+        if (hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) hist[st[OXB_ST_NGEN]] = tok;
+        st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
+        st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
+        __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __hip_atomic_store(&p.state[OXB_ST_LM_COUNTER], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x[t][d] = E[id_t][d] (f16 -> f32); ids out of range give zeros.
 // ids == nullptr: the single id is the decode state's current token.
 __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t *__restrict__ E, int V,
                                                         int D, const int *__restrict__ ids,
+                                                        int ids_stride,
                                                         const int *__restrict__ state,
                                                         float *__restrict__ x) {
     const int t = blockIdx.x;
-    const int id = ids ? ids[t] : state[OXB_ST_TOKEN];
+    const int id = ids ? ids[(size_t)t * ids_stride] : state[OXB_ST_TOKEN];
     for (int d = threadIdx.x; d < D; d += 256)
         x[(size_t)t * D + d] =
             (id >= 0 && id < V) ? __half2float(__ushort_as_half(E[(size_t)id * D + d])) : 0.0f;
@@ -276,29 +308,55 @@ __global__ void repack_tiled_kernel(const uint4 *__restrict__ src, uint4 *__rest
 
 using namespace oxb;
 
-extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
-                                  const void *E, int V, int D, float *logits, int *state,
-                                  int *tok_hist, int advance, void *stream) {
-    OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512,
-                "lm_head: hidden %d must be a multiple of 512 and <= 2560", D);
-    OXB_REQUIRE(V > 0, "lm_head: vocab %d", V);
-    OXB_REQUIRE(((uintptr_t)state & 7) == 0, "lm_head: state must be 8-byte aligned");
-    LmParams p{x, gamma, eps, (const uint4 *)E, V, D, logits, state, tok_hist, advance};
-    // 4 tiles per workgroup: ~2 workgroups per CU for a 128k vocabulary
-    const int grid = ((V + 63) / 64 + 3) / 4;
-    hipStream_t s = (hipStream_t)stream;
-    switch (D / 512) {
-#define OXB_NL(n)                                                                   \
-    case n:                                                                         \
-        hipLaunchKernelGGL(lm_head_kernel<n>, dim3(grid), dim3(256), 0, s, p);      \
+template <int NV>
+static int lm_launch(const LmParams &p, hipStream_t s) {
+    const int grid = ((p.V + 63) / 64 + 3) / 4;   // 4 tiles per workgroup
+    switch (p.D / 512) {
+#define OXB_NL(n)                                                                      \
+    case n:                                                                            \
+        hipLaunchKernelGGL((lm_head_kernel<n, NV>), dim3(grid), dim3(256), 0, s, p);   \
         break;
         OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5)
 #undef OXB_NL
         default:
-            oxb::set_error("lm_head: hidden %d unsupported (512 .. 2560)", D);
+            oxb::set_error("lm_head: hidden %d unsupported (512 .. 2560)", p.D);
             return -1;
     }
     OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+extern "C" int oxb_lm_head_argmax(const float *x, const float *gamma, float eps,
+                                  const void *E, int V, int D, float *logits, int *state,
+                                  int *tok_hist, int advance, void *stream) {
+    return oxb_lm_head_argmax_batch(x, (size_t)D, gamma, eps, E, V, D, logits, state,
+                                    OXB_STATE_INTS, tok_hist, 0, 1, advance, stream);
+}
+
+extern "C" int oxb_lm_head_argmax_batch(const float *x, size_t x_stride, const float *gamma,
+                                        float eps, const void *E, int V, int D, float *logits,
+                                        int *state, int state_stride, int *tok_hist,
+                                        int hist_stride, int n_rows, int advance, void *stream) {
+    OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512,
+                "lm_head: hidden %d must be a multiple of 512 and <= 2560", D);
+    OXB_REQUIRE(V > 0, "lm_head: vocab %d", V);
+    OXB_REQUIRE(n_rows > 0, "lm_head: %d rows", n_rows);
+    OXB_REQUIRE(((uintptr_t)state & 7) == 0 && state_stride % 2 == 0 &&
+                    (n_rows == 1 || state_stride >= OXB_STATE_INTS),
+                "lm_head: state blocks must be 8-byte aligned and not overlap");
+    hipStream_t s = (hipStream_t)stream;
+    // rows in groups of 4 (one pass over the table each), then 2, then 1
+    for (int r0 = 0; r0 < n_rows;) {
+        const int left = n_rows - r0;
+        const int nv = left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        LmParams p{x + (size_t)r0 * x_stride, gamma, eps, (const uint4 *)E, V, D,
+                   logits + (size_t)r0 * V, state + (size_t)r0 * state_stride,
+                   tok_hist ? tok_hist + (size_t)r0 * hist_stride : nullptr, advance,
+                   x_stride, state_stride, hist_stride};
+        const int rc = nv == 4 ? lm_launch<4>(p, s) : nv == 2 ? lm_launch<2>(p, s) : lm_launch<1>(p, s);
+        if (rc) return rc;
+        r0 += nv;
+    }
     return 0;
 }
 
@@ -316,10 +374,23 @@ extern "C" int oxb_embedding(const uint16_t *E, int V, int D, const int *ids, in
                              const int *state, float *x, void *stream) {
     OXB_REQUIRE(n_tok > 0 && D > 0, "embedding: bad shape");
     hipLaunchKernelGGL(embedding_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, E, V, D,
-                       ids, state, x);
+                       ids, 1, state, x);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
+
+namespace oxb {
+// Rows t = 0..n_tok-1 from ids[t * ids_stride] (e.g. the token fields of a
+// batch's state blocks).
+int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
+                      float *x, void *stream) {
+    OXB_REQUIRE(n_tok > 0 && D > 0 && ids, "embedding: bad shape");
+    hipLaunchKernelGGL(embedding_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, E, V, D,
+                       ids, ids_stride, nullptr, x);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+}  // namespace oxb
 
 extern "C" int oxb_repack_i2s_tiled(const void *natural, void *tiled, int N, int K,
                                     void *stream) {

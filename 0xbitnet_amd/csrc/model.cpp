@@ -551,22 +551,23 @@ int oxb_model::ensure_prefill(int n) {
 
 // Prefill n tokens (nn/model.rs:193-266 with n > 1): per-row norm+quantize,
 // MFMA GEMMs with fused epilogues, causal attention, then the LM head on the
-// last row (advance = n).
-int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
+// last row (advance = n).  The target names the sequence's caches, RoPE
+// table, state block and position (the model's own, or a batch slot's).
+int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg) {
     if (ensure_prefill(n)) return -1;
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
-    if (oxb_embedding(embed, V, D, pids, n, state, px, s)) return -1;
-    const size_t kv_layer = (size_t)Hkv * max_seq * hd;
+    if (oxb_embedding(embed, V, D, pids, n, tg.state, px, s)) return -1;
+    const size_t kv_layer = (size_t)Hkv * tg.max_seq * hd;
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];
-        uint16_t *kc = kcache + l * kv_layer, *vc = vcache + l * kv_layer;
+        uint16_t *kc = tg.kcache + l * kv_layer, *vc = tg.vcache + l * kv_layer;
         if (oxb_quantize_rows_tiled(px, L.attn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
-        if (oxb_gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n, pos,
-                         pq, kc, vc, max_seq, rope, s))
+        if (oxb_gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n,
+                         tg.pos, pq, kc, vc, tg.max_seq, tg.rope, s))
             return -1;
-        if (oxb_attn_prefill(pq, kc, vc, n, pos, H, Hkv, hd, max_seq, pattn, s)) return -1;
+        if (oxb_attn_prefill(pq, kc, vc, n, tg.pos, H, Hkv, hd, tg.max_seq, pattn, s)) return -1;
         if (oxb_quantize_rows_tiled(pattn, L.attn_sub, 1e-5f, n, Dq, pX, pscale, psum, s)) return -1;
         if (oxb_gemm_i8(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1, s))
             return -1;
@@ -582,7 +583,11 @@ int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
             return -1;
     }
     return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed_lm, V, D, logits,
-                              state, tok_hist, n, s);
+                              tg.state, tg.tok_hist, n, s);
+}
+
+int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
+    return enqueue_prefill_to(ids, n, SeqTarget{kcache, vcache, max_seq, rope, state, tok_hist, pos});
 }
 
 // ---------------------------------------------------------------------------

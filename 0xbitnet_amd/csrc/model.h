@@ -60,6 +60,16 @@ struct oxb_model {
     void *dalloc(size_t bytes);
     int enqueue_decode_step(bool fused_attn);
     int ensure_prefill(int n);
+    // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state
+    // block, token history and position
+    struct SeqTarget {
+        uint16_t *kcache, *vcache;
+        int max_seq;
+        const float *rope;
+        int *state, *tok_hist;
+        int pos;
+    };
+    int enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &t);
     int enqueue_prefill(const int32_t *ids, int n);
     int capture_graph(bool fused_attn);
     // the graph for a step whose token sits at position p (captured on first use)

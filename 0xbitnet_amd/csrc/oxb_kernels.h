@@ -4,3 +4,20 @@
 
 extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float eps, int n_tok,
                                        int D, void *Xt, float *scales, int *sums, void *stream);
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace oxb {
+// Batched-decode helpers (rows are independent single-token steps).
+int gemm_rows(const void *W, const int8_t *X, const float *xscale, const int *xsum,
+              const float *wscale, int N, int K, int n_tok, float *Y, int epilogue,
+              bool gemv_order, void *stream);
+int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int *xsum,
+                  const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok,
+                  const int *tok_pos, int tok_pos_stride, size_t kv_tok_stride, float *q_out,
+                  uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
+                  bool gemv_order, void *stream);
+int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
+                      float *x, void *stream);
+}  // namespace oxb

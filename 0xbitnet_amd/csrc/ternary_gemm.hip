@@ -45,7 +45,11 @@ struct GemmParams {
     // optional: token t is at position tok_pos[t] of its own cache, which
     // starts kv_tok_stride elements after token t-1's (batched decode)
     const int *tok_pos;
+    int tok_pos_stride;    // ints between consecutive tokens' positions
     size_t kv_tok_stride;
+    // 1: one-token GEMV rounding (f32(acc) * ws) * is (sh/ternary_gemv.wgsl:94-95),
+    // for rows that are independent single-token steps (batched decode)
+    int gemv_order;
 };
 
 __device__ inline v4i plane(uint4 w, int g) {
@@ -74,9 +78,14 @@ __device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int 
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         a[v] = c[v] - xs;
-        // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
-        const float sc = p.wscale[n0 + v] * is;
-        y[v] = (float)a[v] * sc;
+        if (p.gemv_order) {
+            y[v] = (float)a[v] * p.wscale[n0 + v];
+            y[v] = y[v] * is;
+        } else {
+            // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
+            const float sc = p.wscale[n0 + v] * is;
+            y[v] = (float)a[v] * sc;
+        }
     }
     if (p.acc_out) *(int4 *)(p.acc_out + (size_t)t * p.N + n0) = make_int4(a[0], a[1], a[2], a[3]);
     if constexpr (EPI == GE_STORE) {
@@ -92,7 +101,7 @@ __device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int 
         g1 = g1 * g1;
         *(float2 *)(p.Y + (size_t)t * (p.N >> 1) + (n0 >> 1)) = make_float2(g0 * y[1], g1 * y[3]);
     } else {  // GE_QKV
-        const int pos = p.tok_pos ? p.tok_pos[t] : p.pos0 + t;
+        const int pos = p.tok_pos ? p.tok_pos[(size_t)t * p.tok_pos_stride] : p.pos0 + t;
         if (pos < 0 || pos >= p.max_seq) return;   // host checks too; never write out of range
         const int Dk = p.Dq + p.Dkv;
         float o[4] = {y[0], y[1], y[2], y[3]};
@@ -372,3 +381,62 @@ extern "C" int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *x
     p.pos0 = pos0;
     return gemm_launch<GE_QKV>(p, stream);
 }
+
+namespace oxb {
+
+int gemm_rows(const void *W, const int8_t *X, const float *xscale, const int *xsum,
+              const float *wscale, int N, int K, int n_tok, float *Y, int epilogue,
+              bool gemv_order, void *stream) {
+    if (gemm_check(N, K, n_tok)) return -1;
+    GemmParams p{};
+    p.W = (const uint4 *)W;
+    p.X = (const uint4 *)X;
+    p.xscale = xscale;
+    p.xsum = xsum;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.n_tok = n_tok;
+    p.Y = Y;
+    p.gemv_order = gemv_order ? 1 : 0;
+    switch (epilogue) {
+        case GE_STORE: return gemm_launch<GE_STORE>(p, stream);
+        case GE_RESID: return gemm_launch<GE_RESID>(p, stream);
+        case GE_GATEUP: return gemm_launch<GE_GATEUP>(p, stream);
+        default: set_error("ternary GEMM: epilogue %d unsupported here", epilogue); return -1;
+    }
+}
+
+int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int *xsum,
+                  const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok,
+                  const int *tok_pos, int tok_pos_stride, size_t kv_tok_stride, float *q_out,
+                  uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
+                  bool gemv_order, void *stream) {
+    const int N = Dq + 2 * Dkv;
+    if (gemm_check(N, K, n_tok)) return -1;
+    OXB_REQUIRE(Dq % 32 == 0 && Dkv % 32 == 0 && hd % 16 == 0, "gemm qkv: bad head split");
+    GemmParams p{};
+    p.W = (const uint4 *)W;
+    p.X = (const uint4 *)X;
+    p.xscale = xscale;
+    p.xsum = xsum;
+    p.wscale = wscale;
+    p.N = N;
+    p.K = K;
+    p.n_tok = n_tok;
+    p.q_out = q_out;
+    p.kcache = kcache;
+    p.vcache = vcache;
+    p.rope = (const float2 *)rope_cs;
+    p.Dq = Dq;
+    p.Dkv = Dkv;
+    p.hd = hd;
+    p.max_seq = max_seq;
+    p.tok_pos = tok_pos;
+    p.tok_pos_stride = tok_pos_stride;
+    p.kv_tok_stride = kv_tok_stride;
+    p.gemv_order = gemv_order ? 1 : 0;
+    return gemm_launch<GE_QKV>(p, stream);
+}
+
+}  // namespace oxb

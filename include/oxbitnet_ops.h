@@ -128,6 +128,13 @@ int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcac
                     const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
                     float *out, void *stream);
 
+/* Decode attention for a batch of independent sequences: sequence z uses
+ * q + z*H*128, caches kcache/vcache + z*kv_stride, position pos[z*pos_stride],
+ * scores + z*H*max_seq and out + z*H*128; each as oxb_attn_decode. */
+int oxb_attn_decode_batch(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                          const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
+                          int Hkv, int hd, int max_seq, float *scores, float *out, void *stream);
+
 /* The same decode attention as one kernel: one 1024-thread workgroup per KV
  * head computes scores, softmax and P.V in LDS (no scores buffer), same
  * result bits.  Faster for short caches (one CU per KV head streams the
@@ -164,6 +171,14 @@ size_t oxb_lm_bytes(int V, int D);
 int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const void *E_lm, int V,
                        int D, float *logits, int *state, int *tok_hist, int advance,
                        void *stream);
+/* The same for n_rows independent rows (x rows x_stride floats apart; row r
+ * uses the state block state + r*state_stride and history tok_hist +
+ * r*hist_stride; logits [n_rows][V]).  Rows share each pass over the table
+ * (4 per pass); each row's logits and token are those of the one-row call. */
+int oxb_lm_head_argmax_batch(const float *x, size_t x_stride, const float *gamma, float eps,
+                             const void *E_lm, int V, int D, float *logits, int *state,
+                             int state_stride, int *tok_hist, int hist_stride, int n_rows,
+                             int advance, void *stream);
 
 /* ---- model (ids level) ------------------------------------------------------
  * The ids-level seam the parity and benchmark harnesses drive: the
@@ -198,6 +213,23 @@ int oxb_model_position(const oxb_model *m);
 int oxb_model_set_token(oxb_model *m, int32_t tok);
 /* One decode step from the current token, logits to host (nullable). */
 int oxb_model_step(oxb_model *m, float *logits_host);
+
+/* ---- batched greedy decode (no counterpart in the reference) --------------
+ * B independent sequences (slots) on one loaded model, each with its own KV
+ * cache of max_seq positions; a step advances every slot by one token in one
+ * hipGraph replay.  Each slot's tokens and logits equal those of the
+ * one-sequence engine (oxb_model_forward / oxb_model_step) on its prompt. */
+typedef struct oxb_batch oxb_batch;
+oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq);
+void oxb_batch_free(oxb_batch *b);
+/* Prefill n >= 2 prompt tokens into a slot (appended at its position);
+ * returns the slot's greedy next token, -1 on error. */
+int oxb_batch_prefill(oxb_batch *b, int slot, const int32_t *ids, int n);
+/* n_steps greedy steps for all slots; tokens_out [batch][n_steps] (host). */
+int oxb_batch_decode_greedy(oxb_batch *b, int n_steps, int32_t *tokens_out);
+int oxb_batch_position(const oxb_batch *b, int slot);
+/* Logits of the last decode step, [batch][V] (host). */
+int oxb_batch_logits(const oxb_batch *b, float *logits_host);
 
 #ifdef __cplusplus
 }

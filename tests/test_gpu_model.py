@@ -192,3 +192,53 @@ def test_python_bitnet_api():
     assert repr(bn) == "BitNet(disposed)"
     with pytest.raises(RuntimeError, match="disposed"):
         bn.generate("x", print)
+
+
+@pytest.mark.parametrize("B", [1, 3, 5, 17])
+def test_batched_decode_equals_single_sequences(B):
+    """Slots decoded together give each slot's one-sequence tokens and logits
+    bit for bit (B = 17: two token tiles in the GEMMs, LM head groups 4+1)."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    rng = np.random.default_rng(100 + B)
+    prompts = [rng.integers(0, cfg.vocab, int(rng.integers(2, 40))).astype(np.int32)
+               for _ in range(B)]
+    steps = 12
+    m = pkg.Model(path, max_seq=128)
+    ref_toks, ref_logits = [], []
+    for pr in prompts:
+        m.reset()
+        tok, _ = m.forward(pr, want_logits=False)
+        toks = [tok]
+        logits = None
+        for _ in range(steps):
+            tok, logits = m.step()
+            toks.append(tok)
+        ref_toks.append(toks)
+        ref_logits.append(logits)
+    b = pkg.Batch(m, B, 96)
+    first = [b.prefill(i, pr) for i, pr in enumerate(prompts)]
+    got = b.decode_greedy(steps)
+    last = b.logits()
+    for i in range(B):
+        assert [first[i]] + got[i].tolist() == ref_toks[i], f"slot {i}"
+        assert np.array_equal(last[i].view(np.uint32), ref_logits[i].view(np.uint32)), f"slot {i}"
+        assert b.position(i) == len(prompts[i]) + steps
+    with pytest.raises(pkg.NativeError, match="overflow"):
+        b.decode_greedy(200)
+    b.close()
+    m.close()
+
+
+def test_batch_rejects_unprefilled_slot():
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    m = pkg.Model(path, max_seq=64)
+    b = pkg.Batch(m, 2, 64)
+    b.prefill(0, np.array([1, 2, 3], np.int32))
+    with pytest.raises(pkg.NativeError, match="no prompt"):
+        b.decode_greedy(1)
+    with pytest.raises(pkg.NativeError, match=">= 2 tokens"):
+        b.prefill(1, np.array([5], np.int32))
+    b.close()
+    m.close()
