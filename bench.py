@@ -18,8 +18,8 @@ The JSON line also carries
                 both sweep shapes (TOPS, and GB/s of the algorithmic bytes);
   prefill_block the 512-token prefill block: RMSNorm + quantize, fused
                 gate|up GEMM with relu^2 * up, subln + requantize, down GEMM;
-  long_context  2048-token prefill, then bs=1 greedy decode up to 2560
-                cached positions;
+  long_context  2048-token prefill, then greedy decode up to 2560 cached
+                positions at batch 1, 8 and 32 (independent sequences);
   cpu_baseline  the CPU oracle (C restatement of the reference arithmetic,
                 OpenMP) decoding on the same model: a bounded sample of
                 steps after a short prompt.
@@ -220,29 +220,52 @@ def prefill_block(ops, synth, M: int = 512, iters: int = 20) -> dict:
                        "(subln), gemm down"}
 
 
-def long_context(pkg, synth, path: str, prompt_len: int = 2048, steps: int = 512) -> dict:
-    """2048-token prefill, then bs=1 greedy decode to 2560 cached positions."""
+def long_context(pkg, synth, path: str, prompt_len: int = 2048, steps: int = 512,
+                 batches=(1, 8, 32)) -> dict:
+    """2048-token prefill (per sequence), then greedy decode to 2560 cached
+    positions at batch 1 (one-sequence engine) and 8 / 32 (batched engine,
+    independent seeded prompts)."""
+    import importlib as _il
+    ops = _il.import_module("0xbitnet_amd.ops")
+    max_seq = prompt_len + steps + 8
+    m = pkg.Model(path, max_seq=max_seq)
     rng = np.random.default_rng(4096)
     prompt = rng.integers(0, synth.BITNET_2B.vocab, prompt_len).astype(np.int32)
-    m = pkg.Model(path, max_seq=prompt_len + steps + 8)
     m.forward(prompt[:64], want_logits=False)   # warm-up (graph capture, code paths)
     m.decode_greedy(4)
     m.reset()
-    import importlib as _il
-    ops = _il.import_module("0xbitnet_amd.ops")
     ops.sync()
     t0 = time.perf_counter()
     m.forward(prompt, want_logits=False)
     ops.sync()
     pf = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    m.decode_greedy(steps)
-    ops.sync()
-    dt = time.perf_counter() - t0
+    out = {"prompt_tokens": prompt_len, "decode_tokens": steps, "kv_positions_max": prompt_len + steps,
+           "prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(prompt_len / pf, 1)}
+    rows = []
+    for B in batches:
+        if B == 1:
+            t0 = time.perf_counter()
+            m.decode_greedy(steps)
+            ops.sync()
+            dt = time.perf_counter() - t0
+        else:
+            b = pkg.Batch(m, B, max_seq)
+            for i in range(B):
+                p_i = np.random.default_rng([4096, i]).integers(0, synth.BITNET_2B.vocab,
+                                                                 prompt_len).astype(np.int32)
+                b.prefill(i, p_i)
+            b.decode_greedy(2)                      # graph capture
+            t0 = time.perf_counter()
+            b.decode_greedy(steps - 2)
+            ops.sync()
+            dt = (time.perf_counter() - t0) * steps / (steps - 2)
+            b.close()
+        rows.append({"batch": B, "decode_tok_s": round(B * steps / dt, 1),
+                     "ms_per_step": round(dt * 1e3 / steps, 3)})
+        log(f"long context bs={B}: {B * steps / dt:.1f} tok/s ({dt * 1e3 / steps:.3f} ms/step)")
     m.close()
-    return {"prompt_tokens": prompt_len, "decode_tokens": steps, "batch": 1,
-            "prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(prompt_len / pf, 1),
-            "decode_tok_s": round(steps / dt, 2), "kv_positions_max": prompt_len + steps}
+    out["decode"] = rows
+    return out
 
 
 def calib_copy(ops, mib: int) -> None:
@@ -362,7 +385,7 @@ def main() -> int:
         log(f"prefill block M=512: {pb['ms']} ms {pb['TOPS']} TOPS")
         extra["prefill_block"] = pb
         lc = long_context(pkg, synth, path)
-        log(f"long context: prefill {lc['prefill_ms']} ms, decode {lc['decode_tok_s']} tok/s")
+        log(f"long context: prefill {lc['prefill_ms']} ms")
         extra["long_context"] = lc
 
     cpu = None
