@@ -129,9 +129,9 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 //     w + 4); one lane per position runs the 128-term chain; scores[h][s]
 //     to global.
 //  B  softmax + P.V: grid (Hkv, slices); each workgroup takes the G heads of
-//     one KV head and 64/G of the 128 dims, i.e. exactly one wave of 64
-//     sequential sums.  The other waves load the scores, run the softmax
-//     reductions and stage the V slice (as f32, transposed) in LDS, so the
+//     one KV head and a slice of the 128 dims: min(4, 2G) waves of 64
+//     sequential sums (lane = one (head, dim) output).  The softmax runs one
+//     wave per head, the V slice is staged (as f32, transposed) in LDS, so a
 //     summing wave reads 4 steps per LDS load.
 // ---------------------------------------------------------------------------
 constexpr int kScoreP = 64;   // positions per scores workgroup (one per lane)
@@ -271,6 +271,16 @@ __device__ inline void wave_softmax_row(float *row, const float *__restrict__ sr
     for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
 }
 
+// P.V work split: a wave covers the G heads x 64/G dims (one output per
+// lane).  Narrow: one summing wave per workgroup (the most workgroups, each
+// streaming the least V: best while the grid fits the chip).  Wide: min(4, 2G)
+// summing waves per workgroup (all 128 dims when G <= 2): 4x the chains per
+// CU once a batch oversubscribes the chip.
+__host__ __device__ constexpr int pv_dims_per_wave(int G) { return 64 / G; }
+__host__ __device__ constexpr int pv_waves(int G, bool wide) {
+    return !wide ? 1 : 2 * G < 4 ? 2 * G : 4;
+}
+
 // acc + sum_{s < n} p[s] * v[s], one product and one add at a time in order
 // of s.  The LDS operands of the next 16 positions are read while the
 // current 16 are summed (p and v 16-byte aligned).
@@ -328,7 +338,7 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     return acc;
 }
 
-template <int G>
+template <int G, bool WIDE>
 __global__ __launch_bounds__(256) void attn_pv_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
@@ -340,18 +350,20 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
         pos_ptr += (size_t)z * pos_stride;
         out += (size_t)z * H * kHd;
     }
-    constexpr int DW = 64 / G;               // dims per workgroup
-    constexpr int PPP = DW / 8;              // uint4 (8 f16) per position of the slice
-    constexpr int kVChunk = kVFloats / DW;   // positions staged per pass
-    constexpr int kVS = kVChunk + 4;         // padded row: the DW rows start in different banks
+    constexpr int DWW = pv_dims_per_wave(G);     // a wave: G heads x DWW dims, one per lane
+    constexpr int WPB = pv_waves(G, WIDE);       // summing waves per workgroup
+    constexpr int DWB = DWW * WPB;               // dims per workgroup
+    constexpr int PPP = DWB / 8;                 // uint4 (8 f16) per position of the slice
+    constexpr int kVChunk = kVFloats / DWB;      // positions staged per pass
+    constexpr int kVS = kVChunk + 4;             // padded row: the rows start in different banks
     constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
     extern __shared__ __align__(16) float pr[];   // [G][Spad] scores, then probabilities
-    __shared__ __align__(16) float vt[DW * kVS];  // V slice, [d][s] f32
+    __shared__ __align__(16) float vt[DWB * kVS];  // V slice, [d][s] f32
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
     const int Spad = (S + 3) & ~3;
-    const int hk = blockIdx.x, d0 = blockIdx.y * DW;
+    const int hk = blockIdx.x, d0 = blockIdx.y * DWB;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
 
@@ -372,8 +384,9 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     for (int g = w; g < G; g += 4)
         wave_softmax_row(pr + g * Spad, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane);
 
-    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s
-    const int g = lane / DW, dd = lane % DW;
+    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s;
+    // waves < WPB each run 64 such chains (heads lane / DWW, dims w*DWW + lane % DWW)
+    const int g = lane / DWW, dd = w * DWW + lane % DWW;
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += kVChunk) {
         const int n = min(kVChunk, S - c0);
@@ -391,9 +404,9 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
         }
         __syncthreads();
         if (c0 + kVChunk < S) load_chunk(c0 + kVChunk);
-        if (tid < 64) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc);
+        if (w < WPB) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc);
     }
-    if (tid < 64) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
+    if (w < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -593,14 +606,33 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     const size_t smem = (size_t)G * ((max_seq + 3) & ~3) * sizeof(float);
-    static size_t configured = 0;
-    if (smem > 32 * 1024 && smem > configured) {
-        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_pv_kernel<G>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        configured = smem;
+    // wide when the narrow grid exceeds ~2 workgroups per CU
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
     }
-    hipLaunchKernelGGL(attn_pv_kernel<G>, dim3(Hkv, G * kHd / 64, batch), dim3(256), smem, s,
-                       scores, vc, pos, max_seq, out, kv_stride, pos_stride);
+    const long narrow_blocks = (long)Hkv * (kHd / pv_dims_per_wave(G)) * batch;
+    const bool wide = narrow_blocks > 2L * cus;
+    static size_t configured[2] = {0, 0};
+    if (smem > 32 * 1024 && smem > configured[wide]) {
+        OXB_CHECK_HIP(hipFuncSetAttribute(
+            wide ? (const void *)attn_pv_kernel<G, true> : (const void *)attn_pv_kernel<G, false>,
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        configured[wide] = smem;
+    }
+    if (wide) {
+        constexpr int DWB = pv_dims_per_wave(G) * pv_waves(G, true);
+        hipLaunchKernelGGL((attn_pv_kernel<G, true>), dim3(Hkv, kHd / DWB, batch), dim3(256),
+                           smem, s, scores, vc, pos, max_seq, out, kv_stride, pos_stride);
+    } else {
+        constexpr int DWB = pv_dims_per_wave(G);
+        hipLaunchKernelGGL((attn_pv_kernel<G, false>), dim3(Hkv, kHd / DWB, batch), dim3(256),
+                           smem, s, scores, vc, pos, max_seq, out, kv_stride, pos_stride);
+    }
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }

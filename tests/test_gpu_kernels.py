@@ -232,6 +232,36 @@ def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
+                                       (9, 8, 8, 512)])
+def test_attn_decode_batch_bitexact(B, H, Hkv, S):
+    """Batched decode attention (per-slot caches and positions; B = 16 and 40
+    take the wide P.V layout): every slot equals the oracle."""
+    rng = np.random.default_rng(B * 13 + H)
+    hd = 128
+    q = rng.standard_normal((B, H * hd)).astype(np.float32)
+    kc = (rng.standard_normal((B, Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((B, Hkv, S, hd)).astype(np.float16)
+    pos = rng.integers(0, S, B).astype(np.int32)
+    pos[0] = S - 1
+    st = np.zeros((B, 8), np.int32)
+    st[:, 0] = pos
+    L = ops.lib()
+    dq = ops.DeviceArray.from_host(q)
+    dk = ops.DeviceArray.from_host(kc.view(np.uint16))
+    dv = ops.DeviceArray.from_host(vc.view(np.uint16))
+    dst = ops.DeviceArray.from_host(st)
+    sc = ops.DeviceArray((B * H * S,), np.float32)
+    out = ops.DeviceArray((B, H * hd), np.float32)
+    ops.check(L.oxb_attn_decode_batch(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H, Hkv,
+                                      hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
+    ops.sync()
+    got = out.download()
+    for z in range(B):
+        ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(pos[z]) + 1, H, Hkv, hd)
+        assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"slot {z}"
+
+
 def test_attn_decode_fused_rejects_unsupported():
     L = ops.lib()
     assert not L.oxb_attn_decode_fused_supported(32, 4, 128, 512)     # 8 heads per KV head
