@@ -75,6 +75,10 @@ SIGNATURES = {
     "oxb_event_record": (C.c_int, [vp, vp]),
     "oxb_event_sync": (C.c_int, [vp]),
     "oxb_event_elapsed_ms": (C.c_float, [vp, vp]),
+    "oxb_stream_begin_capture": (C.c_int, [vp]),
+    "oxb_stream_end_capture": (vp, [vp]),
+    "oxb_graph_launch": (C.c_int, [vp, vp]),
+    "oxb_graph_destroy": (C.c_int, [vp]),
     "oxb_device_info": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                   C.POINTER(C.c_size_t)]),
     # kernels

@@ -281,16 +281,17 @@ __host__ __device__ constexpr int pv_waves(int G, bool wide) {
     return !wide ? 1 : 2 * G < 4 ? 2 * G : 4;
 }
 
-// acc + sum_{s < n} p[s] * v[s], one product and one add at a time in order
-// of s.  The LDS operands of the next 16 positions are read while the
-// current 16 are summed (p and v 16-byte aligned).
-__device__ inline float pv_chain(const float *p, const float *v, int n, float acc) {
+// acc + sum_{s < n} p[s] * v[s ^ sw], one product and one add at a time in
+// order of s.  The LDS operands of the next 16 positions are read while the
+// current 16 are summed (p and v 16-byte aligned).  sw is a multiple of 4
+// (an XOR swizzle of the staged row that keeps groups of 4 positions whole).
+__device__ inline float pv_chain(const float *p, const float *v, int n, float acc, int sw = 0) {
     auto ld = [&](float4 (&P)[4], float4 (&V)[4], int at) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             P[j] = *(const float4 *)(p + at + 4 * j);
-            V[j] = *(const float4 *)(v + at + 4 * j);
+            V[j] = *(const float4 *)(v + ((at + 4 * j) ^ sw));
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -325,14 +326,14 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     }
     for (; s + 4 <= n; s += 4) {
         const float4 p4 = *(const float4 *)(p + s);
-        const float4 v4 = *(const float4 *)(v + s);
+        const float4 v4 = *(const float4 *)(v + (s ^ sw));
         float m0 = p4.x * v4.x; acc = acc + m0;
         float m1 = p4.y * v4.y; acc = acc + m1;
         float m2 = p4.z * v4.z; acc = acc + m2;
         float m3 = p4.w * v4.w; acc = acc + m3;
     }
     for (; s < n; ++s) {
-        float m = p[s] * v[s];
+        float m = p[s] * v[s ^ sw];
         acc = acc + m;
     }
     return acc;
@@ -356,6 +357,11 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     constexpr int PPP = DWB / 8;                 // uint4 (8 f16) per position of the slice
     constexpr int kVChunk = kVFloats / DWB;      // positions staged per pass
     constexpr int kVS = kVChunk + 4;             // padded row: the rows start in different banks
+    // Staging: a wave writes 64 / PPP positions x PPP uint4 of 8 dims; the
+    // dims 8h + e of one e share a bank for every h (8 kVS = 0 mod 32 banks),
+    // so position s of dim row d is stored at s ^ swz(d / 8): 2 lanes/bank.
+    auto swz = [](int h) { return PPP >= 8 ? 4 * (h & 7) : PPP == 4 ? 16 * (h & 3) : 0; };
+    static_assert(PPP != 4 || kVChunk >= 64, "swizzle stays inside the chunk");
     constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
     extern __shared__ __align__(16) float pr[];   // [G][Spad] scores, then probabilities
     __shared__ __align__(16) float vt[DWB * kVS];  // V slice, [d][s] f32
@@ -367,18 +373,19 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
 
-    // V slice of the first chunk: issued before anything else
-    uint4 r[kLoads];
-    auto load_chunk = [&](int c0) {
-        const int n = min(kVChunk, S - c0);
+    // V slices of the first two chunks, issued before anything else.  Rows
+    // past the cache length are clamped to its last row (staged, never read),
+    // so the loads stay branch-free and the waits exact.
+    auto load_chunk = [&](uint4 (&r)[kLoads], int c0) {
 #pragma unroll
         for (int k = 0; k < kLoads; ++k) {
             const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
-            r[k] = s < n ? *(const uint4 *)(Vh + (size_t)(c0 + s) * kHd + 8 * h)
-                         : make_uint4(0, 0, 0, 0);
+            r[k] = *(const uint4 *)(Vh + (size_t)min(c0 + s, S - 1) * kHd + 8 * h);
         }
     };
-    load_chunk(0);
+    uint4 ra[kLoads], rb[kLoads];
+    load_chunk(ra, 0);
+    load_chunk(rb, min(kVChunk, S - 1));
 
     // each wave owns heads w, w+4: load its score rows and run their softmax
     for (int g = w; g < G; g += 4)
@@ -394,17 +401,22 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
 #pragma unroll
         for (int k = 0; k < kLoads; ++k) {
             const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
-            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+            const uint32_t wv[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float2 f = __half22float2(*(const __half2 *)&wv[e]);
-                vt[(8 * h + 2 * e) * kVS + s] = f.x;
-                vt[(8 * h + 2 * e + 1) * kVS + s] = f.y;
+                const int ss = s ^ swz(h);
+                vt[(8 * h + 2 * e) * kVS + ss] = f.x;
+                vt[(8 * h + 2 * e + 1) * kVS + ss] = f.y;
             }
         }
         __syncthreads();
-        if (c0 + kVChunk < S) load_chunk(c0 + kVChunk);
-        if (w < WPB) acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc);
+        // two chunks in flight while this one is summed
+#pragma unroll
+        for (int k = 0; k < kLoads; ++k) ra[k] = rb[k];
+        load_chunk(rb, min(c0 + 2 * kVChunk, S - 1));
+        if (w < WPB)
+            acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc, swz(dd >> 3));
     }
     if (w < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }

@@ -129,6 +129,36 @@ extern "C" int oxb_event_sync(void *ev) {
     return 0;
 }
 
+extern "C" int oxb_stream_begin_capture(void *stream) {
+    OXB_REQUIRE(stream, "stream capture needs a created stream (not the null stream)");
+    OXB_CHECK_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+extern "C" void *oxb_stream_end_capture(void *stream) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (g) (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        set_error("stream capture: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    return (void *)ge;
+}
+
+extern "C" int oxb_graph_launch(void *graph, void *stream) {
+    OXB_REQUIRE(graph, "oxb_graph_launch: null graph");
+    OXB_CHECK_HIP(hipGraphLaunch((hipGraphExec_t)graph, (hipStream_t)stream));
+    return 0;
+}
+
+extern "C" int oxb_graph_destroy(void *graph) {
+    if (graph) OXB_CHECK_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return 0;
+}
+
 extern "C" float oxb_event_elapsed_ms(void *start, void *stop) {
     float ms = -1.0f;
     hipError_t e = hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop);

@@ -131,9 +131,9 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [TT][256].
-__host__ __device__ inline size_t gemv_smem(int K, int TT) {
-    return (size_t)K + (256 + 4 + 4 + 256 * TT) * 4;
+// LDS of the GEMV: xq [K] int8 | red [256] f32 | wmax [4] | wq [4] | wpart [TT][64 NW].
+__host__ __device__ inline size_t gemv_smem(int K, int TT, int NW = 4) {
+    return (size_t)K + (256 + 4 + 4 + 64 * NW * TT) * 4;
 }
 
 // x[t + 256 j], gamma[t + 256 j] for K == 256 * NREG (no clamps needed).
@@ -156,10 +156,15 @@ __device__ inline void load_row_exact(const float *__restrict__ x, const float *
 // EXACT: K == 256 * NREG.  TT: 16-row tiles per workgroup (> 1 amortises the
 // prologue over more rows when the grid would otherwise oversubscribe the
 // CUs, e.g. the 13824-row gate|up GEMV); each chunk's activations are read
-// from LDS once for all TT tiles.
-template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT>
-__global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
-    static_assert(TT == 1 || PF != 4, "multi-batch streaming is single-tile");
+// from LDS once for all TT tiles.  NW: waves per workgroup, each taking 1/NW
+// of K.  STREAM: double-buffered batches of PF chunks (else one batch covers
+// a lane's chunks).  Long int8 rows (e.g. K = 28672) stream best with 8 waves
+// and 1-chunk batches: 16 waves per CU keep more loads in flight than 4-chunk
+// batches of 4 waves, at under half the registers.
+template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT, int NW = 4, bool STREAM = PF == 4>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvParams p) {
+    static_assert(TT == 1 || !STREAM, "multi-batch streaming is single-tile");
+    static_assert(NW == 4 || (PRO == PRO_INT8 && NW == 8), "the norm prologue runs on 256 threads");
     extern __shared__ __align__(16) int8_t smem[];
     const int K = p.K;
     int8_t *xq_lds = smem;
@@ -172,10 +177,10 @@ __global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvPar
     const int lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, c = lane >> 4;
     const int KC = K >> 6;
-    const int per = (((KC + 3) >> 2) + 1) & ~1;   // chunks per wave: whole 128-blocks
+    const int per = (((KC + NW - 1) / NW) + 1) & ~1;   // chunks per wave: whole 128-blocks
     const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
     const int cpl = (per + 3) >> 2;               // chunks per lane
-    const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless PF == 4)
+    const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless STREAM)
     const int tile0 = blockIdx.x * TT;
 
     // ---- loads: prologue inputs, then the residual, then the weights -------
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvPar
     float in_scale;
     int xsum = 0;
     if constexpr (PRO == PRO_INT8) {
-        for (int i = tid; i < (K >> 4); i += 256)
+        for (int i = tid; i < (K >> 4); i += 64 * NW)
             ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
         in_scale = p.xscale[0];
         xsum = p.xsum[0];
@@ -282,7 +287,7 @@ __global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvPar
             }
         }
     };
-    if constexpr (PF != 4) {   // the launcher picks PF != 4 only when one batch covers the range
+    if constexpr (!STREAM) {   // the launcher picks one batch only when it covers the range
         mac_batch(A, 0);
     } else {
         int b = 0;
@@ -301,14 +306,14 @@ __global__ __launch_bounds__(256, PF * TT <= 3 ? 4 : 2) void gemv_kernel(GemvPar
         }
     }
 
-    // ---- reduction: 16 partials per row (4 lanes x 4 waves) through LDS ----
+    // ---- reduction: 4 NW partials per row (4 lanes x NW waves) through LDS --
 #pragma unroll
-    for (int t = 0; t < TT; ++t) wpart[t * 256 + tid] = acc[t].codes();
+    for (int t = 0; t < TT; ++t) wpart[t * 64 * NW + tid] = acc[t].codes();
     __syncthreads();
     if (tid >= 16 * TT) return;
     int a = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) a += wpart[(tid >> 4) * 256 + k * 16 + r];
+    for (int k = 0; k < 4 * NW; ++k) a += wpart[(tid >> 4) * 64 * NW + k * 16 + r];
     if constexpr (PRO == PRO_QUANT) xsum = wq[0] + wq[1] + wq[2] + wq[3];
     a -= xsum;
     const int n = tile0 * 16 + tid;
@@ -420,27 +425,27 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT = 1>
+template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT = 1, int NW = 4, bool STREAM = PF == 4>
 static int launch_n(const GemvParams &p, hipStream_t s) {
-    const size_t sm = gemv_smem(p.K, TT);
+    const size_t sm = gemv_smem(p.K, TT, NW);
     if (sm > 64 * 1024) {
         static bool raised = false;   // per instantiation
         if (!raised) {
             OXB_CHECK_HIP(hipFuncSetAttribute(
-                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT>,
+                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT, NW, STREAM>,
                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT>), dim3(p.N / (16 * TT)),
-                       dim3(256), sm, s, p);
+    hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT, NW, STREAM>),
+                       dim3(p.N / (16 * TT)), dim3(64 * NW), sm, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
 // NREG = ceil(K/256) bucket for PRO_QUANT (EXACT when K == 256 * NREG), all of
 // a lane's weight chunks in one batch.  PRO_INT8: PF from the chunks per
-// lane, 4-chunk batches double-buffered when one batch does not cover them.
+// lane; past 3 chunks per lane, 8 waves stream 1-chunk batches double-buffered.
 // Grids over ~3 workgroups per CU take 4 tiles per workgroup.
 template <int PRO, int EPI>
 static int launch(const GemvParams &p, hipStream_t s) {
@@ -449,7 +454,7 @@ static int launch(const GemvParams &p, hipStream_t s) {
     if constexpr (PRO == PRO_INT8) {
         if (cpl <= 1) return launch_n<PRO, EPI, 1, 1, false>(p, s);
         if (cpl <= 3) return launch_n<PRO, EPI, 1, 3, false>(p, s);
-        return launch_n<PRO, EPI, 1, 4, false>(p, s);
+        return launch_n<PRO, EPI, 1, 1, false, 1, 8, true>(p, s);
     } else {
         if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1, false>(p, s);
         if (p.K == 2560) {

@@ -11,8 +11,9 @@ the timed region).  value = decode tokens / second.
 
 The JSON line also carries
   roofline      the ternary GEMV (int8 activations, 2-bit weights) at
-                N=8192 x K=28672, M=1, timed with HIP events over launches that
-                rotate 16 distinct weight copies (940 MB > the 256 MB MALL);
+                N=8192 x K=28672, M=1: 400 launches that rotate 16 distinct
+                weight copies (940 MB > the 256 MB MALL), captured as one
+                graph and timed with HIP events (median of 5 replays);
   gemv_sweep    the same for the other decode/sweep shapes;
   gemm_sweep    the ternary GEMM on int8 MFMA at M = 8 .. 4096 tokens for
                 both sweep shapes (TOPS, and GB/s of the algorithmic bytes);
@@ -66,8 +67,9 @@ def measured_traffic() -> int | None:
 
 def gemv_roofline(ops, synth, N: int, K: int, copies: int, iters: int) -> dict:
     """Average duration of the int8 ternary GEMV over `iters` launches that
-    rotate through `copies` distinct weight buffers, timed by HIP events on
-    the launch stream."""
+    rotate through `copies` distinct weight buffers, captured as one graph
+    (so the host's per-call cost does not set the rate) and timed by HIP
+    events on the launch stream; the median of 5 replays."""
     L = ops.lib()
     rng = np.random.default_rng([N, K])
     Wn = synth.random_i2s(rng, N, K)
@@ -87,13 +89,24 @@ def gemv_roofline(ops, synth, N: int, K: int, copies: int, iters: int) -> dict:
         ops.check(L.oxb_gemv_i8(Ws[i].ptr, dx.ptr, ds.ptr, dsum.ptr, dw.ptr, N, K, y.ptr, None,
                                 stream), "gemv")
     ops.check(L.oxb_stream_sync(stream))
-    ops.check(L.oxb_event_record(e0, stream))
+    ops.check(L.oxb_stream_begin_capture(stream), "capture")
     for i in range(iters):
         ops.check(L.oxb_gemv_i8(Ws[i % copies].ptr, dx.ptr, ds.ptr, dsum.ptr, dw.ptr, N, K, y.ptr,
                                 None, stream), "gemv")
-    ops.check(L.oxb_event_record(e1, stream))
-    ops.check(L.oxb_event_sync(e1))
-    ms = L.oxb_event_elapsed_ms(e0, e1) / iters
+    graph = L.oxb_stream_end_capture(stream)
+    if not graph:
+        ops.check(-1, "capture")
+    ops.check(L.oxb_graph_launch(graph, stream))   # warm-up replay
+    ops.check(L.oxb_stream_sync(stream))
+    reps = []
+    for _ in range(5):   # median of 5 replays (single replays vary by ~+-3%)
+        ops.check(L.oxb_event_record(e0, stream))
+        ops.check(L.oxb_graph_launch(graph, stream))
+        ops.check(L.oxb_event_record(e1, stream))
+        ops.check(L.oxb_event_sync(e1))
+        reps.append(L.oxb_event_elapsed_ms(e0, e1) / iters)
+    ms = float(np.median(reps))
+    L.oxb_graph_destroy(graph)
     L.oxb_event_destroy(e0)
     L.oxb_event_destroy(e1)
     L.oxb_stream_destroy(stream)
@@ -108,20 +121,40 @@ def gemv_roofline(ops, synth, N: int, K: int, copies: int, iters: int) -> dict:
 MFMA_I8_PEAK_TOPS = 5000.0
 
 
-def _timed(L, stream, fn, iters: int) -> float:
-    """Mean ms per call of fn(i) over iters launches on `stream` (HIP events)."""
+def _timed(L, stream, fn, iters: int, reps: int = 3) -> float:
+    """Mean ms per call of fn(i) over iters calls on `stream`: the calls are
+    captured as one graph (fn(0) runs once before, uncaptured), replayed
+    once to warm up, then timed with HIP events; the median of `reps`."""
     e0, e1 = L.oxb_event_create(), L.oxb_event_create()
     fn(0)
-    L.oxb_stream_sync(stream)
-    L.oxb_event_record(e0, stream)
+    ops_check = _native_check(L)
+    ops_check(L.oxb_stream_sync(stream))
+    ops_check(L.oxb_stream_begin_capture(stream))
     for i in range(iters):
         fn(i)
-    L.oxb_event_record(e1, stream)
-    L.oxb_event_sync(e1)
-    ms = L.oxb_event_elapsed_ms(e0, e1) / iters
+    graph = L.oxb_stream_end_capture(stream)
+    if not graph:
+        ops_check(-1)
+    ops_check(L.oxb_graph_launch(graph, stream))
+    ops_check(L.oxb_stream_sync(stream))
+    times = []
+    for _ in range(reps):
+        ops_check(L.oxb_event_record(e0, stream))
+        ops_check(L.oxb_graph_launch(graph, stream))
+        ops_check(L.oxb_event_record(e1, stream))
+        ops_check(L.oxb_event_sync(e1))
+        times.append(L.oxb_event_elapsed_ms(e0, e1) / iters)
+    L.oxb_graph_destroy(graph)
     L.oxb_event_destroy(e0)
     L.oxb_event_destroy(e1)
-    return ms
+    return float(np.median(times))
+
+
+def _native_check(L):
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(L.oxb_last_error().decode())
+    return check
 
 
 def _host_tiles(rng, M: int, K: int):

@@ -56,6 +56,13 @@ int oxb_event_destroy(void *ev);
 int oxb_event_record(void *ev, void *stream);
 int oxb_event_sync(void *ev);
 float oxb_event_elapsed_ms(void *start, void *stop);
+/* Stream capture: replay a fixed launch sequence as one graph (no host cost per
+ * launch).  end_capture returns the executable graph, NULL on error.  No
+ * counterpart in the reference (wgpu submits command buffers instead). */
+int oxb_stream_begin_capture(void *stream);
+void *oxb_stream_end_capture(void *stream);
+int oxb_graph_launch(void *graph, void *stream);
+int oxb_graph_destroy(void *graph);
 /* name (NUL-terminated, truncated to len), CU count, peak clock kHz, HBM bytes */
 int oxb_device_info(char *name, int len, int *cus, int *clock_khz, size_t *hbm_bytes);
 

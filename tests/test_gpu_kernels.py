@@ -30,7 +30,9 @@ def _gemv_case(N, K, seed):
     return Wn, q[0], float(s[0])
 
 
-@pytest.mark.parametrize("N,K", [(6912, 2560), (16, 128), (48, 384), (2560, 6912)])
+# K = 4224: 66 chunks of 64, a ragged split over 8 waves; K = 65536: the maximum
+@pytest.mark.parametrize("N,K", [(6912, 2560), (16, 128), (48, 384), (2560, 6912), (16, 4224),
+                                 (32, 65536)])
 def test_gemv_i8_bitexact(N, K):
     Wn, xq, xs = _gemv_case(N, K, seed=N + K)
     ws = np.full(N, _scale_config1(1), np.float32)
