@@ -208,6 +208,117 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 
 
 // ---------------------------------------------------------------------------
+// LDS-staged GEMM for n_tok > 64.  Workgroup tile: 32*FW features x 32*TW
+// tokens; 4 waves in a 2x2 grid, each FW x TW MFMA tiles of 16x16, so every
+// A operand (a weight plane) feeds TW MFMAs and every B operand FW.  K runs
+// in stages of 4 chunks (256 k), double-buffered in LDS; the weights stay
+// 2-bit in LDS and are unpacked into A operands in registers.
+//   W stage: [32FW rows][4 chunks] x 16 B; chunk c of row f at slot
+//            4f + (c ^ (f/4 % 4)): 16 lanes reading (row r, chunk q) and 16
+//            lanes writing (chunk c, row r) both hit 16 distinct bank groups.
+//   X stage: [32TW tokens][16 units] x 16 B, unit u = 4c + g (chunk c, plane
+//            g); unit u of token t at slot 16t + (u ^ (5t % 16)): readers
+//            (tokens r = 0..15, one unit) and writers (tokens r = 0..3 x 4
+//            planes) both hit 16 distinct bank groups.
+// Token tiles past the activation buffer are clamped to its last tile; their
+// accumulators are never stored.
+// ---------------------------------------------------------------------------
+template <int EPI, int FW, int TW>
+__global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
+    constexpr int FT = 32 * FW, TK = 32 * TW;      // features, tokens per workgroup
+    constexpr int WU = FT * 4, XU = TK * 16;       // 16-byte units per stage
+    constexpr int WPT = WU / 256, XPT = XU / 256;  // per thread
+    __shared__ uint4 sw[2][WU];
+    __shared__ uint4 sx[2][XU];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, q = lane >> 4;
+    const int KC = p.K >> 6, steps = KC >> 2;
+    const int ftile0 = blockIdx.x * (FT / 16), ttile0 = blockIdx.y * (TK / 16);
+    const int ntt = (p.n_tok + 15) >> 4;
+    const int wf = (w & 1) * FW, wt = (w >> 1) * TW;   // this wave's local tiles
+
+    // this thread's staging units: W unit tid + 256k is (local tile fi, chunk
+    // c, row rr); X unit tid + 256k is (local tile ti, chunk c, token rr, plane g)
+    uint4 rw[WPT], rx[XPT];
+    size_t wsrc[WPT], xsrc[XPT];   // global offsets of stage 0, in uint4
+    int wdst[WPT], xdst[XPT];      // LDS slots
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int i = tid + 256 * k, fi = i >> 6, c = (i >> 4) & 3, rr = i & 15;
+        const int f = (fi << 4) | rr;
+        wsrc[k] = ((size_t)(ftile0 + fi) * KC + c) * 16 + rr;
+        wdst[k] = 4 * f + (c ^ ((f >> 2) & 3));
+    }
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        const int i = tid + 256 * k, ti = i >> 8, c = (i >> 6) & 3, rr = (i >> 2) & 15, g = i & 3;
+        const int tt = min(ttile0 + ti, ntt - 1), t = (ti << 4) | rr, u = (c << 2) | g;
+        xsrc[k] = (((size_t)tt * KC + c) * 16 + rr) * 4 + g;
+        xdst[k] = 16 * t + (u ^ ((5 * t) & 15));
+    }
+    v4i acc[FW][TW];
+#pragma unroll
+    for (int i = 0; i < FW; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    // stage s of a unit is 4 chunks further: 64 uint4 of W, 256 of X
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) rw[k] = load_nt(p.W + wsrc[k]);
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) rx[k] = p.X[xsrc[k]];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) sw[0][wdst[k]] = rw[k];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) sx[0][xdst[k]] = rx[k];
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int b = s & 1;
+        // the next stage (the last iteration reloads its own: branch-free)
+        const int sn = min(s + 1, steps - 1);
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) rw[k] = load_nt(p.W + wsrc[k] + (size_t)sn * 64);
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) rx[k] = p.X[xsrc[k] + (size_t)sn * 256];
+        uint4 wu[FW];
+#pragma unroll
+        for (int i = 0; i < FW; ++i) {
+            const int f = (wf + i) * 16 + r;
+            wu[i] = sw[b][4 * f + (q ^ ((f >> 2) & 3))];
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i a[FW];
+#pragma unroll
+            for (int i = 0; i < FW; ++i) a[i] = plane(wu[i], g);
+#pragma unroll
+            for (int j = 0; j < TW; ++j) {
+                const int t = (wt + j) * 16 + r;
+                const v4i bx = as_v4i(sx[b][16 * t + (((q << 2) | g) ^ ((5 * t) & 15))]);
+#pragma unroll
+                for (int i = 0; i < FW; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bx, acc[i][j], 0, 0, 0);
+            }
+        }
+        // into the idle buffer: its last reads ended before the previous barrier
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) sw[b ^ 1][wdst[k]] = rw[k];
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) sx[b ^ 1][xdst[k]] = rx[k];
+        __syncthreads();
+    }
+
+    // epilogue: lane holds features 16 ftile + 4q + v of token 16 ttile + r
+#pragma unroll
+    for (int i = 0; i < FW; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j) {
+            const int t = (ttile0 + wt + j) * 16 + r;
+            if (t < p.n_tok) gemm_store<EPI>(p, acc[i][j], t, (ftile0 + wf + i) * 16 + 4 * q);
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM for n_tok <= 64 (batched decode, small-M sweeps): the GEMV's
 // decomposition with MFMA inside.  A workgroup owns TF 16-row feature tiles
 // and all TT = ceil(n_tok/16) token tiles; its 4 waves split K (in 4-chunk
@@ -308,9 +419,17 @@ static int skinny_launch(const GemmParams &p, hipStream_t s) {
     return 0;
 }
 
+template <int EPI, int FW, int TW>
+static int lds_launch(const GemmParams &p, hipStream_t s) {
+    dim3 grid(p.N / (32 * FW), (p.n_tok + 32 * TW - 1) / (32 * TW));
+    hipLaunchKernelGGL((gemm_lds_kernel<EPI, FW, TW>), grid, dim3(256), 0, s, p);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
 // n_tok <= 64: skinny kernel (2 feature tiles per workgroup once there are
 // 3+ token tiles and enough rows, to halve the activation re-reads); else
-// the 64x64 tiled kernel.
+// the LDS-staged kernel (the 64x64 register-tiled kernel for N % 64 != 0).
 template <int EPI>
 static int gemm_launch(const GemmParams &p, void *stream) {
     hipStream_t s = (hipStream_t)stream;
@@ -324,6 +443,14 @@ static int gemm_launch(const GemmParams &p, void *stream) {
             default: return two ? skinny_launch<EPI, 4, 2>(p, s) : skinny_launch<EPI, 4, 1>(p, s);
         }
     }
+    // LDS-staged tiles: the largest of 128x128, 128x64, 64x128, 64x64 whose
+    // grid still gives every CU a workgroup (N a multiple of the tile).
+    const int cus = 256;
+    auto blocks = [&](int ft, int tk) { return (long)(p.N / ft) * ((p.n_tok + tk - 1) / tk); };
+    if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 4, 4>(p, s);
+    if (p.N % 128 == 0 && blocks(128, 64) >= cus) return lds_launch<EPI, 4, 2>(p, s);
+    if (p.N % 64 == 0 && blocks(64, 128) >= cus) return lds_launch<EPI, 2, 4>(p, s);
+    if (p.N % 64 == 0) return lds_launch<EPI, 2, 2>(p, s);
     dim3 grid((p.N + 63) / 64, (p.n_tok + 63) / 64);
     hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());

@@ -286,8 +286,11 @@ def test_attn_prefill_causal_bitexact():
     assert np.array_equal(out, ref)
 
 
+# n > 64: the LDS-staged kernel at its four tile shapes -- 128x128 (8192, 1024),
+# 128x64 (6912, 512), 64x128 with a ragged last token tile (4032, 650), 64x64
+# (2560, 512) -- and the register-tiled kernel for N % 64 != 0 (32, 65)
 @pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
-                                   (32, 256, 65),
+                                   (32, 256, 65), (8192, 256, 1024), (4032, 256, 650),
                                    # n <= 64: the skinny kernel, 1..4 token tiles, 1 or 2
                                    # feature tiles per workgroup, uneven K splits over waves
                                    (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
@@ -309,9 +312,10 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
-def test_gemm_epilogues():
-    rng = np.random.default_rng(31)
-    K, F, n = 2560, 6912, 40
+@pytest.mark.parametrize("n", [40, 130])
+def test_gemm_epilogues(n):
+    rng = np.random.default_rng(31 + n)
+    K, F = 2560, 6912
     wg, wu = ternary(rng, F, K), ternary(rng, F, K)
     inter = np.empty((2 * F, K), np.int8)
     inter[0::2], inter[1::2] = wg, wu
