@@ -223,6 +223,60 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 // Token tiles past the activation buffer are clamped to its last tile; their
 // accumulators are never stored.
 // ---------------------------------------------------------------------------
+// Staging of one stage: this thread's WPT weight and XPT activation units
+// (global offsets of stage 0 in uint4; stage st is 64 uint4 of W and 256 of
+// X further) into registers, and from registers into its LDS slots.
+template <int WPT, int XPT>
+__device__ __forceinline__ void gemm_stage_load(u32x4_t (&rw)[WPT], u32x4_t (&rx)[XPT],
+                                                const uint4 *W, const uint4 *X,
+                                                const size_t (&wsrc)[WPT],
+                                                const size_t (&xsrc)[XPT], int st) {
+#pragma unroll
+    for (int k = 0; k < WPT; ++k)
+        rw[k] = __builtin_nontemporal_load((const u32x4_t *)(W + wsrc[k] + (size_t)st * 64));
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) rx[k] = *(const u32x4_t *)(X + xsrc[k] + (size_t)st * 256);
+}
+
+template <int WPT, int XPT>
+__device__ __forceinline__ void gemm_stage_store(const u32x4_t (&rw)[WPT],
+                                                 const u32x4_t (&rx)[XPT], uint4 *swb,
+                                                 uint4 *sxb, const int (&wdst)[WPT],
+                                                 const int (&xdst)[XPT]) {
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) *(u32x4_t *)(swb + wdst[k]) = rw[k];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) *(u32x4_t *)(sxb + xdst[k]) = rx[k];
+}
+
+// One LDS stage (4 chunks) of a wave's FW x TW tiles: per plane g, FW A
+// operands unpacked from the 2-bit weights and TW B operands, FW*TW MFMAs.
+// Slots follow the swizzles of gemm_lds_kernel's stage layouts.
+template <int FW, int TW>
+__device__ __forceinline__ void gemm_mma_stage(v4i (&acc)[FW][TW], const uint4 *swb,
+                                               const uint4 *sxb, int wf, int wt, int r, int q) {
+    uint4 wu[FW];
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+        const int f = (wf + i) * 16 + r;
+        wu[i] = swb[4 * f + (q ^ ((f >> 2) & 3))];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        v4i a[FW];
+#pragma unroll
+        for (int i = 0; i < FW; ++i) a[i] = plane(wu[i], g);
+#pragma unroll
+        for (int j = 0; j < TW; ++j) {
+            const int t = (wt + j) * 16 + r;
+            const v4i bv = as_v4i(sxb[16 * t + (((q << 2) | g) ^ ((5 * t) & 15))]);
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bv, acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
 template <int EPI, int FW, int TW>
 __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
     constexpr int FT = 32 * FW, TK = 32 * TW;      // features, tokens per workgroup
@@ -239,7 +293,6 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
 
     // this thread's staging units: W unit tid + 256k is (local tile fi, chunk
     // c, row rr); X unit tid + 256k is (local tile ti, chunk c, token rr, plane g)
-    uint4 rw[WPT], rx[XPT];
     size_t wsrc[WPT], xsrc[XPT];   // global offsets of stage 0, in uint4
     int wdst[WPT], xdst[XPT];      // LDS slots
 #pragma unroll
@@ -262,51 +315,29 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < TW; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-    // stage s of a unit is 4 chunks further: 64 uint4 of W, 256 of X
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) rw[k] = load_nt(p.W + wsrc[k]);
-#pragma unroll
-    for (int k = 0; k < XPT; ++k) rx[k] = p.X[xsrc[k]];
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) sw[0][wdst[k]] = rw[k];
-#pragma unroll
-    for (int k = 0; k < XPT; ++k) sx[0][xdst[k]] = rx[k];
+    // Two register sets hold stages s+1 and s+2 while stage s is multiplied,
+    // so each stage's loads have two stages of MFMA work to arrive.  Loads
+    // past the last stage reload the last one (branch-free; never stored).
+    u32x4_t aw[WPT], ax[XPT], bw[WPT], bx_[XPT];
+    const int last = steps - 1;
+    gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, 0);
+    gemm_stage_store(aw, ax, sw[0], sx[0], wdst, xdst);
+    gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(1, last));
     __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        const int b = s & 1;
-        // the next stage (the last iteration reloads its own: branch-free)
-        const int sn = min(s + 1, steps - 1);
-#pragma unroll
-        for (int k = 0; k < WPT; ++k) rw[k] = load_nt(p.W + wsrc[k] + (size_t)sn * 64);
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) rx[k] = p.X[xsrc[k] + (size_t)sn * 256];
-        uint4 wu[FW];
-#pragma unroll
-        for (int i = 0; i < FW; ++i) {
-            const int f = (wf + i) * 16 + r;
-            wu[i] = sw[b][4 * f + (q ^ ((f >> 2) & 3))];
-        }
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v4i a[FW];
-#pragma unroll
-            for (int i = 0; i < FW; ++i) a[i] = plane(wu[i], g);
-#pragma unroll
-            for (int j = 0; j < TW; ++j) {
-                const int t = (wt + j) * 16 + r;
-                const v4i bx = as_v4i(sx[b][16 * t + (((q << 2) | g) ^ ((5 * t) & 15))]);
-#pragma unroll
-                for (int i = 0; i < FW; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bx, acc[i][j], 0, 0, 0);
-            }
-        }
-        // into the idle buffer: its last reads ended before the previous barrier
-#pragma unroll
-        for (int k = 0; k < WPT; ++k) sw[b ^ 1][wdst[k]] = rw[k];
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) sx[b ^ 1][xdst[k]] = rx[k];
+    // iteration s: load stage s+2, multiply stage s (buffer s&1), store stage
+    // s+1 into the idle buffer (its last reads ended before the previous barrier)
+    int s = 0;
+    for (; s + 2 <= steps; s += 2) {
+        gemm_stage_load(bw, bx_, p.W, p.X, wsrc, xsrc, min(s + 2, last));
+        gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);
+        gemm_stage_store(aw, ax, sw[1], sx[1], wdst, xdst);
+        __syncthreads();
+        gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(s + 3, last));
+        gemm_mma_stage<FW, TW>(acc, sw[1], sx[1], wf, wt, r, q);
+        gemm_stage_store(bw, bx_, sw[0], sx[0], wdst, xdst);
         __syncthreads();
     }
+    if (s < steps) gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);   // odd count: buffer 0
 
     // epilogue: lane holds features 16 ftile + 4q + v of token 16 ttile + r
 #pragma unroll
