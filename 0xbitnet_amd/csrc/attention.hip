@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
     const int S = pos + 1;
     const float *qrow = q + (size_t)qi * H * kHd + (size_t)hk * G * kHd;
     for (int i = tid; i < G * kHd; i += 256) qs[i] = qrow[i];
-    __syncthreads();
+    lds_barrier();
 
     const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
     const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd;
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
 #pragma unroll
         for (int g = 0; g < G; ++g) sc[g * S + s] = dot[g] * scale;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- softmax per head, in the shader's order --------------------------
 #pragma unroll 1
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void attn_exact_kernel(
         const float inv = 1.0f / block256_tree_sum(part, red);
         for (int s = tid; s < S; s += 256) sc[g * S + s] = oxb_expf(sc[g * S + s] - m) * inv;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- P.V: G*128 sequential sums over s, NC per thread -----------------
     constexpr int NC = G * kHd > 256 ? G * kHd / 256 : 1;
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         const int i = tid + 256 * k;
         ks[i >> 4][i & 15] = kt[k];
     }
-    __syncthreads();
+    lds_barrier();
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
@@ -214,37 +214,82 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
 
 constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB, plus row padding)
 
+// The shaders' 256-thread halving tree s[t] += s[t + stride], stride
+// 128 .. 1, with s[4l + i] in component i of lane l: strides 128 .. 4 pair
+// lanes 32 .. 1 apart (shuffles, then DPP row_shl), strides 2 and 1 pair
+// components in lane 0.  Returns s[0] to every lane.
+__device__ inline float tree256_sum4(const float (&c)[4]) {
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = c[i];
+        v = v + __shfl_down(v, 32, 64);
+        v = v + __shfl_down(v, 16, 64);
+        v = v + __int_as_float(dpp0<0x108, 0xf>(__float_as_int(v)));
+        v = v + __int_as_float(dpp0<0x104, 0xf>(__float_as_int(v)));
+        v = v + __int_as_float(dpp0<0x102, 0xf>(__float_as_int(v)));
+        v = v + __int_as_float(dpp0<0x101, 0xf>(__float_as_int(v)));
+        a[i] = v;
+    }
+    const float r = (a[0] + a[2]) + (a[1] + a[3]);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+}
+
+// Softmax of one score row held in registers: NJ groups of 256 positions,
+// lane l component i holding thread t = 4l + i's positions 256j + 4l + i.
+// Branch-free (loads clamped to the row, selects instead of guards) so all
+// NJ*4 loads are in flight at once and the waits stay exact.
+template <int NJ>
+__device__ __forceinline__ void softmax_row_regs(float *row, const float *__restrict__ src, int S,
+                                                 int Spad, int lane) {
+    float x[NJ][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[j][i] = src[min(256 * j + 4 * lane + i, S - 1)];
+    float m = -3.402823e+38f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, x[j][i]);   // clamped copies repeat s = S-1
+    m = wave_max_dpp(m);
+    float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = oxb_expf(x[j][i] - m);
+            x[j][i] = 256 * j + 4 * lane + i < S ? e : 0.0f;
+            c[i] = c[i] + x[j][i];
+        }
+    const float inv = 1.0f / tree256_sum4(c);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int s0 = 256 * j + 4 * lane;   // Spad is a multiple of 4
+        if (s0 < Spad)
+            *(float4 *)(row + s0) =
+                make_float4(x[j][0] * inv, x[j][1] * inv, x[j][2] * inv, x[j][3] * inv);
+    }
+}
+
 // Softmax of one score row (global src, S values) by one wave into the LDS
 // row, in the order of sh/softmax.wgsl:25-80 for a 256-thread workgroup:
-// lane l plays threads l, l+64, l+128, l+192, each summing its strided
-// positions in order (out-of-range positions add an exact +0); the tree's
-// first two levels pair those four in the lane, wave_tree_sum does the rest.
-// exp(x - max) is evaluated once: the shader's normalisation pass evaluates
-// it again with the same operands.  The max is exact in any order.
-// Rows of up to 512 positions stay in registers; longer rows go through LDS.
-__device__ inline void wave_softmax_row(float *row, const float *__restrict__ src, int S,
+// thread t sums exp(x - max) over positions t, t + 256, ... in order (out-of-
+// range positions add an exact +0), then the halving tree.  Up to 4096
+// positions the row is held in registers (softmax_row_regs); longer rows are
+// staged through LDS.  exp(x - max) is evaluated once: the shader's
+// normalisation pass evaluates it again with the same operands.  The max is
+// exact in any order.
+__device__ __forceinline__ void wave_softmax_row(float *row, const float *__restrict__ src, int S,
                                         int Spad, int lane) {
-    if (S <= 512) {
-        float x[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = src[min(lane + 64 * k, S - 1)];
-        float m = -3.402823e+38f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (lane + 64 * k < S) m = fmaxf(m, x[k]);
-        m = wave_max_dpp(m);
-        float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            x[k] = lane + 64 * k < S ? oxb_expf(x[k] - m) : 0.0f;
-            p[k & 3] = p[k & 3] + x[k];
-        }
-        const float inv = 1.0f / wave_tree_sum((p[0] + p[2]) + (p[1] + p[3]));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int s = lane + 64 * k;
-            if (s < Spad) row[s] = s < S ? x[k] * inv : 0.0f;
-        }
+    if (S <= 4096) {
+        const int nj = (S + 255) >> 8;
+        if (nj <= 1) softmax_row_regs<1>(row, src, S, Spad, lane);
+        else if (nj <= 2) softmax_row_regs<2>(row, src, S, Spad, lane);
+        else if (nj <= 4) softmax_row_regs<4>(row, src, S, Spad, lane);
+        else if (nj <= 8) softmax_row_regs<8>(row, src, S, Spad, lane);
+        else if (nj <= 12) softmax_row_regs<12>(row, src, S, Spad, lane);
+        else softmax_row_regs<16>(row, src, S, Spad, lane);
         return;
     }
     for (int base = 0; base < S; base += 512) {   // stage the row, 8 loads in flight
@@ -397,7 +442,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += kVChunk) {
         const int n = min(kVChunk, S - c0);
-        __syncthreads();  // probabilities ready / previous chunk consumed
+        lds_barrier();  // probabilities ready / previous chunk consumed
 #pragma unroll
         for (int k = 0; k < kLoads; ++k) {
             const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
@@ -410,7 +455,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
                 vt[(8 * h + 2 * e + 1) * kVS + ss] = f.y;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // two chunks in flight while this one is summed
 #pragma unroll
         for (int k = 0; k < kLoads; ++k) ra[k] = rb[k];
@@ -478,13 +523,13 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
     const int g = w >> 2, pg = w & 3;   // this wave's head and position group
     for (int c0 = 0; c0 < S; c0 += kFusedKC) {
-        if (c0) __syncthreads();        // the previous chunk's rows are consumed
+        if (c0) lds_barrier();        // the previous chunk's rows are consumed
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = tid + 1024 * k;
             ks[i >> 4][i & 15] = kt[k];
         }
-        __syncthreads();
+        lds_barrier();
         if (c0 + kFusedKC < S) load_k(kt, c0 + kFusedKC);
         const int s = c0 + pg * 64 + lane;
         if (g < G && s < S) {
@@ -520,7 +565,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
             sc[g * spad_max + s] = dot * scale;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- softmax: wave g < G owns head g's row ------------------------------
     if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane);
@@ -545,7 +590,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += kFusedVC) {
         const int n = min(kFusedVC, S - c0);
-        __syncthreads();   // softmax done / K rows or the previous V chunk consumed
+        lds_barrier();   // softmax done / K rows or the previous V chunk consumed
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
             float4 lo, hi;   // dims 2*lane and 2*lane + 1 at 4 positions
@@ -559,7 +604,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
             *(float4 *)(vt + (2 * lane) * kFusedVS + sr) = lo;
             *(float4 *)(vt + (2 * lane + 1) * kFusedVS + sr) = hi;
         }
-        __syncthreads();
+        lds_barrier();
         if (c0 + kFusedVC < S) load_v(vr, c0 + kFusedVC);
         if (go < G) acc = pv_chain(sc + go * spad_max + c0, vt + d * kFusedVS, n, acc);
     }
@@ -630,7 +675,7 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
     const long narrow_blocks = (long)Hkv * (kHd / pv_dims_per_wave(G)) * batch;
     const bool wide = narrow_blocks > 2L * cus;
     static size_t configured[2] = {0, 0};
-    if (smem > 32 * 1024 && smem > configured[wide]) {
+    if (smem > configured[wide]) {
         OXB_CHECK_HIP(hipFuncSetAttribute(
             wide ? (const void *)attn_pv_kernel<G, true> : (const void *)attn_pv_kernel<G, false>,
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));

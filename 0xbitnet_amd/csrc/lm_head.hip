@@ -56,13 +56,6 @@ __device__ inline bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-// Barrier that orders LDS only: a plain __syncthreads() would also wait for
-// the weight prefetch in flight.
-__device__ inline void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // 8 leaves (half of a 16-leaf group) of one row: 8*NJ pairs = 2*NJ uint4.
 // Each product is fma(h, e, +0): the same value as h*e except that a -0

@@ -70,26 +70,36 @@ __device__ inline uint4 load_nt(const uint4 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences
+// global memory, which makes every wave wait for all of its loads in flight
+// (weight or V prefetch for later stages) at each barrier; the kernels'
+// barriers only hand LDS data between waves.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // f32 workgroup sum in the shaders' tree order for a 256-thread block.
 // Every thread passes its strided partial; the result is returned to all.
 // red must hold >= 256 floats of LDS.
 __device__ inline float block256_tree_sum(float part, float *red) {
     const int t = threadIdx.x;
     red[t] = part;
-    __syncthreads();
+    lds_barrier();
     if (t < 128) red[t] = red[t] + red[t + 128];
-    __syncthreads();
+    lds_barrier();
     if (t < 64) red[t] = red[t] + red[t + 64];
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
         float v = red[t];
 #pragma unroll
         for (int s = 32; s > 0; s >>= 1) v = v + __shfl_down(v, s, 64);
         if (t == 0) red[0] = v;
     }
-    __syncthreads();
+    lds_barrier();
     float r = red[0];
-    __syncthreads();
+    lds_barrier();
     return r;
 }
 
@@ -98,9 +108,9 @@ __device__ inline float block256_max(float v, float *red) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
     if ((t & 63) == 0) red[t >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
+    lds_barrier();
     return r;
 }
 
@@ -109,9 +119,9 @@ __device__ inline int block256_isum(int v, int *red) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
     if ((t & 63) == 0) red[t >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     int r = red[0] + red[1] + red[2] + red[3];
-    __syncthreads();
+    lds_barrier();
     return r;
 }
 
@@ -152,9 +162,9 @@ __device__ inline float wave_nonneg_max_dpp(float f) {
 __device__ inline float block256_tree_sum_fast(float part, float *red) {
     const int t = threadIdx.x;
     red[t] = part;
-    __syncthreads();
+    lds_barrier();
     if (t < 64) red[256 + t] = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
-    __syncthreads();
+    lds_barrier();
     float a[64];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -179,7 +189,7 @@ __device__ inline float block256_tree_sum_fast(float part, float *red) {
 __device__ inline float block256_tree_sum_1b(float part, float *red) {
     const int t = threadIdx.x;
     red[t] = part;
-    __syncthreads();
+    lds_barrier();
     const int i = t & 15;
     float u[4];
 #pragma unroll

@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
     gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, 0);
     gemm_stage_store(aw, ax, sw[0], sx[0], wdst, xdst);
     gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(1, last));
-    __syncthreads();
+    lds_barrier();
     // iteration s: load stage s+2, multiply stage s (buffer s&1), store stage
     // s+1 into the idle buffer (its last reads ended before the previous barrier)
     int s = 0;
@@ -331,11 +331,11 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
         gemm_stage_load(bw, bx_, p.W, p.X, wsrc, xsrc, min(s + 2, last));
         gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);
         gemm_stage_store(aw, ax, sw[1], sx[1], wdst, xdst);
-        __syncthreads();
+        lds_barrier();
         gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(s + 3, last));
         gemm_mma_stage<FW, TW>(acc, sw[1], sx[1], wf, wt, r, q);
         gemm_stage_store(bw, bx_, sw[0], sx[0], wdst, xdst);
-        __syncthreads();
+        lds_barrier();
     }
     if (s < steps) gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);   // odd count: buffer 0
 
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
     for (int f = 0; f < TF; ++f)
 #pragma unroll
         for (int t = 0; t < TT; ++t) red[w][f * TT + t][lane] = acc[f][t];
-    __syncthreads();
+    lds_barrier();
     const int ntok = p.n_tok;
     for (int i = w; i < NT; i += 4) {
         v4i c = red[0][i][lane];

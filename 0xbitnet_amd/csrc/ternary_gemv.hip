@@ -108,7 +108,7 @@ __device__ inline float norm_quant_regs(float (&v)[NREG], const float (&g)[NREG]
     for (int j = 0; j < NREG; ++j) am = fmaxf(am, fabsf(v[j]));
     am = wave_nonneg_max_dpp(am);
     if ((t & 63) == 0) red[320 + (t >> 6)] = am;
-    __syncthreads();
+    lds_barrier();
     am = fmaxf(fmaxf(red[320], red[321]), fmaxf(red[322], red[323]));
     const float scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
     const float inv = am == 0.0f ? 0.0f : 127.0f / am;     // :68
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
         in_scale = p.xscale[0];
         xsum = p.xsum[0];
-        __syncthreads();
+        lds_barrier();
     } else {
         if constexpr (!EXACT) mask_row<NREG>(K, v, g);
         if (p.gamma) {
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
         for (int j = 0; j < NREG; ++j) am = fmaxf(am, fabsf(v[j]));
         am = wave_nonneg_max_dpp(am);
         if (lane == 0) wmax[w] = am;
-        __syncthreads();
+        lds_barrier();
         am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
         in_scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
         const float inv = am == 0.0f ? 0.0f : 127.0f / am;  // :68
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
                 if (EXACT || tid + 256 * j < K) p.xq_out[tid + 256 * j] = (int8_t)qv[j];
             if (tid == 0 && p.xscale_out) p.xscale_out[0] = in_scale;
         }
-        __syncthreads();   // the int8 vector is complete
+        lds_barrier();   // the int8 vector is complete
     }
 
     // ---- main loop: chunks past this wave's range multiply zero codes ------
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     // ---- reduction: 4 NW partials per row (4 lanes x NW waves) through LDS --
 #pragma unroll
     for (int t = 0; t < TT; ++t) wpart[t * 64 * NW + tid] = acc[t].codes();
-    __syncthreads();
+    lds_barrier();
     if (tid >= 16 * TT) return;
     int a = 0;
 #pragma unroll
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
     float v[kMaxNormReg], g[kMaxNormReg];
     load_row<kMaxNormReg>(x + (size_t)row * D, gamma, D, v, g);
     const float scale = norm_quant_regs<kMaxNormReg>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
-    __syncthreads();
+    lds_barrier();
     for (int i = threadIdx.x; i < (D >> 4); i += 256)
         ((int4 *)(xq + (size_t)row * D))[i] = ((const int4 *)q_lds)[i];
     if (threadIdx.x == 0) {
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
         for (int i = threadIdx.x; i < (D >> 4); i += 256) ((int4 *)q_lds)[i] = make_int4(0, 0, 0, 0);
         if (threadIdx.x < 4) wq[threadIdx.x] = 0;
     }
-    __syncthreads();
+    lds_barrier();
     const int KC = D >> 6, tile = row >> 4, c = row & 15;
     for (int i = threadIdx.x; i < KC * 4; i += 256) {
         const int kc = i >> 2, g = i & 3;
