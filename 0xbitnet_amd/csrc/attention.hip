@@ -239,19 +239,28 @@ __device__ inline float tree256_sum4(const float (&c)[4]) {
 // lane l component i holding thread t = 4l + i's positions 256j + 4l + i.
 // Branch-free (loads clamped to the row, selects instead of guards) so all
 // NJ*4 loads are in flight at once and the waits stay exact.
-template <int NJ>
+// VEC: src is 16-byte aligned, one float4 load per group (clamped to the last
+// whole float4 below Spad, which the row holds); else four clamped loads.
+template <int NJ, bool VEC>
 __device__ __forceinline__ void softmax_row_regs(float *row, const float *__restrict__ src, int S,
                                                  int Spad, int lane) {
     float x[NJ][4];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < NJ; ++j) {
+        if constexpr (VEC) {
+            const float4 v = *(const float4 *)(src + min(256 * j + 4 * lane, Spad - 4));
+            x[j][0] = v.x; x[j][1] = v.y; x[j][2] = v.z; x[j][3] = v.w;
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[j][i] = src[min(256 * j + 4 * lane + i, S - 1)];
+            for (int i = 0; i < 4; ++i) x[j][i] = src[min(256 * j + 4 * lane + i, S - 1)];
+        }
+    }
     float m = -3.402823e+38f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) m = fmaxf(m, x[j][i]);   // clamped copies repeat s = S-1
+        for (int i = 0; i < 4; ++i)
+            if (VEC ? 256 * j + 4 * lane + i < S : true) m = fmaxf(m, x[j][i]);   // clamped copies repeat s = S-1
     m = wave_max_dpp(m);
     float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -276,20 +285,29 @@ __device__ __forceinline__ void softmax_row_regs(float *row, const float *__rest
 // row, in the order of sh/softmax.wgsl:25-80 for a 256-thread workgroup:
 // thread t sums exp(x - max) over positions t, t + 256, ... in order (out-of-
 // range positions add an exact +0), then the halving tree.  Up to 4096
-// positions the row is held in registers (softmax_row_regs); longer rows are
-// staged through LDS.  exp(x - max) is evaluated once: the shader's
+// positions the row is held in registers (softmax_row_regs; vec: src is
+// 16-byte aligned and holds Spad values); longer rows are staged through LDS.  exp(x - max) is evaluated once: the shader's
 // normalisation pass evaluates it again with the same operands.  The max is
 // exact in any order.
 __device__ __forceinline__ void wave_softmax_row(float *row, const float *__restrict__ src, int S,
-                                        int Spad, int lane) {
+                                                 int Spad, int lane, bool vec) {
     if (S <= 4096) {
         const int nj = (S + 255) >> 8;
-        if (nj <= 1) softmax_row_regs<1>(row, src, S, Spad, lane);
-        else if (nj <= 2) softmax_row_regs<2>(row, src, S, Spad, lane);
-        else if (nj <= 4) softmax_row_regs<4>(row, src, S, Spad, lane);
-        else if (nj <= 8) softmax_row_regs<8>(row, src, S, Spad, lane);
-        else if (nj <= 12) softmax_row_regs<12>(row, src, S, Spad, lane);
-        else softmax_row_regs<16>(row, src, S, Spad, lane);
+        if (vec) {
+            if (nj <= 1) softmax_row_regs<1, true>(row, src, S, Spad, lane);
+            else if (nj <= 2) softmax_row_regs<2, true>(row, src, S, Spad, lane);
+            else if (nj <= 4) softmax_row_regs<4, true>(row, src, S, Spad, lane);
+            else if (nj <= 8) softmax_row_regs<8, true>(row, src, S, Spad, lane);
+            else if (nj <= 12) softmax_row_regs<12, true>(row, src, S, Spad, lane);
+            else softmax_row_regs<16, true>(row, src, S, Spad, lane);
+        } else {
+            if (nj <= 1) softmax_row_regs<1, false>(row, src, S, Spad, lane);
+            else if (nj <= 2) softmax_row_regs<2, false>(row, src, S, Spad, lane);
+            else if (nj <= 4) softmax_row_regs<4, false>(row, src, S, Spad, lane);
+            else if (nj <= 8) softmax_row_regs<8, false>(row, src, S, Spad, lane);
+            else if (nj <= 12) softmax_row_regs<12, false>(row, src, S, Spad, lane);
+            else softmax_row_regs<16, false>(row, src, S, Spad, lane);
+        }
         return;
     }
     for (int base = 0; base < S; base += 512) {   // stage the row, 8 loads in flight
@@ -434,7 +452,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
 
     // each wave owns heads w, w+4: load its score rows and run their softmax
     for (int g = w; g < G; g += 4)
-        wave_softmax_row(pr + g * Spad, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane);
+        wave_softmax_row(pr + g * Spad, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
+                         (max_seq & 3) == 0);
 
     // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s;
     // waves < WPB each run 64 such chains (heads lane / DWW, dims w*DWW + lane % DWW)
@@ -568,7 +587,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     lds_barrier();
 
     // ---- softmax: wave g < G owns head g's row ------------------------------
-    if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane);
+    if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane, true);
 
     // ---- P.V: lane = output (head go, dim d), waves < 2G ----------------------
     // Staging: wave w gathers positions 4w..4w+3 (+64 on the second pass) of

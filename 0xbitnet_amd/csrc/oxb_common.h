@@ -251,10 +251,10 @@ __device__ inline float wave_max(float v) {
 // Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2, so k*head is exact,
 // plus the tail), degree-7 Taylor polynomial of e^r by Horner, ldexp by k.
 // Every step is a separately rounded f32 op (no contraction); ~2 ulp.
+// Branch-free: the polynomial path runs for every x and the special cases
+// are selected afterwards (NaN last), which gives the same value as testing
+// them first and lets many independent exps interleave.
 __device__ inline float oxb_expf(float x) {
-    if (x != x) return x;
-    if (x < -103.972084f) return 0.0f;
-    if (x > 88.7228394f) return __builtin_inff();
     const float kf = rintf(x * 1.44269502f);
     float r = x - kf * 0.693145751953125f;
     r = r - kf * 1.42860677e-06f;
@@ -266,7 +266,11 @@ __device__ inline float oxb_expf(float x) {
     p = p * r + 0.5f;
     p = p * r + 1.0f;
     p = p * r + 1.0f;
-    return ldexpf(p, (int)kf);
+    // |k| <= 150 in range; the clamp keeps the conversion defined elsewhere
+    float y = ldexpf(p, (int)fminf(fmaxf(kf, -200.0f), 200.0f));
+    y = x > 88.7228394f ? __builtin_inff() : y;
+    y = x < -103.972084f ? 0.0f : y;
+    return x != x ? x : y;
 }
 
 // sh/quantize.wgsl:59,68,71 for one value given the row absmax.

@@ -206,7 +206,9 @@ def _oracle_attn(q, kc16, vc16, n, S, H, Hkv, hd):
 @pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (64, 20, 5, 512),
                                          (200, 20, 5, 512), (511, 20, 5, 512), (300, 8, 8, 4096),
                                          (700, 16, 8, 1024), (4095, 20, 5, 4096), (100, 16, 2, 256),
-                                         (2599, 20, 5, 2600)])
+                                         (2599, 20, 5, 2600),
+                                         # cache length not a multiple of 4: per-element score loads
+                                         (200, 20, 5, 515), (514, 20, 5, 515)])
 def test_attn_decode_bitexact(pos, H, Hkv, S):
     rng = np.random.default_rng(pos + H)
     hd = 128
