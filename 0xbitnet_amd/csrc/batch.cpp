@@ -45,10 +45,10 @@ struct oxb_batch {
     std::vector<int> pos, ngen;           // host mirrors per slot
     std::vector<void *> allocs;
 
-    ~oxb_batch() {
-        if (graph) hipGraphExecDestroy(graph);
-        for (void *p : allocs) hipFree(p);
-        if (pinned) hipHostFree(pinned);
+    ~oxb_batch() {   // teardown: errors have no caller to go to
+        if (graph) (void)hipGraphExecDestroy(graph);
+        for (void *p : allocs) (void)hipFree(p);
+        if (pinned) (void)hipHostFree(pinned);
     }
     void *dalloc(size_t bytes) {
         void *p = nullptr;
@@ -106,7 +106,7 @@ int oxb_batch::capture() {
     const int rc = enqueue_step();
     hipError_t e = hipStreamEndCapture(m->stream, &g);
     if (rc) {
-        if (g) hipGraphDestroy(g);
+        if (g) (void)hipGraphDestroy(g);
         return -1;
     }
     if (e != hipSuccess) {
@@ -114,7 +114,7 @@ int oxb_batch::capture() {
         return -1;
     }
     e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
         graph = nullptr;
         set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
@@ -196,7 +196,7 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
 
 extern "C" void oxb_batch_free(oxb_batch *b) {
     if (!b) return;
-    hipStreamSynchronize(b->m->stream);
+    (void)hipStreamSynchronize(b->m->stream);   // teardown: nothing to report to
     delete b;
 }
 

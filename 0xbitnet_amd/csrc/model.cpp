@@ -35,13 +35,13 @@ using namespace oxb;
         }                                                                               \
     } while (0)
 
-oxb_model::~oxb_model() {
-    if (stream) hipStreamSynchronize(stream);
-    if (graph) hipGraphExecDestroy(graph);
-    if (graph_fused) hipGraphExecDestroy(graph_fused);
-    for (void *p : allocations) hipFree(p);
-    if (pinned) hipHostFree(pinned);
-    if (stream) hipStreamDestroy(stream);
+oxb_model::~oxb_model() {   // teardown: errors have no caller to go to
+    if (stream) (void)hipStreamSynchronize(stream);
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (graph_fused) (void)hipGraphExecDestroy(graph_fused);
+    for (void *p : allocations) (void)hipFree(p);
+    if (pinned) (void)hipHostFree(pinned);
+    if (stream) (void)hipStreamDestroy(stream);
     delete gguf;
 }
 
@@ -507,7 +507,7 @@ int oxb_model::capture_graph(bool fused_attn) {
     int rc = enqueue_decode_step(fused_attn);
     hipError_t e = hipStreamEndCapture(stream, &g);
     if (rc) {
-        if (g) hipGraphDestroy(g);
+        if (g) (void)hipGraphDestroy(g);
         return -1;
     }
     if (e != hipSuccess) {
@@ -515,7 +515,7 @@ int oxb_model::capture_graph(bool fused_attn) {
         return -1;
     }
     e = hipGraphInstantiate(&slot, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
         slot = nullptr;
         set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
