@@ -289,11 +289,13 @@ def test_attn_prefill_causal_bitexact():
     assert np.array_equal(out, ref)
 
 
-# n > 64: the LDS-staged kernel at its four tile shapes -- 128x128 (8192, 1024),
-# 128x64 (6912, 512), 64x128 with a ragged last token tile (4032, 650), 64x64
-# (2560, 512) -- and the register-tiled kernel for N % 64 != 0 (32, 65)
+# n > 64: the LDS-staged kernel at its tile shapes -- 128x128 (8192, 1024 and
+# 4224, 1024), 128x64 (6912, 512), 64x128 with a ragged last token tile
+# (4032, 650), 64x64 (2560, 512) -- and the register-tiled kernel for
+# N % 64 != 0 (32, 65)
 @pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
-                                   (32, 256, 65), (8192, 256, 1024), (4032, 256, 650),
+                                   (32, 256, 65), (8192, 256, 1024), (4224, 256, 1024),
+                                   (4032, 256, 650),
                                    # n <= 64: the skinny kernel, 1..4 token tiles, 1 or 2
                                    # feature tiles per workgroup, uneven K splits over waves
                                    (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
