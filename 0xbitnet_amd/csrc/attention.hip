@@ -10,117 +10,15 @@
 // reference (score -3.4e38) contribute exact zeros to every sum, so a query
 // at absolute position `pos` is computed over S = pos + 1 positions.
 //
-// One workgroup per (query, KV head) handles the whole GQA group of G q
-// heads, so each cached K/V row is read once per group.  The scores never
-// leave LDS.  Cache layout: [Hkv][max_seq][128] f16 bits.
+// Each workgroup handles the whole GQA group of G q heads of a KV head, so
+// each cached K/V row is read once per group (prefill: once per group and
+// pair of queries).  Cache layout: [Hkv][max_seq][128] f16 bits.
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
 namespace oxb {
 
 constexpr int kHd = 128;
-
-template <int G>
-__global__ __launch_bounds__(256) void attn_exact_kernel(
-    const float *__restrict__ q, const uint16_t *__restrict__ kc,
-    const uint16_t *__restrict__ vc, const int *__restrict__ pos_ptr, int pos0, int H,
-    int max_seq, float scale, float *__restrict__ out) {
-    extern __shared__ __align__(16) float smem[];
-    float *qs = smem;                 // [G][128]
-    float *sc = qs + G * kHd;         // [G][S]
-    __shared__ float red[256];
-
-    const int tid = threadIdx.x;
-    const int qi = blockIdx.x, hk = blockIdx.y;
-    const int pos = pos_ptr ? *pos_ptr : pos0 + qi;
-    if (pos < 0 || pos >= max_seq) return;  // host checks too; never read out of range
-    const int S = pos + 1;
-    const float *qrow = q + (size_t)qi * H * kHd + (size_t)hk * G * kHd;
-    for (int i = tid; i < G * kHd; i += 256) qs[i] = qrow[i];
-    lds_barrier();
-
-    const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
-    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd;
-
-    // ---- scores: one position per thread, G dot products of 128 terms ------
-    for (int s = tid; s < S; s += 256) {
-        uint4 kr[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) kr[i] = K4[(size_t)s * 16 + i];
-        float dot[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) dot[g] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const __half2 *hh = (const __half2 *)&kr[i];
-#pragma unroll
-            for (int k2 = 0; k2 < 4; ++k2) {
-                const float2 kf = __half22float2(hh[k2]);
-                const int d = i * 8 + k2 * 2;
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    float m0 = qs[g * kHd + d] * kf.x;
-                    dot[g] = dot[g] + m0;
-                    float m1 = qs[g * kHd + d + 1] * kf.y;
-                    dot[g] = dot[g] + m1;
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) sc[g * S + s] = dot[g] * scale;
-    }
-    lds_barrier();
-
-    // ---- softmax per head, in the shader's order --------------------------
-#pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        float m = -3.402823e+38f;
-        for (int s = tid; s < S; s += 256) m = fmaxf(m, sc[g * S + s]);
-        m = block256_max(m, red);
-        float part = 0.0f;
-        for (int s = tid; s < S; s += 256) part = part + oxb_expf(sc[g * S + s] - m);
-        const float inv = 1.0f / block256_tree_sum(part, red);
-        for (int s = tid; s < S; s += 256) sc[g * S + s] = oxb_expf(sc[g * S + s] - m) * inv;
-    }
-    lds_barrier();
-
-    // ---- P.V: G*128 sequential sums over s, NC per thread -----------------
-    constexpr int NC = G * kHd > 256 ? G * kHd / 256 : 1;
-    if (tid >= G * kHd) return;
-    const int d = tid % kHd;
-    int gg[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) gg[c] = (tid + 256 * c) / kHd;
-    float acc[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
-    constexpr int U = 16;
-    int s = 0;
-    for (; s + U <= S; s += U) {
-        float v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            v[u] = __half2float(__ushort_as_half(Vh[(size_t)(s + u) * kHd + d]));
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                float m = sc[gg[c] * S + s + u] * v[u];
-                acc[c] = acc[c] + m;
-            }
-    }
-    for (; s < S; ++s) {
-        const float v = __half2float(__ushort_as_half(Vh[(size_t)s * kHd + d]));
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            float m = sc[gg[c] * S + s] * v;
-            acc[c] = acc[c] + m;
-        }
-    }
-    float *orow = out + (size_t)qi * H * kHd + (size_t)hk * G * kHd;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) orow[gg[c] * kHd + d] = acc[c];
-}
 
 // ---------------------------------------------------------------------------
 // Decode (one query at position *pos, S = pos + 1), two kernels:
@@ -486,6 +384,147 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Prefill: one workgroup per (Q consecutive queries, KV head); query i of
+// the block sits at position pos0 + q0 + i and attends over S_i = its
+// position + 1 cached positions (causal).  Each K row is read once for the
+// Q x G score rows (one position per thread, Q*G chains of 128 terms in
+// order of d), each score row's softmax runs on one wave in the 256-thread
+// order (wave_softmax_row), and each thread runs Q*G*128/256 P.V sums that
+// share its dim d, one V element per step for all of them, each summed in
+// order of s over its own query's S_i.  Queries past n_q repeat the last one
+// and are not stored.  LDS: q [Q*G][128] f32 | scores [Q*G][Sw] f32, Sw =
+// the longest row rounded up to 4 (positions a row does not attend to are
+// never written or read).
+// ---------------------------------------------------------------------------
+constexpr int kPrefillThreads = 256;
+
+template <int G, int Q>
+__global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+    int pos0, int n_q, int H, int max_seq, float scale, float *__restrict__ out) {
+    constexpr int R = Q * G;   // score rows: query r / G, head r % G
+    extern __shared__ __align__(16) float smem[];
+    float *qs = smem;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int q0 = blockIdx.x * Q, hk = blockIdx.y;
+    int Sq[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) Sq[i] = pos0 + min(q0 + i, n_q - 1) + 1;
+    const int Smax = Sq[Q - 1];
+    if (Smax > max_seq) return;   // host checks too; never read out of range
+    const int Sw = (Smax + 3) & ~3;
+    float *sc = qs + R * kHd;
+    for (int i = tid; i < R * kHd; i += kPrefillThreads) {
+        const int r = i / kHd, qi = min(q0 + r / G, n_q - 1);
+        qs[i] = q[(size_t)qi * H * kHd + (size_t)(hk * G + r % G) * kHd + i % kHd];
+    }
+    lds_barrier();
+
+    // ---- scores: one position per thread, R chains of 128 terms -----------
+    const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
+    for (int s = tid; s < Smax; s += kPrefillThreads) {
+        // q stays in LDS (read per use, broadcast): hoisting R x 128 values
+        // out of this loop would not fit in registers
+        asm volatile("" ::: "memory");
+        uint4 kr[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kr[i] = K4[(size_t)s * 16 + i];
+        // rows in passes of up to 4 chains over the K row held in registers
+        constexpr int RG = R < 4 ? R : 4;
+#pragma unroll 1
+        for (int r0 = 0; r0 < R; r0 += RG) {
+            float dot[RG];
+#pragma unroll
+            for (int r = 0; r < RG; ++r) dot[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {   // dims 8i .. 8i+7
+                const __half2 *hh = (const __half2 *)&kr[i];
+                float kf[8];
+#pragma unroll
+                for (int k2 = 0; k2 < 4; ++k2) {
+                    const float2 f = __half22float2(hh[k2]);
+                    kf[2 * k2] = f.x;
+                    kf[2 * k2 + 1] = f.y;
+                }
+#pragma unroll
+                for (int r = 0; r < RG; ++r) {   // q as two broadcast float4 reads
+                    const float4 qa = *(const float4 *)(qs + (r0 + r) * kHd + 8 * i);
+                    const float4 qb = *(const float4 *)(qs + (r0 + r) * kHd + 8 * i + 4);
+                    const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        float m = qq[e] * kf[e];
+                        dot[r] = dot[r] + m;
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RG; ++r)
+                if (s < Sq[(r0 + r) / G]) sc[(r0 + r) * Sw + s] = dot[r] * scale;
+        }
+    }
+    lds_barrier();
+
+    // ---- softmax: one wave per row --------------------------------------------
+    for (int r = w; r < R; r += kPrefillThreads / 64) wave_softmax_row(sc + r * Sw, sc + r * Sw, Sq[r / G], Sw, lane, true);
+    lds_barrier();
+
+    // ---- P.V: thread t, dim t % 128, rows t / 128 + (threads / 128) c ---------------
+    constexpr int NC = R * kHd / kPrefillThreads > 0 ? R * kHd / kPrefillThreads : 1;
+    if (tid >= R * kHd) return;
+    const int d = tid % kHd;
+    const uint16_t *Vd = vc + (size_t)hk * max_seq * kHd + d;
+    int rr[NC], Sc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        rr[c] = tid / kHd + (kPrefillThreads / kHd) * c;
+        Sc[c] = Sq[rr[c] / G];
+    }
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+    const int S0 = Sq[0];   // every row attends at least this far
+    constexpr int U = 16;
+    int s = 0;
+    for (; s + U <= S0; s += U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __half2float(__ushort_as_half(Vd[(size_t)(s + u) * kHd]));
+#pragma unroll
+        for (int u4 = 0; u4 < U; u4 += 4) {
+            float4 pc[NC];   // probabilities of 4 positions per chain (broadcast reads)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                float m0 = pc[c].x * v[u4];
+                acc[c] = acc[c] + m0;
+                float m1 = pc[c].y * v[u4 + 1];
+                acc[c] = acc[c] + m1;
+                float m2 = pc[c].z * v[u4 + 2];
+                acc[c] = acc[c] + m2;
+                float m3 = pc[c].w * v[u4 + 3];
+                acc[c] = acc[c] + m3;
+            }
+        }
+    }
+    for (; s < Smax; ++s) {   // the last < U common positions, then the longer rows' tails
+        const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (s < Sc[c]) {
+                float m = sc[rr[c] * Sw + s] * v;
+                acc[c] = acc[c] + m;
+            }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int qi = q0 + rr[c] / G;
+        if (qi < n_q) out[(size_t)qi * H * kHd + (size_t)(hk * G + rr[c] % G) * kHd + d] = acc[c];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode, one kernel: one 1024-thread workgroup per KV head does scores,
 // softmax and P.V for its G <= 4 query heads, so a layer's attention is one
 // launch and the scores never leave LDS.  Same arithmetic as the two-kernel
@@ -630,38 +669,57 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     if (go < G) out[(size_t)(hk * G + go) * kHd + d] = acc;
 }
 
-template <int G>
-static int launch_exact(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
-                        int pos0, int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
-                        hipStream_t s) {
-    const size_t smem = (size_t)(G * kHd + G * s_max) * sizeof(float);
+// LDS of the prefill kernel for R score rows of up to s_max positions
+__host__ __device__ inline size_t prefill_smem(int R, int s_max) {
+    return (size_t)R * (kHd + ((s_max + 3) & ~3)) * sizeof(float);
+}
+constexpr size_t kPrefillLds = 150 * 1024;
+
+template <int G, int Q>
+static int launch_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int pos0,
+                          int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
+                          hipStream_t s) {
+    const size_t smem = prefill_smem(G * Q, s_max);
     static size_t configured = 0;
     if (smem > 64 * 1024 && smem > configured) {
-        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_exact_kernel<G>,
+        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_prefill_kernel<G, Q>,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
         configured = smem;
     }
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
-    hipLaunchKernelGGL(attn_exact_kernel<G>, dim3(n_q, Hkv), dim3(256), smem, s, q, kc, vc, pos,
-                       pos0, H, max_seq, scale, out);
+    hipLaunchKernelGGL((attn_prefill_kernel<G, Q>), dim3((n_q + Q - 1) / Q, Hkv), dim3(kPrefillThreads), smem,
+                       s, q, kc, vc, pos0, n_q, H, max_seq, scale, out);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-static int dispatch(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
-                    int pos0, int n_q, int H, int Hkv, int hd, int max_seq, int s_max, float *out,
-                    void *stream) {
+// pairs of queries for G >= 4 when both fit the LDS budget (smaller groups
+// keep one query per workgroup: their pair variants do not fit registers)
+template <int G>
+static int launch_prefill_g(const float *q, const uint16_t *kc, const uint16_t *vc, int pos0,
+                            int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
+                            hipStream_t s) {
+    if constexpr (G >= 4) {
+        if (prefill_smem(2 * G, s_max) <= kPrefillLds)
+            return launch_prefill<G, 2>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+    }
+    return launch_prefill<G, 1>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+}
+
+static int dispatch_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int pos0,
+                            int n_q, int H, int Hkv, int hd, int max_seq, int s_max, float *out,
+                            void *stream) {
     OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
     const int G = H / Hkv;
-    OXB_REQUIRE((size_t)G * (s_max + kHd) * 4 <= 150 * 1024,
+    OXB_REQUIRE(prefill_smem(G, s_max) <= kPrefillLds,
                 "attention: %d heads per KV head x %d positions exceed the LDS budget", G, s_max);
     hipStream_t s = (hipStream_t)stream;
     switch (G) {
-        case 1: return launch_exact<1>(q, kc, vc, pos, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
-        case 2: return launch_exact<2>(q, kc, vc, pos, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
-        case 4: return launch_exact<4>(q, kc, vc, pos, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
-        case 8: return launch_exact<8>(q, kc, vc, pos, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+        case 1: return launch_prefill_g<1>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+        case 2: return launch_prefill_g<2>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+        case 4: return launch_prefill_g<4>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
+        case 8: return launch_prefill_g<8>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
         default:
             oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
             return -1;
@@ -801,6 +859,6 @@ extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const ui
                                 int n_tok, int pos0, int H, int Hkv, int hd, int max_seq,
                                 float *out, void *stream) {
     OXB_REQUIRE(n_tok > 0 && pos0 >= 0 && pos0 + n_tok <= max_seq, "prefill attention: bad range");
-    return dispatch(q, kcache, vcache, nullptr, pos0, n_tok, H, Hkv, hd, max_seq, pos0 + n_tok, out,
-                    stream);
+    return dispatch_prefill(q, kcache, vcache, pos0, n_tok, H, Hkv, hd, max_seq, pos0 + n_tok, out,
+                            stream);
 }

@@ -277,10 +277,15 @@ def test_attn_decode_fused_rejects_unsupported():
                         np.zeros((4, 8, 128), np.float16), 3, 32, 4, 128, 8, fused=True)
 
 
-def test_attn_prefill_causal_bitexact():
-    rng = np.random.default_rng(21)
-    H, Hkv, hd, S = 20, 5, 128, 256
-    pos0, n = 30, 100
+# G = 4 and 8 take query pairs (an odd n leaves a lone last query); (0, 257)
+# pairs rows of 256 and 257 positions; G = 1, 2 one query per workgroup
+@pytest.mark.parametrize("H,Hkv,S,pos0,n", [(20, 5, 256, 30, 100), (20, 5, 512, 0, 257),
+                                            (16, 2, 1200, 900, 31), (8, 8, 300, 5, 40),
+                                            (16, 8, 300, 100, 33), (20, 5, 2100, 2040, 9),
+                                            (20, 5, 64, 0, 1)])
+def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
+    rng = np.random.default_rng(21 + n)
+    hd = 128
     q = rng.standard_normal((n, H * hd)).astype(np.float32)
     kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
     vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
