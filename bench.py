@@ -30,6 +30,10 @@ The JSON line also carries
 runs only the 8192 x 28672 GEMV (plus, with --calib-mib, one device copy of
 that many MiB, the calibration kernel for the FETCH_SIZE / WRITE_SIZE
 counters) -- the command the rocprofv3 --pmc runs profile.
+
+    python bench.py --long-context-only [--lc-batches 1,8,32] [--lc-steps 512]
+
+runs only the long-context section.
 """
 from __future__ import annotations
 
@@ -262,18 +266,19 @@ def long_context(pkg, synth, path: str, prompt_len: int = 2048, steps: int = 512
     ops = _il.import_module("0xbitnet_amd.ops")
     max_seq = prompt_len + steps + 8
     m = pkg.Model(path, max_seq=max_seq)
-    rng = np.random.default_rng(4096)
-    prompt = rng.integers(0, synth.BITNET_2B.vocab, prompt_len).astype(np.int32)
-    m.forward(prompt[:64], want_logits=False)   # warm-up (graph capture, code paths)
-    m.decode_greedy(4)
-    m.reset()
-    ops.sync()
-    t0 = time.perf_counter()
-    m.forward(prompt, want_logits=False)
-    ops.sync()
-    pf = time.perf_counter() - t0
-    out = {"prompt_tokens": prompt_len, "decode_tokens": steps, "kv_positions_max": prompt_len + steps,
-           "prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(prompt_len / pf, 1)}
+    out = {"prompt_tokens": prompt_len, "decode_tokens": steps, "kv_positions_max": prompt_len + steps}
+    if 1 in batches:   # the one-sequence engine: timed prefill, then its decode below
+        rng = np.random.default_rng(4096)
+        prompt = rng.integers(0, synth.BITNET_2B.vocab, prompt_len).astype(np.int32)
+        m.forward(prompt[:64], want_logits=False)   # warm-up (graph capture, code paths)
+        m.decode_greedy(4)
+        m.reset()
+        ops.sync()
+        t0 = time.perf_counter()
+        m.forward(prompt, want_logits=False)
+        ops.sync()
+        pf = time.perf_counter() - t0
+        out.update({"prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(prompt_len / pf, 1)})
     rows = []
     for B in batches:
         if B == 1:
@@ -346,6 +351,11 @@ def main() -> int:
                     help="skip the GEMM sweep, prefill block and long-context runs")
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--calib-mib", type=int, default=0)
+    ap.add_argument("--long-context-only", action="store_true",
+                    help="run only the long-context section (2048-token prefill, decode at the "
+                         "batch sizes of --lc-batches)")
+    ap.add_argument("--lc-batches", default="1,8,32")
+    ap.add_argument("--lc-steps", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
@@ -367,6 +377,11 @@ def main() -> int:
     t = time.time()
     path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
     log(f"model file {path} ({os.path.getsize(path) / 1e9:.2f} GB, {time.time() - t:.1f}s)")
+    if args.long_context_only:
+        lc = long_context(pkg, synth, path, steps=args.lc_steps,
+                          batches=tuple(int(b) for b in args.lc_batches.split(",")))
+        print(json.dumps({"long_context": lc}), flush=True)
+        return 0
     t = time.time()
     max_seq = args.prompt + args.steps + args.warmup + 8
     model = pkg.Model(path, max_seq=max_seq)
