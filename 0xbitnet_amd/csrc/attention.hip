@@ -548,6 +548,36 @@ __host__ __device__ inline size_t attn_fused_smem(int G, int max_seq) {
     return kFusedBuf + (size_t)G * ((max_seq + 3) & ~3) * 4 + (size_t)G * kHd * 4;
 }
 
+// K rows c0 .. c0+255 of the chunk (thread i: row i/16, uint4 column i%16),
+// clamped to the cache length (rows past it are staged but never used).
+// A wave whose 4 rows all lie past S loads nothing (a wave-uniform branch).
+__device__ __forceinline__ void fused_load_k(u32x4_t (&kt)[4], const uint4 *__restrict__ K4, int c0,
+                                             int S, int tid) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = tid + 1024 * k;
+        const int wave_row = c0 + ((i & ~63) >> 4);   // the wave's first row
+        kt[k] = wave_row < S
+                    ? *(const u32x4_t *)(K4 + (size_t)min(c0 + (i >> 4), S - 1) * 16 + (i & 15))
+                    : u32x4_t{0, 0, 0, 0};
+    }
+}
+
+// V rows of a 128-position chunk: wave w rows c0 + 4w .. +3 (+64 on the
+// second pass), lane l the f16 pair of dims 2l, 2l+1; clamped and skipped
+// like K.
+__device__ __forceinline__ void fused_load_v(uint32_t (&vr)[2][4], const uint32_t *__restrict__ V2,
+                                             int c0, int S, int w, int lane) {
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const bool any = c0 + pass * 64 + 4 * w < S;   // wave-uniform
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            vr[pass][j] = any ? V2[(size_t)min(c0 + pass * 64 + 4 * w + j, S - 1) * (kHd / 2) + lane]
+                              : 0u;
+    }
+}
+
 template <int G>
 __global__ __launch_bounds__(1024) void attn_fused_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
@@ -568,16 +598,8 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
 
     // ---- scores ------------------------------------------------------------
-    auto load_k = [&](uint4 (&kt)[4], int c0) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = tid + 1024 * k;   // row i/16, column i%16 of the chunk
-            const int row = c0 + (i >> 4);
-            kt[k] = row < S ? K4[(size_t)row * 16 + (i & 15)] : make_uint4(0, 0, 0, 0);
-        }
-    };
-    uint4 kt[4];
-    load_k(kt, 0);
+    u32x4_t kt[4];   // native vectors: HIP's uint4 struct copies left this array in scratch
+    fused_load_k(kt, K4, 0, S, tid);
     if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
     const int g = w >> 2, pg = w & 3;   // this wave's head and position group
     for (int c0 = 0; c0 < S; c0 += kFusedKC) {
@@ -585,26 +607,27 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = tid + 1024 * k;
-            ks[i >> 4][i & 15] = kt[k];
+            *(u32x4_t *)&ks[i >> 4][i & 15] = kt[k];
         }
         lds_barrier();
-        if (c0 + kFusedKC < S) load_k(kt, c0 + kFusedKC);
+        fused_load_k(kt, K4, c0 + kFusedKC, S, tid);   // clamped past S (branch-free)
         const int s = c0 + pg * 64 + lane;
         if (g < G && s < S) {
-            // 128-term chain in two halves (q half and K half in registers);
-            // products fma(q, k, +0) = q*k up to the sign of a zero product
+            // 128-term chain in four quarters (q quarter and K quarter in
+            // registers); products fma(q, k, +0) = q*k up to the sign of a
+            // zero product
             float dot = 0.0f;
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                float4 qv[16];
-                uint4 kr[8];
+            for (int quarter = 0; quarter < 4; ++quarter) {
+                float4 qv[8];
+                uint4 kr[4];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) qv[i] = qs[g * 32 + half * 16 + i];
+                for (int i = 0; i < 8; ++i) qv[i] = qs[g * 32 + quarter * 8 + i];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) kr[i] = ks[pg * 64 + lane][half * 8 + i];
+                for (int i = 0; i < 4; ++i) kr[i] = ks[pg * 64 + lane][quarter * 4 + i];
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < 4; ++i) {
                     const float qq[8] = {qv[2 * i].x, qv[2 * i].y, qv[2 * i].z, qv[2 * i].w,
                                          qv[2 * i + 1].x, qv[2 * i + 1].y, qv[2 * i + 1].z,
                                          qv[2 * i + 1].w};
@@ -625,6 +648,13 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     }
     lds_barrier();
 
+    // V rows of the first two P.V chunks, in flight through the softmax; rows
+    // past S are clamped (staged, never summed)
+    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd);
+    uint32_t va[2][4], vb[2][4];
+    fused_load_v(va, V2, 0, S, w, lane);
+    fused_load_v(vb, V2, kFusedVC, S, w, lane);
+
     // ---- softmax: wave g < G owns head g's row ------------------------------
     if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane, true);
 
@@ -633,18 +663,6 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     // the chunk, lane l the f16 pair of dims 2l, 2l+1: four row-coalesced
     // 4-byte loads, then one float4 (4 positions) per dim into vt[d][s].
     const int go = w >> 1, d = ((w & 1) << 6) | lane;
-    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd);
-    auto load_v = [&](uint32_t (&vr)[2][4], int c0) {
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int sr = c0 + pass * 64 + 4 * w + j;
-                vr[pass][j] = sr < S ? V2[(size_t)sr * (kHd / 2) + lane] : 0u;
-            }
-    };
-    uint32_t vr[2][4];
-    load_v(vr, 0);
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += kFusedVC) {
         const int n = min(kFusedVC, S - c0);
@@ -652,10 +670,10 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
             float4 lo, hi;   // dims 2*lane and 2*lane + 1 at 4 positions
-            float2 f0 = __half22float2(*(const __half2 *)&vr[pass][0]);
-            float2 f1 = __half22float2(*(const __half2 *)&vr[pass][1]);
-            float2 f2 = __half22float2(*(const __half2 *)&vr[pass][2]);
-            float2 f3 = __half22float2(*(const __half2 *)&vr[pass][3]);
+            float2 f0 = __half22float2(*(const __half2 *)&va[pass][0]);
+            float2 f1 = __half22float2(*(const __half2 *)&va[pass][1]);
+            float2 f2 = __half22float2(*(const __half2 *)&va[pass][2]);
+            float2 f3 = __half22float2(*(const __half2 *)&va[pass][3]);
             lo = make_float4(f0.x, f1.x, f2.x, f3.x);
             hi = make_float4(f0.y, f1.y, f2.y, f3.y);
             const int sr = pass * 64 + 4 * w;
@@ -663,7 +681,12 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
             *(float4 *)(vt + (2 * lane + 1) * kFusedVS + sr) = hi;
         }
         lds_barrier();
-        if (c0 + kFusedVC < S) load_v(vr, c0 + kFusedVC);
+        // two chunks in flight while this one is summed
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) va[pass][j] = vb[pass][j];
+        fused_load_v(vb, V2, c0 + 2 * kFusedVC, S, w, lane);
         if (go < G) acc = pv_chain(sc + go * spad_max + c0, vt + d * kFusedVS, n, acc);
     }
     if (go < G) out[(size_t)(hk * G + go) * kHd + d] = acc;
