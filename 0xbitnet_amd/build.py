@@ -11,6 +11,7 @@ import argparse
 import concurrent.futures as cf
 import glob
 import os
+import re
 import subprocess
 import sys
 
@@ -32,6 +33,49 @@ COMMON = [
 DEVICE = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+def _check_resources(src: str, stderr: str) -> str:
+    """Parse the compiler's kernel-resource-usage remarks for one source.
+
+    Every kernel must run without a private segment: no scratch bytes per lane,
+    no VGPR spills and no dynamic stack (a spill to scratch turns register
+    traffic into memory traffic on the hot path).  SGPR spills land in VGPR
+    lanes and are allowed.  Returns the remarks, one kernel per line, and raises
+    when a kernel breaks the rule.
+    """
+    rows, bad, name = [], [], None
+    for line in stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            rows.append([name])
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+?(?: \[[^]]+\])?): (\S+) \[-Rpass", line)
+        if m and name is not None:
+            key, val = m.group(1), m.group(2)
+            rows[-1].append(f"{key}={val}")
+            if key.startswith(("ScratchSize", "VGPRs Spill", "Dynamic Stack")) and val not in ("0", "False"):
+                bad.append(f"{name}: {key} = {val}")
+    if bad:
+        raise RuntimeError(f"{os.path.basename(src)}: kernels use scratch memory:\n  " + "\n  ".join(bad))
+    return "\n".join(" ".join(r) for r in rows) + "\n"
+
+
+def _diagnostics(stderr: str) -> list[str]:
+    """Compiler output minus the resource remarks (and their source excerpts) and
+    the host pass's note that it does not know the packed-fp32 feature."""
+    keep, in_remark = [], False
+    for line in stderr.splitlines():
+        if "kernel-resource-usage" in line:
+            in_remark = True
+            continue
+        if in_remark and re.match(r"^\s*\d*\s*\|", line):
+            continue
+        in_remark = False
+        if "packed-fp32-ops" not in line:
+            keep.append(line)
+    return keep
+
+
 def _deps() -> list[str]:
     return glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(HERE, "..", "include", "*.h"))
 
@@ -44,7 +88,7 @@ def _compile(src: str, force: bool) -> str:
             return obj
     cmd = [HIPCC] + COMMON
     if src.endswith(".hip"):
-        cmd += DEVICE + ["-x", "hip"]
+        cmd += DEVICE + ["-Rpass-analysis=kernel-resource-usage", "-x", "hip"]
     else:
         cmd += ["-D__HIP_PLATFORM_AMD__"]
     cmd += ["-c", src, "-o", obj + ".tmp"]
@@ -52,7 +96,10 @@ def _compile(src: str, force: bool) -> str:
     if r.returncode != 0:
         sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
         raise RuntimeError(f"compile failed: {os.path.basename(src)}")
-    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if src.endswith(".hip"):
+        with open(obj + ".resources.txt", "w") as f:
+            f.write(_check_resources(src, r.stderr))
+    err = "\n".join(_diagnostics(r.stderr))
     if err.strip():
         sys.stderr.write(err + "\n")
     os.replace(obj + ".tmp", obj)

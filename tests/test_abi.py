@@ -130,3 +130,37 @@ def test_i2s_pack_known_bytes():
     for fill, u32 in ((-1, 0), (1, 0xAAAAAAAA), (0, 0x55555555)):
         b = synth.i2s_pack(np.full((1, 128), fill, np.int8))
         assert int(b[0, :4].view("<u4")[0]) == u32
+
+
+def _build_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("oxb_build", os.path.join(ROOT, "0xbitnet_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_build_rejects_kernels_with_scratch():
+    b = _build_module()
+    head = "k.hip:1:1: remark: Function Name: kern [-Rpass-analysis=kernel-resource-usage]\n"
+    row = "k.hip:1:1: remark:     {}: {} [-Rpass-analysis=kernel-resource-usage]\n"
+    ok = head + row.format("VGPRs", 64) + row.format("ScratchSize [bytes/lane]", 0) + \
+        row.format("SGPRs Spill", 12) + row.format("VGPRs Spill", 0) + row.format("Dynamic Stack", "False")
+    assert "ScratchSize [bytes/lane]=0" in b._check_resources("k.hip", ok)
+    for key, val in (("ScratchSize [bytes/lane]", 80), ("VGPRs Spill", 3), ("Dynamic Stack", "True")):
+        with pytest.raises(RuntimeError, match="scratch"):
+            b._check_resources("k.hip", head + row.format(key, val))
+
+
+def test_built_kernels_have_no_private_segment():
+    bdir = os.path.join(ROOT, "0xbitnet_amd", "_build")
+    srcs = [f for f in os.listdir(os.path.join(ROOT, "0xbitnet_amd", "csrc")) if f.endswith(".hip")]
+    reports = [os.path.join(bdir, f + ".o.resources.txt") for f in srcs]
+    if not all(os.path.exists(r) for r in reports):
+        pytest.skip("library built without resource reports")
+    n = 0
+    for r in reports:
+        for line in open(r):
+            n += 1
+            assert "ScratchSize [bytes/lane]=0" in line and "VGPRs Spill=0" in line, line
+    assert n >= 20
