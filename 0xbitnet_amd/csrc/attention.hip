@@ -63,9 +63,6 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         const int i = tid + 256 * k, row = i >> 4;
         kt[k] = K4[(size_t)min(s0 + row, S - 1) * 16 + (i & 15)];
     }
-    // the G q rows to LDS (one float4 per thread); read back as broadcasts
-    __shared__ __align__(16) float4 qs[G * 32];
-    if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int i = tid + 256 * k;
@@ -75,38 +72,34 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
-    // this lane's K row into registers, then each head's q row (LDS broadcast):
-    // the 128-step chain below then waits on nothing
+    // this lane's K row into registers; the head's q row is wave-uniform and
+    // read with scalar loads, so each step of the chain is one v_fma_mix
+    // (q operand in an SGPR) and one add
     uint4 kr16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kr16[i] = ks[lane][i];
+    const int wu = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
-        const float4 *qg = qs + (w + 4 * h) * 32;
-        float4 qv[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) qv[i] = qg[i];
-        __builtin_amdgcn_sched_barrier(0);
+        const float *__restrict__ qg = q + (size_t)(hk * G + wu + 4 * h) * kHd;
         // products as fma(q, k, +0): equal to q*k but for the sign of a zero
         // product, which cannot change a sum that starts at +0
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint4 kr = kr16[i];
-            const float4 qa = qv[2 * i], qb = qv[2 * i + 1];
-            const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
             const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
                 const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
                 const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
-                const float m0 = __builtin_fmaf(qq[2 * k2], k0, 0.0f);
+                const float m0 = __builtin_fmaf(qg[8 * i + 2 * k2], k0, 0.0f);
                 dot = dot + m0;
-                const float m1 = __builtin_fmaf(qq[2 * k2 + 1], k1, 0.0f);
+                const float m1 = __builtin_fmaf(qg[8 * i + 2 * k2 + 1], k1, 0.0f);
                 dot = dot + m1;
             }
         }
-        scores[(size_t)(hk * G + w + 4 * h) * max_seq + s] = dot * scale;
+        scores[(size_t)(hk * G + wu + 4 * h) * max_seq + s] = dot * scale;
     }
 }
 
@@ -324,7 +317,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     auto swz = [](int h) { return PPP >= 8 ? 4 * (h & 7) : PPP == 4 ? 16 * (h & 3) : 0; };
     static_assert(PPP != 4 || kVChunk >= 64, "swizzle stays inside the chunk");
     constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
-    extern __shared__ __align__(16) float pr[];   // [G][Spad] scores, then probabilities
+    extern __shared__ __align__(16) float pr[];   // [G][Sp] scores, then probabilities
     __shared__ __align__(16) float vt[DWB * kVS];  // V slice, [d][s] f32
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
@@ -348,22 +341,19 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     load_chunk(ra, 0);
     load_chunk(rb, min(kVChunk, S - 1));
 
-    // each wave owns heads w, w+4: load its score rows and run their softmax
+    // each wave owns heads w, w+4: load its score rows and run their softmax.
+    // Rows are Sp floats apart, Sp / 4 odd, so that the G rows a summing wave
+    // reads at one step start in different bank groups.
+    const int Sp = ((Spad >> 2) | 1) << 2;
     for (int g = w; g < G; g += 4)
-        wave_softmax_row(pr + g * Spad, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
+        wave_softmax_row(pr + g * Sp, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
                          (max_seq & 3) == 0);
 
-    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s;
-    // waves < WPB each run 64 such chains (heads lane / DWW, dims w*DWW + lane % DWW)
-    const int g = lane / DWW, dd = w * DWW + lane % DWW;
-    float acc = 0.0f;
-    for (int c0 = 0; c0 < S; c0 += kVChunk) {
-        const int n = min(kVChunk, S - c0);
-        lds_barrier();  // probabilities ready / previous chunk consumed
+    auto stage = [&](const uint4 (&r)[kLoads]) {
 #pragma unroll
         for (int k = 0; k < kLoads; ++k) {
             const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
-            const uint32_t wv[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
+            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float2 f = __half22float2(*(const __half2 *)&wv[e]);
@@ -372,15 +362,35 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
                 vt[(8 * h + 2 * e + 1) * kVS + ss] = f.y;
             }
         }
+    };
+    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s;
+    // waves < WPB each run 64 such chains (heads lane / DWW, dims w*DWW + lane % DWW).
+    // Chunks alternate between the two register sets: a set is refilled (two
+    // chunks ahead) as soon as it is staged, so no load is waited for early.
+    // The summing roles rotate with the block index so that workgroups sharing
+    // a CU sum on different SIMDs.
+    const int ws = (w - (int)((blockIdx.x + 3 * blockIdx.y + blockIdx.z) & 3)) & 3;
+    const int g = lane / DWW, dd = ws * DWW + lane % DWW;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < S; c0 += 2 * kVChunk) {
+        lds_barrier();  // probabilities ready / previous chunk consumed
+        stage(ra);
         lds_barrier();
-        // two chunks in flight while this one is summed
-#pragma unroll
-        for (int k = 0; k < kLoads; ++k) ra[k] = rb[k];
-        load_chunk(rb, min(c0 + 2 * kVChunk, S - 1));
-        if (w < WPB)
-            acc = pv_chain(pr + g * Spad + c0, vt + dd * kVS, n, acc, swz(dd >> 3));
+        load_chunk(ra, min(c0 + 2 * kVChunk, S - 1));
+        if (ws < WPB)
+            acc = pv_chain(pr + g * Sp + c0, vt + dd * kVS, min(kVChunk, S - c0), acc, swz(dd >> 3));
+        const int c1 = c0 + kVChunk;
+        if (c1 < S) {
+            lds_barrier();
+            stage(rb);
+            lds_barrier();
+            load_chunk(rb, min(c1 + 2 * kVChunk, S - 1));
+            if (ws < WPB)
+                acc = pv_chain(pr + g * Sp + c1, vt + dd * kVS, min(kVChunk, S - c1), acc,
+                               swz(dd >> 3));
+        }
     }
-    if (w < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
+    if (ws < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -525,27 +535,29 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Decode, one kernel: one 1024-thread workgroup per KV head does scores,
-// softmax and P.V for its G <= 4 query heads, so a layer's attention is one
-// launch and the scores never leave LDS.  Same arithmetic as the two-kernel
-// path (and the shaders).  Positions are taken in chunks: 256 K rows (wave
-// w: head w/4, positions (w%4)*64 + lane of the chunk), then 128 V rows
-// staged as f32 [128 dims][128 + 4 pad] (lane = one output (head, dim)).
+// Decode, one kernel: two 1024-thread workgroups per KV head (one per half of
+// the 128 dims) each compute the scores and softmax of its G <= 4 query
+// heads, then the P.V sums of their half of the dims, so a layer's attention
+// is one launch and the scores never leave LDS.  Same arithmetic as the
+// two-kernel path (and the shaders).  Positions are taken in chunks: 256 K
+// rows (wave w: head w%4, positions (w/4)*64 + lane of the chunk), then 256 V
+// rows staged as f32 [64 dims][256 + 4 pad]; wave g < G sums head g (lane =
+// one dim), so the summing waves sit on four SIMDs.
 // Rows past the cache length are neither loaded nor used.
-// Faster than the two-kernel path only for short caches (each KV head's
-// K/V streams through one CU, ~30 GB/s): ~1 us less per layer at 64-128
-// positions, slower past ~200.  The host picks it by position.
-// LDS (dynamic): buf 69632 B (K chunk [256][17 uint4] | V chunk [128][132] f32)
-// | scores [G][Spad_max] f32 | q [G][128] f32.
+// The scores are computed twice (once per half), which costs little next to
+// the P.V chains it halves.  The host picks this kernel or the two-kernel path
+// by position.
+// LDS (dynamic): buf 69632 B (K chunk [256][17 uint4] | V chunk [64][260] f32)
+// | scores [G][Spad_max] f32.
 // ---------------------------------------------------------------------------
 constexpr int kFusedKC = 256;               // K rows per chunk
-constexpr int kFusedVC = 128;               // V rows per chunk
+constexpr int kFusedVC = 256;               // V rows per chunk
 constexpr int kFusedVS = kFusedVC + 4;      // padded V row (floats)
-constexpr size_t kFusedBuf = (size_t)kFusedKC * 17 * 16;   // 69632 B >= 128*132*4
-static_assert((size_t)kHd * kFusedVS * 4 <= kFusedBuf, "V chunk must fit the K chunk buffer");
+constexpr size_t kFusedBuf = (size_t)kFusedKC * 17 * 16;   // 69632 B >= 64*260*4
+static_assert((size_t)(kHd / 2) * kFusedVS * 4 <= kFusedBuf, "V chunk must fit the K chunk buffer");
 
 __host__ __device__ inline size_t attn_fused_smem(int G, int max_seq) {
-    return kFusedBuf + (size_t)G * ((max_seq + 3) & ~3) * 4 + (size_t)G * kHd * 4;
+    return kFusedBuf + (size_t)G * ((max_seq + 3) & ~3) * 4;
 }
 
 // K rows c0 .. c0+255 of the chunk (thread i: row i/16, uint4 column i%16),
@@ -563,18 +575,31 @@ __device__ __forceinline__ void fused_load_k(u32x4_t (&kt)[4], const uint4 *__re
     }
 }
 
-// V rows of a 128-position chunk: wave w rows c0 + 4w .. +3 (+64 on the
-// second pass), lane l the f16 pair of dims 2l, 2l+1; clamped and skipped
-// like K.
-__device__ __forceinline__ void fused_load_v(uint32_t (&vr)[2][4], const uint32_t *__restrict__ V2,
+// V rows of a 256-position chunk for one half of the dims: thread (wave w,
+// lane l) takes rows c0 + 8q .. +7, q = 2w + l/32, and the f16 pair l % 32
+// of the half (row-coalesced 128-byte loads); clamped to the cache length,
+// and a wave whose 16 rows all lie past S loads nothing (wave-uniform).
+__device__ __forceinline__ void fused_load_v(uint32_t (&vr)[8], const uint32_t *__restrict__ V2,
                                              int c0, int S, int w, int lane) {
+    const int q = 2 * w + (lane >> 5), p = lane & 31;
+    const bool any = c0 + 16 * w < S;   // wave-uniform
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-        const bool any = c0 + pass * 64 + 4 * w < S;   // wave-uniform
+    for (int j = 0; j < 8; ++j)
+        vr[j] = any ? V2[(size_t)min(c0 + 8 * q + j, S - 1) * (kHd / 2) + p] : 0u;
+}
+
+// The staged rows as f32 V^T [dim][position]: dims 2p, 2p+1 of the half,
+// positions 8q .. 8q+7 of the chunk (two float4 per dim).
+__device__ __forceinline__ void fused_stage_v(float *vt, const uint32_t (&vr)[8], int w, int lane) {
+    const int q = 2 * w + (lane >> 5), p = lane & 31;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            vr[pass][j] = any ? V2[(size_t)min(c0 + pass * 64 + 4 * w + j, S - 1) * (kHd / 2) + lane]
-                              : 0u;
+    for (int h = 0; h < 2; ++h) {
+        const float2 f0 = __half22float2(*(const __half2 *)&vr[4 * h]);
+        const float2 f1 = __half22float2(*(const __half2 *)&vr[4 * h + 1]);
+        const float2 f2 = __half22float2(*(const __half2 *)&vr[4 * h + 2]);
+        const float2 f3 = __half22float2(*(const __half2 *)&vr[4 * h + 3]);
+        *(float4 *)(vt + (2 * p) * kFusedVS + 8 * q + 4 * h) = make_float4(f0.x, f1.x, f2.x, f3.x);
+        *(float4 *)(vt + (2 * p + 1) * kFusedVS + 8 * q + 4 * h) = make_float4(f0.y, f1.y, f2.y, f3.y);
     }
 }
 
@@ -588,7 +613,6 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     float *vt = (float *)smem_f;
     const int spad_max = (max_seq + 3) & ~3;
     float *sc = (float *)(smem_f + kFusedBuf);           // [G][spad_max]
-    float4 *qs = (float4 *)(sc + (size_t)G * spad_max);   // [G][32]
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
     const int S = pos + 1;
@@ -596,100 +620,112 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     const int hk = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
+    const int half = blockIdx.y;   // this workgroup's half of the dims
+    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + half * 32;
+
+    // Up to 512 positions every K and V load is issued here, so the kernel
+    // waits for memory once; longer caches refill each register set as soon
+    // as it is consumed.
+    u32x4_t ka[4], kb[4];   // native vectors: HIP's uint4 struct copies land in scratch
+    uint32_t va[8], vb[8];
+    fused_load_k(ka, K4, 0, S, tid);
+    fused_load_k(kb, K4, kFusedKC, S, tid);
+    fused_load_v(va, V2, 0, S, w, lane);
+    fused_load_v(vb, V2, kFusedVC, S, w, lane);
 
     // ---- scores ------------------------------------------------------------
-    u32x4_t kt[4];   // native vectors: HIP's uint4 struct copies left this array in scratch
-    fused_load_k(kt, K4, 0, S, tid);
-    if (tid < G * 32) qs[tid] = ((const float4 *)(q + (size_t)hk * G * kHd))[tid];
-    const int g = w >> 2, pg = w & 3;   // this wave's head and position group
-    for (int c0 = 0; c0 < S; c0 += kFusedKC) {
-        if (c0) lds_barrier();        // the previous chunk's rows are consumed
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = tid + 1024 * k;
-            *(u32x4_t *)&ks[i >> 4][i & 15] = kt[k];
-        }
-        lds_barrier();
-        fused_load_k(kt, K4, c0 + kFusedKC, S, tid);   // clamped past S (branch-free)
+    // this wave's head and position group: consecutive waves (which sit on
+    // different SIMDs) take different heads, so a partly filled chunk still
+    // spreads its chains over the four SIMDs
+    const int g = w & 3, pg = w >> 2;
+    // 128-term chain of position c0 + pg*64 + lane: the K row from LDS in
+    // quarters (the next quarter read while one is summed), the head's q row
+    // (wave-uniform) through scalar loads, so each step is one v_fma_mix with
+    // an SGPR operand and one add; products fma(q, k, +0) = q*k up to the
+    // sign of a zero product
+    auto chain = [&](int c0) {
         const int s = c0 + pg * 64 + lane;
         if (g < G && s < S) {
-            // 128-term chain in four quarters (q quarter and K quarter in
-            // registers); products fma(q, k, +0) = q*k up to the sign of a
-            // zero product
+            const float *__restrict__ qg =
+                q + (size_t)(hk * G + __builtin_amdgcn_readfirstlane(g)) * kHd;
+            const uint4 *row = ks[pg * 64 + lane];
             float dot = 0.0f;
+            uint4 kq[2][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kq[0][i] = row[i];
 #pragma unroll
             for (int quarter = 0; quarter < 4; ++quarter) {
-                float4 qv[8];
-                uint4 kr[4];
+                if (quarter < 3) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) qv[i] = qs[g * 32 + quarter * 8 + i];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) kr[i] = ks[pg * 64 + lane][quarter * 4 + i];
-                __builtin_amdgcn_sched_barrier(0);
+                    for (int i = 0; i < 4; ++i) kq[(quarter + 1) & 1][i] = row[4 * (quarter + 1) + i];
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float qq[8] = {qv[2 * i].x, qv[2 * i].y, qv[2 * i].z, qv[2 * i].w,
-                                         qv[2 * i + 1].x, qv[2 * i + 1].y, qv[2 * i + 1].z,
-                                         qv[2 * i + 1].w};
-                    const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+                    const uint4 kr = kq[quarter & 1][i];
+                    const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
+                    const int d0 = 32 * quarter + 8 * i;
 #pragma unroll
                     for (int k2 = 0; k2 < 4; ++k2) {
                         const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
                         const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
-                        const float m0 = __builtin_fmaf(qq[2 * k2], k0, 0.0f);
+                        const float m0 = __builtin_fmaf(qg[d0 + 2 * k2], k0, 0.0f);
                         dot = dot + m0;
-                        const float m1 = __builtin_fmaf(qq[2 * k2 + 1], k1, 0.0f);
+                        const float m1 = __builtin_fmaf(qg[d0 + 2 * k2 + 1], k1, 0.0f);
                         dot = dot + m1;
                     }
                 }
             }
             sc[g * spad_max + s] = dot * scale;
         }
+    };
+    auto store_k = [&](const u32x4_t (&kt)[4]) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = tid + 1024 * k;
+            *(u32x4_t *)&ks[i >> 4][i & 15] = kt[k];
+        }
+    };
+    for (int c0 = 0; c0 < S; c0 += 2 * kFusedKC) {
+        if (c0) lds_barrier();   // the previous chunk's rows are consumed
+        store_k(ka);
+        lds_barrier();
+        fused_load_k(ka, K4, c0 + 2 * kFusedKC, S, tid);   // nothing past S
+        chain(c0);
+        const int c1 = c0 + kFusedKC;
+        if (c1 < S) {
+            lds_barrier();
+            store_k(kb);
+            lds_barrier();
+            fused_load_k(kb, K4, c1 + 2 * kFusedKC, S, tid);
+            chain(c1);
+        }
     }
     lds_barrier();
-
-    // V rows of the first two P.V chunks, in flight through the softmax; rows
-    // past S are clamped (staged, never summed)
-    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd);
-    uint32_t va[2][4], vb[2][4];
-    fused_load_v(va, V2, 0, S, w, lane);
-    fused_load_v(vb, V2, kFusedVC, S, w, lane);
 
     // ---- softmax: wave g < G owns head g's row ------------------------------
     if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane, true);
 
-    // ---- P.V: lane = output (head go, dim d), waves < 2G ----------------------
-    // Staging: wave w gathers positions 4w..4w+3 (+64 on the second pass) of
-    // the chunk, lane l the f16 pair of dims 2l, 2l+1: four row-coalesced
-    // 4-byte loads, then one float4 (4 positions) per dim into vt[d][s].
-    const int go = w >> 1, d = ((w & 1) << 6) | lane;
+    // ---- P.V: wave g < G sums head g, lane = dim 64*half + lane --------------
+    // Chunks alternate between the two register sets, each refilled (two
+    // chunks ahead) once staged.
     float acc = 0.0f;
-    for (int c0 = 0; c0 < S; c0 += kFusedVC) {
-        const int n = min(kFusedVC, S - c0);
+    for (int c0 = 0; c0 < S; c0 += 2 * kFusedVC) {
         lds_barrier();   // softmax done / K rows or the previous V chunk consumed
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-            float4 lo, hi;   // dims 2*lane and 2*lane + 1 at 4 positions
-            float2 f0 = __half22float2(*(const __half2 *)&va[pass][0]);
-            float2 f1 = __half22float2(*(const __half2 *)&va[pass][1]);
-            float2 f2 = __half22float2(*(const __half2 *)&va[pass][2]);
-            float2 f3 = __half22float2(*(const __half2 *)&va[pass][3]);
-            lo = make_float4(f0.x, f1.x, f2.x, f3.x);
-            hi = make_float4(f0.y, f1.y, f2.y, f3.y);
-            const int sr = pass * 64 + 4 * w;
-            *(float4 *)(vt + (2 * lane) * kFusedVS + sr) = lo;
-            *(float4 *)(vt + (2 * lane + 1) * kFusedVS + sr) = hi;
-        }
+        fused_stage_v(vt, va, w, lane);
         lds_barrier();
-        // two chunks in flight while this one is summed
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) va[pass][j] = vb[pass][j];
-        fused_load_v(vb, V2, c0 + 2 * kFusedVC, S, w, lane);
-        if (go < G) acc = pv_chain(sc + go * spad_max + c0, vt + d * kFusedVS, n, acc);
+        fused_load_v(va, V2, c0 + 2 * kFusedVC, S, w, lane);
+        if (w < G) acc = pv_chain(sc + w * spad_max + c0, vt + lane * kFusedVS, min(kFusedVC, S - c0), acc);
+        const int c1 = c0 + kFusedVC;
+        if (c1 < S) {
+            lds_barrier();
+            fused_stage_v(vt, vb, w, lane);
+            lds_barrier();
+            fused_load_v(vb, V2, c1 + 2 * kFusedVC, S, w, lane);
+            if (w < G)
+                acc = pv_chain(sc + w * spad_max + c1, vt + lane * kFusedVS, min(kFusedVC, S - c1), acc);
+        }
     }
-    if (go < G) out[(size_t)(hk * G + go) * kHd + d] = acc;
+    if (w < G) out[(size_t)(hk * G + w) * kHd + 64 * half + lane] = acc;
 }
 
 // LDS of the prefill kernel for R score rows of up to s_max positions
@@ -762,8 +798,9 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
-    const size_t smem = (size_t)G * ((max_seq + 3) & ~3) * sizeof(float);
-    // wide when the narrow grid exceeds ~2 workgroups per CU
+    const size_t smem = (size_t)G * (((max_seq + 3) & ~3) + 4) * sizeof(float);
+    // wide once the narrow grid exceeds one workgroup per CU: co-resident
+    // narrow workgroups share SIMDs, and each repeats the softmax of its G rows
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -773,7 +810,7 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
             cus = 256;
     }
     const long narrow_blocks = (long)Hkv * (kHd / pv_dims_per_wave(G)) * batch;
-    const bool wide = narrow_blocks > 2L * cus;
+    const bool wide = narrow_blocks > cus;
     static size_t configured[2] = {0, 0};
     if (smem > configured[wide]) {
         OXB_CHECK_HIP(hipFuncSetAttribute(
@@ -851,7 +888,7 @@ static int launch_fused(const float *q, const uint16_t *kc, const uint16_t *vc, 
         configured = smem;
     }
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
-    hipLaunchKernelGGL(attn_fused_kernel<G>, dim3(Hkv), dim3(1024), smem, s, q, kc, vc, pos,
+    hipLaunchKernelGGL(attn_fused_kernel<G>, dim3(Hkv, 2), dim3(1024), smem, s, q, kc, vc, pos,
                        max_seq, scale, out);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;

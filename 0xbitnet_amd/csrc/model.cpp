@@ -429,11 +429,11 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
-    // one-kernel decode attention while the cache holds <= 192 positions: it
-    // saves a launch but streams each KV head's cache through one CU, which
-    // loses to the two-kernel path (spread over the chip) beyond ~200
+    // one-kernel decode attention while the cache holds <= 256 positions: it
+    // saves a launch but computes each KV head's scores on two CUs, which
+    // loses to the two-kernel path (scores spread over the chip) beyond ~260
     // positions (MI355X, 2B shape).  OXB_ATTN_FUSED_MAX_S overrides (0: off).
-    m->fused_max_s = 192;
+    m->fused_max_s = 256;
     if (const char *env = getenv("OXB_ATTN_FUSED_MAX_S")) m->fused_max_s = atoi(env);
     if (!oxb_attn_decode_fused_supported(m->H, m->Hkv, m->hd, m->max_seq)) m->fused_max_s = 0;
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);

@@ -248,24 +248,24 @@ __device__ inline float wave_max(float v) {
 }
 
 // exp(x) for the softmax, fixed so that host and device give the same bits:
-// Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2, so k*head is exact,
-// plus the tail), degree-7 Taylor polynomial of e^r by Horner, ldexp by k.
-// Every step is a separately rounded f32 op (no contraction); ~2 ulp.
+// Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2 plus the tail),
+// degree-7 Taylor polynomial of e^r by Horner, ldexp by k.  Every step after
+// the first product is an explicit fused multiply-add (one IEEE rounding,
+// the same on the host's fmaf); ~1 ulp.
 // Branch-free: the polynomial path runs for every x and the special cases
 // are selected afterwards (NaN last), which gives the same value as testing
 // them first and lets many independent exps interleave.
 __device__ inline float oxb_expf(float x) {
     const float kf = rintf(x * 1.44269502f);
-    float r = x - kf * 0.693145751953125f;
-    r = r - kf * 1.42860677e-06f;
-    float p = 1.98412701e-04f;
-    p = p * r + 1.38888892e-03f;
-    p = p * r + 8.33333377e-03f;
-    p = p * r + 4.16666679e-02f;
-    p = p * r + 1.66666672e-01f;
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
+    float r = __builtin_fmaf(-kf, 0.693145751953125f, x);
+    r = __builtin_fmaf(-kf, 1.42860677e-06f, r);
+    float p = __builtin_fmaf(1.98412701e-04f, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
     // |k| <= 150 in range; the clamp keeps the conversion defined elsewhere
     float y = ldexpf(p, (int)fminf(fmaxf(kf, -200.0f), 200.0f));
     y = x > 88.7228394f ? __builtin_inff() : y;

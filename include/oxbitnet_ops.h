@@ -142,10 +142,11 @@ int oxb_attn_decode_batch(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                           int Hkv, int hd, int max_seq, float *scores, float *out, void *stream);
 
-/* The same decode attention as one kernel: one 1024-thread workgroup per KV
- * head computes scores, softmax and P.V in LDS (no scores buffer), same
- * result bits.  Faster for short caches (one CU per KV head streams the
- * whole cache); H/Hkv <= 4 and the LDS of oxb_attn_decode_fused_supported. */
+/* The same decode attention as one kernel: two 1024-thread workgroups per KV
+ * head (one per half of the dims) compute scores, softmax and P.V in LDS (no
+ * scores buffer), same result bits.  Faster for short caches (each KV head's
+ * scores run on two CUs); H/Hkv <= 4 and the LDS of
+ * oxb_attn_decode_fused_supported. */
 int oxb_attn_decode_fused_supported(int H, int Hkv, int hd, int max_seq);
 int oxb_attn_decode_fused(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                           const int *pos, int H, int Hkv, int hd, int max_seq, float *out,

@@ -73,25 +73,24 @@ uint16_t oxo_f32_to_f16(float f) {
 }
 
 /* ------------------------------------------------------------------------ */
-/* exp: Cody-Waite range reduction + degree-7 Taylor polynomial.  Every op is */
-/* a separately rounded f32 op, so the same steps give the same bits on any  */
-/* IEEE machine without FMA contraction.                                     */
+/* exp: Cody-Waite range reduction + degree-7 Taylor polynomial, every step a */
+/* fused multiply-add (fmaf: one IEEE rounding), so the same steps give the  */
+/* same bits on any IEEE machine with a correctly rounded fma.               */
 /* ------------------------------------------------------------------------ */
 float oxo_expf(float x) {
     if (x != x) return x;
     if (x < -103.972084f) return 0.0f;
     if (x > 88.7228394f) return INFINITY;
     const float kf = rintf(x * 1.44269502f);   /* round(x / ln2) */
-    float r = x - kf * 0.693145751953125f;     /* ln2 head: k*head is exact */
-    r = r - kf * 1.42860677e-06f;              /* ln2 tail */
-    float p = 1.98412701e-04f;                 /* 1/7! */
-    p = p * r + 1.38888892e-03f;               /* 1/6! */
-    p = p * r + 8.33333377e-03f;               /* 1/5! */
-    p = p * r + 4.16666679e-02f;               /* 1/4! */
-    p = p * r + 1.66666672e-01f;               /* 1/3! */
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
+    float r = fmaf(-kf, 0.693145751953125f, x); /* ln2 head */
+    r = fmaf(-kf, 1.42860677e-06f, r);          /* ln2 tail */
+    float p = fmaf(1.98412701e-04f, r, 1.38888892e-03f); /* 1/7!, 1/6! */
+    p = fmaf(p, r, 8.33333377e-03f);           /* 1/5! */
+    p = fmaf(p, r, 4.16666679e-02f);           /* 1/4! */
+    p = fmaf(p, r, 1.66666672e-01f);           /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
     return ldexpf(p, (int)kf);
 }
 

@@ -18,8 +18,10 @@
  *   - WGSL inverseSqrt(v) is restated as 1.0f / sqrtf(v);
  *   - WGSL exp() (implementation-defined) is restated as oxo_expf: Cody-Waite
  *     reduction x = k*ln2 + r (ln2 split into a 15-bit head and a tail),
- *     degree-7 Taylor polynomial of e^r by Horner, then ldexp(p, k); max
- *     error ~2 ulp, pinned against double-precision exp in the tests;
+ *     degree-7 Taylor polynomial of e^r by Horner, then ldexp(p, k), every
+ *     step an explicit fmaf (the one place fused ops are used: fmaf is
+ *     correctly rounded on host and device alike); max error ~1 ulp,
+ *     pinned against double-precision exp in the tests;
  *   - WGSL round() is round-half-to-even (rintf), NOT the TS spec's
  *     Math.round (ts/reference.ts:70), which differs on .5 ties;
  *   - workgroup reductions follow the shaders' order exactly: 256 strided
