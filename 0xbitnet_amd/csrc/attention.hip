@@ -6,6 +6,9 @@
 //   softmax  sh/softmax.wgsl:25-80     max; 256 strided partial sums of
 //            exp(x - max) + halving tree; p = exp(x - max) * (1 / sum)
 //   P.V      sh/attention.wgsl:79-105  out[d] = sum_s p[s]*v[s][d] in order of s
+// Each `sum += a * b` step of the dot products and P.V sums is one fused
+// multiply-add (one rounding; WGSL lets the driver contract these, and the
+// restatement fixes the fused form on host and device alike).
 // orchestrated by nn/attention.rs:85-124.  Causally masked positions of the
 // reference (score -3.4e38) contribute exact zeros to every sum, so a query
 // at absolute position `pos` is computed over S = pos + 1 positions.
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
     // this lane's K row into registers; the head's q row is wave-uniform and
     // read with scalar loads, so each step of the chain is one v_fma_mix
-    // (q operand in an SGPR) and one add
+    // (q operand in an SGPR, k converted from f16 inside the instruction)
     uint4 kr16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kr16[i] = ks[lane][i];
@@ -82,8 +85,6 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
         const float *__restrict__ qg = q + (size_t)(hk * G + wu + 4 * h) * kHd;
-        // products as fma(q, k, +0): equal to q*k but for the sign of a zero
-        // product, which cannot change a sum that starts at +0
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -93,10 +94,8 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
             for (int k2 = 0; k2 < 4; ++k2) {
                 const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
                 const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
-                const float m0 = __builtin_fmaf(qg[8 * i + 2 * k2], k0, 0.0f);
-                dot = dot + m0;
-                const float m1 = __builtin_fmaf(qg[8 * i + 2 * k2 + 1], k1, 0.0f);
-                dot = dot + m1;
+                dot = __builtin_fmaf(qg[8 * i + 2 * k2], k0, dot);
+                dot = __builtin_fmaf(qg[8 * i + 2 * k2 + 1], k1, dot);
             }
         }
         scores[(size_t)(hk * G + wu + 4 * h) * max_seq + s] = dot * scale;
@@ -235,7 +234,7 @@ __host__ __device__ constexpr int pv_waves(int G, bool wide) {
     return !wide ? 1 : 2 * G < 4 ? 2 * G : 4;
 }
 
-// acc + sum_{s < n} p[s] * v[s ^ sw], one product and one add at a time in
+// acc + sum_{s < n} p[s] * v[s ^ sw], one fused multiply-add at a time in
 // order of s.  The LDS operands of the next 16 positions are read while the
 // current 16 are summed (p and v 16-byte aligned).  sw is a multiple of 4
 // (an XOR swizzle of the staged row that keeps groups of 4 positions whole).
@@ -252,10 +251,10 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     auto mac = [&](const float4 (&P)[4], const float4 (&V)[4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            float m0 = P[j].x * V[j].x; acc = acc + m0;
-            float m1 = P[j].y * V[j].y; acc = acc + m1;
-            float m2 = P[j].z * V[j].z; acc = acc + m2;
-            float m3 = P[j].w * V[j].w; acc = acc + m3;
+            acc = __builtin_fmaf(P[j].x, V[j].x, acc);
+            acc = __builtin_fmaf(P[j].y, V[j].y, acc);
+            acc = __builtin_fmaf(P[j].z, V[j].z, acc);
+            acc = __builtin_fmaf(P[j].w, V[j].w, acc);
         }
     };
     int s = 0;
@@ -281,15 +280,12 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     for (; s + 4 <= n; s += 4) {
         const float4 p4 = *(const float4 *)(p + s);
         const float4 v4 = *(const float4 *)(v + (s ^ sw));
-        float m0 = p4.x * v4.x; acc = acc + m0;
-        float m1 = p4.y * v4.y; acc = acc + m1;
-        float m2 = p4.z * v4.z; acc = acc + m2;
-        float m3 = p4.w * v4.w; acc = acc + m3;
+        acc = __builtin_fmaf(p4.x, v4.x, acc);
+        acc = __builtin_fmaf(p4.y, v4.y, acc);
+        acc = __builtin_fmaf(p4.z, v4.z, acc);
+        acc = __builtin_fmaf(p4.w, v4.w, acc);
     }
-    for (; s < n; ++s) {
-        float m = p[s] * v[s ^ sw];
-        acc = acc + m;
-    }
+    for (; s < n; ++s) acc = __builtin_fmaf(p[s], v[s ^ sw], acc);
     return acc;
 }
 
@@ -463,8 +459,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
                     const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        float m = qq[e] * kf[e];
-                        dot[r] = dot[r] + m;
+                        dot[r] = __builtin_fmaf(qq[e], kf[e], dot[r]);
                     }
                 }
             }
@@ -507,14 +502,10 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
             for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                float m0 = pc[c].x * v[u4];
-                acc[c] = acc[c] + m0;
-                float m1 = pc[c].y * v[u4 + 1];
-                acc[c] = acc[c] + m1;
-                float m2 = pc[c].z * v[u4 + 2];
-                acc[c] = acc[c] + m2;
-                float m3 = pc[c].w * v[u4 + 3];
-                acc[c] = acc[c] + m3;
+                acc[c] = __builtin_fmaf(pc[c].x, v[u4], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].y, v[u4 + 1], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].z, v[u4 + 2], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].w, v[u4 + 3], acc[c]);
             }
         }
     }
@@ -522,10 +513,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
         const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
 #pragma unroll
         for (int c = 0; c < NC; ++c)
-            if (s < Sc[c]) {
-                float m = sc[rr[c] * Sw + s] * v;
-                acc[c] = acc[c] + m;
-            }
+            if (s < Sc[c]) acc[c] = __builtin_fmaf(sc[rr[c] * Sw + s], v, acc[c]);
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -641,8 +629,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     // 128-term chain of position c0 + pg*64 + lane: the K row from LDS in
     // quarters (the next quarter read while one is summed), the head's q row
     // (wave-uniform) through scalar loads, so each step is one v_fma_mix with
-    // an SGPR operand and one add; products fma(q, k, +0) = q*k up to the
-    // sign of a zero product
+    // an SGPR operand
     auto chain = [&](int c0) {
         const int s = c0 + pg * 64 + lane;
         if (g < G && s < S) {
@@ -668,10 +655,8 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
                     for (int k2 = 0; k2 < 4; ++k2) {
                         const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
                         const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
-                        const float m0 = __builtin_fmaf(qg[d0 + 2 * k2], k0, 0.0f);
-                        dot = dot + m0;
-                        const float m1 = __builtin_fmaf(qg[d0 + 2 * k2 + 1], k1, 0.0f);
-                        dot = dot + m1;
+                        dot = __builtin_fmaf(qg[d0 + 2 * k2], k0, dot);
+                        dot = __builtin_fmaf(qg[d0 + 2 * k2 + 1], k1, dot);
                     }
                 }
             }

@@ -345,20 +345,15 @@ void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
         for (int kp = 0; kp < S; kp++) { /* sh/attention.wgsl:48-58 */
             const float *kv = kc + ((size_t)kp * Hkv + kvh) * hd;
             float dot = 0.0f;
-            for (int d = 0; d < hd; d++) {
-                float m = qv[d] * kv[d];
-                dot = dot + m;
-            }
+            for (int d = 0; d < hd; d++) dot = fmaf(qv[d], kv[d], dot); /* fused: see header */
             int causal = kp > qp + (S - n_tok);
             sc[kp] = causal ? -3.402823e+38f : dot * scale;
         }
         softmax_row(sc, S, pr);
         for (int d = 0; d < hd; d++) { /* sh/attention.wgsl:96-104 */
             float sum = 0.0f;
-            for (int s = 0; s < S; s++) {
-                float m = pr[s] * vc[((size_t)s * Hkv + kvh) * hd + d];
-                sum = sum + m;
-            }
+            for (int s = 0; s < S; s++) /* fused: see header */
+                sum = fmaf(pr[s], vc[((size_t)s * Hkv + kvh) * hd + d], sum);
             out[((size_t)qp * H + h) * hd + d] = sum;
         }
         free(sc);
