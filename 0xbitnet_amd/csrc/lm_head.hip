@@ -58,10 +58,9 @@ __device__ inline bool better(float v, int i, float bv, int bi) {
 
 
 // 8 leaves (half of a 16-leaf group) of one row: 8*NJ pairs = 2*NJ uint4.
-// Each product is fma(h, e, +0): the same value as h*e except that a -0
-// product becomes +0, which cannot change the running sum (it starts at +0
-// and a round-to-nearest sum is -0 only if both terms are -0).  The fma
-// takes the f16 operand directly (v_fma_mix_f32), one op instead of two.
+// Each step of a leaf's sum is one fused multiply-add acc = fma(h, e, acc)
+// (the restatement's rounding for sh/f32_matmul.wgsl's `sum += a * b`) that
+// takes the f16 operand directly (v_fma_mix_f32).
 template <int NJ>
 __device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk) {
     float L[8];
@@ -75,10 +74,8 @@ __device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk
             const float2 hh = hk[u];
             const float e0 = __half2float(__ushort_as_half((uint16_t)(word & 0xffffu)));
             const float e1 = __half2float(__ushort_as_half((uint16_t)(word >> 16)));
-            const float m0 = __builtin_fmaf(hh.x, e0, 0.0f);
-            acc = acc + m0;
-            const float m1 = __builtin_fmaf(hh.y, e1, 0.0f);
-            acc = acc + m1;
+            acc = __builtin_fmaf(hh.x, e0, acc);
+            acc = __builtin_fmaf(hh.y, e1, acc);
         }
         L[m] = acc;
     }

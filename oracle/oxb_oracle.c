@@ -382,11 +382,9 @@ void oxo_lm_head(const float *h, const uint16_t *E, int V, int D, float *logits)
         for (int tid = 0; tid < WG; tid++) { /* sh/f32_matmul.wgsl:51-57 */
             float acc = 0.0f;
             for (int dh = tid; dh < Dh; dh += WG) {
-                int d = dh * 2;
-                float m0 = h[d] * oxo_f16_to_f32(e[d]);
-                acc = acc + m0;
-                float m1 = h[d + 1] * oxo_f16_to_f32(e[d + 1]);
-                acc = acc + m1;
+                int d = dh * 2; /* fused steps: see header */
+                acc = fmaf(h[d], oxo_f16_to_f32(e[d]), acc);
+                acc = fmaf(h[d + 1], oxo_f16_to_f32(e[d + 1]), acc);
             }
             p[tid] = acc;
         }

@@ -16,10 +16,11 @@
  *   - every f32 op is a separately rounded IEEE op: no implicit FMA
  *     contraction (built with -ffp-contract=off).  Explicit fused
  *     multiply-adds (fmaf, one rounding, the same bits on host and device)
- *     are used in two places: the attention dot products and P.V sums
- *     (sh/attention.wgsl:48-58,96-104: `sum += a * b`, which WGSL lets the
+ *     are used in three places: the attention dot products and P.V sums
+ *     (sh/attention.wgsl:48-58,96-104) and the LM-head dot products
+ *     (sh/f32_matmul.wgsl:51-57), all `sum += a * b`, which WGSL lets the
  *     driver contract into an fma, so the reference's own rounding there is
- *     driver-defined) and oxo_expf below;
+ *     driver-defined; and oxo_expf below;
  *   - WGSL inverseSqrt(v) is restated as 1.0f / sqrtf(v);
  *   - WGSL exp() (implementation-defined) is restated as oxo_expf: Cody-Waite
  *     reduction x = k*ln2 + r (ln2 split into a 15-bit head and a tail),
