@@ -223,7 +223,13 @@ def test_attn_decode_bitexact(pos, H, Hkv, S):
 @pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (255, 20, 5, 512),
                                          (256, 20, 5, 512), (300, 20, 5, 408), (511, 20, 5, 512),
                                          (700, 8, 4, 1024), (1500, 20, 5, 4096),
-                                         (4095, 20, 5, 4096), (129, 4, 4, 256)])
+                                         (4095, 20, 5, 4096), (129, 4, 4, 256),
+                                         # K chunk pairs (512 rows) and V chunk pairs exactly,
+                                         # and one past
+                                         (511, 20, 5, 1024), (512, 20, 5, 1024),
+                                         (767, 20, 5, 1024), (1023, 20, 5, 1024),
+                                         # odd lengths: P.V tails of 1..15 positions
+                                         (6, 20, 5, 64), (98, 20, 5, 99)])
 def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     """One-kernel decode attention: same bits as the oracle (and the split path)."""
     assert ops.lib().oxb_attn_decode_fused_supported(H, Hkv, 128, S)
