@@ -188,6 +188,7 @@ __device__ __forceinline__ void wave_softmax_row(float *row, const float *__rest
             else if (nj <= 2) softmax_row_regs<2, true>(row, src, S, Spad, lane);
             else if (nj <= 4) softmax_row_regs<4, true>(row, src, S, Spad, lane);
             else if (nj <= 8) softmax_row_regs<8, true>(row, src, S, Spad, lane);
+            else if (nj <= 10) softmax_row_regs<10, true>(row, src, S, Spad, lane);
             else if (nj <= 12) softmax_row_regs<12, true>(row, src, S, Spad, lane);
             else softmax_row_regs<16, true>(row, src, S, Spad, lane);
         } else {
