@@ -38,6 +38,7 @@ struct oxb_batch {
     float *rope = nullptr;                // [max_seq][hd/2] (cos, sin)
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
     float *scores = nullptr, *logits = nullptr, *xscale = nullptr;
+    float *hn = nullptr;                  // [B][D] LM-head pair tables (normalised rows)
     int *xsum = nullptr;
     void *X = nullptr;                    // token-tiled int8 rows
     int *pinned = nullptr;
@@ -95,8 +96,8 @@ int oxb_batch::enqueue_step() {
         if (gemm_rows(L.wd, (const int8_t *)X, xscale, xsum, L.sd, D, F, B, x, 1, true, s))
             return -1;
     }
-    return oxb_lm_head_argmax_batch(x, (size_t)D, M.final_norm, M.eps, M.embed_lm, M.V, D,
-                                    logits, state, OXB_STATE_INTS, tok_hist, hist_cap, B, 1, s);
+    return lm_head_argmax_rows(x, (size_t)D, M.final_norm, M.eps, M.embed_lm, M.V, D, logits,
+                               state, OXB_STATE_INTS, tok_hist, hist_cap, B, 1, hn, s);
 }
 
 int oxb_batch::capture() {
@@ -161,11 +162,12 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
     b->h = (float *)b->dalloc((size_t)batch * F * 4);
     b->scores = (float *)b->dalloc((size_t)batch * m->H * max_seq * 4);
     b->logits = (float *)b->dalloc((size_t)batch * m->V * 4);
+    b->hn = (float *)b->dalloc((size_t)batch * D * 4);
     b->xscale = (float *)b->dalloc((size_t)rows * 4);
     b->xsum = (int *)b->dalloc((size_t)rows * 4);
     b->X = b->dalloc((size_t)rows * std::max(D, F));
     bool ok = b->kcache && b->vcache && b->state && b->tok_hist && b->rope && b->x && b->q &&
-              b->attn && b->h && b->scores && b->logits && b->xscale && b->xsum && b->X;
+              b->attn && b->h && b->scores && b->logits && b->hn && b->xscale && b->xsum && b->X;
     if (ok && hipHostMalloc((void **)&b->pinned, (size_t)batch * OXB_STATE_INTS * 4,
                             hipHostMallocDefault) != hipSuccess) {
         set_error("hipHostMalloc failed");

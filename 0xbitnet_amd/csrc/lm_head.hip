@@ -86,6 +86,73 @@ __device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk
     return L[0];
 }
 
+// The same 8 leaves for NV rows at once, h read from the global pair table
+// hk [8*NJ][NV] (pair u of every row contiguous): the address is
+// workgroup-uniform, so the pairs arrive through scalar loads and enter each
+// v_fma_mix as SGPR operands (no LDS traffic); one E word feeds NV rows.
+template <int NJ, int NV>
+__device__ inline void lm_half_group_rows(const uint4 (&e)[2 * NJ], const float2 *__restrict__ hk,
+                                          float (&g)[NV]) {
+    float L[NV][8];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) L[v][m] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int u = m * NJ + j;
+            const uint32_t word = (&e[u >> 2].x)[u & 3];
+            const float e0 = __half2float(__ushort_as_half((uint16_t)(word & 0xffffu)));
+            const float e1 = __half2float(__ushort_as_half((uint16_t)(word >> 16)));
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const float2 hh = hk[u * NV + v];
+                L[v][m] = __builtin_fmaf(hh.x, e0, L[v][m]);
+                L[v][m] = __builtin_fmaf(hh.y, e1, L[v][m]);
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+        for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+            for (int m = 0; m < 8; m += 2 * st) L[v][m] = L[v][m] + L[v][m + st];
+        g[v] = L[v][0];
+    }
+}
+
+// Final RMSNorm of row blockIdx.x (sh/rmsnorm.wgsl order, as the LM head's
+// own prologue) into the pair table hn [256*NJ][nv]: pair u of every row of
+// the pass contiguous, in the order the LM head consumes them.
+template <int NJ>
+__global__ __launch_bounds__(256) void lm_norm_pairs_kernel(const float *__restrict__ x,
+                                                             size_t x_stride,
+                                                             const float *__restrict__ gamma,
+                                                             float eps, int D, int nv,
+                                                             float2 *__restrict__ hn) {
+    __shared__ float red[324];
+    const int v = blockIdx.x, tid = threadIdx.x;
+    x += (size_t)v * x_stride;
+    float ss = 0.0f;
+    for (int c = tid; c < D; c += 256) {
+        const float xv = x[c];
+        const float sq = xv * xv;
+        ss = ss + sq;
+    }
+    const float sum = block256_tree_sum_fast(ss, red);
+    const float rms = 1.0f / sqrtf(sum / (float)D + eps);
+    for (int u = tid; u < 256 * NJ; u += 256) {
+        const int i = u / NJ, j = u % NJ;
+        const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
+        const int d0 = 2 * (t + 256 * j);
+        const float a0 = x[d0] * rms, a1 = x[d0 + 1] * rms;
+        hn[(size_t)u * nv + v] = make_float2(a0 * gamma[d0], a1 * gamma[d0 + 1]);
+    }
+}
+
 // One workgroup per lm tile at a time (tiles blockIdx.x + i*gridDim.x); its
 // 4 waves split the tile's 32 half-groups (8 leaves each) 8 apiece and
 // stream them double-buffered, so 20 KiB per wave stay in flight.  The 16
@@ -97,10 +164,12 @@ __device__ inline float lm_half_group(const uint4 (&e)[2 * NJ], const float2 *hk
 // ticket, so the ticket order covers every max.  No cache-wide fences: a
 // release/acquire per block writes back and invalidates the L2 and cost
 // ~0.25 us per block.
-template <int NJ, int NV>  // D = 512 * NJ; NV rows of x (one pass over E)
-__global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
+// HG: the normalised rows come from the pair table p_hn (lm_norm_pairs_kernel)
+// instead of the workgroup's own prologue.
+template <int NJ, int NV, bool HG = false>  // D = 512 * NJ; NV rows of x (one pass over E)
+__global__ __launch_bounds__(256) void lm_head_kernel(LmParams p, const float2 *__restrict__ p_hn) {
     __shared__ float red[324];
-    __shared__ __align__(16) float2 hp[NV][256 * NJ];   // h pairs in consumption order
+    __shared__ __align__(16) float2 hp[HG ? 1 : NV][HG ? 2 : 256 * NJ];   // h pairs in consumption order
     __shared__ float Tl[NV][2][16][64];                  // group sums, double-buffered per tile
     __shared__ float bval[NV][4];
     __shared__ int bidx[NV][4];
@@ -129,7 +198,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
 
     // final RMSNorm (sh/rmsnorm.wgsl order) of each row straight into its pair table
 #pragma unroll 1
-    for (int v = 0; v < NV; ++v) {
+    for (int v = 0; v < (HG ? 0 : NV); ++v) {
         const float *x = p.x + (size_t)v * p.x_stride;
         float ss = 0.0f;
         for (int c = tid; c < D; c += 256) {
@@ -144,10 +213,10 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
             const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
             const int d0 = 2 * (t + 256 * j);
             const float a0 = x[d0] * rms, a1 = x[d0 + 1] * rms;
-            hp[v][u] = make_float2(a0 * p.gamma[d0], a1 * p.gamma[d0 + 1]);
+            if constexpr (!HG) hp[v][u] = make_float2(a0 * p.gamma[d0], a1 * p.gamma[d0 + 1]);
         }
     }
-    __syncthreads();
+    if constexpr (!HG) __syncthreads();
 
     float best[NV];
     int besti[NV];
@@ -180,8 +249,13 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p) {
         }
     };
     auto half_groups = [&](const uint4 (&e)[HQ], int hg, float (&g)[NV]) {
+        if constexpr (HG) {
+            const int hgu = __builtin_amdgcn_readfirstlane(hg);   // wave-uniform
+            lm_half_group_rows<NJ, NV>(e, p_hn + (size_t)hgu * 8 * NJ * NV, g);
+        } else {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) g[v] = lm_half_group<NJ>(e, hp[v] + hg * 8 * NJ);
+            for (int v = 0; v < NV; ++v) g[v] = lm_half_group<NJ>(e, hp[v] + hg * 8 * NJ);
+        }
     };
     int s = 0;
     float g0[NV], g1[NV];
@@ -298,13 +372,16 @@ __global__ void repack_tiled_kernel(const uint4 *__restrict__ src, uint4 *__rest
 
 using namespace oxb;
 
-template <int NV>
-static int lm_launch(const LmParams &p, hipStream_t s) {
+template <int NV, bool HG = false>
+static int lm_launch(const LmParams &p, hipStream_t s, const float2 *hn = nullptr) {
     const int grid = ((p.V + 63) / 64 + 3) / 4;   // 4 tiles per workgroup
     switch (p.D / 512) {
-#define OXB_NL(n)                                                                      \
-    case n:                                                                            \
-        hipLaunchKernelGGL((lm_head_kernel<n, NV>), dim3(grid), dim3(256), 0, s, p);   \
+#define OXB_NL(n)                                                                              \
+    case n:                                                                                    \
+        if constexpr (HG)                                                                      \
+            hipLaunchKernelGGL((lm_norm_pairs_kernel<n>), dim3(NV), dim3(256), 0, s, p.x,      \
+                               p.x_stride, p.gamma, p.eps, p.D, NV, (float2 *)hn);            \
+        hipLaunchKernelGGL((lm_head_kernel<n, NV, HG>), dim3(grid), dim3(256), 0, s, p, hn);   \
         break;
         OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5)
 #undef OXB_NL
@@ -349,6 +426,41 @@ extern "C" int oxb_lm_head_argmax_batch(const float *x, size_t x_stride, const f
     }
     return 0;
 }
+
+namespace oxb {
+// The batched LM head with a workspace hn of n_rows * D floats: rows in passes
+// of 8 (then 4, 2, 1), each pass's normalised rows written once as a pair
+// table that the LM head reads through scalar loads.  Same logits and tokens
+// as oxb_lm_head_argmax_batch.
+int lm_head_argmax_rows(const float *x, size_t x_stride, const float *gamma, float eps,
+                        const void *E, int V, int D, float *logits, int *state, int state_stride,
+                        int *tok_hist, int hist_stride, int n_rows, int advance, float *hn,
+                        void *stream) {
+    OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512,
+                "lm_head: hidden %d must be a multiple of 512 and <= 2560", D);
+    OXB_REQUIRE(V > 0 && n_rows > 0 && hn, "lm_head: vocab %d, %d rows", V, n_rows);
+    OXB_REQUIRE(((uintptr_t)state & 7) == 0 && state_stride % 2 == 0 &&
+                    (n_rows == 1 || state_stride >= OXB_STATE_INTS),
+                "lm_head: state blocks must be 8-byte aligned and not overlap");
+    hipStream_t s = (hipStream_t)stream;
+    for (int r0 = 0; r0 < n_rows;) {
+        const int left = n_rows - r0;
+        const int nv = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        LmParams p{x + (size_t)r0 * x_stride, gamma, eps, (const uint4 *)E, V, D,
+                   logits + (size_t)r0 * V, state + (size_t)r0 * state_stride,
+                   tok_hist ? tok_hist + (size_t)r0 * hist_stride : nullptr, advance,
+                   x_stride, state_stride, hist_stride};
+        const float2 *h = (const float2 *)(hn + (size_t)r0 * D);
+        const int rc = nv == 8   ? lm_launch<8, true>(p, s, h)
+                       : nv == 4 ? lm_launch<4, true>(p, s, h)
+                       : nv == 2 ? lm_launch<2, true>(p, s, h)
+                                 : lm_launch<1, true>(p, s, h);
+        if (rc) return rc;
+        r0 += nv;
+    }
+    return 0;
+}
+}  // namespace oxb
 
 extern "C" int oxb_repack_lm(const uint16_t *E, void *E_lm, int V, int D, void *stream) {
     OXB_REQUIRE(D % 512 == 0 && D <= 5 * 512 && V > 0, "repack_lm: bad shape V %d D %d", V, D);

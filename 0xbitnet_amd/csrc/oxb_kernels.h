@@ -20,4 +20,9 @@ int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int
                   bool gemv_order, void *stream);
 int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
                       float *x, void *stream);
+// Batched LM head with a workspace of n_rows * D floats (lm_head.hip).
+int lm_head_argmax_rows(const float *x, size_t x_stride, const float *gamma, float eps,
+                        const void *E, int V, int D, float *logits, int *state, int state_stride,
+                        int *tok_hist, int hist_stride, int n_rows, int advance, float *hn,
+                        void *stream);
 }  // namespace oxb

@@ -197,7 +197,8 @@ def test_python_bitnet_api():
 @pytest.mark.parametrize("B", [1, 3, 5, 17])
 def test_batched_decode_equals_single_sequences(B):
     """Slots decoded together give each slot's one-sequence tokens and logits
-    bit for bit (B = 17: two token tiles in the GEMMs, LM head groups 4+1)."""
+    bit for bit (B = 17: two token tiles in the GEMMs, LM head passes 8+8+1;
+    B = 5: 4+1)."""
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
     rng = np.random.default_rng(100 + B)
