@@ -6,9 +6,10 @@
 // rs/nn/attention.rs:171-184 (QKV epilogue), sh/activation.wgsl +
 // sh/elementwise.wgsl (gate/up epilogue, residual epilogue).
 //
-// One workgroup (4 waves) owns one 16-row tile.  The 4 waves split the
-// tile's K range into whole 128-blocks; inside a wave lane l streams chunks
-// (row l%16, kc0 + l/16 + 4j), so every wave load is one contiguous KiB.
+// One workgroup (4 or 8 waves) owns one 16-row tile.  Lane l of wave w
+// streams chunks (row l%16, 4 NW j + 4w + l/16): every wave load is one
+// contiguous KiB, and at each step j the workgroup's waves read one
+// contiguous 4 NW KiB stretch of the tile.
 // All loads are branch-free (clamped addresses, masked values; none at all
 // when K is a multiple of 256) so the compiler's memory counters stay exact:
 // the weights are in flight while the prologue runs.  The prologue keeps
@@ -177,9 +178,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     const int lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, c = lane >> 4;
     const int KC = K >> 6;
-    const int per = (((KC + NW - 1) / NW) + 1) & ~1;   // chunks per wave: whole 128-blocks
-    const int kc0 = min(w * per, KC), kc1 = min(KC, kc0 + per);   // empty only if KC < 4 waves
-    const int cpl = (per + 3) >> 2;               // chunks per lane
+    // chunk j of lane (c, wave w): kc = 4 NW j + 4w + c, so at each step the
+    // workgroup's waves read 4 NW consecutive chunks (one contiguous 4 NW KiB
+    // stretch of the tile) rather than NW separate ones
+    const int cpl = (KC + 4 * NW - 1) / (4 * NW);   // chunks per lane
     const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless STREAM)
     const int tile0 = blockIdx.x * TT;
 
@@ -198,8 +200,8 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             const uint4 *tw = p.W + (size_t)(tile0 + t) * KC * 16;
 #pragma unroll
             for (int u = 0; u < PF; ++u) {
-                const int kc = kc0 + c + 4 * (b * PF + u);
-                dst[t][u] = load_nt(tw + (size_t)min(kc, kc1 - 1) * 16 + r);
+                const int kc = 4 * NW * (b * PF + u) + 4 * w + c;
+                dst[t][u] = load_nt(tw + (size_t)min(kc, KC - 1) * 16 + r);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -265,13 +267,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
         lds_barrier();   // the int8 vector is complete
     }
 
-    // ---- main loop: chunks past this wave's range multiply zero codes ------
+    // ---- main loop: chunks past K multiply zero codes -----------------------
     CodeAcc acc[TT];
     auto mac_batch = [&](const uint4 (&src)[TT][PF], int b) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
-            const int kc = kc0 + c + 4 * (b * PF + u);
-            const int kcl = min(kc, kc1 - 1);   // own range (kc1 >= 1)
+            const int kc = 4 * NW * (b * PF + u) + 4 * w + c;
+            const int kcl = min(kc, KC - 1);
             const int xo = (kcl >> 1) * 128 + (kcl & 1) * 16;
             const int4 x0 = *(const int4 *)(xq_lds + xo);
             const int4 x1 = *(const int4 *)(xq_lds + xo + 32);
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             const int4 x3 = *(const int4 *)(xq_lds + xo + 96);
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
-                const uint4 wv = kc < kc1 ? src[t][u] : make_uint4(0, 0, 0, 0);
+                const uint4 wv = kc < KC ? src[t][u] : make_uint4(0, 0, 0, 0);
                 acc[t].add(wv.x, x0.x, x1.x, x2.x, x3.x);
                 acc[t].add(wv.y, x0.y, x1.y, x2.y, x3.y);
                 acc[t].add(wv.z, x0.z, x1.z, x2.z, x3.z);
