@@ -25,12 +25,12 @@ struct ParseError : std::runtime_error {
 struct Reader {
     const uint8_t *p;
     size_t n, off = 0;
-    void need(size_t k) {
-        if (off + k > n) {
+    void need(uint64_t k) {
+        if (k > n - off) {  // off <= n always; this form cannot wrap
             char buf[160];
             snprintf(buf, sizeof buf,
-                     "GGUF parse error: Unexpected EOF at offset %zu (need %zu bytes, have %zu)",
-                     off, k, n);
+                     "GGUF parse error: Unexpected EOF at offset %zu (need %llu bytes, have %zu)",
+                     off, (unsigned long long)k, n);
             throw ParseError(buf);
         }
     }
@@ -51,7 +51,14 @@ struct Reader {
     }
 };
 
-GgufValue read_value(Reader &r, uint32_t ty) {
+// Smallest encoding of one value of each metadata type (a string is its u64
+// length, an array its u32 type + u64 length); 0 for unknown types.
+uint64_t min_value_bytes(uint32_t ty) {
+    static const uint8_t kMin[13] = {1, 1, 2, 2, 4, 4, 4, 1, 8, 12, 8, 8, 8};
+    return ty < 13 ? kMin[ty] : 0;
+}
+
+GgufValue read_value(Reader &r, uint32_t ty, int depth = 0) {
     GgufValue v;
     switch (ty) {
         case 0: v.kind = GgufValue::U64; v.u = r.rd<uint8_t>(); break;
@@ -67,9 +74,12 @@ GgufValue read_value(Reader &r, uint32_t ty) {
             v.kind = GgufValue::ARR;
             uint32_t et = r.rd<uint32_t>();
             uint64_t len = r.rd<uint64_t>();
-            if (len > r.n) throw ParseError("GGUF parse error: array length exceeds file size");
-            v.arr.reserve((size_t)len);
-            for (uint64_t k = 0; k < len; ++k) v.arr.push_back(read_value(r, et));
+            if (depth >= 4) throw ParseError("GGUF parse error: arrays nested more than 4 deep");
+            const uint64_t each = min_value_bytes(et);
+            if (each && len > (r.n - r.off) / each)
+                throw ParseError("GGUF parse error: array length exceeds file size");
+            if (each) v.arr.reserve((size_t)len);
+            for (uint64_t k = 0; k < len; ++k) v.arr.push_back(read_value(r, et, depth + 1));
             break;
         }
         case 10: v.kind = GgufValue::U64; v.u = r.rd<uint64_t>(); break;
@@ -168,7 +178,15 @@ GgufFile *gguf_open(const char *path) {
             t.name = r.str();
             uint32_t nd = r.rd<uint32_t>();
             if (nd > 8) throw ParseError("GGUF parse error: tensor rank > 8");
-            for (uint32_t d = 0; d < nd; ++d) t.shape.push_back(r.rd<uint64_t>());
+            // The element count must not wrap: every stored type takes at
+            // least 54/256 byte per element, so a count above 8x the file
+            // size cannot describe data inside it.
+            uint64_t elems = 1;
+            for (uint32_t d = 0; d < nd; ++d) {
+                t.shape.push_back(r.rd<uint64_t>());
+                if (__builtin_mul_overflow(elems, t.shape.back(), &elems) || elems > 8 * (uint64_t)size)
+                    throw ParseError("GGUF parse error: tensor " + t.name + " element count exceeds file size");
+            }
             t.type = r.rd<uint32_t>();
             t.offset = r.rd<uint64_t>();
             g->tensors.push_back(std::move(t));
@@ -184,7 +202,8 @@ GgufFile *gguf_open(const char *path) {
                 snprintf(buf, sizeof buf, "Unsupported GGML type: %u", t.type);
                 throw ParseError(buf);
             }
-            if (g->data_offset + t.offset + (uint64_t)pb > size) {
+            if (g->data_offset > size || t.offset > size - g->data_offset ||
+                (uint64_t)pb > size - g->data_offset - t.offset) {
                 char buf[256];
                 snprintf(buf, sizeof buf,
                          "GGUF parse error: tensor %s data [%llu, +%lld) exceeds file size %zu",

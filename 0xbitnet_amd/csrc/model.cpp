@@ -160,7 +160,7 @@ bool get_i2s(const GgufFile &g, const GgufTensor *t, const std::string &hf, int 
         return false;
     }
     // GGUF shape is [in, out] (ne0 = K): model/loader.rs:131-133
-    if (t->shape.size() < 2 || (int)t->shape[0] != K || (int)t->shape[1] != N) {
+    if (t->shape.size() < 2 || t->shape[0] != (uint64_t)K || t->shape[1] != (uint64_t)N) {
         set_error("tensor %s: shape [%llu, %llu] does not match [%d, %d]", t->name.c_str(),
                   (unsigned long long)(t->shape.size() > 0 ? t->shape[0] : 0),
                   (unsigned long long)(t->shape.size() > 1 ? t->shape[1] : 0), K, N);
@@ -292,12 +292,29 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->eps = meta_f32(*g, arch, "attention.layer_norm_rms_epsilon", 1e-5f);
     m->rope_theta = meta_f32(*g, arch, "rope.freq_base", is_b25 ? 500000.0f : 10000.0f);
     m->relu2 = is_b25;
-    m->hd = m->D / m->H;
     m->max_seq = max_seq > 0 ? max_seq : 4096;  // lib.rs:93
+    // Metadata is untrusted: every count must be positive and fit the int
+    // arithmetic below, and each layer needs at least nine tensors in the file
+    // (seven ternary, two norms), which bounds block_count before anything is
+    // sized by it.
+    const uint32_t kMaxDim = 1u << 20;
+    for (int v : {m->D, m->F, m->H, m->Hkv, m->V, m->n_layers}) {
+        if (v <= 0 || (uint32_t)v > kMaxDim) {
+            set_error("invalid model metadata: layers %d hidden %d ffn %d heads %d kv_heads %d vocab %d",
+                      m->n_layers, m->D, m->F, m->H, m->Hkv, m->V);
+            return nullptr;
+        }
+    }
+    if ((size_t)m->n_layers * 9 > g->tensors.size()) {
+        set_error("invalid model metadata: block_count %d but the file holds %zu tensors", m->n_layers,
+                  g->tensors.size());
+        return nullptr;
+    }
+    m->hd = m->D / m->H;
     const int D = m->D, F = m->F, H = m->H, Hkv = m->Hkv, hd = m->hd;
     const int Dq = H * hd, Dkv = Hkv * hd;
     log_msg(1, "config: arch=%s layers=%d hidden=%d ffn=%d heads=%d kv_heads=%d head_dim=%d vocab=%d",
-            arch.c_str(), m->n_layers, D, F, H, Hkv, hd, m->V);
+            arch.c_str(), m->n_layers, m->D, m->F, m->H, m->Hkv, m->hd, m->V);
     if (hd != 128 || D % H != 0) {
         set_error("unsupported shape: head_dim %d (hidden %d / heads %d); the kernels need 128", hd, D, H);
         return nullptr;
@@ -340,7 +357,7 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
                 }
                 continue;
             }
-            if ((int)ls.norm[k]->n_elements() != norm_dim[k] ||
+            if (ls.norm[k]->n_elements() != (uint64_t)norm_dim[k] ||
                 (ls.norm[k]->type != GGML_F32 && ls.norm[k]->type != GGML_F16)) {
                 set_error("tensor %s: expected %d F32/F16 elements", ls.norm[k]->name.c_str(), norm_dim[k]);
                 return nullptr;

@@ -106,6 +106,50 @@ def test_missing_tensor_error(tmp_path):
     assert _err() == 'Missing weight tensor: "model.layers.0.self_attn.q_proj.weight"'
 
 
+def _patch_u32_meta(data: bytes, key: str, value: int) -> bytes:
+    """Overwrite the u32 value of metadata `key` in a GGUF image."""
+    i = data.find(synth._s(key))
+    assert i > 0
+    j = i + len(synth._s(key))
+    assert struct.unpack_from("<I", data, j)[0] == 4   # GGUF u32
+    return data[:j + 4] + struct.pack("<I", value) + data[j + 8:]
+
+
+def test_corrupt_metadata_is_rejected_before_sizing(tmp_path):
+    """Counts read from the file are checked before anything is sized or
+    divided by them; malformed lengths are parse errors, not allocations."""
+    cfg = synth.small_config(n_layers=1, vocab=300)
+    path = str(tmp_path / "m.gguf")
+    synth.write_gguf(path, cfg, seed=3)
+    data = open(path, "rb").read()
+    L = nat.lib()
+    a = "bitnet-25"
+    for key, val, msg in ((f"{a}.block_count", 0xF0000000, "invalid model metadata"),
+                          (f"{a}.block_count", 1000, "invalid model metadata: block_count 1000 but the file holds 13"),
+                          (f"{a}.attention.head_count", 0, "invalid model metadata"),
+                          (f"{a}.attention.head_count_kv", 0, "invalid model metadata"),
+                          (f"{a}.embedding_length", 0x80000000, "invalid model metadata")):
+        assert not L.oxbitnet_load(_write(tmp_path, "c.gguf", _patch_u32_meta(data, key, val)), None)
+        assert _err().startswith(msg), (key, val, _err())
+    hdr = struct.pack("<IIQQ", 0x46554747, 3, 0, 1)
+    # string length near 2^64: must not wrap the bounds check
+    assert not L.oxbitnet_load(_write(tmp_path, "s.gguf", hdr + struct.pack("<Q", 2**64 - 4)), None)
+    assert _err().startswith("GGUF parse error: Unexpected EOF")
+    # u32 array claiming more elements than bytes remain
+    arr = synth._s("x") + struct.pack("<IIQ", 9, 4, 1 << 40)
+    assert not L.oxbitnet_load(_write(tmp_path, "a.gguf", hdr + arr), None)
+    assert _err() == "GGUF parse error: array length exceeds file size"
+    # arrays nested deeper than any GGUF writer produces
+    nest = synth._s("x") + struct.pack("<I", 9) + struct.pack("<IQ", 9, 1) * 6 + struct.pack("<IQ", 4, 0)
+    assert not L.oxbitnet_load(_write(tmp_path, "n.gguf", hdr + nest), None)
+    assert _err() == "GGUF parse error: arrays nested more than 4 deep"
+    # tensor whose element count wraps 2^64
+    t = synth._s("w") + struct.pack("<I", 2) + struct.pack("<QQ", 2**33, 2**31) + struct.pack("<IQ", 0, 0)
+    assert not L.oxbitnet_load(_write(tmp_path, "t.gguf", struct.pack("<IIQQ", 0x46554747, 3, 1, 0) + t),
+                               None)
+    assert _err() == "GGUF parse error: tensor w element count exceeds file size"
+
+
 def test_synthetic_writer_roundtrip(tmp_path):
     import oracle as O
     cfg = synth.small_config(n_layers=1, vocab=300)
