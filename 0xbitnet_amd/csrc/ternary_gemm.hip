@@ -17,8 +17,11 @@
 // reference's int32 accumulator: acc = C(codes) - sum_k x[t][k].
 //
 // Token-tiled activation layout (written by oxb_quantize_rows_tiled):
-//   [n_tok/16 tiles][KC][16 tokens][64 B], 64 B = planes g = 0..3 x 16 B of
-//   x[t][(kc/2)*128 + g*32 + (kc%2)*16 + 0..15].
+//   [n_tok/16 tiles][K/256 stages][4 planes g][4 chunks c][16 tokens][16 B],
+//   the 16 B of (g, chunk kc = 4*stage + c, token t) being
+//   x[t][(kc/2)*128 + g*32 + (kc%2)*16 + 0..15].  For one plane, the B
+//   operands of a stage's four chunks are 1 KB in lane order, so global
+//   loads, LDS stores and LDS operand reads are all contiguous per wave.
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
@@ -68,22 +71,60 @@ __device__ inline v4i as_v4i(uint4 u) {
     return a;
 }
 
-// Epilogue for one lane's 4 accumulators: features n0 .. n0+3 of token t.
+// Epilogue inputs, loaded in two groups before any result is stored so that a
+// lane's loads are in flight together: per token (xsum, xscale, position) and
+// per tile (RESID: the old residual; QKV: the RoPE (cos, sin) of the tile's
+// two pairs).  Tokens past n_tok read token n_tok-1's values; their results
+// are never stored.
+struct EpiTok {
+    int xs;
+    float is;
+    int pos;
+};
+
 template <int EPI>
-__device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int n0) {
-    const int xs = p.xsum[t];
-    const float is = p.xscale[t];
+__device__ inline EpiTok epi_tok(const GemmParams &p, int t) {
+    const int tc = min(t, p.n_tok - 1);
+    EpiTok e;
+    e.xs = p.xsum[tc];
+    e.is = p.xscale[tc];
+    e.pos = 0;
+    if constexpr (EPI == GE_QKV)
+        e.pos = p.tok_pos ? p.tok_pos[(size_t)tc * p.tok_pos_stride] : p.pos0 + tc;
+    return e;
+}
+
+template <int EPI>
+__device__ inline float4 epi_old(const GemmParams &p, int t, int n0, const EpiTok &e) {
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (EPI == GE_RESID) {
+        o = *(const float4 *)(p.Y + (size_t)min(t, p.n_tok - 1) * p.N + n0);
+    } else if constexpr (EPI == GE_QKV) {
+        if (n0 < p.Dq + p.Dkv && e.pos >= 0 && e.pos < p.max_seq) {
+            const int d0 = (n0 < p.Dq ? n0 : n0 - p.Dq) % p.hd;   // multiple of 4
+            o = *(const float4 *)(p.rope + (size_t)e.pos * (p.hd >> 1) + (d0 >> 1));
+        }
+    }
+    return o;
+}
+
+// Epilogue for one lane's 4 accumulators: features n0 .. n0+3 of token t, with
+// ws = wscale[n0 .. n0+3] and the inputs above.
+template <int EPI>
+__device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int n0,
+                                  const EpiTok &e, const float4 &ws4, const float4 &old) {
+    const float ws[4] = {ws4.x, ws4.y, ws4.z, ws4.w};
     float y[4];
     int32_t a[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        a[v] = c[v] - xs;
+        a[v] = c[v] - e.xs;
         if (p.gemv_order) {
-            y[v] = (float)a[v] * p.wscale[n0 + v];
-            y[v] = y[v] * is;
+            y[v] = (float)a[v] * ws[v];
+            y[v] = y[v] * e.is;
         } else {
             // shaders/ternary_gemm.wgsl:132-133: f32(acc) * (w_scale * in_scale)
-            const float sc = p.wscale[n0 + v] * is;
+            const float sc = ws[v] * e.is;
             y[v] = (float)a[v] * sc;
         }
     }
@@ -91,28 +132,25 @@ __device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int 
     if constexpr (EPI == GE_STORE) {
         *(float4 *)(p.Y + (size_t)t * p.N + n0) = make_float4(y[0], y[1], y[2], y[3]);
     } else if constexpr (EPI == GE_RESID) {
-        float4 *dst = (float4 *)(p.Y + (size_t)t * p.N + n0);
-        float4 o = *dst;
-        o.x = o.x + y[0]; o.y = o.y + y[1]; o.z = o.z + y[2]; o.w = o.w + y[3];
-        *dst = o;
+        *(float4 *)(p.Y + (size_t)t * p.N + n0) =
+            make_float4(old.x + y[0], old.y + y[1], old.z + y[2], old.w + y[3]);
     } else if constexpr (EPI == GE_GATEUP) {
         float g0 = fmaxf(0.0f, y[0]), g1 = fmaxf(0.0f, y[2]);
         g0 = g0 * g0;
         g1 = g1 * g1;
         *(float2 *)(p.Y + (size_t)t * (p.N >> 1) + (n0 >> 1)) = make_float2(g0 * y[1], g1 * y[3]);
     } else {  // GE_QKV
-        const int pos = p.tok_pos ? p.tok_pos[(size_t)t * p.tok_pos_stride] : p.pos0 + t;
+        const int pos = e.pos;
         if (pos < 0 || pos >= p.max_seq) return;   // host checks too; never write out of range
         const int Dk = p.Dq + p.Dkv;
         float o[4] = {y[0], y[1], y[2], y[3]};
         if (n0 < Dk) {
-            const int d0 = (n0 < p.Dq ? n0 : n0 - p.Dq) % p.hd;
+            const float2 cs[2] = {make_float2(old.x, old.y), make_float2(old.z, old.w)};
 #pragma unroll
             for (int pr = 0; pr < 2; ++pr) {
-                const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d0 >> 1) + pr];
                 const float x0 = y[2 * pr], x1 = y[2 * pr + 1];
-                float a0 = x0 * cs.x, a1 = x1 * cs.y;
-                float b0 = x0 * cs.y, b1 = x1 * cs.x;
+                float a0 = x0 * cs[pr].x, a1 = x1 * cs[pr].y;
+                float b0 = x0 * cs[pr].y, b1 = x1 * cs[pr].x;
                 o[2 * pr] = a0 - a1;
                 o[2 * pr + 1] = b0 + b1;
             }
@@ -152,8 +190,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 
     const uint4 *Wt0 = p.W + (size_t)(f0 >> 4) * KC * 16;
     const uint4 *Wt1 = p.W + (size_t)((f1ok ? f0 + 16 : f0) >> 4) * KC * 16;
-    const uint4 *Xt0 = p.X + ((size_t)tt0 * KC * 16) * 4;
-    const uint4 *Xt1 = p.X + ((size_t)(t1ok ? tt0 + 1 : tt0) * KC * 16) * 4;
+    const uint4 *Xt0 = p.X + (size_t)tt0 * KC * 64 + q * 16 + r;
+    const uint4 *Xt1 = p.X + (size_t)(t1ok ? tt0 + 1 : tt0) * KC * 64 + q * 16 + r;
 
     const int steps = KC >> 2;
     uint4 wa[2], xa[2][4];
@@ -161,12 +199,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
         const int kc = 4 * s + q;
         wv[0] = load_nt(Wt0 + (size_t)kc * 16 + r);
         wv[1] = load_nt(Wt1 + (size_t)kc * 16 + r);
-        const uint4 *x0 = Xt0 + ((size_t)kc * 16 + r) * 4;
-        const uint4 *x1 = Xt1 + ((size_t)kc * 16 + r) * 4;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            xv[0][g] = x0[g];
-            xv[1][g] = x1[g];
+            xv[0][g] = Xt0[(size_t)(4 * s + g) * 64];
+            xv[1][g] = Xt1[(size_t)(4 * s + g) * 64];
         }
     };
     load(0, wa, xa);
@@ -193,6 +229,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     }
 
     // epilogue: lane holds features n = f0 + ft*16 + 4q + v of token t
+    const int fn[2] = {f0 + 4 * q, (f1ok ? f0 + 16 : f0) + 4 * q};
+    EpiTok e[2];
+    float4 ws[2], old[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) e[tt] = epi_tok<EPI>(p, (tt0 + tt) * 16 + r);
+#pragma unroll
+    for (int ft = 0; ft < 2; ++ft) {
+        ws[ft] = *(const float4 *)(p.wscale + fn[ft]);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) old[ft][tt] = epi_old<EPI>(p, (tt0 + tt) * 16 + r, fn[ft], e[tt]);
+    }
 #pragma unroll
     for (int ft = 0; ft < 2; ++ft) {
         if (ft == 1 && !f1ok) continue;
@@ -201,28 +248,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             if (tt == 1 && !t1ok) continue;
             const int t = (tt0 + tt) * 16 + r;
             if (t >= p.n_tok) continue;
-            gemm_store<EPI>(p, acc[ft][tt], t, f0 + ft * 16 + 4 * q);
+            gemm_store<EPI>(p, acc[ft][tt], t, fn[ft], e[tt], ws[ft], old[ft][tt]);
         }
     }
 }
 
 
 // ---------------------------------------------------------------------------
-// LDS-staged GEMM for n_tok > 64.  Workgroup tile: 32*FW features x 32*TW
-// tokens; 4 waves in a 2x2 grid, each FW x TW MFMA tiles of 16x16, so every
-// A operand (a weight plane) feeds TW MFMAs and every B operand FW.  K runs
-// in stages of 4 chunks (256 k), double-buffered in LDS; the weights stay
-// 2-bit in LDS and are unpacked into A operands in registers.
-//   W stage: [32FW rows][4 chunks] x 16 B; chunk c of row f at slot
-//            4f + (c ^ (f/4 % 4)): 16 lanes reading (row r, chunk q) and 16
-//            lanes writing (chunk c, row r) both hit 16 distinct bank groups.
-//   X stage: [32TW tokens][16 units] x 16 B, unit u = 4c + g (chunk c, plane
-//            g); unit u of token t at slot 16t + (u ^ (5t % 16)): readers
-//            (tokens r = 0..15, one unit) and writers (tokens r = 0..3 x 4
-//            planes) both hit 16 distinct bank groups.
-// Token tiles past the activation buffer are clamped to its last tile; their
+// LDS-staged GEMM for n_tok > 64, on v_mfma_i32_32x32x32_i8 (A = 32x32,
+// B = 32x32, C = 32x32 in 16 registers).  On gfx950 one wave issues this
+// MFMA at ~85% of the chip's int8 rate, against ~50% for 16x16x64, so the
+// product keeps its rate while the other wave of a SIMD waits on a barrier.
+//   A: lane l supplies feature row l%32 of a 32-row tile and 16 codes of
+//      chunk 2cp + l/32 of the stage's chunk pair cp, one bit plane g at a
+//      time (4 planes per packed 16 B).
+//   B: lane l supplies token l%32 of a 32-token tile and the same 16 k.
+//   C: lane l holds features 8(v/4) + 4(l/32) + v%4 (v = 0..15) of token l%32.
+// Workgroup tile: 32*MF*NWF features x 64*MT tokens; NWF x 2 waves (NWF
+// along features), each MF x MT MFMA tiles.  The 256 x 128 tile (NWF = 4,
+// 512 threads, one workgroup per CU) stages 40% fewer bytes per output than
+// two 128 x 128 workgroups; staging is the largest cost after the MFMAs.  K runs in stages of 4 chunks (256 k), double-buffered
+// in LDS; the weights stay 2-bit in LDS and are unpacked in registers.  The
+// stage buffers are ordered so that each operand read is one contiguous 1 KB
+// in lane order (the ds_read_b128 pattern that runs at full LDS rate on
+// gfx950; bank-permuting swizzles measured at half rate):
+//   W stage: [2 chunk pairs cp][2MF row pairs][2 chunks h][2 tiles][16 rows]
+//   X stage: [4 planes g][2 chunk pairs cp][2MT token pairs][2 chunks h]
+//            [2 tiles][16 tokens]   (16 B units)
+// Each thread stages the units whose LDS slots are tid + 256k, so the LDS
+// writes are contiguous too; their global sources are 256 B runs.  Token
+// tiles past the activation buffer are clamped to its last tile; their
 // accumulators are never stored.
 // ---------------------------------------------------------------------------
+typedef int v16i __attribute__((ext_vector_type(16)));
+
 // Staging of one stage: this thread's WPT weight and XPT activation units
 // (global offsets of stage 0 in uint4; stage st is 64 uint4 of W and 256 of
 // X further) into registers, and from registers into its LDS slots.
@@ -238,115 +297,233 @@ __device__ __forceinline__ void gemm_stage_load(u32x4_t (&rw)[WPT], u32x4_t (&rx
     for (int k = 0; k < XPT; ++k) rx[k] = *(const u32x4_t *)(X + xsrc[k] + (size_t)st * 256);
 }
 
-template <int WPT, int XPT>
+template <int WPT, int XPT, int NTH>
 __device__ __forceinline__ void gemm_stage_store(const u32x4_t (&rw)[WPT],
                                                  const u32x4_t (&rx)[XPT], uint4 *swb,
-                                                 uint4 *sxb, const int (&wdst)[WPT],
-                                                 const int (&xdst)[XPT]) {
+                                                 uint4 *sxb, int tid) {
 #pragma unroll
-    for (int k = 0; k < WPT; ++k) *(u32x4_t *)(swb + wdst[k]) = rw[k];
+    for (int k = 0; k < WPT; ++k) *(u32x4_t *)(swb + tid + NTH * k) = rw[k];
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) *(u32x4_t *)(sxb + xdst[k]) = rx[k];
+    for (int k = 0; k < XPT; ++k) *(u32x4_t *)(sxb + tid + NTH * k) = rx[k];
 }
 
-// One LDS stage (4 chunks) of a wave's FW x TW tiles: per plane g, FW A
-// operands unpacked from the 2-bit weights and TW B operands, FW*TW MFMAs.
-// Slots follow the swizzles of gemm_lds_kernel's stage layouts.
-template <int FW, int TW>
-__device__ __forceinline__ void gemm_mma_stage(v4i (&acc)[FW][TW], const uint4 *swb,
-                                               const uint4 *sxb, int wf, int wt, int r, int q) {
-    uint4 wu[FW];
+// One LDS stage of a wave's MF x MT tiles (wf, wt: its first row pair and
+// token pair in the workgroup; NF, NT: the workgroup's row and token pairs).
+template <int MF, int MT, int NF, int NT>
+__device__ __forceinline__ void gemm_mma_stage(v16i (&acc)[MF][MT], const uint4 *swb,
+                                               const uint4 *sxb, int wf, int wt, int l) {
 #pragma unroll
-    for (int i = 0; i < FW; ++i) {
-        const int f = (wf + i) * 16 + r;
-        wu[i] = swb[4 * f + (q ^ ((f >> 2) & 3))];
-    }
+    for (int cp = 0; cp < 2; ++cp) {
+        uint4 wu[MF];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        v4i a[FW];
+        for (int i = 0; i < MF; ++i) wu[i] = swb[(cp * NF + wf + i) * 64 + l];
 #pragma unroll
-        for (int i = 0; i < FW; ++i) a[i] = plane(wu[i], g);
+        for (int g = 0; g < 4; ++g) {
+            v4i a[MF];
 #pragma unroll
-        for (int j = 0; j < TW; ++j) {
-            const int t = (wt + j) * 16 + r;
-            const v4i bv = as_v4i(sxb[16 * t + (((q << 2) | g) ^ ((5 * t) & 15))]);
+            for (int i = 0; i < MF; ++i) a[i] = plane(wu[i], g);
 #pragma unroll
-            for (int i = 0; i < FW; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bv, acc[i][j], 0, 0, 0);
+            for (int j = 0; j < MT; ++j) {
+                const v4i bv = as_v4i(sxb[((g * 2 + cp) * NT + wt + j) * 64 + l]);
+#pragma unroll
+                for (int i = 0; i < MF; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bv, acc[i][j], 0, 0, 0);
+            }
         }
     }
 }
 
-template <int EPI, int FW, int TW>
-__global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmParams p) {
-    constexpr int FT = 32 * FW, TK = 32 * TW;      // features, tokens per workgroup
+// Epilogue of the LDS-staged kernels: register v of tile (i, j) holds feature
+// 32(fp) + 8(v/4) + 4(l/32) + v%4 of token 32(tp) + l%32; stored as 4 groups
+// of 4 consecutive features, with every input loaded before the first store.
+template <int EPI, int MF, int MT>
+__device__ __forceinline__ void gemm_lds_epilogue(const GemmParams &p, const v16i (&acc)[MF][MT],
+                                                  int ftile0, int ttile0, int wf, int wt, int l) {
+    EpiTok e[MT];
+    float4 ws[MF][4], old[MF][MT][4];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) e[j] = epi_tok<EPI>(p, (ttile0 + 2 * (wt + j)) * 16 + (l & 31));
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+            const int n0 = (ftile0 + 2 * (wf + i)) * 16 + 8 * v4 + 4 * (l >> 5);
+            ws[i][v4] = *(const float4 *)(p.wscale + n0);
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+                old[i][j][v4] = epi_old<EPI>(p, (ttile0 + 2 * (wt + j)) * 16 + (l & 31), n0, e[j]);
+        }
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+            const int t = (ttile0 + 2 * (wt + j)) * 16 + (l & 31);
+            if (t >= p.n_tok) continue;
+#pragma unroll
+            for (int v4 = 0; v4 < 4; ++v4) {
+                const v4i c = {acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2],
+                               acc[i][j][4 * v4 + 3]};
+                gemm_store<EPI>(p, c, t, (ftile0 + 2 * (wf + i)) * 16 + 8 * v4 + 4 * (l >> 5), e[j],
+                                ws[i][v4], old[i][j][v4]);
+            }
+        }
+}
+
+template <int EPI, int MF, int MT, int NWF>
+__global__ __launch_bounds__(128 * NWF, 4 / NWF) void gemm_lds_kernel(GemmParams p) {
+    constexpr int NTH = 128 * NWF;                 // threads
+    constexpr int NF = NWF * MF, NT = 2 * MT;      // 32-row / 32-token pairs per workgroup
+    constexpr int FT = 32 * NF, TK = 32 * NT;      // features, tokens per workgroup
     constexpr int WU = FT * 4, XU = TK * 16;       // 16-byte units per stage
-    constexpr int WPT = WU / 256, XPT = XU / 256;  // per thread
+    constexpr int WPT = WU / NTH, XPT = XU / NTH;  // per thread
+    static_assert(WPT * NTH == WU && XPT * NTH == XU, "stage units must split evenly");
     __shared__ uint4 sw[2][WU];
     __shared__ uint4 sx[2][XU];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int r = lane & 15, q = lane >> 4;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
     const int KC = p.K >> 6, steps = KC >> 2;
     const int ftile0 = blockIdx.x * (FT / 16), ttile0 = blockIdx.y * (TK / 16);
     const int ntt = (p.n_tok + 15) >> 4;
-    const int wf = (w & 1) * FW, wt = (w >> 1) * TW;   // this wave's local tiles
+    const int wf = (w % NWF) * MF, wt = (w / NWF) * MT;   // this wave's row / token pairs
 
-    // this thread's staging units: W unit tid + 256k is (local tile fi, chunk
-    // c, row rr); X unit tid + 256k is (local tile ti, chunk c, token rr, plane g)
-    size_t wsrc[WPT], xsrc[XPT];   // global offsets of stage 0, in uint4
-    int wdst[WPT], xdst[XPT];      // LDS slots
+    // global sources of this thread's LDS slots i = tid + NTH*k (stage 0);
+    // within a slot's 64-unit block, unit u = 32h + 16*tile + row/token
+    size_t wsrc[WPT], xsrc[XPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int i = tid + 256 * k, fi = i >> 6, c = (i >> 4) & 3, rr = i & 15;
-        const int f = (fi << 4) | rr;
-        wsrc[k] = ((size_t)(ftile0 + fi) * KC + c) * 16 + rr;
-        wdst[k] = 4 * f + (c ^ ((f >> 2) & 3));
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int cp = blk / NF, fp = blk % NF, h = u >> 5, ft = 2 * fp + ((u >> 4) & 1);
+        wsrc[k] = ((size_t)(ftile0 + ft) * KC + 2 * cp + h) * 16 + (u & 15);
     }
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
-        const int i = tid + 256 * k, ti = i >> 8, c = (i >> 6) & 3, rr = (i >> 2) & 15, g = i & 3;
-        const int tt = min(ttile0 + ti, ntt - 1), t = (ti << 4) | rr, u = (c << 2) | g;
-        xsrc[k] = (((size_t)tt * KC + c) * 16 + rr) * 4 + g;
-        xdst[k] = 16 * t + (u ^ ((5 * t) & 15));
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int tp = blk % NT, gc = blk / NT, cp = gc & 1, g = gc >> 1, h = u >> 5;
+        const int tt = min(ttile0 + 2 * tp + ((u >> 4) & 1), ntt - 1);
+        xsrc[k] = (size_t)tt * KC * 64 + g * 64 + (2 * cp + h) * 16 + (u & 15);
     }
-    v4i acc[FW][TW];
+    v16i acc[MF][MT];
 #pragma unroll
-    for (int i = 0; i < FW; ++i)
+    for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int j = 0; j < TW; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     // Two register sets hold stages s+1 and s+2 while stage s is multiplied,
     // so each stage's loads have two stages of MFMA work to arrive.  Loads
     // past the last stage reload the last one (branch-free; never stored).
+    // The scheduling barriers keep each stage's loads at the top of its half
+    // (left alone, the compiler sinks them below the MFMAs) and its stores
+    // after the MFMAs.
     u32x4_t aw[WPT], ax[XPT], bw[WPT], bx_[XPT];
     const int last = steps - 1;
     gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, 0);
-    gemm_stage_store(aw, ax, sw[0], sx[0], wdst, xdst);
+    gemm_stage_store<WPT, XPT, NTH>(aw, ax, sw[0], sx[0], tid);
     gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(1, last));
     lds_barrier();
-    // iteration s: load stage s+2, multiply stage s (buffer s&1), store stage
-    // s+1 into the idle buffer (its last reads ended before the previous barrier)
     int s = 0;
     for (; s + 2 <= steps; s += 2) {
         gemm_stage_load(bw, bx_, p.W, p.X, wsrc, xsrc, min(s + 2, last));
-        gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);
-        gemm_stage_store(aw, ax, sw[1], sx[1], wdst, xdst);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_mma_stage<MF, MT, NF, NT>(acc, sw[0], sx[0], wf, wt, l);
+        gemm_stage_store<WPT, XPT, NTH>(aw, ax, sw[1], sx[1], tid);
         lds_barrier();
         gemm_stage_load(aw, ax, p.W, p.X, wsrc, xsrc, min(s + 3, last));
-        gemm_mma_stage<FW, TW>(acc, sw[1], sx[1], wf, wt, r, q);
-        gemm_stage_store(bw, bx_, sw[0], sx[0], wdst, xdst);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_mma_stage<MF, MT, NF, NT>(acc, sw[1], sx[1], wf, wt, l);
+        gemm_stage_store<WPT, XPT, NTH>(bw, bx_, sw[0], sx[0], tid);
         lds_barrier();
     }
-    if (s < steps) gemm_mma_stage<FW, TW>(acc, sw[0], sx[0], wf, wt, r, q);   // odd count: buffer 0
+    if (s < steps) gemm_mma_stage<MF, MT, NF, NT>(acc, sw[0], sx[0], wf, wt, l);   // odd count: buffer 0
 
-    // epilogue: lane holds features 16 ftile + 4q + v of token 16 ttile + r
+    gemm_lds_epilogue<EPI, MF, MT>(p, acc, ftile0, ttile0, wf, wt, l);
+}
+
+// The same tiles with direct global -> LDS staging (global_load_lds_dwordx4:
+// each lane's 16 B land at the wave's LDS base + 16 * lane, which is exactly
+// the slot order above), so staging takes no VGPRs and no LDS store
+// instructions.  Three stage buffers (144 KB at 256 x 128) let each stage's
+// loads be issued two stages ahead, with one barrier per stage:
+//   iteration s: wait for this thread's stage-s loads (stage s+1 may still be
+//   in flight), barrier (every thread's stage s has landed, and every wave is
+//   done reading the buffer that stage s+2 reuses), issue stage s+2, multiply
+//   stage s.
+// The loads are issued from inline assembly with explicit vmcnt waits: the
+// compiler's builtin for them makes every later LDS read wait for all
+// outstanding loads, which would serialise the prefetch.  The compiler does
+// not count these loads, so its own vmcnt waits can only come out stricter.
+__device__ __forceinline__ void lds_dma16(const void *g, const uint4 *lds_wave_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(g)
+                 : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // s_waitcnt immediate: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int EPI, int MF, int MT, int NWF>
+__global__ __launch_bounds__(128 * NWF, 1) void gemm_dma_kernel(GemmParams p) {
+    constexpr int NTH = 128 * NWF;
+    constexpr int NF = NWF * MF, NT = 2 * MT;
+    constexpr int FT = 32 * NF, TK = 32 * NT;
+    constexpr int WU = FT * 4, XU = TK * 16;
+    constexpr int WPT = WU / NTH, XPT = XU / NTH, LPT = WPT + XPT;
+    static_assert(WPT * NTH == WU && XPT * NTH == XU, "stage units must split evenly");
+    __shared__ uint4 sw[3][WU];
+    __shared__ uint4 sx[3][XU];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    const int KC = p.K >> 6, steps = KC >> 2;
+    const int ftile0 = blockIdx.x * (FT / 16), ttile0 = blockIdx.y * (TK / 16);
+    const int ntt = (p.n_tok + 15) >> 4;
+    const int wf = (w % NWF) * MF, wt = (w / NWF) * MT;
+
+    // global sources of this thread's LDS slots i = tid + NTH*k (stage 0),
+    // as in gemm_lds_kernel
+    const uint4 *wsrc[WPT], *xsrc[XPT];
 #pragma unroll
-    for (int i = 0; i < FW; ++i)
+    for (int k = 0; k < WPT; ++k) {
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int cp = blk / NF, fp = blk % NF, h = u >> 5, ft = 2 * fp + ((u >> 4) & 1);
+        wsrc[k] = p.W + ((size_t)(ftile0 + ft) * KC + 2 * cp + h) * 16 + (u & 15);
+    }
 #pragma unroll
-        for (int j = 0; j < TW; ++j) {
-            const int t = (ttile0 + wt + j) * 16 + r;
-            if (t < p.n_tok) gemm_store<EPI>(p, acc[i][j], t, (ftile0 + wf + i) * 16 + 4 * q);
-        }
+    for (int k = 0; k < XPT; ++k) {
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int tp = blk % NT, gc = blk / NT, cp = gc & 1, g = gc >> 1, h = u >> 5;
+        const int tt = min(ttile0 + 2 * tp + ((u >> 4) & 1), ntt - 1);
+        xsrc[k] = p.X + (size_t)tt * KC * 64 + g * 64 + (2 * cp + h) * 16 + (u & 15);
+    }
+    auto issue = [&](int st, int b) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) lds_dma16(wsrc[k] + (size_t)st * 64, sw[b] + NTH * k + 64 * w);
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) lds_dma16(xsrc[k] + (size_t)st * 256, sx[b] + NTH * k + 64 * w);
+    };
+    v16i acc[MF][MT];
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    issue(0, 0);
+    if (steps > 1) issue(1, 1);
+    int b = 0;   // buffer of stage s
+    for (int s = 0; s < steps; ++s) {
+        if (s + 1 < steps) wait_vmcnt<LPT>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (s + 2 < steps) issue(s + 2, b == 0 ? 2 : b - 1);
+        gemm_mma_stage<MF, MT, NF, NT>(acc, sw[b], sx[b], wf, wt, l);
+        b = b == 2 ? 0 : b + 1;
+    }
+    gemm_lds_epilogue<EPI, MF, MT>(p, acc, ftile0, ttile0, wf, wt, l);
 }
 
 // ---------------------------------------------------------------------------
@@ -381,9 +558,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
             wv[f] = load_nt(p.W + ((size_t)(ftile0 + f) * KC + kc) * 16 + r);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
-            const uint4 *x = p.X + (((size_t)t * KC + kc) * 16 + r) * 4;
+            const uint4 *x = p.X + (size_t)t * KC * 64 + (size_t)s * 256 + q * 16 + r;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) xv[t][g] = x[g];
+            for (int g = 0; g < 4; ++g) xv[t][g] = x[g * 64];
         }
     };
     auto mac = [&](const uint4 (&wv)[TF], const uint4 (&xv)[TT][4]) {
@@ -427,8 +604,11 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
         v4i c = red[0][i][lane];
 #pragma unroll
         for (int k = 1; k < 4; ++k) c += red[k][i][lane];
-        const int f = i / TT, t = (i % TT) * 16 + r;
-        if (t < ntok) gemm_store<EPI>(p, c, t, (ftile0 + f) * 16 + 4 * q);
+        const int f = i / TT, t = (i % TT) * 16 + r, n0 = (ftile0 + f) * 16 + 4 * q;
+        const EpiTok e = epi_tok<EPI>(p, t);
+        const float4 ws = *(const float4 *)(p.wscale + n0);
+        const float4 old = epi_old<EPI>(p, t, n0, e);
+        if (t < ntok) gemm_store<EPI>(p, c, t, n0, e, ws, old);
     }
 }
 
@@ -450,10 +630,20 @@ static int skinny_launch(const GemmParams &p, hipStream_t s) {
     return 0;
 }
 
-template <int EPI, int FW, int TW>
+template <int EPI, int MF, int MT, int NWF>
+static int dma_launch(const GemmParams &p, hipStream_t s) {
+    constexpr int FT = 32 * MF * NWF, TK = 64 * MT;
+    dim3 grid(p.N / FT, (p.n_tok + TK - 1) / TK);
+    hipLaunchKernelGGL((gemm_dma_kernel<EPI, MF, MT, NWF>), grid, dim3(128 * NWF), 0, s, p);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int EPI, int MF, int MT, int NWF = 2>
 static int lds_launch(const GemmParams &p, hipStream_t s) {
-    dim3 grid(p.N / (32 * FW), (p.n_tok + 32 * TW - 1) / (32 * TW));
-    hipLaunchKernelGGL((gemm_lds_kernel<EPI, FW, TW>), grid, dim3(256), 0, s, p);
+    constexpr int FT = 32 * MF * NWF, TK = 64 * MT;
+    dim3 grid(p.N / FT, (p.n_tok + TK - 1) / TK);
+    hipLaunchKernelGGL((gemm_lds_kernel<EPI, MF, MT, NWF>), grid, dim3(128 * NWF), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -478,10 +668,11 @@ static int gemm_launch(const GemmParams &p, void *stream) {
     // grid still gives every CU a workgroup (N a multiple of the tile).
     const int cus = 256;
     auto blocks = [&](int ft, int tk) { return (long)(p.N / ft) * ((p.n_tok + tk - 1) / tk); };
-    if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 4, 4>(p, s);
-    if (p.N % 128 == 0 && blocks(128, 64) >= cus) return lds_launch<EPI, 4, 2>(p, s);
-    if (p.N % 64 == 0 && blocks(64, 128) >= cus) return lds_launch<EPI, 2, 4>(p, s);
-    if (p.N % 64 == 0) return lds_launch<EPI, 2, 2>(p, s);
+    if (p.N % 256 == 0 && blocks(256, 128) >= cus * 3 / 4) return dma_launch<EPI, 2, 2, 4>(p, s);
+    if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 2, 2>(p, s);
+    if (p.N % 128 == 0 && blocks(128, 64) >= cus) return lds_launch<EPI, 2, 1>(p, s);
+    if (p.N % 64 == 0 && blocks(64, 128) >= cus) return lds_launch<EPI, 1, 2>(p, s);
+    if (p.N % 64 == 0) return lds_launch<EPI, 1, 1>(p, s);
     dim3 grid((p.N + 63) / 64, (p.n_tok + 63) / 64);
     hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());

@@ -390,8 +390,10 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
 
 // ---------------------------------------------------------------------------
 // Same row transform, writing the token-tiled int8 layout the MFMA GEMM reads:
-// [ceil16(n_tok)/16][K/64][16 tokens][4 planes x 16 B].  Rows past n_tok
-// (padding to 16) are zeros with scale 1 and sum 0.
+// [ceil16(n_tok)/16][K/256 stages][4 planes g][4 chunks c][16 tokens][16 B],
+// the 16 B of (g, chunk kc = 4*stage + c) holding k = (kc/2)*128 + g*32 +
+// (kc%2)*16 + 0..15.  Rows past n_tok (padding to 16) are zeros with scale 1
+// and sum 0.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
     const float *__restrict__ x, const float *__restrict__ gamma, float eps, int D, int n_tok,
@@ -416,7 +418,8 @@ __global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
     for (int i = threadIdx.x; i < KC * 4; i += 256) {
         const int kc = i >> 2, g = i & 3;
         const int src = (kc >> 1) * 128 + g * 32 + (kc & 1) * 16;
-        Xt[(((size_t)tile * KC + kc) * 16 + c) * 4 + g] = *(const uint4 *)(q_lds + src);
+        Xt[(size_t)tile * KC * 64 + ((kc >> 2) * 4 + g) * 64 + (kc & 3) * 16 + c] =
+            *(const uint4 *)(q_lds + src);
     }
     if (threadIdx.x == 0) {
         scales[row] = scale;

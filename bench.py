@@ -163,8 +163,8 @@ def _native_check(L):
 
 def _host_tiles(rng, M: int, K: int):
     """int8 activations of M seeded N(0,1) rows (per-token absmax, RNE, +-127)
-    in the GEMM's token-tiled layout [Mpad/16][K/64][16 tokens][4 planes x 16],
-    plane g of chunk kc holding k = (kc//2)*128 + g*32 + (kc%2)*16 + j;
+    in the GEMM's token-tiled layout [Mpad/16][K/256][4 planes][4 chunks][16 tokens][16],
+    plane g of chunk kc = 4*stage + c holding k = (kc//2)*128 + g*32 + (kc%2)*16 + j;
     returns (tiles, scales, sums) with rows past M zero (scale 1, sum 0)."""
     mpad = (M + 63) // 64 * 64
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -172,7 +172,8 @@ def _host_tiles(rng, M: int, K: int):
     q = np.clip(np.rint(x * (np.float32(127.0) / am)), -127, 127).astype(np.int8)
     Q = np.zeros((mpad, K), np.int8)
     Q[:M] = q
-    t = Q.reshape(mpad // 16, 16, K // 128, 4, 2, 16).transpose(0, 2, 4, 1, 3, 5)
+    # k = stage*256 + (c//2)*128 + g*32 + (c%2)*16 + j
+    t = Q.reshape(mpad // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
     sc = np.ones(mpad, np.float32)
     sc[:M] = (am[:, 0] / np.float32(127.0)).astype(np.float32)
     sm = np.zeros(mpad, np.int32)

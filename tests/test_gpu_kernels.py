@@ -300,13 +300,14 @@ def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
     assert np.array_equal(out, ref)
 
 
-# n > 64: the LDS-staged kernel at its tile shapes -- 128x128 (8192, 1024 and
-# 4224, 1024), 128x64 (6912, 512), 64x128 with a ragged last token tile
-# (4032, 650), 64x64 (2560, 512) -- and the register-tiled kernel for
-# N % 64 != 0 (32, 65)
+# n > 64: the DMA-staged 256x128 kernel (8192 x 1024 with one K stage; 8192 x
+# 1000 and 8192 x 900 with 10 and 3 stages and a ragged last token tile), the
+# LDS-staged kernel at 128x128 (4224, 1024), 128x64 (6912, 512), 64x128 with a
+# ragged last token tile (4032, 650), 64x64 (2560, 512) -- and the
+# register-tiled kernel for N % 64 != 0 (32, 65)
 @pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
                                    (32, 256, 65), (8192, 256, 1024), (4224, 256, 1024),
-                                   (4032, 256, 650),
+                                   (4032, 256, 650), (8192, 2560, 1000), (8192, 768, 900),
                                    # n <= 64: the skinny kernel, 1..4 token tiles, 1 or 2
                                    # feature tiles per workgroup, uneven K splits over waves
                                    (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
@@ -328,7 +329,7 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
-@pytest.mark.parametrize("n", [40, 130])
+@pytest.mark.parametrize("n", [40, 130, 600])   # skinny, 128x64 LDS-staged, 256x128 DMA-staged
 def test_gemm_epilogues(n):
     rng = np.random.default_rng(31 + n)
     K, F = 2560, 6912
