@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     }
 }
 
-constexpr int kVFloats = 8192;  // LDS floats of the staged V slice (32 KiB, plus row padding)
+// P.V association (the oracle's OXO_PV_BLOCK): positions are summed in blocks
+// of kPvBlock in order of s, and the block sums are added in block order.
+constexpr int kPvBlock = 256;  // LDS floats of the staged V slice (32 KiB, plus row padding)
 
 // The shaders' 256-thread halving tree s[t] += s[t + stride], stride
 // 128 .. 1, with s[4l + i] in component i of lane l: strides 128 .. 4 pair
@@ -225,15 +227,13 @@ __device__ __forceinline__ void wave_softmax_row(float *row, const float *__rest
     for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
 }
 
-// P.V work split: a wave covers the G heads x 64/G dims (one output per
-// lane).  Narrow: one summing wave per workgroup (the most workgroups, each
-// streaming the least V: best while the grid fits the chip).  Wide: min(4, 2G)
-// summing waves per workgroup (all 128 dims when G <= 2): 4x the chains per
-// CU once a batch oversubscribes the chip.
+// P.V split of the two-kernel path: a wave covers the G heads x 64/G dims of
+// its workgroup (one output per lane); the workgroup's NWV waves take the
+// kPvBlock-position blocks in turn, so a long cache is summed as
+// ceil(blocks / NWV) chains of kPvBlock steps instead of one chain of S.
 __host__ __device__ constexpr int pv_dims_per_wave(int G) { return 64 / G; }
-__host__ __device__ constexpr int pv_waves(int G, bool wide) {
-    return !wide ? 1 : 2 * G < 4 ? 2 * G : 4;
-}
+constexpr int kPvStage = 2048;   // f32 of V a wave stages at a time (8 KiB)
+constexpr int kWideVFloats = 8192;   // f32 of V the wide kernel stages per chunk (32 KiB)
 
 // acc + sum_{s < n} p[s] * v[s ^ sw], one fused multiply-add at a time in
 // order of s.  The LDS operands of the next 16 positions are read while the
@@ -290,8 +290,120 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     return acc;
 }
 
-template <int G, bool WIDE>
-__global__ __launch_bounds__(256) void attn_pv_kernel(
+// Decode P.V: workgroup (KV head hk, dims d0 .. d0 + 64/G - 1, sequence z),
+// NWV waves.  Waves g < G run head g's softmax into LDS.  Then wave w sums
+// the P.V blocks w, w + NWV, ... (lane: head lane / DWW, dim d0 + lane %
+// DWW), staging each block's V slice in sub-chunks of kSub positions into its
+// own LDS region (f32, [dim][position]); the block sums go to LDS and wave 0
+// adds them in block order (sh/attention.wgsl:96-101, blocked as the oracle).
+// A wave's V sub-chunks are loaded two ahead in alternating register sets,
+// the first two before the softmax.  Rows past the cache length are clamped
+// to its last row (staged, never summed), so loads stay branch-free.
+template <int G, int NWV>
+__global__ __launch_bounds__(64 * NWV) void attn_pv_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
+    int pos_stride) {
+    {   // sequence blockIdx.z of a batch
+        const int z = blockIdx.z, H = gridDim.x * G;
+        scores += (size_t)z * H * max_seq;
+        vc += (size_t)z * kv_stride;
+        pos_ptr += (size_t)z * pos_stride;
+        out += (size_t)z * H * kHd;
+    }
+    constexpr int DWW = pv_dims_per_wave(G);   // dims of the workgroup
+    constexpr int PPP = DWW / 8;               // uint4 (8 f16) per position of the slice
+    constexpr int kSub = kPvStage / DWW;       // positions per staged sub-chunk
+    constexpr int SPB = kPvBlock / kSub;       // sub-chunks per block
+    constexpr int kVS = kSub + 4;              // padded row
+    constexpr int kLd = kSub * PPP / 64;       // uint4 per lane per sub-chunk
+    static_assert(PPP >= 1 && kLd * 64 == kSub * PPP && SPB * kSub == kPvBlock, "P.V staging shape");
+    extern __shared__ __align__(16) float pr[];   // [G][Sp] probabilities | [blocks][64] block sums
+    __shared__ __align__(16) float vt[NWV][DWW * kVS];
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1;
+    const int Spad = (S + 3) & ~3;
+    const int Sp = ((Spad >> 2) | 1) << 2;      // Sp / 4 odd: head rows start in different banks
+    const int nb = (S + kPvBlock - 1) / kPvBlock;
+    const int hk = blockIdx.x, d0 = blockIdx.y * DWW;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
+    float *bsum = pr + G * Sp;
+    float *vtw = vt[w];
+
+    // sub-chunk j of this wave: block w + NWV * (j / SPB), part j % SPB
+    auto sub_start = [&](int j) { return (w + NWV * (j / SPB)) * kPvBlock + (j % SPB) * kSub; };
+    auto load_sub = [&](uint4 (&r)[kLd], int st) {
+#pragma unroll
+        for (int k = 0; k < kLd; ++k) {
+            const int i = lane + 64 * k, sl = i / PPP, h = i % PPP;
+            r[k] = *(const uint4 *)(Vh + (size_t)min(st + sl, S - 1) * kHd + 8 * h);
+        }
+    };
+    auto stage_sub = [&](const uint4 (&r)[kLd]) {
+#pragma unroll
+        for (int k = 0; k < kLd; ++k) {
+            const int i = lane + 64 * k, sl = i / PPP, h = i % PPP;
+            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 f = __half22float2(*(const __half2 *)&wv[e]);
+                vtw[(8 * h + 2 * e) * kVS + sl] = f.x;
+                vtw[(8 * h + 2 * e + 1) * kVS + sl] = f.y;
+            }
+        }
+    };
+    // loads are unconditional (a start past the cache reads its last row), so
+    // the waits before each staging count exactly the loads issued after it
+    uint4 ra[kLd], rb[kLd];
+    load_sub(ra, sub_start(0));
+    load_sub(rb, sub_start(1));
+
+    for (int g = w; g < G; g += NWV)
+        wave_softmax_row(pr + g * Sp, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
+                         (max_seq & 3) == 0);
+    lds_barrier();
+
+    const int g = lane / DWW, dd = lane % DWW;
+    const float *prg = pr + g * Sp;
+    const float *vrow = vtw + dd * kVS;
+    float part = 0.0f;
+    // one sub-chunk: stage it (the wave's own region; LDS runs a wave's
+    // accesses in order, so the chain below reads what was just written and
+    // the next staging follows this chain's reads), refill its register set
+    // two sub-chunks ahead, sum it into the block's partial
+    auto step = [&](uint4 (&r)[kLd], int j) {
+        const int st = sub_start(j);
+        stage_sub(r);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        load_sub(r, sub_start(j + 2));
+        part = pv_chain(prg + st, vrow, min(kSub, S - st), part);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if ((j + 1) % SPB == 0 || st + kSub >= S) {   // block done
+            bsum[(w + NWV * (j / SPB)) * 64 + lane] = part;
+            part = 0.0f;
+        }
+    };
+    for (int j = 0; sub_start(j) < S; j += 2) {
+        step(ra, j);
+        if (sub_start(j + 1) >= S) break;
+        step(rb, j + 1);
+    }
+    lds_barrier();
+    if (w == 0) {
+        float tot = bsum[lane];
+        for (int b = 1; b < nb; ++b) tot = tot + bsum[b * 64 + lane];
+        out[(size_t)(hk * G + g) * kHd + d0 + dd] = tot;
+    }
+}
+
+// Decode P.V for grids wider than the chip (large batches): workgroup (KV
+// head, 16 G dims, sequence), 4 waves, min(4, 2G) of them summing (one chain
+// per lane over the whole cache, blocked as above), the V slice staged for
+// the workgroup in chunks; one softmax per 16 G dims instead of per 64 / G.
+template <int G>
+__global__ __launch_bounds__(256) void attn_pv_wide_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
     int pos_stride) {
@@ -303,17 +415,17 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
         out += (size_t)z * H * kHd;
     }
     constexpr int DWW = pv_dims_per_wave(G);     // a wave: G heads x DWW dims, one per lane
-    constexpr int WPB = pv_waves(G, WIDE);       // summing waves per workgroup
+    constexpr int WPB = 2 * G < 4 ? 2 * G : 4;   // summing waves per workgroup
     constexpr int DWB = DWW * WPB;               // dims per workgroup
     constexpr int PPP = DWB / 8;                 // uint4 (8 f16) per position of the slice
-    constexpr int kVChunk = kVFloats / DWB;      // positions staged per pass
+    constexpr int kVChunk = kWideVFloats / DWB;  // positions staged per pass
     constexpr int kVS = kVChunk + 4;             // padded row: the rows start in different banks
     // Staging: a wave writes 64 / PPP positions x PPP uint4 of 8 dims; the
     // dims 8h + e of one e share a bank for every h (8 kVS = 0 mod 32 banks),
     // so position s of dim row d is stored at s ^ swz(d / 8): 2 lanes/bank.
     auto swz = [](int h) { return PPP >= 8 ? 4 * (h & 7) : PPP == 4 ? 16 * (h & 3) : 0; };
     static_assert(PPP != 4 || kVChunk >= 64, "swizzle stays inside the chunk");
-    constexpr int kLoads = kVFloats / 8 / 256;   // uint4 per thread per chunk
+    constexpr int kLoads = kWideVFloats / 8 / 256;   // uint4 per thread per chunk
     extern __shared__ __align__(16) float pr[];   // [G][Sp] scores, then probabilities
     __shared__ __align__(16) float vt[DWB * kVS];  // V slice, [d][s] f32
     const int pos = *pos_ptr;
@@ -368,23 +480,30 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     // a CU sum on different SIMDs.
     const int ws = (w - (int)((blockIdx.x + 3 * blockIdx.y + blockIdx.z) & 3)) & 3;
     const int g = lane / DWW, dd = ws * DWW + lane % DWW;
-    float acc = 0.0f;
+    // blocked P.V: a chunk (kVChunk divides kPvBlock) adds to the block's
+    // partial; a finished block's partial is added to the total in order
+    static_assert(kPvBlock % kVChunk == 0, "chunks tile the P.V blocks");
+    float acc = 0.0f, part = 0.0f;
+    auto chain = [&](int c) {
+        part = pv_chain(pr + g * Sp + c, vt + dd * kVS, min(kVChunk, S - c), part, swz(dd >> 3));
+        if ((c + kVChunk) % kPvBlock == 0 || c + kVChunk >= S) {
+            acc = c < kPvBlock ? part : acc + part;
+            part = 0.0f;
+        }
+    };
     for (int c0 = 0; c0 < S; c0 += 2 * kVChunk) {
         lds_barrier();  // probabilities ready / previous chunk consumed
         stage(ra);
         lds_barrier();
         load_chunk(ra, min(c0 + 2 * kVChunk, S - 1));
-        if (ws < WPB)
-            acc = pv_chain(pr + g * Sp + c0, vt + dd * kVS, min(kVChunk, S - c0), acc, swz(dd >> 3));
+        if (ws < WPB) chain(c0);
         const int c1 = c0 + kVChunk;
         if (c1 < S) {
             lds_barrier();
             stage(rb);
             lds_barrier();
             load_chunk(rb, min(c1 + 2 * kVChunk, S - 1));
-            if (ws < WPB)
-                acc = pv_chain(pr + g * Sp + c1, vt + dd * kVS, min(kVChunk, S - c1), acc,
-                               swz(dd >> 3));
+            if (ws < WPB) chain(c1);
         }
     }
     if (ws < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
@@ -486,35 +605,47 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
         rr[c] = tid / kHd + (kPrefillThreads / kHd) * c;
         Sc[c] = Sq[rr[c] / G];
     }
+    // blocks of kPvBlock positions: each block's sum starts at zero and is
+    // added to the row's total in block order (rows skip blocks past their end)
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
     const int S0 = Sq[0];   // every row attends at least this far
     constexpr int U = 16;
-    int s = 0;
-    for (; s + U <= S0; s += U) {
-        float v[U];
+    static_assert(kPvBlock % U == 0, "blocks hold whole unrolled steps");
+    for (int b0 = 0; b0 < Smax; b0 += kPvBlock) {
+        float part[NC];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = __half2float(__ushort_as_half(Vd[(size_t)(s + u) * kHd]));
+        for (int c = 0; c < NC; ++c) part[c] = 0.0f;
+        const int e0 = min(b0 + kPvBlock, S0), e1 = min(b0 + kPvBlock, Smax);
+        int s = b0;
+        for (; s + U <= e0; s += U) {
+            float v[U];
 #pragma unroll
-        for (int u4 = 0; u4 < U; u4 += 4) {
-            float4 pc[NC];   // probabilities of 4 positions per chain (broadcast reads)
+            for (int u = 0; u < U; ++u) v[u] = __half2float(__ushort_as_half(Vd[(size_t)(s + u) * kHd]));
 #pragma unroll
-            for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
+            for (int u4 = 0; u4 < U; u4 += 4) {
+                float4 pc[NC];   // probabilities of 4 positions per chain (broadcast reads)
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                acc[c] = __builtin_fmaf(pc[c].x, v[u4], acc[c]);
-                acc[c] = __builtin_fmaf(pc[c].y, v[u4 + 1], acc[c]);
-                acc[c] = __builtin_fmaf(pc[c].z, v[u4 + 2], acc[c]);
-                acc[c] = __builtin_fmaf(pc[c].w, v[u4 + 3], acc[c]);
+                for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    part[c] = __builtin_fmaf(pc[c].x, v[u4], part[c]);
+                    part[c] = __builtin_fmaf(pc[c].y, v[u4 + 1], part[c]);
+                    part[c] = __builtin_fmaf(pc[c].z, v[u4 + 2], part[c]);
+                    part[c] = __builtin_fmaf(pc[c].w, v[u4 + 3], part[c]);
+                }
             }
         }
-    }
-    for (; s < Smax; ++s) {   // the last < U common positions, then the longer rows' tails
-        const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
+        for (; s < e1; ++s) {   // the last < U common positions, then the longer rows' tails
+            const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                if (s < Sc[c]) part[c] = __builtin_fmaf(sc[rr[c] * Sw + s], v, part[c]);
+        }
 #pragma unroll
         for (int c = 0; c < NC; ++c)
-            if (s < Sc[c]) acc[c] = __builtin_fmaf(sc[rr[c] * Sw + s], v, acc[c]);
+            if (b0 < Sc[c]) acc[c] = b0 == 0 ? part[c] : acc[c] + part[c];
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -693,14 +824,19 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
 
     // ---- P.V: wave g < G sums head g, lane = dim 64*half + lane --------------
     // Chunks alternate between the two register sets, each refilled (two
-    // chunks ahead) once staged.
+    // chunks ahead) once staged.  A chunk is one P.V block: its sum starts
+    // at zero and is added to the total in block order.
+    static_assert(kFusedVC == kPvBlock, "a V chunk is one P.V block");
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += 2 * kFusedVC) {
         lds_barrier();   // softmax done / K rows or the previous V chunk consumed
         fused_stage_v(vt, va, w, lane);
         lds_barrier();
         fused_load_v(va, V2, c0 + 2 * kFusedVC, S, w, lane);
-        if (w < G) acc = pv_chain(sc + w * spad_max + c0, vt + lane * kFusedVS, min(kFusedVC, S - c0), acc);
+        if (w < G) {
+            const float part = pv_chain(sc + w * spad_max + c0, vt + lane * kFusedVS, min(kFusedVC, S - c0), 0.0f);
+            acc = c0 == 0 ? part : acc + part;
+        }
         const int c1 = c0 + kFusedVC;
         if (c1 < S) {
             lds_barrier();
@@ -708,7 +844,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
             lds_barrier();
             fused_load_v(vb, V2, c1 + 2 * kFusedVC, S, w, lane);
             if (w < G)
-                acc = pv_chain(sc + w * spad_max + c1, vt + lane * kFusedVS, min(kFusedVC, S - c1), acc);
+                acc = acc + pv_chain(sc + w * spad_max + c1, vt + lane * kFusedVS, min(kFusedVC, S - c1), 0.0f);
         }
     }
     if (w < G) out[(size_t)(hk * G + w) * kHd + 64 * half + lane] = acc;
@@ -784,9 +920,21 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
-    const size_t smem = (size_t)G * (((max_seq + 3) & ~3) + 4) * sizeof(float);
-    // wide once the narrow grid exceeds one workgroup per CU: co-resident
-    // narrow workgroups share SIMDs, and each repeats the softmax of its G rows
+    // LDS: the G probability rows (each padded to an odd multiple of 4) and
+    // the block sums; 8 summing waves when their staging fits beside them
+    const size_t smem = ((size_t)G * ((((max_seq + 3) & ~3) >> 2 | 1) << 2) +
+                         (size_t)((max_seq + kPvBlock - 1) / kPvBlock) * 64) * sizeof(float);
+    constexpr size_t stage8 = (size_t)8 * pv_dims_per_wave(G) * (kPvStage / pv_dims_per_wave(G) + 4) * 4;
+    // (G = 1: the 8-wave variant needs more than 256 VGPRs; 4 waves only)
+    const bool eight = G > 1 && smem + stage8 <= 160 * 1024;
+    static size_t configured[2] = {0, 0};
+    if (smem > configured[eight]) {
+        OXB_CHECK_HIP(hipFuncSetAttribute(
+            eight ? (const void *)attn_pv_kernel<G, G == 1 ? 4 : 8> : (const void *)attn_pv_kernel<G, 4>,
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        configured[eight] = smem;
+    }
+    const dim3 grid(Hkv, kHd / pv_dims_per_wave(G), batch);
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -795,24 +943,26 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
             cus <= 0)
             cus = 256;
     }
-    const long narrow_blocks = (long)Hkv * (kHd / pv_dims_per_wave(G)) * batch;
-    const bool wide = narrow_blocks > cus;
-    static size_t configured[2] = {0, 0};
-    if (smem > configured[wide]) {
-        OXB_CHECK_HIP(hipFuncSetAttribute(
-            wide ? (const void *)attn_pv_kernel<G, true> : (const void *)attn_pv_kernel<G, false>,
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        configured[wide] = smem;
+    if ((long)grid.x * grid.y * grid.z > cus) {   // wide: one softmax per 16 G dims
+        constexpr int DWB = pv_dims_per_wave(G) * (2 * G < 4 ? 2 * G : 4);
+        const size_t wsmem = (size_t)G * (((max_seq + 3) & ~3) + 4) * sizeof(float);
+        static size_t wconfigured = 0;
+        if (wsmem > wconfigured) {
+            OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_pv_wide_kernel<G>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)wsmem));
+            wconfigured = wsmem;
+        }
+        hipLaunchKernelGGL((attn_pv_wide_kernel<G>), dim3(Hkv, kHd / DWB, batch), dim3(256), wsmem, s,
+                           scores, vc, pos, max_seq, out, kv_stride, pos_stride);
+        OXB_CHECK_HIP(hipGetLastError());
+        return 0;
     }
-    if (wide) {
-        constexpr int DWB = pv_dims_per_wave(G) * pv_waves(G, true);
-        hipLaunchKernelGGL((attn_pv_kernel<G, true>), dim3(Hkv, kHd / DWB, batch), dim3(256),
-                           smem, s, scores, vc, pos, max_seq, out, kv_stride, pos_stride);
-    } else {
-        constexpr int DWB = pv_dims_per_wave(G);
-        hipLaunchKernelGGL((attn_pv_kernel<G, false>), dim3(Hkv, kHd / DWB, batch), dim3(256),
-                           smem, s, scores, vc, pos, max_seq, out, kv_stride, pos_stride);
-    }
+    if (eight)
+        hipLaunchKernelGGL((attn_pv_kernel<G, G == 1 ? 4 : 8>), grid, dim3(G == 1 ? 256 : 512), smem, s,
+                           scores, vc, pos, max_seq, out, kv_stride, pos_stride);
+    else
+        hipLaunchKernelGGL((attn_pv_kernel<G, 4>), grid, dim3(256), smem, s, scores, vc, pos,
+                           max_seq, out, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }

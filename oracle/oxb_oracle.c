@@ -350,11 +350,22 @@ void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
             sc[kp] = causal ? -3.402823e+38f : dot * scale;
         }
         softmax_row(sc, S, pr);
-        for (int d = 0; d < hd; d++) { /* sh/attention.wgsl:96-104 */
-            float sum = 0.0f;
-            for (int s = 0; s < S; s++) /* fused: see header */
-                sum = fmaf(pr[s], vc[((size_t)s * Hkv + kvh) * hd + d], sum);
-            out[((size_t)qp * H + h) * hd + d] = sum;
+        /* sh/attention.wgsl:96-104 sums p[s] * v[s][d] over s in one loop.  Here
+         * the query's own positions (the masked ones contribute exact zeros)
+         * are summed in blocks of OXO_PV_BLOCK in order of s, and the block
+         * sums are added in block order; up to OXO_PV_BLOCK positions this is
+         * the shader's loop itself.  See the header. */
+        const int Sq = qp + (S - n_tok) + 1;
+        for (int d = 0; d < hd; d++) {
+            float total = 0.0f;
+            for (int b0 = 0; b0 < Sq; b0 += OXO_PV_BLOCK) {
+                const int e = b0 + OXO_PV_BLOCK < Sq ? b0 + OXO_PV_BLOCK : Sq;
+                float part = 0.0f;
+                for (int s = b0; s < e; s++) /* fused: see header */
+                    part = fmaf(pr[s], vc[((size_t)s * Hkv + kvh) * hd + d], part);
+                total = b0 == 0 ? part : total + part;
+            }
+            out[((size_t)qp * H + h) * hd + d] = total;
         }
         free(sc);
         free(pr);

@@ -97,7 +97,16 @@ void oxo_rope(const float *x, int n_tok, int heads, int hd, int pos_offset,
  *      sh/attention.wgsl:79-105 (attn_v); orchestration
  *      rs/nn/attention.rs:85-124 -------------------------------------------
  * q: [n_tok][H][hd]; K, V caches: [S][Hkv][hd] (S = positions incl. the new
- * ones); out: [n_tok][H][hd]. */
+ * ones); out: [n_tok][H][hd].
+ * P.V association: the shader sums p[s] * v[s][d] in one loop over s.  Here
+ * each query's positions are summed in blocks of OXO_PV_BLOCK = 256 in order
+ * of s (one fmaf per step), and the block sums are added in block order, so
+ * that the device can run the blocks of a long cache side by side instead of
+ * one dependent chain per output.  For up to 256 positions this is the
+ * shader's loop exactly; beyond, it is another association of the same sum,
+ * whose distance from the one-loop order is pinned in the tests (far inside
+ * the path's 1e-3 tolerance). */
+#define OXO_PV_BLOCK 256
 void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
                    int S, int H, int Hkv, int hd, float *out);
 /* softmax rows in place order: sh/softmax.wgsl */
