@@ -339,6 +339,21 @@ def cpu_baseline(synth, path: str, prompt: np.ndarray, steps: int) -> dict:
                       f"2B-shape model (C oracle, OpenMP over rows, f16-rounded KV)"}
 
 
+def gemm_extras(ops, synth) -> dict:
+    """The ternary GEMM sweep (28672x8192 and 8192x28672 at M = 8 .. 4096) and
+    the 512-token prefill block."""
+    gs = []
+    for N, K in ((28672, 8192), (8192, 28672)):
+        for M in (8, 64, 512, 4096):
+            copies = 8 if M <= 64 else 2
+            r = gemm_sweep(ops, synth, N, K, M, copies=copies, iters=40 if M < 4096 else 10)
+            gs.append(r)
+            log(f"gemm {N}x{K} M={M}: {r['us']} us {r['TOPS']} TOPS {r['GBps']} GB/s")
+    pb = prefill_block(ops, synth)
+    log(f"prefill block M=512: {pb['ms']} ms {pb['TOPS']} TOPS")
+    return {"gemm_sweep": gs, "prefill_block": pb}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,6 +370,8 @@ def main() -> int:
     ap.add_argument("--long-context-only", action="store_true",
                     help="run only the long-context section (2048-token prefill, decode at the "
                          "batch sizes of --lc-batches)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the ternary GEMM sweep and the 512-token prefill block")
     ap.add_argument("--lc-batches", default="1,8,32")
     ap.add_argument("--lc-steps", type=int, default=512)
     args = ap.parse_args()
@@ -368,6 +385,9 @@ def main() -> int:
     synth = importlib.import_module("0xbitnet_amd.synth")
     info = ops.device_info()
     log(f"device {info['name']} CUs {info['cus']}")
+    if args.gemm_only:
+        print(json.dumps(gemm_extras(ops, synth)), flush=True)
+        return 0
     if args.roofline_only:
         roof = gemv_roofline(ops, synth, 8192, 28672, copies=16, iters=400)
         if args.calib_mib:
@@ -422,17 +442,7 @@ def main() -> int:
 
     extra = {}
     if not args.no_extra:
-        gs = []
-        for N, K in ((28672, 8192), (8192, 28672)):
-            for M in (8, 64, 512, 4096):
-                copies = 8 if M <= 64 else 2
-                r = gemm_sweep(ops, synth, N, K, M, copies=copies, iters=40 if M < 4096 else 10)
-                gs.append(r)
-                log(f"gemm {N}x{K} M={M}: {r['us']} us {r['TOPS']} TOPS {r['GBps']} GB/s")
-        extra["gemm_sweep"] = gs
-        pb = prefill_block(ops, synth)
-        log(f"prefill block M=512: {pb['ms']} ms {pb['TOPS']} TOPS")
-        extra["prefill_block"] = pb
+        extra.update(gemm_extras(ops, synth))
         lc = long_context(pkg, synth, path)
         log(f"long context: prefill {lc['prefill_ms']} ms")
         extra["long_context"] = lc
