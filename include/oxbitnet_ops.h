@@ -115,6 +115,10 @@ int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_row
                         int8_t *xq, float *scales, int *sums, void *stream);
 
 /* Ternary GEMM on int8 MFMA: Y[t][n] = (float)acc[t][n] * (wscale[n] * xscale[t]).
+ * X is the token-tiled int8 layout written by oxb_quantize_rows_tiled:
+ * [ceil16(n_tok)/16][K/256][4 planes][4 chunks][16 tokens][16 B], the 16 B of
+ * (plane g, chunk kc = 4*stage + c, token) holding x[(kc/2)*128 + g*32 +
+ * (kc%2)*16 + 0..15] (N multiple of 32, K of 256).
  * epilogue: 0 store, 1 residual add (Y += ...), 2 gate|up fusion (Y is
  * [n_tok][N/2]), 3 q|k|v + RoPE + KV append (qkv_* arguments used).
  * Replaces shaders/ternary_gemm.wgsl:40-136 dispatched by nn/bitlinear.rs:207-247. */
@@ -128,8 +132,10 @@ int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, cons
 
 /* ---- attention ------------------------------------------------------------ */
 /* Decode attention for one token over L = *pos + 1 cached positions, in the
- * reference's order (f32 result identical to the shaders' arithmetic on the
- * f16-rounded cache).  q, out: [H*128] f32; scores: [H][max_seq] f32 scratch.  Replaces nn/attention.rs:109-118
+ * reference's order for the scores and softmax, with P.V summed in blocks of
+ * 256 positions whose sums are added in order (for L <= 256 the shaders' one
+ * loop; f32 result identical to the oracle's arithmetic on the f16-rounded
+ * cache).  q, out: [H*128] f32; scores: [H][max_seq] f32 scratch.  Replaces nn/attention.rs:109-118
  * (scores, softmax, P.V dispatches). */
 int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                     const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
