@@ -442,12 +442,13 @@ __global__ __launch_bounds__(128 * NWF, 4 / NWF) void gemm_lds_kernel(GemmParams
 // The same tiles with direct global -> LDS staging (global_load_lds_dwordx4:
 // each lane's 16 B land at the wave's LDS base + 16 * lane, which is exactly
 // the slot order above), so staging takes no VGPRs and no LDS store
-// instructions.  Three stage buffers (144 KB at 256 x 128) let each stage's
-// loads be issued two stages ahead, with one barrier per stage:
-//   iteration s: wait for this thread's stage-s loads (stage s+1 may still be
-//   in flight), barrier (every thread's stage s has landed, and every wave is
-//   done reading the buffer that stage s+2 reuses), issue stage s+2, multiply
-//   stage s.
+// instructions.  NBUF stage buffers let each stage's loads be issued NBUF-1
+// stages ahead (256 x 128: 3 buffers, 144 KB; small tiles, whose stages are
+// short, 4 or more), with one barrier per stage:
+//   iteration s: wait for this thread's stage-s loads (later stages may still
+//   be in flight), barrier (every thread's stage s has landed, and every wave
+//   is done reading the buffer that stage s+NBUF-1 reuses), issue stage
+//   s+NBUF-1, multiply stage s.
 // The loads are issued from inline assembly with explicit vmcnt waits: the
 // compiler's builtin for them makes every later LDS read wait for all
 // outstanding loads, which would serialise the prefetch.  The compiler does
@@ -466,16 +467,23 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int EPI, int MF, int MT, int NWF>
-__global__ __launch_bounds__(128 * NWF, 1) void gemm_dma_kernel(GemmParams p) {
+// workgroups per CU that the LDS of a DMA-staged tile allows (160 KB)
+__host__ __device__ constexpr int dma_occupancy(int MF, int MT, int NWF, int NBUF) {
+    return 160 * 1024 / (NBUF * (32 * NWF * MF * 4 + 64 * MT * 16) * 16) >= 2 ? 2 : 1;
+}
+
+template <int EPI, int MF, int MT, int NWF, int NBUF>
+__global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void gemm_dma_kernel(
+    GemmParams p) {
     constexpr int NTH = 128 * NWF;
     constexpr int NF = NWF * MF, NT = 2 * MT;
     constexpr int FT = 32 * NF, TK = 32 * NT;
     constexpr int WU = FT * 4, XU = TK * 16;
     constexpr int WPT = WU / NTH, XPT = XU / NTH, LPT = WPT + XPT;
     static_assert(WPT * NTH == WU && XPT * NTH == XU, "stage units must split evenly");
-    __shared__ uint4 sw[3][WU];
-    __shared__ uint4 sx[3][XU];
+    static_assert(NBUF >= 3 && (NBUF - 2) * LPT < 64, "vmcnt holds the loads in flight");
+    __shared__ uint4 sw[NBUF][WU];
+    __shared__ uint4 sx[NBUF][XU];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
     const int KC = p.K >> 6, steps = KC >> 2;
     const int ftile0 = blockIdx.x * (FT / 16), ttile0 = blockIdx.y * (TK / 16);
@@ -512,16 +520,25 @@ __global__ __launch_bounds__(128 * NWF, 1) void gemm_dma_kernel(GemmParams p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-    issue(0, 0);
-    if (steps > 1) issue(1, 1);
+    for (int st = 0; st < NBUF - 1; ++st)
+        if (st < steps) issue(st, st);
     int b = 0;   // buffer of stage s
     for (int s = 0; s < steps; ++s) {
-        if (s + 1 < steps) wait_vmcnt<LPT>();
-        else wait_vmcnt<0>();
+        // stages s+1 .. min(s+NBUF-2, steps-1) may stay in flight
+        const int later = min(NBUF - 2, steps - 1 - s);
+        if constexpr (NBUF == 3) {
+            if (later == 1) wait_vmcnt<LPT>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= NBUF - 2) wait_vmcnt<(NBUF - 2) * LPT>();
+            else if (later == 2) wait_vmcnt<2 * LPT>();
+            else if (later == 1) wait_vmcnt<LPT>();
+            else wait_vmcnt<0>();
+        }
         lds_barrier();
-        if (s + 2 < steps) issue(s + 2, b == 0 ? 2 : b - 1);
+        if (s + NBUF - 1 < steps) issue(s + NBUF - 1, b == 0 ? NBUF - 1 : b - 1);
         gemm_mma_stage<MF, MT, NF, NT>(acc, sw[b], sx[b], wf, wt, l);
-        b = b == 2 ? 0 : b + 1;
+        b = b == NBUF - 1 ? 0 : b + 1;
     }
     gemm_lds_epilogue<EPI, MF, MT>(p, acc, ftile0, ttile0, wf, wt, l);
 }
@@ -630,11 +647,11 @@ static int skinny_launch(const GemmParams &p, hipStream_t s) {
     return 0;
 }
 
-template <int EPI, int MF, int MT, int NWF>
+template <int EPI, int MF, int MT, int NWF, int NBUF>
 static int dma_launch(const GemmParams &p, hipStream_t s) {
     constexpr int FT = 32 * MF * NWF, TK = 64 * MT;
     dim3 grid(p.N / FT, (p.n_tok + TK - 1) / TK);
-    hipLaunchKernelGGL((gemm_dma_kernel<EPI, MF, MT, NWF>), grid, dim3(128 * NWF), 0, s, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<EPI, MF, MT, NWF, NBUF>), grid, dim3(128 * NWF), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -668,11 +685,11 @@ static int gemm_launch(const GemmParams &p, void *stream) {
     // grid still gives every CU a workgroup (N a multiple of the tile).
     const int cus = 256;
     auto blocks = [&](int ft, int tk) { return (long)(p.N / ft) * ((p.n_tok + tk - 1) / tk); };
-    if (p.N % 256 == 0 && blocks(256, 128) >= cus * 3 / 4) return dma_launch<EPI, 2, 2, 4>(p, s);
+    if (p.N % 256 == 0 && blocks(256, 128) >= cus * 3 / 4) return dma_launch<EPI, 2, 2, 4, 3>(p, s);
     if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 2, 2>(p, s);
     if (p.N % 128 == 0 && blocks(128, 64) >= cus) return lds_launch<EPI, 2, 1>(p, s);
     if (p.N % 64 == 0 && blocks(64, 128) >= cus) return lds_launch<EPI, 1, 2>(p, s);
-    if (p.N % 64 == 0) return lds_launch<EPI, 1, 1>(p, s);
+    if (p.N % 64 == 0) return dma_launch<EPI, 1, 1, 2, 4>(p, s);
     dim3 grid((p.N + 63) / 64, (p.n_tok + 63) / 64);
     hipLaunchKernelGGL((gemm_kernel<EPI>), grid, dim3(256), 0, s, p);
     OXB_CHECK_HIP(hipGetLastError());

@@ -303,11 +303,14 @@ def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
 # n > 64: the DMA-staged 256x128 kernel (8192 x 1024 with one K stage; 8192 x
 # 1000 and 8192 x 900 with 10 and 3 stages and a ragged last token tile), the
 # LDS-staged kernel at 128x128 (4224, 1024), 128x64 (6912, 512), 64x128 with a
-# ragged last token tile (4032, 650), 64x64 (2560, 512) -- and the
-# register-tiled kernel for N % 64 != 0 (32, 65)
+# ragged last token tile (4032, 650), the DMA-staged 64x64 kernel with 4
+# buffers (2560 x 512 with 27 stages; 2 and 3 stages, fewer than it prefetches,
+# with ragged token tiles) -- and the register-tiled kernel for N % 64 != 0
+# (32, 65)
 @pytest.mark.parametrize("N,K,n", [(6912, 2560, 512), (2560, 6912, 512), (640, 2560, 7),
                                    (32, 256, 65), (8192, 256, 1024), (4224, 256, 1024),
                                    (4032, 256, 650), (8192, 2560, 1000), (8192, 768, 900),
+                                   (2560, 512, 100), (1024, 768, 70),
                                    # n <= 64: the skinny kernel, 1..4 token tiles, 1 or 2
                                    # feature tiles per workgroup, uneven K splits over waves
                                    (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
