@@ -339,6 +339,34 @@ def cpu_baseline(synth, path: str, prompt: np.ndarray, steps: int) -> dict:
                       f"2B-shape model (C oracle, OpenMP over rows, f16-rounded KV)"}
 
 
+def cpu_kernels(synth) -> list:
+    """The oracle's GEMV / GEMM on the host cores at the ternary-matmul configs:
+    6912x2560 M=1 (the FFN up-projection GEMV) and 28672x8192 at M = 1, 8, 64;
+    the same algorithmic bytes and ops as the GPU figures."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # the checker, timed here as the reported CPU baseline
+    rng = np.random.default_rng(5)
+    out = []
+    for N, K, M, reps in ((6912, 2560, 1, 50), (28672, 8192, 1, 20), (28672, 8192, 8, 5),
+                          (28672, 8192, 64, 3)):
+        Wn = synth.i2s_pack(rng.integers(-1, 2, size=(N, K)).astype(np.int8))
+        X = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+        sc = np.full(M, 0.01, np.float32)
+        run = ((lambda: O.gemv(Wn, X[0], 0.0158, 0.01, K)) if M == 1
+               else (lambda: O.gemm(Wn, X, 0.0158, sc, K)))
+        run()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            run()
+        dt = (time.perf_counter() - t0) / reps
+        nbytes = N * K // 4 + M * K + 4 * M * N + 4
+        out.append({"N": N, "K": K, "M": M, "us": round(dt * 1e6, 1),
+                    "GBps": round(nbytes / dt / 1e9, 2), "GOPS": round(2 * M * N * K / dt / 1e9, 2),
+                    "cores": O.num_threads()})
+        log(f"cpu {N}x{K} M={M}: {dt * 1e3:.2f} ms {out[-1]['GBps']} GB/s {out[-1]['GOPS']} GOPS")
+    return out
+
+
 def gemm_extras(ops, synth) -> dict:
     """The ternary GEMM sweep (28672x8192 and 8192x28672 at M = 8 .. 4096) and
     the 512-token prefill block."""
@@ -452,6 +480,7 @@ def main() -> int:
         t = time.time()
         cpu = cpu_baseline(synth, path, prompt[:8].astype(np.uint32), args.cpu_steps)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads ({time.time() - t:.1f}s)")
+        extra["cpu_kernels"] = cpu_kernels(synth)
 
     # bytes per decode step at the mean KV length of the timed run
     cfg = synth.BITNET_2B
