@@ -453,11 +453,17 @@ __global__ __launch_bounds__(128 * NWF, 4 / NWF) void gemm_lds_kernel(GemmParams
 // compiler's builtin for them makes every later LDS read wait for all
 // outstanding loads, which would serialise the prefetch.  The compiler does
 // not count these loads, so its own vmcnt waits can only come out stricter.
+// The LDS base goes through m0, which the asm saves and restores itself (m0 is
+// a reserved register: declaring it clobbered is not allowed).
 __device__ __forceinline__ void lds_dma16(const void *g, const uint4 *lds_wave_base) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)lds_wave_base);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(g)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(g)
+        : "memory");
 }
 
 template <int N>
