@@ -187,7 +187,7 @@ __device__ inline float block256_tree_sum_fast(float part, float *red) {
 // strides 8..1 and lane 0 holds the shader's sum.  red >= 256 floats; all
 // 256 threads must call; result to all threads.
 __device__ inline float block256_tree_sum_1b(float part, float *red) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 255;   // a 256-thread group, red its own 256 slots
     red[t] = part;
     lds_barrier();
     const int i = t & 15;

@@ -63,7 +63,7 @@ struct GemvParams {
 template <int NREG>
 __device__ inline void load_row(const float *__restrict__ x, const float *__restrict__ gamma,
                                 int D, float (&v)[NREG], float (&g)[NREG]) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 255;   // a 256-thread row group
     const float *gp = gamma ? gamma : x;   // loads stay unconditional
 #pragma unroll
     for (int j = 0; j < NREG; ++j) {
@@ -75,7 +75,7 @@ __device__ inline void load_row(const float *__restrict__ x, const float *__rest
 
 template <int NREG>
 __device__ inline void mask_row(int D, float (&v)[NREG], float (&g)[NREG]) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 255;
 #pragma unroll
     for (int j = 0; j < NREG; ++j) {
         const bool in = t + j * 256 < D;
@@ -87,7 +87,7 @@ __device__ inline void mask_row(int D, float (&v)[NREG], float (&g)[NREG]) {
 template <int NREG>
 __device__ inline float norm_quant_regs(float (&v)[NREG], const float (&g)[NREG], bool norm,
                                         float eps, int D, int8_t *xq_lds, float *red, int *wq) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 255;
     mask_row<NREG>(D, v, const_cast<float (&)[NREG]>(g));
     if (norm) {
         float ss = 0.0f;   // columns past D hold +0 and add exactly nothing
@@ -393,37 +393,48 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
 // [ceil16(n_tok)/16][K/256 stages][4 planes g][4 chunks c][16 tokens][16 B],
 // the 16 B of (g, chunk kc = 4*stage + c) holding k = (kc/2)*128 + g*32 +
 // (kc%2)*16 + 0..15.  Rows past n_tok (padding to 16) are zeros with scale 1
-// and sum 0.
+// and sum 0.  A workgroup takes 2 consecutive rows, one per 256-thread group
+// (each in the shaders' 256-thread order), so that its stores are 32-byte
+// runs of 2 tokens instead of one token's scattered 16-byte pieces (4 rows
+// per workgroup would need more than the 128 VGPRs of a 1024-thread wave).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void quantize_rows_tiled_kernel(
+constexpr int kTiledRows = 2;
+
+__global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     const float *__restrict__ x, const float *__restrict__ gamma, float eps, int D, int n_tok,
     uint4 *__restrict__ Xt, float *__restrict__ scales, int *__restrict__ sums) {
     extern __shared__ __align__(16) int8_t smem[];
-    int8_t *q_lds = smem;
-    float *red = (float *)(smem + ((D + 15) & ~15));
+    const int grp = threadIdx.x >> 8, tl = threadIdx.x & 255;
+    const int dpad = (D + 15) & ~15;
+    int8_t *q_lds = smem + grp * dpad;
+    float *red = (float *)(smem + kTiledRows * dpad) + grp * 328;
     int *wq = (int *)(red + 324);
-    const int row = blockIdx.x;
+    const int row = blockIdx.x * kTiledRows + grp;
     float scale = 1.0f;
-    int sumq = 0;
     if (row < n_tok) {
         float v[kMaxNormReg], g[kMaxNormReg];
         load_row<kMaxNormReg>(x + (size_t)row * D, gamma, D, v, g);
         scale = norm_quant_regs<kMaxNormReg>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
     } else {
-        for (int i = threadIdx.x; i < (D >> 4); i += 256) ((int4 *)q_lds)[i] = make_int4(0, 0, 0, 0);
-        if (threadIdx.x < 4) wq[threadIdx.x] = 0;
+        // padding rows: the group still meets the row path's barriers (one in
+        // the norm's tree sum, one for the absmax)
+        for (int i = tl; i < (D >> 4); i += 256) ((int4 *)q_lds)[i] = make_int4(0, 0, 0, 0);
+        if (gamma != nullptr) (void)block256_tree_sum_1b(0.0f, red);
+        lds_barrier();
+        if (tl < 4) wq[tl] = 0;
     }
     lds_barrier();
-    const int KC = D >> 6, tile = row >> 4, c = row & 15;
-    for (int i = threadIdx.x; i < KC * 4; i += 256) {
-        const int kc = i >> 2, g = i & 3;
-        const int src = (kc >> 1) * 128 + g * 32 + (kc & 1) * 16;
-        Xt[(size_t)tile * KC * 64 + ((kc >> 2) * 4 + g) * 64 + (kc & 3) * 16 + c] =
-            *(const uint4 *)(q_lds + src);
+    const int KC = D >> 6, tile = row >> 4, r0 = (blockIdx.x * kTiledRows) & 15;
+    // unit i: row group i % 2, plane (i / 2) % 4, chunk i / 8
+    for (int i = threadIdx.x; i < KC * 4 * kTiledRows; i += 256 * kTiledRows) {
+        const int rr = i % kTiledRows, gp = (i / kTiledRows) & 3, kc = i / (4 * kTiledRows);
+        const int src = (kc >> 1) * 128 + gp * 32 + (kc & 1) * 16;
+        Xt[(size_t)tile * KC * 64 + ((kc >> 2) * 4 + gp) * 64 + (kc & 3) * 16 + r0 + rr] =
+            *(const uint4 *)(smem + rr * dpad + src);
     }
-    if (threadIdx.x == 0) {
+    if (tl == 0) {
         scales[row] = scale;
-        sums[row] = sumq + wq[0] + wq[1] + wq[2] + wq[3];
+        sums[row] = wq[0] + wq[1] + wq[2] + wq[3];
     }
 }
 
@@ -594,10 +605,10 @@ extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float
     OXB_REQUIRE(D > 0 && D % 256 == 0 && D <= 256 * kMaxNormReg,
                 "quantize_rows_tiled: D %d must be a multiple of 256 and <= %d", D, 256 * kMaxNormReg);
     OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
-    const size_t sm = (size_t)((D + 15) & ~15) + 324 * 4 + 16 + 16;
     const int rows = (n_tok + 15) & ~15;
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(rows), dim3(256), sm, stream, x, gamma,
-                       eps, D, n_tok, (uint4 *)Xt, scales, sums);
+    const size_t sm = (size_t)kTiledRows * (((D + 15) & ~15) + 328 * 4);
+    hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(rows / kTiledRows), dim3(256 * kTiledRows),
+                       sm, stream, x, gamma, eps, D, n_tok, (uint4 *)Xt, scales, sums);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }

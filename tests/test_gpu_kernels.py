@@ -332,7 +332,7 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
-@pytest.mark.parametrize("n", [40, 130, 600])   # skinny, 128x64 LDS-staged, 256x128 DMA-staged
+@pytest.mark.parametrize("n", [40, 41, 130, 600])   # skinny (41: a real and a padding row share a workgroup of the quantizer), 128x64 LDS-staged, 256x128 DMA-staged
 def test_gemm_epilogues(n):
     rng = np.random.default_rng(31 + n)
     K, F = 2560, 6912
