@@ -271,7 +271,9 @@ def long_context(pkg, synth, path: str, prompt_len: int = 2048, steps: int = 512
     if 1 in batches:   # the one-sequence engine: timed prefill, then its decode below
         rng = np.random.default_rng(4096)
         prompt = rng.integers(0, synth.BITNET_2B.vocab, prompt_len).astype(np.int32)
-        m.forward(prompt[:64], want_logits=False)   # warm-up (graph capture, code paths)
+        # warm-up at the full length: graph capture, code paths and the prefill
+        # buffers, which the engine sizes on the first prompt this long
+        m.forward(prompt, want_logits=False)
         m.decode_greedy(4)
         m.reset()
         ops.sync()
