@@ -288,7 +288,9 @@ def test_attn_decode_fused_rejects_unsupported():
 @pytest.mark.parametrize("H,Hkv,S,pos0,n", [(20, 5, 256, 30, 100), (20, 5, 512, 0, 257),
                                             (16, 2, 1200, 900, 31), (8, 8, 300, 5, 40),
                                             (16, 8, 300, 100, 33), (20, 5, 2100, 2040, 9),
-                                            (20, 5, 64, 0, 1)])
+                                            (20, 5, 64, 0, 1),
+                                            # 1001 queries over 4 P.V blocks, a lone last query
+                                            (20, 5, 1100, 50, 1001)])
 def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
     rng = np.random.default_rng(21 + n)
     hd = 128
