@@ -334,6 +334,37 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("N,K,n", [(28672, 8192, 512), (8192, 28672, 4096)])
+def test_gemm_sweep_shapes_bitexact(N, K, n):
+    """The ternary matmul sweep at full size (the 256x128 DMA-staged kernel, 32
+    and 112 K stages): int32 accumulators and outputs equal the oracle's."""
+    rng = np.random.default_rng(N + K + n)
+    w = ternary(rng, N, K)
+    Wn = synth.i2s_pack(w)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    ws = np.full(N, 0.0131, np.float32)
+    q, s = O.quantize(x)
+    acc_o, Y_o = O.gemm(Wn, q, ws, s, K)
+    # rows this long exceed the fused quantizer (D <= 7168): tile the oracle's
+    # int8 rows on the host into the GEMM's layout [n/16][K/256][4 planes]
+    # [4 chunks][16 tokens][16 B], k = stage*256 + (c//2)*128 + g*32 + (c%2)*16 + j
+    tiles = q.reshape(n // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
+    L = ops.lib()
+    Wt = ops.upload_ternary(Wn, K)
+    dX = ops.DeviceArray.from_host(np.ascontiguousarray(tiles).reshape(-1))
+    dsc = ops.DeviceArray.from_host(s)
+    dsm = ops.DeviceArray.from_host(q.astype(np.int64).sum(axis=1).astype(np.int32))
+    dws = ops.DeviceArray.from_host(ws)
+    Y = ops.DeviceArray((n, N), np.float32)
+    acc = ops.DeviceArray((n, N), np.int32)
+    ops.check(L.oxb_gemm_i8(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n, Y.ptr, acc.ptr, 0,
+                            None), "gemm_i8")
+    ops.sync()
+    assert np.array_equal(acc.download(), acc_o)
+    assert np.array_equal(Y.download(), Y_o)
+
+
 @pytest.mark.parametrize("n", [40, 41, 130, 600])   # skinny (41: a real and a padding row share a workgroup of the quantizer), 128x64 LDS-staged, 256x128 DMA-staged
 def test_gemm_epilogues(n):
     rng = np.random.default_rng(31 + n)
