@@ -861,12 +861,7 @@ static int launch_prefill(const float *q, const uint16_t *kc, const uint16_t *vc
                           int n_q, int H, int Hkv, int max_seq, int s_max, float *out,
                           hipStream_t s) {
     const size_t smem = prefill_smem(G * Q, s_max);
-    static size_t configured = 0;
-    if (smem > 64 * 1024 && smem > configured) {
-        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_prefill_kernel<G, Q>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        configured = smem;
-    }
+    if (smem > 64 * 1024 && allow_dynamic_lds((const void *)attn_prefill_kernel<G, Q>)) return -1;
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipLaunchKernelGGL((attn_prefill_kernel<G, Q>), dim3((n_q + Q - 1) / Q, Hkv), dim3(kPrefillThreads), smem,
                        s, q, kc, vc, pos0, n_q, H, max_seq, scale, out);
@@ -927,31 +922,14 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
     constexpr size_t stage8 = (size_t)8 * pv_dims_per_wave(G) * (kPvStage / pv_dims_per_wave(G) + 4) * 4;
     // (G = 1: the 8-wave variant needs more than 256 VGPRs; 4 waves only)
     const bool eight = G > 1 && smem + stage8 <= 160 * 1024;
-    static size_t configured[2] = {0, 0};
-    if (smem > configured[eight]) {
-        OXB_CHECK_HIP(hipFuncSetAttribute(
-            eight ? (const void *)attn_pv_kernel<G, G == 1 ? 4 : 8> : (const void *)attn_pv_kernel<G, 4>,
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        configured[eight] = smem;
-    }
+    if (allow_dynamic_lds(eight ? (const void *)attn_pv_kernel<G, G == 1 ? 4 : 8>
+                                : (const void *)attn_pv_kernel<G, 4>))
+        return -1;
     const dim3 grid(Hkv, kHd / pv_dims_per_wave(G), batch);
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-    }
-    if ((long)grid.x * grid.y * grid.z > cus) {   // wide: one softmax per 16 G dims
+    if ((long)grid.x * grid.y * grid.z > device_cus()) {   // wide: one softmax per 16 G dims
         constexpr int DWB = pv_dims_per_wave(G) * (2 * G < 4 ? 2 * G : 4);
         const size_t wsmem = (size_t)G * (((max_seq + 3) & ~3) + 4) * sizeof(float);
-        static size_t wconfigured = 0;
-        if (wsmem > wconfigured) {
-            OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_pv_wide_kernel<G>,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)wsmem));
-            wconfigured = wsmem;
-        }
+        if (allow_dynamic_lds((const void *)attn_pv_wide_kernel<G>)) return -1;
         hipLaunchKernelGGL((attn_pv_wide_kernel<G>), dim3(Hkv, kHd / DWB, batch), dim3(256), wsmem, s,
                            scores, vc, pos, max_seq, out, kv_stride, pos_stride);
         OXB_CHECK_HIP(hipGetLastError());
@@ -1017,12 +995,7 @@ template <int G>
 static int launch_fused(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                         int Hkv, int max_seq, float *out, hipStream_t s) {
     const size_t smem = attn_fused_smem(G, max_seq);
-    static size_t configured = 0;
-    if (smem > configured) {
-        OXB_CHECK_HIP(hipFuncSetAttribute((const void *)attn_fused_kernel<G>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        configured = smem;
-    }
+    if (allow_dynamic_lds((const void *)attn_fused_kernel<G>)) return -1;
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipLaunchKernelGGL(attn_fused_kernel<G>, dim3(Hkv, 2), dim3(1024), smem, s, q, kc, vc, pos,
                        max_seq, scale, out);

@@ -20,6 +20,14 @@ void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 const char *last_error();
 
+// Raises a kernel's dynamic-LDS ceiling on the current device to what a CU
+// leaves beside the kernel's static LDS, once per (device, kernel) and safe to
+// call from several host threads (the attribute is a ceiling: a launch's own
+// dynamic size still sets its occupancy).  0, or -1 with the error set.
+int allow_dynamic_lds(const void *kernel);
+// Compute units of the current device (queried once; 256 if the query fails).
+int device_cus();
+
 }  // namespace oxb
 
 #define OXB_CHECK_HIP(call)                                                   \

@@ -8,7 +8,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "oxb_common.h"
 #include "oxb_kernels.h"
@@ -17,6 +20,32 @@ namespace oxb {
 
 static thread_local std::string g_error;
 static thread_local bool g_has_error = false;
+
+int allow_dynamic_lds(const void *kernel) {
+    static std::mutex mu;
+    static std::set<std::pair<int, const void *>> done;
+    int dev = 0;
+    OXB_CHECK_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({dev, kernel})) return 0;
+    hipFuncAttributes a{};
+    OXB_CHECK_HIP(hipFuncGetAttributes(&a, kernel));
+    const int room = 160 * 1024 - (int)a.sharedSizeBytes;
+    OXB_CHECK_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, room));
+    done.insert({dev, kernel});
+    return 0;
+}
+
+int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return cus;
+}
 
 void set_error(const char *fmt, ...) {
     char buf[1024];

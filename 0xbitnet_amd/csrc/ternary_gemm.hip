@@ -689,7 +689,7 @@ static int gemm_launch(const GemmParams &p, void *stream) {
     }
     // LDS-staged tiles: the largest of 128x128, 128x64, 64x128, 64x64 whose
     // grid still gives every CU a workgroup (N a multiple of the tile).
-    const int cus = 256;
+    const int cus = device_cus();
     auto blocks = [&](int ft, int tk) { return (long)(p.N / ft) * ((p.n_tok + tk - 1) / tk); };
     if (p.N % 256 == 0 && blocks(256, 128) >= cus * 3 / 4) return dma_launch<EPI, 2, 2, 4, 3>(p, s);
     if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 2, 2>(p, s);

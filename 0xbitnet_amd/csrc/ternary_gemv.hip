@@ -444,15 +444,9 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
 template <int PRO, int EPI, int NREG, int PF, bool EXACT, int TT = 1, int NW = 4, bool STREAM = PF == 4>
 static int launch_n(const GemvParams &p, hipStream_t s) {
     const size_t sm = gemv_smem(p.K, TT, NW);
-    if (sm > 64 * 1024) {
-        static bool raised = false;   // per instantiation
-        if (!raised) {
-            OXB_CHECK_HIP(hipFuncSetAttribute(
-                (const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT, NW, STREAM>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-            raised = true;
-        }
-    }
+    if (sm > 64 * 1024 &&
+        allow_dynamic_lds((const void *)gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT, NW, STREAM>))
+        return -1;
     hipLaunchKernelGGL((gemv_kernel<PRO, EPI, NREG, PF, EXACT, TT, NW, STREAM>),
                        dim3(p.N / (16 * TT)), dim3(64 * NW), sm, s, p);
     OXB_CHECK_HIP(hipGetLastError());
