@@ -194,6 +194,37 @@ def test_python_bitnet_api():
         bn.generate("x", print)
 
 
+def test_two_handles_on_two_threads():
+    """Two models (each its own stream and graphs) prefilled and decoded from
+    two host threads at once give the tokens each gives alone (the C ABI's
+    threading contract: one handle per thread, handles independent)."""
+    import threading
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    rng = np.random.default_rng(77)
+    prompts = [rng.integers(0, cfg.vocab, 30).astype(np.int32) for _ in range(2)]
+    models = [pkg.Model(path, max_seq=160) for _ in range(2)]
+
+    def run(i, out):
+        m = models[i]
+        m.reset()
+        t, _ = m.forward(prompts[i], want_logits=False)
+        out[i] = [t] + m.decode_greedy(100).tolist()
+
+    alone = [None, None]
+    for i in range(2):
+        run(i, alone)
+    together = [None, None]
+    th = [threading.Thread(target=run, args=(i, together)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert together == alone
+    for m in models:
+        m.close()
+
+
 @pytest.mark.parametrize("B", [1, 3, 5, 17])
 def test_batched_decode_equals_single_sequences(B):
     """Slots decoded together give each slot's one-sequence tokens and logits
