@@ -680,11 +680,21 @@ static int gemm_launch(const GemmParams &p, void *stream) {
     if (p.n_tok <= 64) {
         const int tt = (p.n_tok + 15) >> 4;
         const bool two = tt >= 3 && p.N % 32 == 0 && p.N / 32 >= 256;
+        // up to 4 feature tiles per workgroup while the grid still gives every
+        // CU a workgroup (each workgroup reads all of X, so fewer workgroups
+        // re-read it less)
+        const int cus = device_cus();
+        const bool four = p.N % 64 == 0 && p.N / 64 >= cus;
+        const bool pair = p.N % 32 == 0 && p.N / 32 >= cus;
         switch (tt) {
-            case 1: return skinny_launch<EPI, 1, 1>(p, s);
-            case 2: return skinny_launch<EPI, 2, 1>(p, s);
-            case 3: return two ? skinny_launch<EPI, 3, 2>(p, s) : skinny_launch<EPI, 3, 1>(p, s);
-            default: return two ? skinny_launch<EPI, 4, 2>(p, s) : skinny_launch<EPI, 4, 1>(p, s);
+            case 1: return four ? skinny_launch<EPI, 1, 4>(p, s)
+                                : pair ? skinny_launch<EPI, 1, 2>(p, s) : skinny_launch<EPI, 1, 1>(p, s);
+            case 2: return four ? skinny_launch<EPI, 2, 4>(p, s)
+                                : pair ? skinny_launch<EPI, 2, 2>(p, s) : skinny_launch<EPI, 2, 1>(p, s);
+            case 3: return four ? skinny_launch<EPI, 3, 4>(p, s)
+                                : two ? skinny_launch<EPI, 3, 2>(p, s) : skinny_launch<EPI, 3, 1>(p, s);
+            default: return four ? skinny_launch<EPI, 4, 4>(p, s)
+                                 : two ? skinny_launch<EPI, 4, 2>(p, s) : skinny_launch<EPI, 4, 1>(p, s);
         }
     }
     // LDS-staged tiles: the largest of 128x128, 128x64, 64x128, 64x64 whose

@@ -317,7 +317,10 @@ def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
                                    # feature tiles per workgroup, uneven K splits over waves
                                    (2560, 6912, 8), (3840, 2560, 16), (2560, 2560, 32),
                                    (8192, 2560, 40), (8192, 512, 64), (256, 1280, 64),
-                                   (96, 256, 1)])
+                                   (96, 256, 1),
+                                   # 4 / 2 feature tiles per workgroup at 1-4 token tiles
+                                   (16384, 512, 8), (28672, 256, 20), (8192, 1024, 16),
+                                   (16384, 512, 40), (28672, 256, 64)])
 def test_gemm_mfma_bitexact(N, K, n):
     rng = np.random.default_rng(N + n)
     w = ternary(rng, N, K)
