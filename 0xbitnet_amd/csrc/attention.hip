@@ -850,6 +850,181 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     if (w < G) out[(size_t)(hk * G + w) * kHd + 64 * half + lane] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Decode, one workgroup per query head (grid: heads x sequences), 256
+// threads, up to 256 * NJ cached positions (NJ = 1 or 2).  Built for latency:
+//  - thread t computes the scores of positions t + 256 j from its own K rows,
+//    loaded straight into registers at kernel start and clamped to the cache
+//    extent (rows at or past S are stale but in bounds and never used), so
+//    no load waits for the position; the head's q row is an SGPR operand of
+//    each v_fma_mix step (scalar loads), and its eight cache lines are
+//    fetched while the K rows are in flight;
+//  - the softmax runs on all four waves in the shader's order: thread t's
+//    strided partial exp(x_t - max) + exp(x_{t+256} - max), then the halving
+//    tree (strides 128 and 64 through LDS, 32 .. 1 in one wave);
+//  - P.V: wave w sums 256-position block w / 2 for dim 64 (w % 2) + lane, its
+//    V elements loaded into registers with 16-bit loads one 64-position chunk
+//    ahead (no LDS staging); the two block sums are added in block order.
+// Same arithmetic as the other decode kernels, so the same bits.
+// ---------------------------------------------------------------------------
+constexpr int kHeadChunk = 64;   // V positions per register chunk
+
+template <int NJ>
+__global__ __launch_bounds__(256) void attn_head_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
+    size_t kv_stride, int pos_stride) {
+    static_assert(NJ == 1 || NJ == 2, "attn_head_kernel: up to 512 positions");
+    __shared__ __align__(16) float pr[256 * NJ];   // probabilities
+    __shared__ float red[256];
+    __shared__ float wmax[4];
+    __shared__ float inv_s;
+    __shared__ float bsum[kHd];                  // block 1's sums
+    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int hk = h / G;
+    const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
+    kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    u32x4_t kr[NJ][16];   // K rows tid + 256 j, 128 f16 each
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const u32x4_t *row = (const u32x4_t *)(kc + (size_t)min(tid + 256 * j, max_seq - 1) * kHd);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kr[j][i] = row[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float qw[kHd / 16];   // one dword per 64-byte line of the q row
+#pragma unroll
+    for (int i = 0; i < kHd / 16; ++i) qw[i] = qh[16 * i];
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    asm volatile("" ::"s"(pos), "s"(qw[0]), "s"(qw[1]), "s"(qw[2]), "s"(qw[3]), "s"(qw[4]),
+                 "s"(qw[5]), "s"(qw[6]), "s"(qw[7]));
+    // a position out of range (the host checks it too) computes one position
+    // and stores nothing
+    const bool valid = pos >= 0 && pos < max_seq && pos < 256 * NJ;
+    const int S = valid ? pos + 1 : 1;
+
+    // this wave's P.V block and dim; its first V chunk goes out now.  V
+    // chunks are read unclamped (64 rows from a chunk start below S, so at
+    // most 63 rows past the cache extent: the caller pads the cache
+    // allocation by kHeadChunk rows), which keeps each load one instruction
+    // with an immediate offset.
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int d = 64 * (w & 1) + lane, blk = wu >> 1;
+    const int b0 = 256 * blk;
+    const int nb = min(max(S - b0, 0), 256);   // positions of the block (wave-uniform)
+    const uint16_t *__restrict__ vcol = vc + d;
+    auto load_v = [&](uint16_t (&dst)[kHeadChunk], int s0) {
+        const uint16_t *__restrict__ vrow = vcol + (size_t)s0 * kHd;
+#pragma unroll
+        for (int i = 0; i < kHeadChunk; ++i) dst[i] = vrow[i * kHd];
+    };
+    // waves 2-3 have a P.V block only with two position groups
+    const bool pv_wave = NJ == 2 || blk == 0;
+    uint16_t va[kHeadChunk], vb[kHeadChunk];
+    load_v(va, min(b0, S - 1));   // (every wave: a conditional load would wait at the join)
+
+    // ---- scores: 128-term chains in order of d (sh/attention.wgsl:48-58) ----
+    float x[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const u32x4_t kv = kr[j][i];
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const uint32_t kw = kv[k2];
+                const float k0 = __half2float(__ushort_as_half((uint16_t)(kw & 0xffffu)));
+                const float k1 = __half2float(__ushort_as_half((uint16_t)(kw >> 16)));
+                dot = __builtin_fmaf(qh[8 * i + 2 * k2], k0, dot);
+                dot = __builtin_fmaf(qh[8 * i + 2 * k2 + 1], k1, dot);
+            }
+        }
+        x[j] = dot * scale;
+    }
+
+    // ---- softmax (sh/softmax.wgsl:25-80) ------------------------------------
+    float m = -3.402823e+38f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        if (tid + 256 * j < S) m = fmaxf(m, x[j]);
+    m = wave_max_dpp(m);
+    if (lane == 0) wmax[w] = m;
+    lds_barrier();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float e[NJ], part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        e[j] = tid + 256 * j < S ? oxb_expf(x[j] - m) : 0.0f;
+        part = part + e[j];   // thread t's strided partial, in order of j
+    }
+    red[tid] = part;
+    lds_barrier();
+    if (w == 0) {
+        const float a = red[lane] + red[lane + 128];        // stride 128, t = lane
+        const float c = red[lane + 64] + red[lane + 192];   // stride 128, t = lane + 64
+        const float sum = wave_tree_sum(a + c);             // stride 64, then 32 .. 1
+        if (lane == 0) inv_s = 1.0f / sum;
+    }
+    lds_barrier();
+    const float inv = inv_s;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) pr[tid + 256 * j] = e[j] * inv;   // 0 past S
+    lds_barrier();
+
+    // ---- P.V (sh/attention.wgsl:96-104), this wave's block ------------------
+    float acc = 0.0f;
+    auto sum_chunk = [&](const uint16_t (&v)[kHeadChunk], int s0, int n) {
+        const float *p = pr + s0;
+        if (n == kHeadChunk) {
+#pragma unroll
+            for (int i = 0; i < kHeadChunk; i += 4) {
+                const float4 p4 = *(const float4 *)(p + i);
+                acc = __builtin_fmaf(p4.x, __half2float(__ushort_as_half(v[i])), acc);
+                acc = __builtin_fmaf(p4.y, __half2float(__ushort_as_half(v[i + 1])), acc);
+                acc = __builtin_fmaf(p4.z, __half2float(__ushort_as_half(v[i + 2])), acc);
+                acc = __builtin_fmaf(p4.w, __half2float(__ushort_as_half(v[i + 3])), acc);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kHeadChunk; i += 4) {
+                const float4 p4 = *(const float4 *)(p + i);
+                const float pp[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float t = __builtin_fmaf(pp[k], __half2float(__ushort_as_half(v[i + k])), acc);
+                    acc = i + k < n ? t : acc;
+                }
+            }
+        }
+    };
+    // The block's (up to) four chunks as straight-line code, each chunk
+    // loaded one ahead and unconditionally (its start clamped below S): a
+    // load under a branch or carried around a loop makes the compiler copy
+    // its registers where the paths join, which waits for the load on the
+    // spot.  Only the sums are conditional.
+    if (pv_wave) {
+        load_v(vb, min(b0 + kHeadChunk, S - 1));
+        if (nb > 0) sum_chunk(va, b0, min(kHeadChunk, nb));
+        load_v(va, min(b0 + 2 * kHeadChunk, S - 1));
+        if (nb > kHeadChunk) sum_chunk(vb, b0 + kHeadChunk, min(kHeadChunk, nb - kHeadChunk));
+        load_v(vb, min(b0 + 3 * kHeadChunk, S - 1));
+        if (nb > 2 * kHeadChunk)
+            sum_chunk(va, b0 + 2 * kHeadChunk, min(kHeadChunk, nb - 2 * kHeadChunk));
+        if (nb > 3 * kHeadChunk)
+            sum_chunk(vb, b0 + 3 * kHeadChunk, nb - 3 * kHeadChunk);
+    }
+    if constexpr (NJ == 2) {   // blocks added in order: total = part0 + part1
+        if (blk == 1) bsum[d] = acc;
+        lds_barrier();
+        if (blk == 0 && S > 256) acc = acc + bsum[d];
+    }
+    if (blk == 0 && valid) out[((size_t)z * H + h) * kHd + d] = acc;
+}
+
 // LDS of the prefill kernel for R score rows of up to s_max positions
 __host__ __device__ inline size_t prefill_smem(int R, int s_max) {
     return (size_t)R * (kHd + ((s_max + 3) & ~3)) * sizeof(float);
@@ -1030,4 +1205,28 @@ extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const ui
     OXB_REQUIRE(n_tok > 0 && pos0 >= 0 && pos0 + n_tok <= max_seq, "prefill attention: bad range");
     return dispatch_prefill(q, kcache, vcache, pos0, n_tok, H, Hkv, hd, max_seq, pos0 + n_tok, out,
                             stream);
+}
+
+extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                    const int *pos, int pos_stride, size_t kv_stride, int batch,
+                                    int H, int Hkv, int hd, int max_seq, int s_max, float *out,
+                                    void *stream) {
+    OXB_REQUIRE(pos, "attention: pos is NULL");
+    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
+    OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
+                "attention: caches of a batch overlap (stride %zu)", kv_stride);
+    OXB_REQUIRE(s_max >= 1 && s_max <= 512,
+                "per-head decode attention: s_max %d out of range (1..512)", s_max);
+    const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    hipStream_t s = (hipStream_t)stream;
+    if (s_max <= 256)
+        hipLaunchKernelGGL(attn_head_kernel<1>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
+                           pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    else
+        hipLaunchKernelGGL(attn_head_kernel<2>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
+                           pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
 }

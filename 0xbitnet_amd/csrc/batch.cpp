@@ -103,6 +103,7 @@ int oxb_batch::enqueue_step() {
 int oxb_batch::capture() {
     if (graph) return 0;
     hipGraph_t g = nullptr;
+    B_CHECK(hipStreamSynchronize(m->stream));   // capture on an idle stream only
     B_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
     const int rc = enqueue_step();
     hipError_t e = hipStreamEndCapture(m->stream, &g);
@@ -151,8 +152,9 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
     b->slot_kv = b->layer_kv * m->n_layers;
     const int D = m->D, F = m->F, Dq = m->H * m->hd;
     const int rows = (batch + 15) & ~15;
-    b->kcache = (uint16_t *)b->dalloc(b->slot_kv * batch * 2);
-    b->vcache = (uint16_t *)b->dalloc(b->slot_kv * batch * 2);
+    const size_t pad = (size_t)OXB_KV_PAD_ROWS * m->hd;   // per-head attention reads whole V chunks
+    b->kcache = (uint16_t *)b->dalloc((b->slot_kv * batch + pad) * 2);
+    b->vcache = (uint16_t *)b->dalloc((b->slot_kv * batch + pad) * 2);
     b->state = (int *)b->dalloc((size_t)batch * OXB_STATE_INTS * 4);
     b->tok_hist = (int *)b->dalloc((size_t)batch * b->hist_cap * 4);
     b->rope = (float *)b->dalloc((size_t)max_seq * m->hd * 4);

@@ -5,8 +5,9 @@
 // sh/rmsnorm.wgsl:27-63 (final norm, rs/nn/model.rs:354-391),
 // sh/embedding.wgsl:23-46, rs/sampling.rs:4-80 with top_k = 1 (argmax).
 // The reference reads the 513 KB of logits back to the host every token; here
-// the argmax is reduced on the device (last-block pattern) and written to the
-// decode state, so a decode step never needs the host.
+// the argmax is reduced on the device (one atomic max per block, then a
+// one-block finish kernel) and written to the decode state, so a decode step
+// never needs the host.
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
@@ -158,12 +159,11 @@ __global__ __launch_bounds__(256) void lm_norm_pairs_kernel(const float *__restr
 // stream them double-buffered, so 20 KiB per wave stay in flight.  The 16
 // group sums meet in LDS; one wave per tile folds them, writes the logits and
 // keeps a running argmax.  Block winners meet in one 64-bit atomic max
-// (argmax_key) in the decode state; the last block to take a ticket
-// publishes the token.  Agent-scope atomic RMWs are coherent across the
-// chip's L2s, and each block waits for its max to return before taking its
-// ticket, so the ticket order covers every max.  No cache-wide fences: a
-// release/acquire per block writes back and invalidates the L2 and cost
-// ~0.25 us per block.
+// (argmax_key) in the decode state; lm_finish_kernel, launched right after,
+// publishes the token.  (A last-block ticket would need a release per block
+// to order the maxima before it: an agent-scope release writes back the L2,
+// and with ~63 blocks per XCD those write-backs cost ~9 us per pass, against
+// ~1.6 us for the second launch.)
 // HG: the normalised rows come from the pair table p_hn (lm_norm_pairs_kernel)
 // instead of the workgroup's own prologue.
 template <int NJ, int NV, bool HG = false>  // D = 512 * NJ; NV rows of x (one pass over E)
@@ -285,7 +285,6 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p, const float2 *
     }
     __syncthreads();
     if (tid != 0) return;
-    uint32_t sink = 0;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         float bv = bval[v][0];
@@ -294,28 +293,26 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p, const float2 *
             if (better(bval[v][k], bidx[v][k], bv, bi)) { bv = bval[v][k]; bi = bidx[v][k]; }
         unsigned long long *key =
             (unsigned long long *)(p.state + (size_t)v * p.state_stride + OXB_ST_LM_KEY);
-        sink |= (uint32_t)__hip_atomic_fetch_max(key, argmax_key(bv, bi), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_max(key, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    asm volatile("" ::"v"(sink));   // wait for the maxima before the ticket
-    const int ticket = __hip_atomic_fetch_add(&p.state[OXB_ST_LM_COUNTER], 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    if (ticket != (int)gridDim.x - 1) return;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        int *st = p.state + (size_t)v * p.state_stride;
-        unsigned long long *key = (unsigned long long *)(st + OXB_ST_LM_KEY);
-        const unsigned long long k =
-            __hip_atomic_fetch_or(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int tok = (int)(0xffffffffu - (uint32_t)k);
-        int *hist = p.tok_hist ? p.tok_hist + (size_t)v * p.hist_stride : nullptr;
-        st[OXB_ST_TOKEN] = tok;
-        if (hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) hist[st[OXB_ST_NGEN]] = tok;
-        st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
-        st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
-        __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __hip_atomic_store(&p.state[OXB_ST_LM_COUNTER], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After the LM head (the kernel boundary orders every block's max before
+// this): publish each row's token from its argmax key, append it to the
+// row's history, advance the position and clear the key for the next pass.
+__global__ __launch_bounds__(64) void lm_finish_kernel(LmParams p, int nv) {
+    const int v = threadIdx.x;
+    if (v >= nv) return;
+    int *st = p.state + (size_t)v * p.state_stride;
+    unsigned long long *key = (unsigned long long *)(st + OXB_ST_LM_KEY);
+    const unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int tok = (int)(0xffffffffu - (uint32_t)k);
+    int *hist = p.tok_hist ? p.tok_hist + (size_t)v * p.hist_stride : nullptr;
+    st[OXB_ST_TOKEN] = tok;
+    if (hist && st[OXB_ST_NGEN] < st[OXB_ST_HIST_CAP]) hist[st[OXB_ST_NGEN]] = tok;
+    st[OXB_ST_NGEN] = st[OXB_ST_NGEN] + 1;
+    st[OXB_ST_POS] = st[OXB_ST_POS] + p.advance;
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x[t][d] = E[id_t][d] (f16 -> f32); ids out of range give zeros.
@@ -382,6 +379,7 @@ static int lm_launch(const LmParams &p, hipStream_t s, const float2 *hn = nullpt
             hipLaunchKernelGGL((lm_norm_pairs_kernel<n>), dim3(NV), dim3(256), 0, s, p.x,      \
                                p.x_stride, p.gamma, p.eps, p.D, NV, (float2 *)hn);            \
         hipLaunchKernelGGL((lm_head_kernel<n, NV, HG>), dim3(grid), dim3(256), 0, s, p, hn);   \
+        hipLaunchKernelGGL(lm_finish_kernel, dim3(1), dim3(64), 0, s, p, NV);                  \
         break;
         OXB_NL(1) OXB_NL(2) OXB_NL(3) OXB_NL(4) OXB_NL(5)
 #undef OXB_NL

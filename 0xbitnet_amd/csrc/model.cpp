@@ -37,8 +37,8 @@ using namespace oxb;
 
 oxb_model::~oxb_model() {   // teardown: errors have no caller to go to
     if (stream) (void)hipStreamSynchronize(stream);
-    if (graph) (void)hipGraphExecDestroy(graph);
-    if (graph_fused) (void)hipGraphExecDestroy(graph_fused);
+    for (hipGraphExec_t g : graphs)
+        if (g) (void)hipGraphExecDestroy(g);
     for (void *p : allocations) (void)hipFree(p);
     if (pinned) (void)hipHostFree(pinned);
     if (stream) (void)hipStreamDestroy(stream);
@@ -434,8 +434,9 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
             return nullptr;
     }
 
-    // KV cache and decode buffers
-    const size_t kv_elems = (size_t)m->n_layers * Hkv * m->max_seq * hd;
+    // KV cache and decode buffers (OXB_KV_PAD_ROWS rows of padding past the
+    // last head: the per-head decode attention reads whole V chunks)
+    const size_t kv_elems = (size_t)m->n_layers * Hkv * m->max_seq * hd + (size_t)OXB_KV_PAD_ROWS * hd;
     m->kcache = (uint16_t *)m->dalloc(kv_elems * 2);
     m->vcache = (uint16_t *)m->dalloc(kv_elems * 2);
     m->x = (float *)m->dalloc((size_t)D * 4);
@@ -446,13 +447,15 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
-    // one-kernel decode attention while the cache holds <= 256 positions: it
-    // saves a launch but computes each KV head's scores on two CUs, which
-    // loses to the two-kernel path (scores spread over the chip) beyond ~260
-    // positions (MI355X, 2B shape).  OXB_ATTN_FUSED_MAX_S overrides (0: off).
-    m->fused_max_s = 256;
-    if (const char *env = getenv("OXB_ATTN_FUSED_MAX_S")) m->fused_max_s = atoi(env);
-    if (!oxb_attn_decode_fused_supported(m->H, m->Hkv, m->hd, m->max_seq)) m->fused_max_s = 0;
+    if (const char *env = getenv("OXB_ATTN")) {
+        if (!strcmp(env, "head")) m->attn_mode = 0;
+        else if (!strcmp(env, "fused")) m->attn_mode = 1;
+        else if (!strcmp(env, "split")) m->attn_mode = 2;
+        else {
+            set_error("OXB_ATTN=%s: expected head, fused or split", env);
+            return nullptr;
+        }
+    }
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
     if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist)
         return nullptr;
@@ -483,7 +486,15 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
 // One decode step: embedding of state.token at state.pos -> layers -> LM
 // head + argmax (state.token, state.pos += 1).  Every kernel reads the
 // position from device memory, so the same launch sequence replays as a graph.
-int oxb_model::enqueue_decode_step(bool fused_attn) {
+oxb_model::AttnForm oxb_model::attn_form(int S) const {
+    if (attn_mode == 0 && S <= 256) return ATTN_HEAD1;
+    if (attn_mode == 0 && S <= 512) return ATTN_HEAD2;
+    if (attn_mode == 1 && S <= 256 && oxb_attn_decode_fused_supported(H, Hkv, hd, max_seq))
+        return ATTN_FUSED;
+    return ATTN_SPLIT;
+}
+
+int oxb_model::enqueue_decode_step(AttnForm attn) {
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     int *posp = state + OXB_ST_POS;
@@ -495,12 +506,23 @@ int oxb_model::enqueue_decode_step(bool fused_attn) {
         if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
                               max_seq, rope, posp, s))
             return -1;
-        if (fused_attn ? oxb_attn_decode_fused(q, kc, vc, posp, H, Hkv, hd, max_seq, attn, s)
-                       : oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, attn, s))
-            return -1;
+        int rc;
+        switch (attn) {
+            case ATTN_HEAD1:
+            case ATTN_HEAD2:
+                rc = oxb_attn_decode_head(q, kc, vc, posp, 0, 0, 1, H, Hkv, hd, max_seq,
+                                          attn == ATTN_HEAD1 ? 256 : 512, this->attn, s);
+                break;
+            case ATTN_FUSED:
+                rc = oxb_attn_decode_fused(q, kc, vc, posp, H, Hkv, hd, max_seq, this->attn, s);
+                break;
+            default:
+                rc = oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, this->attn, s);
+        }
+        if (rc) return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
-        if (oxb_bitlinear_gemv(L.wo, attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr, nullptr,
-                               nullptr, s))
+        if (oxb_bitlinear_gemv(L.wo, this->attn, L.attn_sub, 1e-5f, L.so, D, Dq, x, 1, nullptr,
+                               nullptr, nullptr, s))
             return -1;
         if (relu2) {
             if (oxb_bitlinear_gateup(L.wgu, x, L.ffn_norm, eps, L.sgu, 2 * F, D, h, s)) return -1;
@@ -516,12 +538,17 @@ int oxb_model::enqueue_decode_step(bool fused_attn) {
                               1, s);
 }
 
-int oxb_model::capture_graph(bool fused_attn) {
-    hipGraphExec_t &slot = fused_attn ? graph_fused : graph;
+int oxb_model::capture_graph(AttnForm attn) {
+    hipGraphExec_t &slot = graphs[attn];
     if (slot) return 0;
     hipGraph_t g = nullptr;
+    // Capture only on an idle stream: no replay of another step graph may
+    // still be queued when capture begins, and the kernels' first launches
+    // (lazy code-object load, LDS attribute set-up) happen with nothing of
+    // this handle in flight.
+    M_CHECK(hipStreamSynchronize(stream));
     M_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_decode_step(fused_attn);
+    int rc = enqueue_decode_step(attn);
     hipError_t e = hipStreamEndCapture(stream, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -541,10 +568,16 @@ int oxb_model::capture_graph(bool fused_attn) {
     return 0;
 }
 
-hipGraphExec_t oxb_model::step_graph(int p) {
-    const bool fused = p + 1 <= fused_max_s;
-    if (capture_graph(fused)) return nullptr;
-    return fused ? graph_fused : graph;
+// Every graph a run of steps will replay is captured before the first of
+// them is launched, so a run that crosses from one attention form to the
+// next never captures while replays are queued.
+int oxb_model::ensure_graphs(int p0, int p1) {
+    for (int p = p0; p < p1;) {
+        const AttnForm f = attn_form(p + 1);
+        if (capture_graph(f)) return -1;
+        while (p < p1 && attn_form(p + 1) == f) ++p;   // the run of positions with this form
+    }
+    return 0;
 }
 
 int oxb_model::ensure_prefill(int n) {
@@ -701,8 +734,8 @@ extern "C" int oxb_model_step(oxb_model *m, float *logits_host) {
     clear_error();
     OXB_REQUIRE(m, "model is NULL");
     OXB_REQUIRE(m->pos + 1 <= m->max_seq, "KV cache full: position %d of %d", m->pos, m->max_seq);
+    if (m->ensure_graphs(m->pos, m->pos + 1)) return -1;
     hipGraphExec_t ge = m->step_graph(m->pos);
-    if (!ge) return -1;
     M_CHECK(hipGraphLaunch(ge, m->stream));
     m->pos += 1;
     m->ngen += 1;
@@ -732,11 +765,8 @@ extern "C" int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *token
                 n_steps, m->max_seq);
     OXB_REQUIRE(m->ngen + n_steps <= m->hist_cap, "token history full");
     const int first = m->ngen;
-    for (int i = 0; i < n_steps; ++i) {
-        hipGraphExec_t ge = m->step_graph(m->pos + i);
-        if (!ge) return -1;
-        M_CHECK(hipGraphLaunch(ge, m->stream));
-    }
+    if (m->ensure_graphs(m->pos, m->pos + n_steps)) return -1;
+    for (int i = 0; i < n_steps; ++i) M_CHECK(hipGraphLaunch(m->step_graph(m->pos + i), m->stream));
     m->pos += n_steps;
     m->ngen += n_steps;
     if (n_steps)

@@ -45,10 +45,18 @@ struct oxb_model {
     int *psum = nullptr, *pids = nullptr;
 
     hipStream_t stream = nullptr;
-    // decode step graphs: two-kernel attention, and one-kernel attention for
-    // caches of up to fused_max_s positions (0: never)
-    hipGraphExec_t graph = nullptr, graph_fused = nullptr;
-    int fused_max_s = 0;
+    // Decode attention forms, chosen per step by the cache length S (the
+    // position + 1); each has its own step graph.
+    //   ATTN_HEAD1 / ATTN_HEAD2: one workgroup per query head, S <= 256 / 512
+    //   ATTN_FUSED: two workgroups per KV head, S <= 256
+    //   ATTN_SPLIT: scores kernel + P.V kernel, any S
+    enum AttnForm { ATTN_HEAD1 = 0, ATTN_HEAD2, ATTN_FUSED, ATTN_SPLIT, ATTN_FORMS };
+    hipGraphExec_t graphs[ATTN_FORMS] = {};
+    // which forms the model uses: 0 per-head kernels up to 512 positions
+    // (default), 1 the fused kernel up to 256, 2 the split kernels only
+    // (OXB_ATTN=head|fused|split when the model loads; all give the same bits)
+    int attn_mode = 0;
+    AttnForm attn_form(int S) const;
     int *pinned = nullptr;      // host-pinned scratch for small readbacks
     int pos = 0;                // host mirror of state[OXB_ST_POS]
     int ngen = 0;               // host mirror of state[OXB_ST_NGEN]
@@ -58,7 +66,7 @@ struct oxb_model {
 
     ~oxb_model();
     void *dalloc(size_t bytes);
-    int enqueue_decode_step(bool fused_attn);
+    int enqueue_decode_step(AttnForm attn);
     int ensure_prefill(int n);
     // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state
     // block, token history and position
@@ -71,9 +79,12 @@ struct oxb_model {
     };
     int enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &t);
     int enqueue_prefill(const int32_t *ids, int n);
-    int capture_graph(bool fused_attn);
-    // the graph for a step whose token sits at position p (captured on first use)
-    hipGraphExec_t step_graph(int p);
+    int capture_graph(AttnForm attn);
+    // capture the graphs of every step at positions [p0, p1) (on an idle
+    // stream, before any of them is replayed)
+    int ensure_graphs(int p0, int p1);
+    // the graph for a step whose token sits at position p (after ensure_graphs)
+    hipGraphExec_t step_graph(int p) const { return graphs[attn_form(p + 1)]; }
 };
 
 namespace oxb {

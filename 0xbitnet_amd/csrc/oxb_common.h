@@ -78,6 +78,15 @@ __device__ inline uint4 load_nt(const uint4 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 0 in a VGPR the compiler cannot see through.  A load indexed by it stays a
+// per-lane value: a load of a uniform address would be copied to an SGPR
+// where it is first used, and that copy waits for the load on the spot.
+__device__ inline int opaque_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences
 // global memory, which makes every wave wait for all of its loads in flight
 // (weight or V prefetch for later stages) at each barrier; the kernels'

@@ -185,14 +185,29 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     const int nb = (cpl + PF - 1) / PF;           // batches (uniform; 1 unless STREAM)
     const int tile0 = blockIdx.x * TT;
 
-    // ---- loads: prologue inputs, then the residual, then the weights -------
+    // ---- loads: every input of the epilogue first (the position, this
+    // thread's row scale, the residual), then the prologue's row, then the
+    // weights, so that the epilogue after the reduction waits on nothing.
+    // All kernel arguments are pinned in SGPRs here: read where they are used,
+    // the late ones are further kernarg round trips at the end of the kernel.
+    asm volatile("" ::"s"(p.x), "s"(p.gamma), "s"(p.eps), "s"(p.y), "s"(p.wscale),
+                 "s"(p.acc_out), "s"(p.xq_out), "s"(p.q_out), "s"(p.kcache), "s"(p.vcache),
+                 "s"(p.rope));
+    const int n_ep = tile0 * 16 + (tid & (16 * TT - 1));   // the row this thread may finish
+    [[maybe_unused]] int pos = 0;
+    // read per lane (an index the compiler cannot see is zero): a uniform
+    // value would be moved to an SGPR, and that copy waits for the load
+    // before the weights are even issued
+    if constexpr (EPI == EPI_QKV) pos = p.pos[opaque_zero()];
+    const float ws_ep = p.wscale[n_ep];
+    float resid = 0.0f;
+    if constexpr (EPI == EPI_RESID) resid = p.y[n_ep];
+    __builtin_amdgcn_sched_barrier(0);
     float v[NREG], g[NREG];
     if constexpr (PRO == PRO_QUANT) {
         if constexpr (EXACT) load_row_exact<NREG>(p.x, p.gamma ? p.gamma : p.x, v, g);
         else load_row<NREG>(p.x, p.gamma, K, v, g);
     }
-    float resid = 0.0f;
-    if constexpr (EPI == EPI_RESID) resid = p.y[tile0 * 16 + (tid & (16 * TT - 1))];
     auto load_batch = [&](uint4 (&dst)[TT][PF], int b) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -209,6 +224,14 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     uint4 A[TT][PF];
     [[maybe_unused]] uint4 B[TT][PF];
     load_batch(A, 0);
+    // RoPE pair of this thread's row at the position (q and k rows), issued
+    // as soon as the position is back; clamped so the load stays in the table
+    [[maybe_unused]] float2 cs = make_float2(1.0f, 0.0f);
+    if constexpr (EPI == EPI_QKV) {
+        const int d = (n_ep < p.Dq ? n_ep : n_ep - p.Dq) % p.hd;
+        const int pc = min(max(pos, 0), p.max_seq - 1);
+        if (n_ep < p.Dq + p.Dkv) cs = p.rope[(size_t)pc * (p.hd >> 1) + (d >> 1)];
+    }
 
     // ---- prologue ---------------------------------------------------------
     float in_scale;
@@ -318,10 +341,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     for (int k = 0; k < 4 * NW; ++k) a += wpart[(tid >> 4) * 64 * NW + k * 16 + r];
     if constexpr (PRO == PRO_QUANT) xsum = wq[0] + wq[1] + wq[2] + wq[3];
     a -= xsum;
-    const int n = tile0 * 16 + tid;
+    const int n = n_ep;   // == tile0 * 16 + tid here
     if (p.acc_out) p.acc_out[n] = a;
     // sh/ternary_gemv.wgsl:94-95: (f32(acc) * scales[row]) * input_scale
-    float yv = (float)a * p.wscale[n];
+    float yv = (float)a * ws_ep;
     yv = yv * in_scale;
 
     if constexpr (EPI == EPI_STORE) {
@@ -337,14 +360,11 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             p.y[n >> 1] = gt * other;     // sh/elementwise.wgsl:32
         }
     } else {  // EPI_QKV
-        const int pos = *p.pos;
         if (pos < 0 || pos >= p.max_seq) return;  // host checks too; never write out of range
         const float other = __shfl_xor(yv, 1, 64);
         const int Dk = p.Dq + p.Dkv;
         float outv = yv;
         if (n < Dk) {  // q or k: RoPE on the interleaved pair (2i, 2i+1)
-            const int d = (n < p.Dq ? n : n - p.Dq) % p.hd;
-            const float2 cs = p.rope[(size_t)pos * (p.hd >> 1) + (d >> 1)];
             if ((n & 1) == 0) {
                 float a0 = yv * cs.x, a1 = other * cs.y;
                 outv = a0 - a1;

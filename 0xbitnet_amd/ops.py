@@ -191,16 +191,30 @@ def gemm(Wt, x: np.ndarray, gamma, eps: float, wscale: np.ndarray, N: int, K: in
     return acc.download(), Y.download(shape=(n, ncol)), sc.download(shape=(n,))
 
 
+KV_PAD_ROWS = 64   # include/oxbitnet_ops.h OXB_KV_PAD_ROWS
+
+
+def _padded_cache(c: np.ndarray, hd: int) -> DeviceArray:
+    """A cache on the device with OXB_KV_PAD_ROWS rows of zeros past its end."""
+    flat = np.ascontiguousarray(c, np.float16).view(np.uint16).reshape(-1)
+    return DeviceArray.from_host(np.concatenate([flat, np.zeros(KV_PAD_ROWS * hd, np.uint16)]))
+
+
 def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, H: int, Hkv: int,
-                hd: int, max_seq: int, fused: bool = False):
+                hd: int, max_seq: int, fused: bool = False, head: bool = False, s_max: int = 0):
     """q [H*hd] f32; caches [Hkv][max_seq][hd] f16; attends over pos+1 positions.
-    fused: the one-kernel variant (oxb_attn_decode_fused)."""
+    fused: the one-kernel variant (oxb_attn_decode_fused); head: one workgroup
+    per query head (oxb_attn_decode_head, caches padded as it requires)."""
     dq = DeviceArray.from_host(np.ascontiguousarray(q, np.float32))
-    dk = DeviceArray.from_host(np.ascontiguousarray(kcache, np.float16).view(np.uint16))
-    dv = DeviceArray.from_host(np.ascontiguousarray(vcache, np.float16).view(np.uint16))
+    dk = _padded_cache(kcache, hd)
+    dv = _padded_cache(vcache, hd)
     dpos = DeviceArray.from_host(np.array([pos], np.int32))
     out = DeviceArray((H * hd,), np.float32)
-    if fused:
+    if head:
+        check(lib().oxb_attn_decode_head(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, 0, 0, 1, H, Hkv, hd,
+                                         max_seq, s_max or pos + 1, out.ptr, None),
+              "attn_decode_head")
+    elif fused:
         check(lib().oxb_attn_decode_fused(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq,
                                           out.ptr, None), "attn_decode_fused")
     else:

@@ -34,10 +34,15 @@ extern "C" {
 #define OXB_ST_POS 0         /* next position (== KV length before the step) */
 #define OXB_ST_TOKEN 1       /* current token id (greedy argmax output)      */
 #define OXB_ST_NGEN 2        /* LM-head invocations since reset              */
-#define OXB_ST_LM_COUNTER 3  /* internal: LM-head last-block ticket          */
+#define OXB_ST_LM_COUNTER 3  /* reserved (kept zero)                         */
 #define OXB_ST_HIST_CAP 4    /* capacity of the token history buffer         */
 #define OXB_ST_LM_KEY 6      /* internal: ints 6-7, LM-head argmax key (u64) */
 #define OXB_STATE_INTS 8
+
+/* Rows (of 128 f16) a cache allocation must extend past its last head's
+ * max_seq rows for oxb_attn_decode_head, which reads V in whole 64-row
+ * chunks from any chunk start below the cache length. */
+#define OXB_KV_PAD_ROWS 64
 
 /* ---- errors, device memory, streams, events (plumbing) ----------------- */
 const char *oxb_last_error(void);
@@ -158,6 +163,21 @@ int oxb_attn_decode_fused(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
                           void *stream);
 
+/* The same decode attention, one 256-thread workgroup per query head and
+ * sequence (grid H x batch), for caches of up to s_max <= 512 positions
+ * (256 * ceil(s_max / 256) positions are supported by the launch).  Built for
+ * latency: K rows load into registers before the position is known, the q
+ * row is an SGPR operand of each score step, the softmax runs on four waves
+ * in the shader's order and the two 256-position P.V blocks on separate
+ * waves; same result bits as oxb_attn_decode.  Sequence z: q + z*H*128,
+ * caches + z*kv_stride, pos[z*pos_stride], out + z*H*128.  The cache
+ * allocations must extend OXB_KV_PAD_ROWS rows past the last head (V is read
+ * in whole chunks).  Replaces nn/attention.rs:109-118 like oxb_attn_decode;
+ * no counterpart of its own in the reference. */
+int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                         const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
+                         int Hkv, int hd, int max_seq, int s_max, float *out, void *stream);
+
 /* Causal prefill attention for n_tok queries at positions pos0.., same order.
  * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
@@ -180,7 +200,9 @@ size_t oxb_lm_bytes(int V, int D);
  * (lowest index on ties) written to state[OXB_ST_TOKEN], appended to
  * tok_hist (if state[OXB_ST_HIST_CAP] allows), state[OXB_ST_POS] += advance.
  * state is 8-byte aligned with OXB_ST_LM_COUNTER and OXB_ST_LM_KEY zero
- * (the kernel leaves them zero).  Replaces nn/model.rs:226-262,
+ * (the call leaves them zero; two launches: the head, whose blocks meet in an
+ * atomic max on OXB_ST_LM_KEY, then a one-block finish that publishes the
+ * token).  Replaces nn/model.rs:226-262,
  * 393-448 plus read_logits (:269-298) and sampling.rs with top_k = 1. */
 int oxb_lm_head_argmax(const float *x, const float *gamma, float eps, const void *E_lm, int V,
                        int D, float *logits, int *state, int *tok_hist, int advance,

@@ -47,11 +47,20 @@ class _Layer(C.Structure):
     ] + [(n, _f32p) for n in ("attn_norm", "ffn_norm", "attn_sub_norm", "ffn_sub_norm")]
 
 
+ProbeFn = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_size_t)
+
+# probe sites of oxo_forward (oxb_oracle.h, OXO_SITE_*)
+SITES = ("x_in", "attn_norm", "qkv_q8", "qkv_scale", "q", "k", "v", "attn", "o_q8", "o_scale",
+         "o", "x_mid", "ffn_norm", "gate", "up", "down_q8", "down_scale", "down", "x_out",
+         "final")
+
+
 class _Model(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "D", "F", "H", "Hkv", "V", "max_seq")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("kv_f16", C.c_int),
         ("embed", _u16p), ("final_norm", _f32p), ("layers", C.POINTER(_Layer)),
         ("kcache", _f32p), ("vcache", _f32p), ("seq_len", C.c_int),
+        ("probe", ProbeFn), ("probe_ud", C.c_void_p),
     ]
 
 
@@ -320,10 +329,26 @@ class Model:
     def seq_len(self) -> int:
         return self._m.seq_len
 
-    def forward(self, ids) -> np.ndarray:
+    def forward(self, ids, trace: dict | None = None) -> np.ndarray:
+        """Logits of the last id.  With `trace` (a dict), every probe site of
+        every layer is copied into trace[(layer, site_name)] as a numpy array
+        with one row per id (int8 for the *_q8 sites, else float32)."""
         ids = _c(ids, np.uint32)
         logits = np.zeros(self.cfg["V"], np.float32)
-        rc = lib().oxo_forward(C.byref(self._m), _p(ids, _u32p), ids.size, _p(logits, _f32p))
+        n = ids.size
+
+        def on_probe(_ud, layer, site, data, nbytes):
+            name = SITES[site]
+            dt = np.int8 if name.endswith("_q8") else np.float32
+            buf = (C.c_char * nbytes).from_address(data)
+            trace[(layer, name)] = np.frombuffer(bytes(buf), dt).reshape(n, -1).copy()
+
+        cb = ProbeFn(on_probe) if trace is not None else ProbeFn()
+        self._m.probe = cb
+        try:
+            rc = lib().oxo_forward(C.byref(self._m), _p(ids, _u32p), n, _p(logits, _f32p))
+        finally:
+            self._m.probe = ProbeFn()
         if rc != 0:
             raise RuntimeError("oracle: KV cache overflow")
         return logits

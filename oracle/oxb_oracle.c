@@ -414,11 +414,17 @@ int oxo_argmax(const float *x, int n) {
 /* whole model                                                               */
 /* ------------------------------------------------------------------------ */
 
+static void probe(const oxo_model *m, int layer, int site, const void *data, size_t bytes) {
+    if (m->probe) m->probe(m->probe_ud, layer, site, data, bytes);
+}
+
 /* rs/nn/bitlinear.rs:52-97: optional RMSNorm (eps hard-coded 1e-5, :112),
- * quantize, then GEMV for one token or GEMM for several. */
-static void bitlinear(const float *in, int n, int in_dim, int out_dim,
-                      const uint8_t *W, float wscale, const float *norm_w,
-                      float *out) {
+ * quantize, then GEMV for one token or GEMM for several.  site_q8 >= 0
+ * reports the int8 input and its scales to the probe (sites site_q8 and
+ * site_q8 + 1). */
+static void bitlinear(const oxo_model *m, int layer, int site_q8, const float *in, int n,
+                      int in_dim, int out_dim, const uint8_t *W, float wscale,
+                      const float *norm_w, float *out) {
     float *normed = NULL;
     const float *src = in;
     if (norm_w) {
@@ -431,6 +437,10 @@ static void bitlinear(const float *in, int n, int in_dim, int out_dim,
     float *ws = (float *)malloc(sizeof(float) * (size_t)out_dim);
     for (int r = 0; r < out_dim; r++) ws[r] = wscale; /* rs/model/loader.rs:131-136 */
     oxo_quantize(src, n, in_dim, q, is);
+    if (site_q8 >= 0) {
+        probe(m, layer, site_q8, q, (size_t)n * in_dim);
+        probe(m, layer, site_q8 + 1, is, sizeof(float) * (size_t)n);
+    }
     if (n == 1)
         oxo_gemv(W, q, ws, is[0], out_dim, in_dim, NULL, out);
     else
@@ -446,17 +456,18 @@ int oxo_forward(oxo_model *m, const uint32_t *ids, int n, float *logits) {
     const int hd = D / H, kvd = Hkv * hd;
     if (m->seq_len + n > m->max_seq) return -1;
     size_t nD = (size_t)n * D;
-    float *x = (float *)malloc(sizeof(float) * nD);
-    float *h = (float *)malloc(sizeof(float) * nD);
-    float *q = (float *)malloc(sizeof(float) * (size_t)n * H * hd);
-    float *k = (float *)malloc(sizeof(float) * (size_t)n * kvd);
-    float *v = (float *)malloc(sizeof(float) * (size_t)n * kvd);
-    float *qr = (float *)malloc(sizeof(float) * (size_t)n * H * hd);
-    float *kr = (float *)malloc(sizeof(float) * (size_t)n * kvd);
-    float *att = (float *)malloc(sizeof(float) * (size_t)n * H * hd);
-    float *o = (float *)malloc(sizeof(float) * nD);
-    float *g = (float *)malloc(sizeof(float) * (size_t)n * F);
-    float *u = (float *)malloc(sizeof(float) * (size_t)n * F);
+    const size_t f4 = sizeof(float);
+    float *x = (float *)malloc(f4 * nD);
+    float *h = (float *)malloc(f4 * nD);
+    float *q = (float *)malloc(f4 * (size_t)n * H * hd);
+    float *k = (float *)malloc(f4 * (size_t)n * kvd);
+    float *v = (float *)malloc(f4 * (size_t)n * kvd);
+    float *qr = (float *)malloc(f4 * (size_t)n * H * hd);
+    float *kr = (float *)malloc(f4 * (size_t)n * kvd);
+    float *att = (float *)malloc(f4 * (size_t)n * H * hd);
+    float *o = (float *)malloc(f4 * nD);
+    float *g = (float *)malloc(f4 * (size_t)n * F);
+    float *u = (float *)malloc(f4 * (size_t)n * F);
 
     oxo_embedding(ids, n, m->embed, m->V, D, x); /* rs/nn/model.rs:213 */
     for (int l = 0; l < m->n_layers; l++) {
@@ -464,14 +475,19 @@ int oxo_forward(oxo_model *m, const uint32_t *ids, int n, float *logits) {
         float *kc = m->kcache + (size_t)l * m->max_seq * kvd;
         float *vc = m->vcache + (size_t)l * m->max_seq * kvd;
         int pos = m->seq_len;
+        probe(m, l, OXO_SITE_X_IN, x, f4 * nD);
         /* rs/nn/transformer.rs:51-75 */
         oxo_rmsnorm(x, L->attn_norm, n, D, m->eps, h);
+        probe(m, l, OXO_SITE_ATTN_NORM, h, f4 * nD);
         /* rs/nn/attention.rs:98-100: q, k, v each quantize the same input */
-        bitlinear(h, n, D, H * hd, L->wq, L->sq, NULL, q);
-        bitlinear(h, n, D, kvd, L->wk, L->sk, NULL, k);
-        bitlinear(h, n, D, kvd, L->wv, L->sv, NULL, v);
+        bitlinear(m, l, OXO_SITE_QKV_Q8, h, n, D, H * hd, L->wq, L->sq, NULL, q);
+        bitlinear(m, l, -1, h, n, D, kvd, L->wk, L->sk, NULL, k);
+        bitlinear(m, l, -1, h, n, D, kvd, L->wv, L->sv, NULL, v);
         oxo_rope(q, n, H, hd, pos, m->rope_theta, qr); /* :103-104 */
         oxo_rope(k, n, Hkv, hd, pos, m->rope_theta, kr);
+        probe(m, l, OXO_SITE_Q, qr, f4 * (size_t)n * H * hd);
+        probe(m, l, OXO_SITE_K, kr, f4 * (size_t)n * kvd);
+        probe(m, l, OXO_SITE_V, v, f4 * (size_t)n * kvd);
         for (size_t i = 0; i < (size_t)n * kvd; i++) { /* append, :182-183 */
             float kv_k = kr[i], kv_v = v[i];
             if (m->kv_f16) {
@@ -482,19 +498,28 @@ int oxo_forward(oxo_model *m, const uint32_t *ids, int n, float *logits) {
             vc[(size_t)pos * kvd + i] = kv_v;
         }
         oxo_attention(qr, kc, vc, n, pos + n, H, Hkv, hd, att);
-        bitlinear(att, n, H * hd, D, L->wo, L->so, L->attn_sub_norm, o);
+        probe(m, l, OXO_SITE_ATTN, att, f4 * (size_t)n * H * hd);
+        bitlinear(m, l, OXO_SITE_O_Q8, att, n, H * hd, D, L->wo, L->so, L->attn_sub_norm, o);
+        probe(m, l, OXO_SITE_O, o, f4 * nD);
         oxo_add(x, o, nD, x); /* residual1 */
+        probe(m, l, OXO_SITE_X_MID, x, f4 * nD);
         oxo_rmsnorm(x, L->ffn_norm, n, D, m->eps, h);
+        probe(m, l, OXO_SITE_FFN_NORM, h, f4 * nD);
         /* rs/nn/ffn.rs:60-80 */
-        bitlinear(h, n, D, F, L->wgate, L->sgate, NULL, g);
-        bitlinear(h, n, D, F, L->wup, L->sup, NULL, u);
+        bitlinear(m, l, -1, h, n, D, F, L->wgate, L->sgate, NULL, g);
+        bitlinear(m, l, -1, h, n, D, F, L->wup, L->sup, NULL, u);
+        probe(m, l, OXO_SITE_GATE, g, f4 * (size_t)n * F);
+        probe(m, l, OXO_SITE_UP, u, f4 * (size_t)n * F);
         oxo_relu2(g, (size_t)n * F, g);
         oxo_mul(g, u, (size_t)n * F, g);
-        bitlinear(g, n, F, D, L->wdown, L->sdown, L->ffn_sub_norm, o);
+        bitlinear(m, l, OXO_SITE_DOWN_Q8, g, n, F, D, L->wdown, L->sdown, L->ffn_sub_norm, o);
+        probe(m, l, OXO_SITE_DOWN, o, f4 * nD);
         oxo_add(x, o, nD, x);
+        probe(m, l, OXO_SITE_X_OUT, x, f4 * nD);
     }
     m->seq_len += n; /* rs/nn/model.rs:222 */
     oxo_rmsnorm(x, m->final_norm, n, D, m->eps, h);
+    probe(m, -1, OXO_SITE_FINAL, h, f4 * nD);
     oxo_lm_head(h + (size_t)(n - 1) * D, m->embed, m->V, D, logits);
 
     free(x); free(h); free(q); free(k); free(v); free(qr); free(kr);

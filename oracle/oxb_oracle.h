@@ -134,6 +134,36 @@ typedef struct {
     const float *ffn_sub_norm;           /* [F],   may be NULL */
 } oxo_layer;
 
+/* Probe sites: oxo_forward hands each intermediate of a layer to the model's
+ * probe callback (if set), all rows of the call at once, so that tests can
+ * check the composition itself (norm placement, residual order, causality,
+ * GQA mapping) and not only the final logits.  Q8 sites are int8 [n][in],
+ * SCALE sites f32 [n]; the rest f32 [n][width]. */
+enum {
+    OXO_SITE_X_IN = 0,      /* residual stream entering the layer      [n][D]   */
+    OXO_SITE_ATTN_NORM,     /* input_layernorm output                  [n][D]   */
+    OXO_SITE_QKV_Q8,        /* int8 input of q/k/v_proj (one per layer) [n][D]  */
+    OXO_SITE_QKV_SCALE,
+    OXO_SITE_Q,             /* q after RoPE                            [n][H*hd] */
+    OXO_SITE_K,             /* k after RoPE, before any f16 rounding   [n][Hkv*hd] */
+    OXO_SITE_V,             /*                                          [n][Hkv*hd] */
+    OXO_SITE_ATTN,          /* attention output (input of o_proj)      [n][H*hd] */
+    OXO_SITE_O_Q8,          /* int8 input of o_proj (after attn_sub_norm) */
+    OXO_SITE_O_SCALE,
+    OXO_SITE_O,             /* o_proj output                           [n][D]   */
+    OXO_SITE_X_MID,         /* residual after attention                [n][D]   */
+    OXO_SITE_FFN_NORM,      /* post_attention_layernorm output         [n][D]   */
+    OXO_SITE_GATE,          /* gate_proj output (before the activation) [n][F]  */
+    OXO_SITE_UP,            /* up_proj output                          [n][F]   */
+    OXO_SITE_DOWN_Q8,       /* int8 input of down_proj (after ffn_sub_norm) */
+    OXO_SITE_DOWN_SCALE,
+    OXO_SITE_DOWN,          /* down_proj output                        [n][D]   */
+    OXO_SITE_X_OUT,         /* residual leaving the layer              [n][D]   */
+    OXO_SITE_FINAL,         /* final RMSNorm output, layer = -1        [n][D]   */
+    OXO_N_SITES
+};
+typedef void (*oxo_probe_fn)(void *ud, int layer, int site, const void *data, size_t bytes);
+
 typedef struct {
     int n_layers, D, F, H, Hkv, V, max_seq;
     float eps, rope_theta;
@@ -143,6 +173,8 @@ typedef struct {
     const oxo_layer *layers;
     float *kcache, *vcache; /* each [n_layers][max_seq][Hkv][hd] */
     int seq_len;
+    oxo_probe_fn probe;     /* optional: intermediates, see OXO_SITE_* */
+    void *probe_ud;
 } oxo_model;
 
 /* Forward n_tok ids at position model->seq_len; writes the last token's

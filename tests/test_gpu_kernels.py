@@ -243,6 +243,63 @@ def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("pos,H,Hkv,S,s_max", [
+    # one position group (up to 256): empty P.V tail, whole and partial chunks
+    (0, 20, 5, 512, 256), (3, 20, 5, 512, 256), (63, 20, 5, 512, 256), (64, 20, 5, 512, 256),
+    (127, 20, 5, 512, 256), (128, 20, 5, 300, 256), (139, 20, 5, 400, 256),
+    (255, 20, 5, 256, 256),
+    # two groups (the second P.V block on waves 2-3): 257 .. 512 positions
+    (256, 20, 5, 512, 512), (300, 20, 5, 512, 512), (383, 20, 5, 384, 512),
+    (511, 20, 5, 512, 512), (10, 20, 5, 512, 512),
+    # other GQA groups; short caches (K rows clamped to the cache extent)
+    (200, 8, 8, 512, 256), (100, 16, 2, 256, 256), (40, 32, 4, 64, 256), (63, 20, 5, 64, 256),
+    (20, 4, 1, 21, 256)])
+def test_attn_decode_head_bitexact(pos, H, Hkv, S, s_max):
+    """Per-query-head decode attention: same bits as the oracle."""
+    rng = np.random.default_rng(pos * 11 + H + s_max)
+    hd = 128
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
+    out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, head=True, s_max=s_max)
+    ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_attn_decode_head_batch_bitexact():
+    """The per-head kernel over a batch of sequences (grid y), each its own
+    cache and position."""
+    B, H, Hkv, S, hd = 5, 20, 5, 448, 128
+    rng = np.random.default_rng(97)
+    q = rng.standard_normal((B, H * hd)).astype(np.float32)
+    kc = (rng.standard_normal((B, Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((B, Hkv, S, hd)).astype(np.float16)
+    pos = np.array([447, 0, 255, 256, 100], np.int32)
+    st = np.zeros((B, 8), np.int32)
+    st[:, 0] = pos
+    L = ops.lib()
+    pad = np.zeros(ops.KV_PAD_ROWS * hd, np.uint16)
+    dq = ops.DeviceArray.from_host(q)
+    dk = ops.DeviceArray.from_host(np.concatenate([kc.view(np.uint16).reshape(-1), pad]))
+    dv = ops.DeviceArray.from_host(np.concatenate([vc.view(np.uint16).reshape(-1), pad]))
+    dst = ops.DeviceArray.from_host(st)
+    out = ops.DeviceArray((B, H * hd), np.float32)
+    ops.check(L.oxb_attn_decode_head(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H, Hkv,
+                                     hd, S, 512, out.ptr, None), "attn_decode_head")
+    ops.sync()
+    got = out.download()
+    for z in range(B):
+        ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(pos[z]) + 1, H, Hkv, hd)
+        assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"slot {z}"
+
+
+def test_attn_decode_head_rejects_long_caches():
+    with pytest.raises(ops.NativeError, match="s_max"):
+        ops.attn_decode(np.zeros(20 * 128, np.float32), np.zeros((5, 600, 128), np.float16),
+                        np.zeros((5, 600, 128), np.float16), 599, 20, 5, 128, 600, head=True,
+                        s_max=600)
+
+
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
                                        (9, 8, 8, 512)])
 def test_attn_decode_batch_bitexact(B, H, Hkv, S):
@@ -338,10 +395,14 @@ def test_gemm_mfma_bitexact(N, K, n):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("N,K,n", [(28672, 8192, 512), (8192, 28672, 4096)])
+@pytest.mark.parametrize("N,K,n", [(28672, 8192, 8), (28672, 8192, 64), (8192, 28672, 8),
+                                   (8192, 28672, 64), (28672, 8192, 512), (8192, 28672, 512),
+                                   (28672, 8192, 4096), (8192, 28672, 4096)])
 def test_gemm_sweep_shapes_bitexact(N, K, n):
-    """The ternary matmul sweep at full size (the 256x128 DMA-staged kernel, 32
-    and 112 K stages): int32 accumulators and outputs equal the oracle's."""
+    """The ternary matmul sweep at full size: the skinny kernel (8 and 64
+    tokens), the 128x128 LDS-staged or 256x128 DMA-staged kernels (512 and 4096
+    tokens, 32 and 112 K stages): int32 accumulators and outputs equal the
+    oracle's."""
     rng = np.random.default_rng(N + K + n)
     w = ternary(rng, N, K)
     Wn = synth.i2s_pack(w)
@@ -351,13 +412,20 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     acc_o, Y_o = O.gemm(Wn, q, ws, s, K)
     # rows this long exceed the fused quantizer (D <= 7168): tile the oracle's
     # int8 rows on the host into the GEMM's layout [n/16][K/256][4 planes]
-    # [4 chunks][16 tokens][16 B], k = stage*256 + (c//2)*128 + g*32 + (c%2)*16 + j
-    tiles = q.reshape(n // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
+    # [4 chunks][16 tokens][16 B], k = stage*256 + (c//2)*128 + g*32 + (c%2)*16 + j;
+    # a partial token tile is padded with zero rows (scale 1, sum 0), as the
+    # device quantizer pads it
+    n16 = (n + 15) // 16 * 16
+    qp = np.zeros((n16, K), np.int8)
+    qp[:n] = q
+    sp = np.ones(n16, np.float32)
+    sp[:n] = s
+    tiles = qp.reshape(n16 // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
     L = ops.lib()
     Wt = ops.upload_ternary(Wn, K)
     dX = ops.DeviceArray.from_host(np.ascontiguousarray(tiles).reshape(-1))
-    dsc = ops.DeviceArray.from_host(s)
-    dsm = ops.DeviceArray.from_host(q.astype(np.int64).sum(axis=1).astype(np.int32))
+    dsc = ops.DeviceArray.from_host(sp)
+    dsm = ops.DeviceArray.from_host(qp.astype(np.int64).sum(axis=1).astype(np.int32))
     dws = ops.DeviceArray.from_host(ws)
     Y = ops.DeviceArray((n, N), np.float32)
     acc = ops.DeviceArray((n, N), np.int32)
