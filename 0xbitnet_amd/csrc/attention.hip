@@ -16,6 +16,8 @@
 // Each workgroup handles the whole GQA group of G q heads of a KV head, so
 // each cached K/V row is read once per group (prefill: once per group and
 // pair of queries).  Cache layout: [Hkv][max_seq][128] f16 bits.
+#include <mutex>
+
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
@@ -1229,4 +1231,57 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
                            pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention that allocates nothing: oxb_attn_decode with its scores
+// scratch in a static device array instead of a caller buffer.  The array is
+// per device (each GPU the library runs on holds its own copy until the
+// process ends); its device address is looked up once per device, on the
+// first call with that device current, and only that address is handed to
+// the kernels.  Calls on one device share the array, so calls that overlap
+// on one GPU race.  Nothing in it needs clearing: the kernels write every
+// score they read (positions < S) before reading it.
+// ---------------------------------------------------------------------------
+namespace oxb {
+constexpr size_t kNoAllocScoreFloats = (size_t)1 << 18;   // 1 MiB: H * max_seq <= 262144
+static __device__ __align__(256) float scratch[kNoAllocScoreFloats];
+constexpr int kMaxDevices = 64;
+
+static float *noalloc_scratch() {
+    static std::mutex mu;
+    static float *ptrs[kMaxDevices] = {};
+    int dev = 0;
+    const hipError_t ed = hipGetDevice(&dev);
+    if (ed != hipSuccess) {
+        set_error("attention (no-alloc): hipGetDevice: %s", hipGetErrorString(ed));
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("attention (no-alloc): device %d beyond the %d supported", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("attention (no-alloc): hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        ptrs[dev] = (float *)p;
+    }
+    return ptrs[dev];
+}
+}  // namespace oxb
+
+extern "C" int oxb_attn_decode_noalloc(const float *q, const uint16_t *kcache,
+                                       const uint16_t *vcache, const int *pos, int H, int Hkv,
+                                       int hd, int max_seq, float *out, void *stream) {
+    OXB_REQUIRE(H > 0 && max_seq > 0 && (size_t)H * max_seq <= kNoAllocScoreFloats,
+                "attention (no-alloc): heads %d x max_seq %d exceed the %zu-score scratch", H,
+                max_seq, kNoAllocScoreFloats);
+    float *scores = noalloc_scratch();
+    if (!scores) return -1;
+    return oxb_attn_decode(q, kcache, vcache, pos, H, Hkv, hd, max_seq, scores, out, stream);
 }

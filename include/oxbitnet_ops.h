@@ -178,6 +178,17 @@ int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t 
                          const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                          int Hkv, int hd, int max_seq, int s_max, float *out, void *stream);
 
+/* oxb_attn_decode without the scores buffer and without allocating: the
+ * scores live in a static device array of the library (one per device, 1 MiB:
+ * H * max_seq <= 262144; larger shapes are rejected), whose address is looked
+ * up on the first call on each device.  Same kernels and result bits as
+ * oxb_attn_decode.  Calls that overlap on one device share the array and
+ * race.  No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under hipGraph capture, allocation-free serving loops). */
+int oxb_attn_decode_noalloc(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                            const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
+                            void *stream);
+
 /* Causal prefill attention for n_tok queries at positions pos0.., same order.
  * q, out: [n_tok][H*128] f32.  Replaces the same three dispatches for n > 1. */
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
