@@ -1027,6 +1027,155 @@ __global__ __launch_bounds__(256) void attn_head_kernel(
     if (blk == 0 && valid) out[((size_t)z * H + h) * kHd + d] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Decode, one workgroup per query head, caches of up to 256 positions in a
+// cache of max_seq >= 256 rows:
+//  - K and V rows below S load coalesced (thread i: uint4 i + 256 k of each,
+//    rows clamped to S - 1) and are staged in LDS, K as [256][17] uint4 (padded rows), V row-major
+//    [256][128] f16; thread t runs the 128-step score chain of position t
+//    from its K row, q as the SGPR operand of each v_fma_mix;
+//  - softmax on the four waves in the shader's order, as attn_head_kernel;
+//  - P.V on waves 0 and 1, one dim per lane: each step one 16-bit LDS read
+//    and one v_fma_mix (the probabilities read four at a time).
+// Same arithmetic, so the same bits.
+// ---------------------------------------------------------------------------
+constexpr int kH256Rows = 256;
+constexpr size_t kH256KBytes = (size_t)kH256Rows * 17 * 16;   // K rows, padded
+constexpr size_t kH256VBytes = (size_t)kH256Rows * kHd * 2;   // V rows
+constexpr size_t kH256Lds = kH256KBytes + kH256VBytes + (256 + 256 + 8) * 4;
+
+__global__ __launch_bounds__(256) void attn_head256_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
+    size_t kv_stride, int pos_stride) {
+    extern __shared__ __align__(16) int8_t smem_h[];
+    u32x4_t (*ks)[17] = (u32x4_t (*)[17])smem_h;
+    u32x4_t *vs4 = (u32x4_t *)(smem_h + kH256KBytes);              // V [256][128] f16
+    const uint16_t *vs = (const uint16_t *)vs4;
+    float *pr = (float *)(smem_h + kH256KBytes + kH256VBytes);      // probabilities [256]
+    float *red = pr + 256;
+    float *wmax = red + 256;                                        // [4], then 1/sum at [4]
+    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int hk = h / G;
+    const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
+    kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    // The position first, then only the rows below S (clamped: the loads stay
+    // branch-free).  Loading all 256 rows without waiting for it was slower:
+    // 128 KB per CU at the CU's ~64 B/cycle, and the bulk loads delay the
+    // position's scalar load too.
+    float qw[kHd / 16];   // one dword per 64-byte line of the q row
+#pragma unroll
+    for (int i = 0; i < kHd / 16; ++i) qw[i] = qh[16 * i];
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    asm volatile("" ::"s"(pos), "s"(qw[0]), "s"(qw[1]), "s"(qw[2]), "s"(qw[3]), "s"(qw[4]),
+                 "s"(qw[5]), "s"(qw[6]), "s"(qw[7]));
+    const bool valid = pos >= 0 && pos < kH256Rows && pos < max_seq;
+    const int S = valid ? pos + 1 : 1;
+    u32x4_t kt[16], vt[16];   // uint4 tid + 256 k of the K and V rows < S
+    const u32x4_t *__restrict__ K4 = (const u32x4_t *)kc;
+    const u32x4_t *__restrict__ V4 = (const u32x4_t *)vc;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) kt[k] = K4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vt[k] = V4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ks[16 * k + (tid >> 4)][tid & 15] = kt[k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vs4[tid + 256 * k] = vt[k];
+    lds_barrier();
+
+    // ---- score of position tid: 128 terms in order of d -----------------
+    float x;
+    {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const u32x4_t kv = ks[tid][i];
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const uint32_t kw = kv[k2];
+                const float k0 = __half2float(__ushort_as_half((uint16_t)(kw & 0xffffu)));
+                const float k1 = __half2float(__ushort_as_half((uint16_t)(kw >> 16)));
+                dot = __builtin_fmaf(qh[8 * i + 2 * k2], k0, dot);
+                dot = __builtin_fmaf(qh[8 * i + 2 * k2 + 1], k1, dot);
+            }
+        }
+        x = dot * scale;
+    }
+
+    // ---- softmax (sh/softmax.wgsl:25-80) --------------------------------------
+    float m = tid < S ? x : -3.402823e+38f;
+    m = wave_max_dpp(m);
+    if (lane == 0) wmax[w] = m;
+    lds_barrier();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float e = tid < S ? oxb_expf(x - m) : 0.0f;
+    red[tid] = e;   // thread t's strided partial: one position (0 + e = e)
+    lds_barrier();
+    if (w == 0) {
+        const float a = red[lane] + red[lane + 128];
+        const float c = red[lane + 64] + red[lane + 192];
+        const float sum = wave_tree_sum(a + c);
+        if (lane == 0) wmax[4] = 1.0f / sum;
+    }
+    lds_barrier();
+    pr[tid] = e * wmax[4];   // 0 past S
+    lds_barrier();
+
+    // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
+    // Blocks of 16 positions, the LDS operands of the next block read while
+    // the current one is summed (positions past S read stale rows and
+    // probabilities 0, and are left out of the sum).
+    if (w < 2) {
+        const uint16_t *vd = vs + 64 * w + lane;   // V[s][d] at vd[s * 128]
+        float acc = 0.0f;
+        auto ld = [&](uint16_t (&V)[16], float4 (&P)[4], int s0) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) P[j] = *(const float4 *)(pr + s0 + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) V[j] = vd[(s0 + j) * kHd];
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto mac = [&](const uint16_t (&V)[16], const float4 (&P)[4]) {   // all 16
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = __builtin_fmaf(P[j].x, __half2float(__ushort_as_half(V[4 * j])), acc);
+                acc = __builtin_fmaf(P[j].y, __half2float(__ushort_as_half(V[4 * j + 1])), acc);
+                acc = __builtin_fmaf(P[j].z, __half2float(__ushort_as_half(V[4 * j + 2])), acc);
+                acc = __builtin_fmaf(P[j].w, __half2float(__ushort_as_half(V[4 * j + 3])), acc);
+            }
+        };
+        auto mac_part = [&](const uint16_t (&V)[16], const float4 (&P)[4], int n) {   // first n
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float pp[4] = {P[j].x, P[j].y, P[j].z, P[j].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float t = __builtin_fmaf(pp[k], __half2float(__ushort_as_half(V[4 * j + k])), acc);
+                    acc = 4 * j + k < n ? t : acc;
+                }
+            }
+        };
+        uint16_t VA[16], VB[16];
+        float4 PA[4], PB[4];
+        ld(VA, PA, 0);
+        for (int s0 = 0; s0 < S; s0 += 32) {   // S and s0 are wave-uniform: no divergence
+            ld(VB, PB, min(s0 + 16, kH256Rows - 16));
+            if (S - s0 >= 16) mac(VA, PA);
+            else mac_part(VA, PA, S - s0);
+            ld(VA, PA, min(s0 + 32, kH256Rows - 16));
+            if (S - s0 >= 32) mac(VB, PB);
+            else if (S - s0 > 16) mac_part(VB, PB, S - s0 - 16);
+        }
+        if (valid) out[((size_t)z * H + h) * kHd + 64 * w + lane] = acc;
+    }
+}
+
 // LDS of the prefill kernel for R score rows of up to s_max positions
 __host__ __device__ inline size_t prefill_smem(int R, int s_max) {
     return (size_t)R * (kHd + ((s_max + 3) & ~3)) * sizeof(float);
@@ -1223,7 +1372,11 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
                 "per-head decode attention: s_max %d out of range (1..512)", s_max);
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipStream_t s = (hipStream_t)stream;
-    if (s_max <= 256)
+    if (s_max <= 256 && max_seq >= kH256Rows) {
+        if (allow_dynamic_lds((const void *)attn_head256_kernel)) return -1;
+        hipLaunchKernelGGL(attn_head256_kernel, dim3(H, batch), dim3(256), kH256Lds, s, q, kcache,
+                           vcache, pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    } else if (s_max <= 256)
         hipLaunchKernelGGL(attn_head_kernel<1>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
                            pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
     else

@@ -434,7 +434,8 @@ def main() -> int:
         print(json.dumps({"long_context": lc}), flush=True)
         return 0
     t = time.time()
-    max_seq = args.prompt + args.steps + args.warmup + 8
+    # the context the C ABI loads with (rs/lib.rs:93: 4096), or more if the run needs it
+    max_seq = max(4096, args.prompt + args.steps + args.warmup + 8)
     model = pkg.Model(path, max_seq=max_seq)
     log(f"loaded in {time.time() - t:.1f}s; weights {model.info['weight_bytes'] / 1e9:.3f} GB")
 
