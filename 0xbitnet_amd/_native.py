@@ -97,6 +97,8 @@ SIGNATURES = {
     "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]),
     "oxb_attn_decode_fused_supported": (C.c_int, [i32, i32, i32, i32]),
     "oxb_attn_decode_fused": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "oxb_sample_logits": (C.c_int32, [vp, C.c_size_t, C.c_float, C.c_size_t, C.c_float, vp,
+                                      C.c_size_t, C.c_float]),
     "oxb_attn_decode_noalloc": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "oxb_attn_decode_head": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                        i32, vp, vp]),

@@ -72,12 +72,15 @@ bool valid_utf8(const char *s) {
 // sampling.rs:4-80, restated: penalty over the recent window (duplicates
 // counted each time), temperature scaling when != 1, top-k threshold
 // (k-th largest value; everything below becomes -inf), softmax, inverse-CDF
-// draw with r = U[0,1) * sum.
-static int32_t sample_token(std::vector<float> &lg, float temperature, size_t top_k,
-                            float repeat_penalty, const int32_t *recent, size_t n_recent,
-                            std::mt19937 &rng) {
-    const size_t V = lg.size();
-    if (repeat_penalty != 1.0f && n_recent) {
+// draw with r = u * sum for u in [0, 1).
+extern "C" int32_t oxb_sample_logits(float *lg, size_t V, float temperature, size_t top_k,
+                                     float repeat_penalty, const int32_t *recent,
+                                     size_t n_recent, float u) {
+    if (!lg || V == 0) {
+        set_error("sample: empty logits");
+        return -1;
+    }
+    if (repeat_penalty != 1.0f && n_recent && recent) {
         for (size_t i = 0; i < n_recent; ++i) {
             const size_t id = (size_t)recent[i];
             if (id < V) lg[id] = lg[id] > 0.0f ? lg[id] / repeat_penalty : lg[id] * repeat_penalty;
@@ -85,29 +88,37 @@ static int32_t sample_token(std::vector<float> &lg, float temperature, size_t to
     }
     if (temperature != 1.0f) {
         const float inv = 1.0f / temperature;
-        for (auto &v : lg) v *= inv;
+        for (size_t i = 0; i < V; ++i) lg[i] *= inv;
     }
     if (top_k > 0 && top_k < V) {
-        std::vector<float> tmp(lg);
+        std::vector<float> tmp(lg, lg + V);
         std::nth_element(tmp.begin(), tmp.begin() + (top_k - 1), tmp.end(), std::greater<float>());
         const float thr = tmp[top_k - 1];
-        for (auto &v : lg)
-            if (v < thr) v = -INFINITY;
+        for (size_t i = 0; i < V; ++i)
+            if (lg[i] < thr) lg[i] = -INFINITY;
     }
     float mx = -INFINITY;
-    for (float v : lg) mx = std::max(mx, v);
+    for (size_t i = 0; i < V; ++i) mx = std::max(mx, lg[i]);
     float sum = 0.0f;
-    for (auto &v : lg) {
-        v = std::exp(v - mx);
-        sum += v;
+    for (size_t i = 0; i < V; ++i) {
+        lg[i] = std::exp(lg[i] - mx);
+        sum += lg[i];
     }
-    const float r = std::uniform_real_distribution<float>(0.0f, 1.0f)(rng) * sum;
+    const float r = u * sum;
     float cum = 0.0f;
     for (size_t i = 0; i < V; ++i) {
         cum += lg[i];
         if (cum >= r) return (int32_t)i;
     }
     return (int32_t)(V - 1);
+}
+
+static int32_t sample_token(std::vector<float> &lg, float temperature, size_t top_k,
+                            float repeat_penalty, const int32_t *recent, size_t n_recent,
+                            std::mt19937 &rng) {
+    const float u = std::uniform_real_distribution<float>(0.0f, 1.0f)(rng);
+    return oxb_sample_logits(lg.data(), lg.size(), temperature, top_k, repeat_penalty, recent,
+                             n_recent, u);
 }
 
 struct GenOpts {

@@ -38,6 +38,11 @@ class Config:
     context: int = 4096
     arch: str = "bitnet-25"
     sub_norms: bool = True
+    # where the hyperparameters live: "" = under the arch name; the reference
+    # loader also reads "llama." / "bitnet." / "bitnet-25." (loader.rs:228-234)
+    meta_prefix: str = ""
+    norm_f16: bool = False     # norm weights stored F16 (converted on load, loader.rs:148-151)
+    eos: int = 257             # tokenizer.ggml.eos_token_id
 
     @property
     def head_dim(self) -> int:
@@ -147,24 +152,25 @@ def _tensor_list(cfg: Config):
     """(name, ggml_type, shape [ne0, ne1], kind) in file order."""
     D, F, hd = cfg.hidden, cfg.ffn, cfg.head_dim
     Dq, Dkv = cfg.heads * hd, cfg.kv_heads * hd
+    nt = GGML_F16 if cfg.norm_f16 else GGML_F32
     out = [("token_embd.weight", GGML_F16, [D, cfg.vocab], "embed")]
     for i in range(cfg.n_layers):
         p = f"blk.{i}."
         out += [
-            (p + "attn_norm.weight", GGML_F32, [D], "norm"),
+            (p + "attn_norm.weight", nt, [D], "norm"),
             (p + "attn_q.weight", GGML_I2_S, [D, Dq], "tern"),
             (p + "attn_k.weight", GGML_I2_S, [D, Dkv], "tern"),
             (p + "attn_v.weight", GGML_I2_S, [D, Dkv], "tern"),
             (p + "attn_output.weight", GGML_I2_S, [Dq, D], "tern"),
-            (p + "ffn_norm.weight", GGML_F32, [D], "norm"),
+            (p + "ffn_norm.weight", nt, [D], "norm"),
             (p + "ffn_gate.weight", GGML_I2_S, [D, F], "tern"),
             (p + "ffn_up.weight", GGML_I2_S, [D, F], "tern"),
             (p + "ffn_down.weight", GGML_I2_S, [F, D], "tern"),
         ]
         if cfg.sub_norms:
-            out += [(p + "attn_sub_norm.weight", GGML_F32, [Dq], "norm"),
-                    (p + "ffn_sub_norm.weight", GGML_F32, [F], "norm")]
-    out.append(("output_norm.weight", GGML_F32, [D], "norm"))
+            out += [(p + "attn_sub_norm.weight", nt, [Dq], "norm"),
+                    (p + "ffn_sub_norm.weight", nt, [F], "norm")]
+    out.append(("output_norm.weight", nt, [D], "norm"))
     return out
 
 
@@ -173,7 +179,7 @@ def _nbytes(typ, shape):
     return {GGML_F32: 4 * n, GGML_F16: 2 * n, GGML_I2_S: (n + 3) // 4 + 32}[typ]
 
 
-def _gen(kind, shape, rng):
+def _gen(kind, shape, rng, typ=GGML_F32):
     if kind == "embed":
         D, V = shape
         out = np.empty((V, D), np.float16)
@@ -183,7 +189,8 @@ def _gen(kind, shape, rng):
             out[r:r + m] = (rng.standard_normal((m, D), dtype=np.float32) * np.float32(0.02))
         return out.tobytes()
     if kind == "norm":
-        return rng.uniform(0.5, 1.5, size=shape[0]).astype(np.float32).tobytes()
+        g = rng.uniform(0.5, 1.5, size=shape[0]).astype(np.float32)
+        return (g.astype(np.float16) if typ == GGML_F16 else g).tobytes()
     K, N = shape
     packed = random_i2s(rng, N, K)
     scale = master_scale(rng)
@@ -193,10 +200,10 @@ def _gen(kind, shape, rng):
 def write_gguf(path: str, cfg: Config = BITNET_2B, seed: int = 1234) -> str:
     """Write a random-init model of shape `cfg`; returns path."""
     tensors = _tensor_list(cfg)
-    a = cfg.arch
+    a = cfg.meta_prefix or cfg.arch
     vocab = synthetic_vocab(cfg.vocab)
     kvs = [
-        _str("general.architecture", a),
+        _str("general.architecture", cfg.arch),
         _str("general.name", "synthetic-bitnet"),
         _u32("general.alignment", ALIGN),
         _u32(f"{a}.block_count", cfg.n_layers),
@@ -211,7 +218,7 @@ def write_gguf(path: str, cfg: Config = BITNET_2B, seed: int = 1234) -> str:
         _str("tokenizer.ggml.model", "gpt2"),
         _strarr("tokenizer.ggml.tokens", vocab),
         _u32("tokenizer.ggml.bos_token_id", 256),
-        _u32("tokenizer.ggml.eos_token_id", 257),
+        _u32("tokenizer.ggml.eos_token_id", cfg.eos),
     ]
     infos, off = [], 0
     for name, typ, shape, _ in tensors:
@@ -227,7 +234,7 @@ def write_gguf(path: str, cfg: Config = BITNET_2B, seed: int = 1234) -> str:
         f.write(b"\0" * ((-len(header)) % ALIGN))
         for idx, (name, typ, shape, kind) in enumerate(tensors):
             rng = np.random.default_rng([seed, idx])
-            data = _gen(kind, shape, rng)
+            data = _gen(kind, shape, rng, typ)
             assert len(data) == _nbytes(typ, shape), name
             f.write(data)
             f.write(b"\0" * ((-len(data)) % ALIGN))

@@ -23,7 +23,9 @@ The JSON line also carries
                 positions at batch 1, 8 and 32 (independent sequences);
   cpu_baseline  the CPU oracle (C restatement of the reference arithmetic,
                 OpenMP) decoding on the same model: a bounded sample of
-                steps after a short prompt.
+                steps after the same 128-token prompt, with the host CPU's
+                name and the reference's two other CPU legs (WGSL on
+                lavapipe, bitnet.cpp) recorded as unavailable.
 
     python bench.py --roofline-only [--calib-mib 256]
 
@@ -322,6 +324,33 @@ def calib_copy(ops, mib: int) -> None:
     b.free()
 
 
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# The reference's other CPU legs for this workload, neither of which can run
+# here: both would need software that is not on the machine and cannot be
+# fetched.
+OTHER_CPU_LEGS = {
+    "wgsl_lavapipe": {
+        "status": "unavailable",
+        "reason": "0xBitNet's own WGSL shaders on a CPU Vulkan adapter (Mesa lavapipe) through "
+                  "wgpu 26 need a Rust toolchain, the wgpu crates and a lavapipe ICD; none is "
+                  "installed and there is no network"},
+    "bitnet_cpp": {
+        "status": "unavailable",
+        "reason": "bitnet.cpp's I2_S kernels come from the reference's vendor/BitNet git "
+                  "submodule, which is not vendored (empty directory); there is no network"},
+}
+
+
 def cpu_baseline(synth, path: str, prompt: np.ndarray, steps: int) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -329,16 +358,20 @@ def cpu_baseline(synth, path: str, prompt: np.ndarray, steps: int) -> dict:
     from helpers import oracle_weights
     cfg, w = oracle_weights(path)
     m = O.Model(cfg, w, max_seq=len(prompt) + steps + 1, kv_f16=True)
+    t0 = time.perf_counter()
     logits = m.forward(prompt)
+    prefill_s = time.perf_counter() - t0
     tok = O.argmax(logits)
     t0 = time.perf_counter()
     for _ in range(steps):
         tok = O.argmax(m.forward(np.array([tok], np.uint32)))
     dt = time.perf_counter() - t0
     return {"value": round(steps / dt, 3), "unit": "tokens/s", "cores": O.num_threads(),
-            "kind": "port",
-            "sample": f"{steps} greedy decode steps after a {len(prompt)}-token prompt on the same "
-                      f"2B-shape model (C oracle, OpenMP over rows, f16-rounded KV)"}
+            "kind": "port", "cpu": cpu_model_name(),
+            "sample": f"{steps} greedy decode steps after the same {len(prompt)}-token prompt on "
+                      f"the same 2B-shape model (C oracle, OpenMP over rows, f16-rounded KV)",
+            "prefill_ms": round(prefill_s * 1e3, 1),
+            "other_cpu_legs": OTHER_CPU_LEGS}
 
 
 def cpu_kernels(synth) -> list:
@@ -481,7 +514,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         t = time.time()
-        cpu = cpu_baseline(synth, path, prompt[:8].astype(np.uint32), args.cpu_steps)
+        cpu = cpu_baseline(synth, path, prompt.astype(np.uint32), args.cpu_steps)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads ({time.time() - t:.1f}s)")
         extra["cpu_kernels"] = cpu_kernels(synth)
 

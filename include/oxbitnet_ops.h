@@ -194,6 +194,18 @@ int oxb_attn_decode_noalloc(const float *q, const uint16_t *kcache, const uint16
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
                      int pos0, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
 
+/* ---- sampling (host) -------------------------------------------------------- */
+/* One draw of rs/sampling.rs:4-80 over logits[V] (modified in place):
+ * repetition penalty over recent[n_recent] (positive logits divided, others
+ * multiplied, once per occurrence), temperature (logits * 1/T when T != 1),
+ * top-k (values below the k-th largest become -inf; k == 0 or >= V keeps all),
+ * softmax, then the first index whose running sum reaches u * sum for the
+ * uniform draw u in [0, 1) (V - 1 if none does).  The C ABI's generate passes
+ * u from its own generator; top_k == 1 without a penalty is the device argmax.
+ * Host code, no GPU. */
+int32_t oxb_sample_logits(float *logits, size_t V, float temperature, size_t top_k,
+                          float repeat_penalty, const int32_t *recent, size_t n_recent, float u);
+
 /* ---- embedding / LM head --------------------------------------------------- */
 /* x[t] = E[ids[t]] (f16 -> f32; out-of-range ids give zeros); ids == NULL reads
  * the decode state's token.  Replaces nn/model.rs:312-352. */

@@ -29,14 +29,21 @@ def absmax_quantize_input(rng, K):
 def oracle_weights(path: str):
     """(cfg dict, weights dict in the oracle's naming) from a synthetic GGUF."""
     meta, t = synth.read_gguf_tensors(path)
-    a = meta["general.architecture"]
-    cfg = dict(n_layers=meta[f"{a}.block_count"], D=meta[f"{a}.embedding_length"],
-               F=meta[f"{a}.feed_forward_length"], H=meta[f"{a}.attention.head_count"],
-               Hkv=meta[f"{a}.attention.head_count_kv"], V=meta[f"{a}.vocab_size"],
-               eps=meta[f"{a}.attention.layer_norm_rms_epsilon"],
-               rope_theta=meta[f"{a}.rope.freq_base"])
+    arch = meta["general.architecture"]
+
+    def get(suffix):   # the loader's prefix order (model/loader.rs:228-234)
+        for pre in (arch, "llama", "bitnet", "bitnet-25"):
+            if f"{pre}.{suffix}" in meta:
+                return meta[f"{pre}.{suffix}"]
+        raise KeyError(suffix)
+
+    cfg = dict(n_layers=get("block_count"), D=get("embedding_length"),
+               F=get("feed_forward_length"), H=get("attention.head_count"),
+               Hkv=get("attention.head_count_kv"), V=get("vocab_size"),
+               eps=get("attention.layer_norm_rms_epsilon"), rope_theta=get("rope.freq_base"))
+    f32 = lambda a: np.asarray(a).astype(np.float32)   # F16 norms widen exactly
     w = {"model.embed_tokens.weight": t["token_embd.weight"].view(np.uint16),
-         "model.norm.weight": t["output_norm.weight"]}
+         "model.norm.weight": f32(t["output_norm.weight"])}
     names = {"attn_q": "self_attn.q_proj", "attn_k": "self_attn.k_proj",
              "attn_v": "self_attn.v_proj", "attn_output": "self_attn.o_proj",
              "ffn_gate": "mlp.gate_proj", "ffn_up": "mlp.up_proj", "ffn_down": "mlp.down_proj"}
@@ -50,7 +57,7 @@ def oracle_weights(path: str):
         for g, h in norms.items():
             key = f"blk.{i}.{g}.weight"
             if key in t:
-                w[f"model.layers.{i}.{h}.weight"] = t[key]
+                w[f"model.layers.{i}.{h}.weight"] = f32(t[key])
     return cfg, w
 
 

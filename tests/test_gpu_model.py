@@ -272,6 +272,138 @@ def test_c_abi_generate_and_chat_greedy():
     L.oxbitnet_free(h)
 
 
+@pytest.mark.parametrize("prefix,f16", [("llama", True), ("bitnet", False), ("bitnet-25", True)])
+def test_loader_metadata_prefix_and_f16_norms(prefix, f16):
+    """model/loader.rs:221-291 reads each hyperparameter under the arch name,
+    then llama., bitnet., bitnet-25.; F16 norm tensors are widened to f32
+    (:148-151).  Files with the metadata under a fallback prefix and with F16
+    norms load and decode bit for bit like the oracle on the same weights."""
+    cfg = synth.small_config(meta_prefix=prefix, norm_f16=f16)
+    path = synth.cached_gguf(cfg, seed=7)
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab, 21).astype(np.int32)
+    assert len(_greedy_parity(path, prompt, 8)) == 9
+
+
+def _byte_decoder():
+    enc = synth._byte_alphabet()
+    return {ch: b for b, ch in enumerate(enc)}
+
+
+def _decode(vocab, dec, i):
+    """tokenizer.rs decode_one for the synthetic vocabulary: byte-level
+    tokens to bytes, specials to b''."""
+    t = vocab[i]
+    if t.startswith("<|") and len(t) > 4:
+        return b""
+    return bytes(dec[c] for c in t)
+
+
+def _greedy_ids(path, ids, n):
+    m = pkg.Model(path, max_seq=64)
+    t, _ = m.forward(np.array(ids, np.int32))
+    out = [t] + m.decode_greedy(n - 1).tolist()
+    m.close()
+    return out
+
+
+def _stream(path, prompt, max_tokens):
+    nat = pkg._native
+    L = nat.lib()
+    h = L.oxbitnet_load(path.encode(), None)
+    assert h, L.oxbitnet_error_message()
+    got = []
+    tf = nat.TokenFn(lambda t, n, ud: (got.append(C.string_at(t, n)), 0)[1])
+    g = L.oxbitnet_default_generate_options()
+    g.max_tokens, g.top_k, g.repeat_penalty = max_tokens, 1, 1.0
+    assert L.oxbitnet_generate(h, prompt.encode(), C.byref(g), tf, None) == 0
+    L.oxbitnet_free(h)
+    return got
+
+
+def test_generate_stops_before_eos():
+    """rs/lib.rs:175-177: a sampled EOS (or EOT) ends the stream and is not
+    emitted.  generate("ab") prefills [BOS, 'a', 'b'] (byte tokens 97, 98);
+    files that differ only in their EOS id stop after 0 and 1 tokens when the
+    EOS is the first and the second greedy token."""
+    base = synth.small_config()
+    ids = _greedy_ids(synth.cached_gguf(base, seed=7), [256, 97, 98], 4)
+    for k in (0, 1):
+        eos = ids[k]
+        stops = {eos, 260}   # the file's EOS and <|eot_id|>
+        want = next(j for j, t in enumerate(ids) if t in stops)
+        path = synth.cached_gguf(synth.small_config(eos=eos), seed=7)
+        got = _stream(path, "ab", 10)
+        assert len(got) == want <= k, (k, eos, ids, got)
+
+
+def _penalised_argmax(logits, recent, penalty):
+    """rs/sampling.rs:14-24 then top-1: each occurrence in the window divides
+    a positive logit (multiplies a negative one) by the penalty, in f32."""
+    lg = logits.astype(np.float32).copy()
+    p = np.float32(penalty)
+    for t in recent:
+        lg[t] = lg[t] / p if lg[t] > 0 else lg[t] * p
+    return int(np.argmax(lg)), lg
+
+
+def test_generate_top1_with_penalty_is_the_host_argmax_of_penalised_logits():
+    """generate with top_k 1 and repeat penalty 1.1 (the last 64 tokens) streams
+    the argmax of the penalised logits that the ids-level engine returns for
+    the same ids, step by step; steps whose top two penalised logits tie are
+    not expected (the sampler would draw between them)."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    n = 24
+    L = pkg._native.lib()
+    h = L.oxbitnet_load(path.encode(), None)
+    assert h, L.oxbitnet_error_message()
+    got = []
+    vocab, dec = synth.synthetic_vocab(cfg.vocab), _byte_decoder()
+    tf = pkg._native.TokenFn(lambda t, k, ud: (got.append(C.string_at(t, k)), 0)[1])
+    g = L.oxbitnet_default_generate_options()
+    g.max_tokens, g.top_k, g.repeat_penalty, g.temperature = n, 1, 1.1, 0.8
+    assert L.oxbitnet_generate(h, b"ab", C.byref(g), tf, None) == 0
+    L.oxbitnet_free(h)
+
+    m = pkg.Model(path, max_seq=64)
+    _, logits = m.forward(np.array([256, 97, 98], np.int32))
+    recent, want = [], []
+    for _ in range(n):
+        t, lg = _penalised_argmax(logits, recent[-64:], 1.1)
+        top2 = np.sort(lg)[-2:]
+        assert top2[0] < top2[1], "tie at the top: the draw is not determined"
+        if t in (257, 260):
+            break
+        recent.append(t)
+        b = _decode(vocab, dec, t)
+        if b"\0" not in b:
+            want.append(b)
+        _, logits = m.forward(np.array([t], np.int32))
+    m.close()
+    assert got == want
+
+
+def test_python_binding_greedy_tokens_are_the_engines():
+    """BitNet.generate (greedy: top_k 1, no penalty) streams the decoded
+    greedy tokens of the ids-level engine for the same prompt ids."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    ids = _greedy_ids(path, [256, 97, 98], 16)
+    vocab, dec = synth.synthetic_vocab(cfg.vocab), _byte_decoder()
+    want = []
+    for i in ids:
+        if i in (257, 260):   # EOS, <|eot_id|>
+            break
+        b = _decode(vocab, dec, i)
+        if b"\0" not in b:   # a token with a NUL is not passed to the callback
+            want.append(b.decode("utf-8", "replace"))
+    bn = pkg.BitNet.load_sync(path)
+    got = []
+    n = bn.generate("ab", got.append, max_tokens=16, top_k=1, repeat_penalty=1.0)
+    bn.dispose()
+    assert n == len(got) and got == want
+
+
 def test_python_bitnet_api():
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
