@@ -29,7 +29,7 @@ class ModelInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "hidden", "ffn", "heads", "kv_heads",
                                         "head_dim", "vocab", "max_seq")] + [
         ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("relu2", C.c_int),
-        ("weight_bytes", C.c_size_t)]
+        ("weight_bytes", C.c_size_t), ("kv_f32", C.c_int)]
 
 
 class GenerateOptions(C.Structure):  # include/oxbitnet.h OxBitNetGenerateOptions
@@ -109,6 +109,7 @@ SIGNATURES = {
     "oxb_lm_bytes": (C.c_size_t, [i32, i32]),
     # model
     "oxb_model_load": (vp, [C.c_char_p, C.c_int]),
+    "oxb_model_load_kv": (vp, [C.c_char_p, C.c_int, C.c_int]),
     "oxb_model_free": (None, [vp]),
     "oxb_model_get_info": (C.c_int, [vp, C.POINTER(ModelInfo)]),
     "oxb_model_reset": (C.c_int, [vp]),

@@ -113,8 +113,11 @@ class BitNet:
 class Model:
     """ids-level engine (include/oxbitnet_ops.h oxb_model_*)."""
 
-    def __init__(self, path: str, max_seq: int = 4096):
-        self._m = lib().oxb_model_load(path.encode(), max_seq)
+    def __init__(self, path: str, max_seq: int = 4096, kv: str = "f16"):
+        """kv: the KV cache type, "f16" (throughput) or "f32" (the reference's)."""
+        if kv not in ("f16", "f32"):
+            raise ValueError(f"kv must be 'f16' or 'f32', not {kv!r}")
+        self._m = lib().oxb_model_load_kv(path.encode(), max_seq, int(kv == "f32"))
         if not self._m:
             raise NativeError(last_error())
         info = ModelInfo()

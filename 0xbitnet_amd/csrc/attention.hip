@@ -1387,6 +1387,99 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
 }
 
 // ---------------------------------------------------------------------------
+// Attention over an f32 KV cache, the reference's cache type
+// (nn/attention.rs:23-48 allocates f32 K/V buffers; sh/attention.wgsl reads
+// them as array<f32>), in the same arithmetic order as the f16 kernels.  A
+// parity mode, not the throughput path: one workgroup per (query head,
+// query), 2 waves.
+//   scores   thread t takes positions t, t + 128, ...: 128 fused steps in
+//            order of d (q from LDS, the K row from HBM), times the scale
+//   softmax  wave 0, the 256-thread order (wave_softmax_row)
+//   P.V      thread d < 128: out[d] = blocks of kPvBlock positions summed in
+//            order of s, block sums added in block order
+// Query qi sits at position pos0 + qi (pos0 = *pos_ptr for a decode step
+// from device state) and attends over S = its position + 1 positions.
+// LDS: q [128] | scores [Sp] | probabilities [Sp], Sp = s_max rounded to 4.
+// ---------------------------------------------------------------------------
+constexpr int kF32Threads = 128;
+constexpr int kF32MaxSeq = OXB_KV_F32_MAX_SEQ;   // LDS rows: 2 x 64 KiB
+
+__global__ __launch_bounds__(kF32Threads) void attn_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int pos0, int G, int max_seq, int s_max, float scale,
+    float *__restrict__ out) {
+    extern __shared__ __align__(16) float lds[];
+    const int h = blockIdx.x, qi = blockIdx.y, H = gridDim.x;
+    const int pos = (pos_ptr ? *pos_ptr : pos0) + qi;
+    if (pos < 0 || pos >= max_seq || pos >= s_max) return;   // launch checks too
+    const int S = pos + 1, Spad = (S + 3) & ~3;
+    const int Sp = (s_max + 3) & ~3;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hk = h / G;
+    float *qs = lds, *sc = lds + kHd, *pr = sc + Sp;
+    const float *K = kc + (size_t)hk * max_seq * kHd;
+    const float *V = vc + (size_t)hk * max_seq * kHd;
+    qs[tid] = q[((size_t)qi * H + h) * kHd + tid];
+    lds_barrier();
+    for (int s = tid; s < S; s += kF32Threads) {
+        const float4 *kr = (const float4 *)(K + (size_t)s * kHd);
+        float dot = 0.0f;
+#pragma unroll 4
+        for (int i = 0; i < kHd / 4; ++i) {
+            const float4 k4 = kr[i];
+            const float4 q4 = *(const float4 *)(qs + 4 * i);
+            dot = __builtin_fmaf(q4.x, k4.x, dot);
+            dot = __builtin_fmaf(q4.y, k4.y, dot);
+            dot = __builtin_fmaf(q4.z, k4.z, dot);
+            dot = __builtin_fmaf(q4.w, k4.w, dot);
+        }
+        sc[s] = dot * scale;
+    }
+    lds_barrier();
+    if (w == 0) wave_softmax_row(pr, sc, S, Spad, lane, false);
+    lds_barrier();
+    const int d = tid;
+    float total = 0.0f;
+    for (int b0 = 0; b0 < S; b0 += kPvBlock) {
+        const int e = min(b0 + kPvBlock, S);
+        float part = 0.0f;
+        int s = b0;
+        for (; s + 8 <= e; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = V[(size_t)(s + k) * kHd + d];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) part = __builtin_fmaf(pr[s + k], v[k], part);
+        }
+        for (; s < e; ++s) part = __builtin_fmaf(pr[s], V[(size_t)s * kHd + d], part);
+        total = b0 == 0 ? part : total + part;
+    }
+    out[((size_t)qi * H + h) * kHd + d] = total;
+}
+
+namespace oxb {
+int attn_f32(const float *q, const float *kcache, const float *vcache, const int *pos_ptr,
+             int pos0, int n_q, int H, int Hkv, int hd, int max_seq, float *out, void *stream) {
+    OXB_REQUIRE(hd == kHd, "attention (f32 cache): head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    OXB_REQUIRE(n_q >= 1 && n_q <= 65535, "attention (f32 cache): %d queries", n_q);
+    OXB_REQUIRE(max_seq >= 1 && max_seq <= kF32MaxSeq,
+                "attention (f32 cache): max_seq %d beyond %d", max_seq, kF32MaxSeq);
+    // decode (position from device state): any position of the cache;
+    // prefill: the block's last position bounds the rows
+    const int s_max = pos_ptr ? max_seq : pos0 + n_q;
+    OXB_REQUIRE(pos_ptr || (pos0 >= 0 && s_max <= max_seq), "attention (f32 cache): bad range");
+    const size_t lds = (size_t)(kHd + 2 * ((s_max + 3) & ~3)) * 4;
+    if (lds > 64 * 1024 && allow_dynamic_lds((const void *)attn_f32_kernel)) return -1;
+    const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    hipLaunchKernelGGL(attn_f32_kernel, dim3(H, n_q), dim3(kF32Threads), lds, (hipStream_t)stream,
+                       q, kcache, vcache, pos_ptr, pos0, H / Hkv, max_seq, s_max, scale, out);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+}  // namespace oxb
+
+// ---------------------------------------------------------------------------
 // Decode attention that allocates nothing: oxb_attn_decode with its scores
 // scratch in a static device array instead of a caller buffer.  The array is
 // per device (each GPU the library runs on holds its own copy until the

@@ -131,6 +131,10 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
         set_error("model is NULL");
         return nullptr;
     }
+    if (m->kv_f32) {
+        set_error("batched decode needs the f16 KV cache (model loaded with an f32 cache)");
+        return nullptr;
+    }
     if (batch < 1 || batch > 1024) {
         set_error("batch %d out of range (1..1024)", batch);
         return nullptr;

@@ -266,7 +266,7 @@ static int upload_fused(oxb_model *m, const std::vector<I2S> &parts, bool interl
     return upload_f32(m, sc, scales);
 }
 
-oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
+oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, int kv) {
     std::unique_ptr<oxb_model> m(new oxb_model());
     GgufFile *g = gguf_open(path);
     if (!g) return nullptr;
@@ -436,9 +436,25 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
 
     // KV cache and decode buffers (OXB_KV_PAD_ROWS rows of padding past the
     // last head: the per-head decode attention reads whole V chunks)
+    if (kv < 0) {
+        kv = 0;
+        if (const char *env = getenv("OXB_KV")) {
+            if (!strcmp(env, "f32")) kv = 1;
+            else if (strcmp(env, "f16")) {
+                set_error("OXB_KV=%s: expected f16 or f32", env);
+                return nullptr;
+            }
+        }
+    }
+    m->kv_f32 = kv == 1;
+    if (m->kv_f32 && m->max_seq > OXB_KV_F32_MAX_SEQ) {
+        set_error("f32 KV cache: max_seq %d beyond %d", m->max_seq, OXB_KV_F32_MAX_SEQ);
+        return nullptr;
+    }
     const size_t kv_elems = (size_t)m->n_layers * Hkv * m->max_seq * hd + (size_t)OXB_KV_PAD_ROWS * hd;
-    m->kcache = (uint16_t *)m->dalloc(kv_elems * 2);
-    m->vcache = (uint16_t *)m->dalloc(kv_elems * 2);
+    const size_t kv_bytes = kv_elems * m->kv_elem_bytes();
+    m->kcache = m->dalloc(kv_bytes);
+    m->vcache = m->dalloc(kv_bytes);
     m->x = (float *)m->dalloc((size_t)D * 4);
     m->q = (float *)m->dalloc((size_t)Dq * 4);
     m->attn = (float *)m->dalloc((size_t)Dq * 4);
@@ -459,8 +475,8 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
     if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist)
         return nullptr;
-    if (hipMemset(m->kcache, 0, kv_elems * 2) != hipSuccess ||
-        hipMemset(m->vcache, 0, kv_elems * 2) != hipSuccess) {
+    if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
+        hipMemset(m->vcache, 0, kv_bytes) != hipSuccess) {
         set_error("hipMemset failed");
         return nullptr;
     }
@@ -487,6 +503,7 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud) {
 // head + argmax (state.token, state.pos += 1).  Every kernel reads the
 // position from device memory, so the same launch sequence replays as a graph.
 oxb_model::AttnForm oxb_model::attn_form(int S) const {
+    if (kv_f32) return ATTN_SPLIT;   // one form (attn_f32) at every length
     if (attn_mode == 0 && S <= 256) return ATTN_HEAD1;
     if (attn_mode == 0 && S <= 512) return ATTN_HEAD2;
     if (attn_mode == 1 && S <= 256 && oxb_attn_decode_fused_supported(H, Hkv, hd, max_seq))
@@ -499,15 +516,19 @@ int oxb_model::enqueue_decode_step(AttnForm attn) {
     const int Dq = H * hd, Dkv = Hkv * hd;
     int *posp = state + OXB_ST_POS;
     if (oxb_embedding(embed, V, D, nullptr, 1, state, x, s)) return -1;
-    const size_t kv_layer = (size_t)Hkv * max_seq * hd;
+    const size_t kv_layer = (size_t)Hkv * max_seq * hd * kv_elem_bytes();
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];
-        uint16_t *kc = kcache + l * kv_layer, *vc = vcache + l * kv_layer;
-        if (oxb_bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kc, vc,
-                              max_seq, rope, posp, s))
+        void *kv_k = (char *)kcache + l * kv_layer, *kv_v = (char *)vcache + l * kv_layer;
+        uint16_t *kc = (uint16_t *)kv_k, *vc = (uint16_t *)kv_v;
+        if (oxb::bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kv_k, kv_v,
+                               kv_f32, max_seq, rope, posp, s))
             return -1;
         int rc;
-        switch (attn) {
+        if (kv_f32)
+            rc = oxb::attn_f32(q, (const float *)kv_k, (const float *)kv_v, posp, 0, 1, H, Hkv, hd,
+                               max_seq, this->attn, s);
+        else switch (attn) {
             case ATTN_HEAD1:
             case ATTN_HEAD2:
                 rc = oxb_attn_decode_head(q, kc, vc, posp, 0, 0, 1, H, Hkv, hd, max_seq,
@@ -609,15 +630,19 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
     if (oxb_embedding(embed, V, D, pids, n, tg.state, px, s)) return -1;
-    const size_t kv_layer = (size_t)Hkv * tg.max_seq * hd;
+    const size_t kv_layer = (size_t)Hkv * tg.max_seq * hd * kv_elem_bytes();
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];
-        uint16_t *kc = tg.kcache + l * kv_layer, *vc = tg.vcache + l * kv_layer;
+        void *kc = (char *)tg.kcache + l * kv_layer, *vc = (char *)tg.vcache + l * kv_layer;
         if (oxb_quantize_rows_tiled(px, L.attn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
-        if (oxb_gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n,
-                         tg.pos, pq, kc, vc, tg.max_seq, tg.rope, s))
+        if (oxb::gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n,
+                          tg.pos, pq, kc, vc, kv_f32, tg.max_seq, tg.rope, s))
             return -1;
-        if (oxb_attn_prefill(pq, kc, vc, n, tg.pos, H, Hkv, hd, tg.max_seq, pattn, s)) return -1;
+        if (kv_f32 ? oxb::attn_f32(pq, (const float *)kc, (const float *)vc, nullptr, tg.pos, n, H,
+                                   Hkv, hd, tg.max_seq, pattn, s)
+                   : oxb_attn_prefill(pq, (const uint16_t *)kc, (const uint16_t *)vc, n, tg.pos, H,
+                                      Hkv, hd, tg.max_seq, pattn, s))
+            return -1;
         if (oxb_quantize_rows_tiled(pattn, L.attn_sub, 1e-5f, n, Dq, pX, pscale, psum, s)) return -1;
         if (oxb_gemm_i8(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1, s))
             return -1;
@@ -668,6 +693,19 @@ extern "C" oxb_model *oxb_model_load(const char *path, int max_seq) {
     return model_load(path, max_seq, nullptr, nullptr);
 }
 
+extern "C" oxb_model *oxb_model_load_kv(const char *path, int max_seq, int kv_f32) {
+    clear_error();
+    if (!path) {
+        set_error("source is NULL");
+        return nullptr;
+    }
+    if (kv_f32 != 0 && kv_f32 != 1) {
+        set_error("kv_f32 must be 0 or 1 (got %d)", kv_f32);
+        return nullptr;
+    }
+    return model_load(path, max_seq, nullptr, nullptr, kv_f32);
+}
+
 extern "C" void oxb_model_free(oxb_model *m) { delete m; }
 
 extern "C" int oxb_model_get_info(const oxb_model *m, oxb_model_info *o) {
@@ -684,6 +722,7 @@ extern "C" int oxb_model_get_info(const oxb_model *m, oxb_model_info *o) {
     o->rope_theta = m->rope_theta;
     o->relu2 = m->relu2 ? 1 : 0;
     o->weight_bytes = m->weight_bytes;
+    o->kv_f32 = m->kv_f32 ? 1 : 0;
     return 0;
 }
 

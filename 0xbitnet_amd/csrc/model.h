@@ -30,7 +30,11 @@ struct oxb_model {
     void *embed_lm = nullptr;    // the same table in the LM head's layout
     float *final_norm = nullptr;
     float *rope = nullptr;       // [max_seq][hd/2] (cos, sin)
-    uint16_t *kcache = nullptr, *vcache = nullptr;  // [L][Hkv][max_seq][hd]
+    // [L][Hkv][max_seq][hd]: f16 bits, or f32 when kv_f32 (the reference's
+    // cache type, nn/attention.rs:23-48; a parity mode of the engine)
+    void *kcache = nullptr, *vcache = nullptr;
+    bool kv_f32 = false;
+    size_t kv_elem_bytes() const { return kv_f32 ? 4 : 2; }
 
     // decode buffers
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr, *scores = nullptr;
@@ -71,7 +75,7 @@ struct oxb_model {
     // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state
     // block, token history and position
     struct SeqTarget {
-        uint16_t *kcache, *vcache;
+        void *kcache, *vcache;   // element type as the model's (kv_f32)
         int max_seq;
         const float *rope;
         int *state, *tok_hist;
@@ -90,6 +94,8 @@ struct oxb_model {
 namespace oxb {
 // Load progress hook used by the C ABI (phase 2 = upload, per tensor).
 typedef void (*LoadHook)(int phase, uint64_t loaded, uint64_t total, void *ud);
-oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud);
+// kv: 0 f16 cache, 1 f32 cache, -1 from the environment (OXB_KV=f16|f32,
+// default f16)
+oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, int kv = -1);
 void log_msg(int level, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 }  // namespace oxb

@@ -18,6 +18,21 @@ int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int
                   const int *tok_pos, int tok_pos_stride, size_t kv_tok_stride, float *q_out,
                   uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
                   bool gemv_order, void *stream);
+// QKV projections that store K/V as f16 bits or, with kv_f32, as f32 (the
+// reference's cache type): one token (GEMV, ternary_gemv.hip) or a prefill
+// block (GEMM, ternary_gemm.hip).
+int bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float eps,
+                  const float *wscale, int Dq, int Dkv, int hd, int K, float *q_out, void *kcache,
+                  void *vcache, bool kv_f32, int max_seq, const float *rope_cs, const int *pos,
+                  void *stream);
+int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
+             const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
+             float *q_out, void *kcache, void *vcache, bool kv_f32, int max_seq,
+             const float *rope_cs, void *stream);
+// Attention over an f32 cache ([Hkv][max_seq][hd]): n_q queries at positions
+// pos0 + i, or one query at *pos_ptr when pos_ptr is given (attention.hip).
+int attn_f32(const float *q, const float *kcache, const float *vcache, const int *pos_ptr,
+             int pos0, int n_q, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
 int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
                       float *x, void *stream);
 // Batched LM head with a workspace of n_rows * D floats (lm_head.hip).

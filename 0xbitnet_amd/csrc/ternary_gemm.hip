@@ -42,7 +42,8 @@ struct GemmParams {
     int32_t *acc_out;      // optional [n_tok][N]
     // QKV
     float *q_out;          // [n_tok][Dq]
-    uint16_t *kcache, *vcache;
+    void *kcache, *vcache;     // f16 bits, or f32 when kv_f32
+    int kv_f32;
     const float2 *rope;
     int Dq, Dkv, hd, max_seq, pos0;
     // optional: token t is at position tok_pos[t] of its own cache, which
@@ -160,10 +161,16 @@ __device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int 
         } else {
             const int j = n0 < Dk ? n0 - p.Dq : n0 - Dk;
             const int head = j / p.hd, d = j % p.hd;
-            uint16_t *cache = (n0 < Dk ? p.kcache : p.vcache) + (p.tok_pos ? t * p.kv_tok_stride : 0);
-            uint16_t *dst = cache + ((size_t)head * p.max_seq + pos) * p.hd + d;
+            const size_t at = (p.tok_pos ? t * p.kv_tok_stride : 0) +
+                              ((size_t)head * p.max_seq + pos) * p.hd + d;
+            void *cache = n0 < Dk ? p.kcache : p.vcache;
+            if (p.kv_f32) {
+                *(float4 *)((float *)cache + at) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                uint16_t *dst = (uint16_t *)cache + at;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
+                for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
+            }
         }
     }
 }
@@ -739,6 +746,16 @@ extern "C" int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *x
                             const int *xsum, const float *wscale, int Dq, int Dkv, int hd, int K,
                             int n_tok, int pos0, float *q_out, uint16_t *kcache,
                             uint16_t *vcache, int max_seq, const float *rope_cs, void *stream) {
+    return oxb::gemm_qkv(W_tiled, X, xscale, xsum, wscale, Dq, Dkv, hd, K, n_tok, pos0, q_out,
+                         kcache, vcache, false, max_seq, rope_cs, stream);
+}
+
+namespace oxb {
+
+int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
+             const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
+             float *q_out, void *kcache, void *vcache, bool kv_f32, int max_seq,
+             const float *rope_cs, void *stream) {
     const int N = Dq + 2 * Dkv;
     if (gemm_check(N, K, n_tok)) return -1;
     OXB_REQUIRE(Dq % 32 == 0 && Dkv % 32 == 0 && hd % 16 == 0, "gemm qkv: bad head split");
@@ -761,10 +778,9 @@ extern "C" int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *x
     p.hd = hd;
     p.max_seq = max_seq;
     p.pos0 = pos0;
+    p.kv_f32 = kv_f32 ? 1 : 0;
     return gemm_launch<GE_QKV>(p, stream);
 }
-
-namespace oxb {
 
 int gemm_rows(const void *W, const int8_t *X, const float *xscale, const int *xsum,
               const float *wscale, int N, int K, int n_tok, float *Y, int epilogue,

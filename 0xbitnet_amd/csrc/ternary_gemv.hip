@@ -23,7 +23,9 @@ namespace oxb {
 constexpr int kMaxNormReg = 28; // f32 values per thread in a norm prologue (D <= 7168)
 
 enum Pro { PRO_INT8 = 0, PRO_QUANT = 1 };           // PRO_QUANT: optional RMSNorm + quantize
-enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GATEUP = 3 };
+// EPI_QKV stores K/V as f16 bits, EPI_QKV32 as f32 (the reference's cache type)
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GATEUP = 3, EPI_QKV32 = 4 };
+__host__ __device__ constexpr bool is_qkv(int epi) { return epi == EPI_QKV || epi == EPI_QKV32; }
 
 struct GemvParams {
     const uint4 *W;        // tile-chunk layout
@@ -44,7 +46,7 @@ struct GemvParams {
     float *xscale_out;     // optional
     // QKV
     float *q_out;          // [Dq]
-    uint16_t *kcache, *vcache;  // [Hkv][max_seq][hd] f16 bits
+    void *kcache, *vcache;  // [Hkv][max_seq][hd] f16 bits (EPI_QKV) or f32 (EPI_QKV32)
     const float2 *rope;    // [max_seq][hd/2] (cos, sin)
     const int *pos;        // device position
     int Dq, Dkv, hd, max_seq;
@@ -198,7 +200,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     // read per lane (an index the compiler cannot see is zero): a uniform
     // value would be moved to an SGPR, and that copy waits for the load
     // before the weights are even issued
-    if constexpr (EPI == EPI_QKV) pos = p.pos[opaque_zero()];
+    if constexpr (is_qkv(EPI)) pos = p.pos[opaque_zero()];
     const float ws_ep = p.wscale[n_ep];
     float resid = 0.0f;
     if constexpr (EPI == EPI_RESID) resid = p.y[n_ep];
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     // RoPE pair of this thread's row at the position (q and k rows), issued
     // as soon as the position is back; clamped so the load stays in the table
     [[maybe_unused]] float2 cs = make_float2(1.0f, 0.0f);
-    if constexpr (EPI == EPI_QKV) {
+    if constexpr (is_qkv(EPI)) {
         const int d = (n_ep < p.Dq ? n_ep : n_ep - p.Dq) % p.hd;
         const int pc = min(max(pos, 0), p.max_seq - 1);
         if (n_ep < p.Dq + p.Dkv) cs = p.rope[(size_t)pc * (p.hd >> 1) + (d >> 1)];
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             gt = gt * gt;
             p.y[n >> 1] = gt * other;     // sh/elementwise.wgsl:32
         }
-    } else {  // EPI_QKV
+    } else {  // EPI_QKV, EPI_QKV32
         if (pos < 0 || pos >= p.max_seq) return;  // host checks too; never write out of range
         const float other = __shfl_xor(yv, 1, 64);
         const int Dk = p.Dq + p.Dkv;
@@ -378,8 +380,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
         } else {
             const int j = n < Dk ? n - p.Dq : n - Dk;
             const int head = j / p.hd, d = j % p.hd;
-            uint16_t *cache = n < Dk ? p.kcache : p.vcache;
-            cache[((size_t)head * p.max_seq + pos) * p.hd + d] = f32_to_f16_bits(outv);
+            const size_t at = ((size_t)head * p.max_seq + pos) * p.hd + d;
+            void *cache = n < Dk ? p.kcache : p.vcache;
+            if constexpr (EPI == EPI_QKV32)
+                ((float *)cache)[at] = outv;
+            else
+                ((uint16_t *)cache)[at] = f32_to_f16_bits(outv);
         }
     }
 }
@@ -570,10 +576,11 @@ extern "C" int oxb_bitlinear_gateup(const void *W_tiled, const float *x, const f
     return launch<PRO_QUANT, EPI_GATEUP>(p, stream);
 }
 
-extern "C" int oxb_bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma,
-                                 float eps, const float *wscale, int Dq, int Dkv, int hd, int K,
-                                 float *q_out, uint16_t *kcache, uint16_t *vcache, int max_seq,
-                                 const float *rope_cs, const int *pos, void *stream_) {
+namespace oxb {
+int bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float eps,
+                  const float *wscale, int Dq, int Dkv, int hd, int K, float *q_out, void *kcache,
+                  void *vcache, bool kv_f32, int max_seq, const float *rope_cs, const int *pos,
+                  void *stream_) {
     OXB_STREAM;
     const int N = Dq + 2 * Dkv;
     if (check_shape(N, K, true)) return -1;
@@ -596,7 +603,16 @@ extern "C" int oxb_bitlinear_qkv(const void *W_tiled, const float *x, const floa
     p.Dkv = Dkv;
     p.hd = hd;
     p.max_seq = max_seq;
-    return launch<PRO_QUANT, EPI_QKV>(p, stream);
+    return kv_f32 ? launch<PRO_QUANT, EPI_QKV32>(p, stream) : launch<PRO_QUANT, EPI_QKV>(p, stream);
+}
+}  // namespace oxb
+
+extern "C" int oxb_bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma,
+                                 float eps, const float *wscale, int Dq, int Dkv, int hd, int K,
+                                 float *q_out, uint16_t *kcache, uint16_t *vcache, int max_seq,
+                                 const float *rope_cs, const int *pos, void *stream_) {
+    return oxb::bitlinear_qkv(W_tiled, x, gamma, eps, wscale, Dq, Dkv, hd, K, q_out, kcache,
+                              vcache, false, max_seq, rope_cs, pos, stream_);
 }
 
 extern "C" int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_rows,

@@ -43,6 +43,9 @@ extern "C" {
  * max_seq rows for oxb_attn_decode_head, which reads V in whole 64-row
  * chunks from any chunk start below the cache length. */
 #define OXB_KV_PAD_ROWS 64
+/* Longest cache of the f32-KV mode (oxb_model_load_kv): its attention holds
+ * a score and a probability row per query in LDS. */
+#define OXB_KV_F32_MAX_SEQ 16384
 
 /* ---- errors, device memory, streams, events (plumbing) ----------------- */
 const char *oxb_last_error(void);
@@ -249,12 +252,20 @@ typedef struct oxb_model_info {
     float rms_eps, rope_theta;
     int relu2;           /* 1: ReLU^2 gate (arch "bitnet-25"), 0: SiLU */
     size_t weight_bytes; /* device bytes held by weights */
+    int kv_f32;          /* 1: f32 KV cache, 0: f16 */
 } oxb_model_info;
 
 /* Parse a GGUF (v2/v3) file, upload and repack.  max_seq <= 0 means 4096
  * (lib.rs:93).  Replaces BitNet::load's model half (lib.rs:77-94,
  * model/loader.rs:75-173, nn/model.rs:42-190). */
 oxb_model *oxb_model_load(const char *path, int max_seq);
+/* The same with the KV cache type chosen: kv_f32 = 0 stores K/V as f16 (the
+ * throughput mode, also oxb_model_load's and oxbitnet_load's default), 1 as
+ * f32, the reference's own cache type (nn/attention.rs:23-48: f32 K/V
+ * buffers), with which every result is the reference arithmetic's; max_seq
+ * <= OXB_KV_F32_MAX_SEQ there, batches (oxb_batch_*) need the f16 cache.
+ * oxb_model_load and oxbitnet_load take the type from OXB_KV=f16|f32. */
+oxb_model *oxb_model_load_kv(const char *path, int max_seq, int kv_f32);
 void oxb_model_free(oxb_model *m);
 int oxb_model_get_info(const oxb_model *m, oxb_model_info *out);
 /* KV length back to 0 (nn/model.rs:300-310). */

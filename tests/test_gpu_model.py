@@ -40,7 +40,7 @@ def _greedy_parity(path, prompt, steps, kv_f16=True, max_seq=None):
     """Prefill + `steps` greedy steps on the GPU and in the oracle: every
     logit bit-equal, every token equal."""
     max_seq = max_seq or (len(prompt) + steps + 2)
-    m = pkg.Model(path, max_seq=max_seq)
+    m = pkg.Model(path, max_seq=max_seq, kv="f16" if kv_f16 else "f32")
     cfg, w = oracle_weights(path)
     om = O.Model(cfg, w, max_seq=max_seq, kv_f16=kv_f16)
     tok, logits = m.forward(prompt)
@@ -66,13 +66,62 @@ def test_small_model_prefill_and_64_greedy_steps():
     assert len(toks) == 65
 
 
-@pytest.mark.skip(reason="the engine stores K/V as f16; the f32-cache mode that matches "
-                         "nn/attention.rs:28-29 is not built yet")
+# ---- the reference's own cache type (f32 K/V, nn/attention.rs:23-48) -------
 def test_small_model_f32_cache_oracle():
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
     prompt = np.random.default_rng(2).integers(0, cfg.vocab, 17).astype(np.int32)
-    _greedy_parity(path, prompt, 16, kv_f16=False)
+    assert len(_greedy_parity(path, prompt, 64, kv_f16=False)) == 65
+
+
+@pytest.mark.parametrize("n_prompt", [1, 255, 300])
+def test_small_model_f32_cache_across_pv_blocks(n_prompt):
+    """Prompts that end before, at and past the first 256-position P.V block,
+    then decode across block boundaries (positions up to 560)."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    prompt = np.random.default_rng([3, n_prompt]).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    _greedy_parity(path, prompt, 560 - n_prompt if n_prompt < 300 else 40, kv_f16=False,
+                   max_seq=600)
+
+
+def test_f32_cache_prefill_then_decode_equals_oracle_paths():
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    ids = np.random.default_rng(6).integers(0, cfg.vocab, 25).astype(np.int32)
+    c, w = oracle_weights(path)
+    m = pkg.Model(path, max_seq=64, kv="f32")
+    assert m.info["kv_f32"] == 1
+    for split in (24, 3):
+        om = O.Model(c, w, max_seq=64, kv_f16=False)
+        m.reset()
+        _, lg = m.forward(ids[:split])
+        _same(lg, om.forward(ids[:split].astype(np.uint32)), f"prefill {split}")
+        for t in ids[split:]:
+            _, lg = m.forward(np.array([t], np.int32))
+            _same(lg, om.forward(np.array([t], np.uint32)), f"decode after {split}")
+    m.close()
+
+
+def test_f32_cache_is_the_mode_that_ran():
+    """The two cache types give different logits (f16 rounding of K/V), the
+    f32 ones equal to the oracle's f32 path; a batch needs the f16 cache."""
+    cfg = synth.small_config()
+    path = synth.cached_gguf(cfg, seed=7)
+    ids = np.random.default_rng(8).integers(0, cfg.vocab, 30).astype(np.int32)
+    out = {}
+    for kv in ("f16", "f32"):
+        m = pkg.Model(path, max_seq=64, kv=kv)
+        out[kv] = m.forward(ids)[1]
+        if kv == "f32":
+            with pytest.raises(pkg.NativeError, match="f16 KV cache"):
+                pkg.Batch(m, 2, 64)
+        m.close()
+    assert not np.array_equal(out["f16"], out["f32"])
+    c, w = oracle_weights(path)
+    _same(out["f32"], O.Model(c, w, max_seq=64, kv_f16=False).forward(ids.astype(np.uint32)), "f32")
+    with pytest.raises(ValueError):
+        pkg.Model(path, kv="bf16")
 
 
 def test_prefill_then_decode_equals_oracle_paths():
@@ -171,6 +220,14 @@ def test_bitnet_2b_shape_greedy_192():
     prompt = np.random.default_rng(2024).integers(0, synth.BITNET_2B.vocab, 128).astype(np.int32)
     toks = _greedy_parity(path, prompt, 192)
     assert len(toks) == 193
+
+
+def test_bitnet_2b_shape_f32_cache_greedy_64():
+    """The 2B shape with the reference's f32 KV cache: 128-token prompt, 64
+    greedy steps, logits bit-equal to the oracle's f32-cache path."""
+    path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
+    prompt = np.random.default_rng(2024).integers(0, synth.BITNET_2B.vocab, 128).astype(np.int32)
+    assert len(_greedy_parity(path, prompt, 64, kv_f16=False)) == 65
 
 
 # ---- long context: 2048-token prefill, then batched decode (bs 8 and 32) ----
