@@ -1028,33 +1028,103 @@ __global__ __launch_bounds__(256) void attn_head_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Decode, one workgroup per query head, caches of up to 256 positions in a
-// cache of max_seq >= 256 rows:
-//  - K and V rows below S load coalesced (thread i: uint4 i + 256 k of each,
-//    rows clamped to S - 1) and are staged in LDS, K as [256][17] uint4 (padded rows), V row-major
-//    [256][128] f16; thread t runs the 128-step score chain of position t
-//    from its K row, q as the SGPR operand of each v_fma_mix;
-//  - softmax on the four waves in the shader's order, as attn_head_kernel;
-//  - P.V on waves 0 and 1, one dim per lane: each step one 16-bit LDS read
-//    and one v_fma_mix (the probabilities read four at a time).
-// Same arithmetic, so the same bits.
+// Decode, one workgroup per query head, caches of up to 256 positions:
+//  - the position first, then every K and V load before the first is
+//    waited for: rows below S (thread i: uint4 i + 256 k of each, coalesced,
+//    rows clamped to S - 1, so the loads are branch-free), and the q row;
+//  - K staged in LDS as [256][17] uint4 (padded rows), q as [128] f32; the
+//    V loads are still landing while thread t runs the 128-step score chain
+//    of position t, q read as LDS broadcasts three 8-term groups ahead (no
+//    scalar loads: their out-of-order returns force full waits in the chain);
+//  - V staged row-major [256][64] dwords after the chain;
+//  - softmax in the shader's order with two exchanges: every wave forms the
+//    row sum from the 256 partials itself;
+//  - P.V on waves 0 (even dims) and 1 (odd dims), lane j summing dim 2j + w:
+//    each LDS read gives it two positions of its dword (ds_read2st64), the
+//    probabilities four at a time; 4-position blocks read three ahead (12
+//    LDS reads in flight, within the 15 the counter tracks), each step one
+//    v_fma_mix on the dword's low or high half.
+// Same arithmetic as the other forms, so the same bits.
 // ---------------------------------------------------------------------------
 constexpr int kH256Rows = 256;
 constexpr size_t kH256KBytes = (size_t)kH256Rows * 17 * 16;   // K rows, padded
 constexpr size_t kH256VBytes = (size_t)kH256Rows * kHd * 2;   // V rows
-constexpr size_t kH256Lds = kH256KBytes + kH256VBytes + (256 + 256 + 8) * 4;
+constexpr size_t kH256Lds = kH256KBytes + kH256VBytes + (kHd + 256 + 256 + 8) * 4;
+
+// acc + sum of p[s] * v_s over the n (all 4 when FULL) positions of a block,
+// in order of s; v_s the low (HI false) or high half of dword V[s]
+template <bool HI, bool FULL>
+__device__ __forceinline__ float pv4(float acc, const uint32_t (&V)[4], const float4 &P, int n = 4) {
+    const float pp[4] = {P.x, P.y, P.z, P.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t u = V[k];
+        const float v = __half2float(__ushort_as_half((uint16_t)(HI ? u >> 16 : u & 0xffffu)));
+        const float t = __builtin_fmaf(pp[k], v, acc);
+        acc = FULL || k < n ? t : acc;
+    }
+    return acc;
+}
+
+// P.V of one wave: lane j's chain over the S positions of dim 2j + HI;
+// vcol = the V rows' dword j (row stride 64 dwords)
+template <bool HI>
+__device__ __forceinline__ float pv_head256(const uint32_t *vcol, const float *pr, int S) {
+    float acc = 0.0f;
+    uint32_t V[4][4];
+    float4 P[4];
+    auto ld = [&](int b, int s) {   // the block at s (clamped into the rows) into ring slot b
+        s = min(s, kH256Rows - 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) V[b][k] = vcol[(s + k) * (kHd / 2)];
+        P[b] = *(const float4 *)(pr + s);
+    };
+    ld(0, 0);
+    ld(1, 4);
+    ld(2, 8);
+    // fully unrolled (exits are wave-uniform branches): across a loop's back
+    // edge the compiler waits for every outstanding LDS read (lgkmcnt(0)),
+    // which would drain the ring once per 16 positions
+    int s0 = 0;
+#pragma unroll
+    for (int it = 0; it < kH256Rows / 16; ++it) {
+        if (s0 + 16 > S) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            ld((j + 3) & 3, s0 + 4 * j + 12);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv4<HI, true>(acc, V[j], P[j]);
+        }
+        s0 += 16;
+    }
+    // the last S - s0 < 16 positions: slots 0..2 hold blocks s0, s0 + 4, s0 + 8
+    ld(3, s0 + 12);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = S - s0 - 4 * j;
+        if (n >= 4) acc = pv4<HI, true>(acc, V[j], P[j]);
+        else if (n > 0) acc = pv4<HI, false>(acc, V[j], P[j], n);
+    }
+    return acc;
+}
 
 __global__ __launch_bounds__(256) void attn_head256_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
     size_t kv_stride, int pos_stride) {
+    // all kernel arguments in SGPRs up front: read where they are used, the
+    // late ones are further kernarg round trips before the position's load
+    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(max_seq), "s"(scale),
+                 "s"(out), "s"(kv_stride), "s"(pos_stride));
     extern __shared__ __align__(16) int8_t smem_h[];
     u32x4_t (*ks)[17] = (u32x4_t (*)[17])smem_h;
-    u32x4_t *vs4 = (u32x4_t *)(smem_h + kH256KBytes);              // V [256][128] f16
-    const uint16_t *vs = (const uint16_t *)vs4;
-    float *pr = (float *)(smem_h + kH256KBytes + kH256VBytes);      // probabilities [256]
-    float *red = pr + 256;
-    float *wmax = red + 256;                                        // [4], then 1/sum at [4]
+    u32x4_t *vs4 = (u32x4_t *)(smem_h + kH256KBytes);              // V [256][64] dwords
+    const uint32_t *vs = (const uint32_t *)vs4;
+    float *qs = (float *)(smem_h + kH256KBytes + kH256VBytes);      // q [128]
+    float *pr = qs + kHd;                                           // probabilities [256]
+    float *red = pr + 256;                                          // partial sums [256]
+    float *wmax = red + 256;                                        // [4]
     const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
@@ -1062,50 +1132,65 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
-    // The position first, then only the rows below S (clamped: the loads stay
-    // branch-free).  Loading all 256 rows without waiting for it was slower:
-    // 128 KB per CU at the CU's ~64 B/cycle, and the bulk loads delay the
-    // position's scalar load too.
-    float qw[kHd / 16];   // one dword per 64-byte line of the q row
-#pragma unroll
-    for (int i = 0; i < kHd / 16; ++i) qw[i] = qh[16 * i];
     const int pos = pos_ptr[(size_t)z * pos_stride];
-    asm volatile("" ::"s"(pos), "s"(qw[0]), "s"(qw[1]), "s"(qw[2]), "s"(qw[3]), "s"(qw[4]),
-                 "s"(qw[5]), "s"(qw[6]), "s"(qw[7]));
+    // the q row first (the oldest load: its wait leaves the K and V loads in
+    // flight); every thread loads, so no load sits under a branch
+    const float4 q4 = ((const float4 *)qh)[tid & 31];
+    __builtin_amdgcn_sched_barrier(0);
     const bool valid = pos >= 0 && pos < kH256Rows && pos < max_seq;
     const int S = valid ? pos + 1 : 1;
-    u32x4_t kt[16], vt[16];   // uint4 tid + 256 k of the K and V rows < S
+    u32x4_t kt[16], vt[16];
     const u32x4_t *__restrict__ K4 = (const u32x4_t *)kc;
     const u32x4_t *__restrict__ V4 = (const u32x4_t *)vc;
 #pragma unroll
     for (int k = 0; k < 16; ++k) kt[k] = K4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
 #pragma unroll
     for (int k = 0; k < 16; ++k) vt[k] = V4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
-
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < 16; ++k) ks[16 * k + (tid >> 4)][tid & 15] = kt[k];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) vs4[tid + 256 * k] = vt[k];
+    // every thread stores (8 store the same float4 to each slot): a store
+    // under a branch would take its load along
+    *(float4 *)(qs + 4 * (tid & 31)) = q4;
     lds_barrier();
 
     // ---- score of position tid: 128 terms in order of d -----------------
     float x;
     {
+        // group i: 8 terms, one K uint4 and two q float4 from LDS, read
+        // three groups ahead (9 LDS reads in flight, in order)
+        constexpr int kAhead = 3;
+        u32x4_t kr[16];
+        float4 qa[16], qb[16];
+        auto ld = [&](int i) {
+            kr[i] = ks[tid][i];
+            qa[i] = *(const float4 *)(qs + 8 * i);
+            qb[i] = *(const float4 *)(qs + 8 * i + 4);
+        };
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) ld(i);
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const u32x4_t kv = ks[tid][i];
+            __builtin_amdgcn_sched_barrier(0);
+            if (i + kAhead < 16) ld(i + kAhead);
+            __builtin_amdgcn_sched_barrier(0);
+            const float qv[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w,
+                                 qb[i].x, qb[i].y, qb[i].z, qb[i].w};
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
-                const uint32_t kw = kv[k2];
+                const uint32_t kw = kr[i][k2];
                 const float k0 = __half2float(__ushort_as_half((uint16_t)(kw & 0xffffu)));
                 const float k1 = __half2float(__ushort_as_half((uint16_t)(kw >> 16)));
-                dot = __builtin_fmaf(qh[8 * i + 2 * k2], k0, dot);
-                dot = __builtin_fmaf(qh[8 * i + 2 * k2 + 1], k1, dot);
+                dot = __builtin_fmaf(qv[2 * k2], k0, dot);
+                dot = __builtin_fmaf(qv[2 * k2 + 1], k1, dot);
             }
         }
         x = dot * scale;
     }
+    // ---- V rows (published by the next barrier) ----------------------------
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vs4[tid + 256 * k] = vt[k];
 
     // ---- softmax (sh/softmax.wgsl:25-80) --------------------------------------
     float m = tid < S ? x : -3.402823e+38f;
@@ -1116,63 +1201,20 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     const float e = tid < S ? oxb_expf(x - m) : 0.0f;
     red[tid] = e;   // thread t's strided partial: one position (0 + e = e)
     lds_barrier();
-    if (w == 0) {
+    float inv;
+    {   // the halving tree, in every wave (identical values)
         const float a = red[lane] + red[lane + 128];
         const float c = red[lane + 64] + red[lane + 192];
-        const float sum = wave_tree_sum(a + c);
-        if (lane == 0) wmax[4] = 1.0f / sum;
+        inv = 1.0f / wave_tree_sum(a + c);
     }
-    lds_barrier();
-    pr[tid] = e * wmax[4];   // 0 past S
+    pr[tid] = e * inv;   // 0 past S
     lds_barrier();
 
     // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
-    // Blocks of 16 positions, the LDS operands of the next block read while
-    // the current one is summed (positions past S read stale rows and
-    // probabilities 0, and are left out of the sum).
     if (w < 2) {
-        const uint16_t *vd = vs + 64 * w + lane;   // V[s][d] at vd[s * 128]
-        float acc = 0.0f;
-        auto ld = [&](uint16_t (&V)[16], float4 (&P)[4], int s0) {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) P[j] = *(const float4 *)(pr + s0 + 4 * j);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) V[j] = vd[(s0 + j) * kHd];
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        auto mac = [&](const uint16_t (&V)[16], const float4 (&P)[4]) {   // all 16
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc = __builtin_fmaf(P[j].x, __half2float(__ushort_as_half(V[4 * j])), acc);
-                acc = __builtin_fmaf(P[j].y, __half2float(__ushort_as_half(V[4 * j + 1])), acc);
-                acc = __builtin_fmaf(P[j].z, __half2float(__ushort_as_half(V[4 * j + 2])), acc);
-                acc = __builtin_fmaf(P[j].w, __half2float(__ushort_as_half(V[4 * j + 3])), acc);
-            }
-        };
-        auto mac_part = [&](const uint16_t (&V)[16], const float4 (&P)[4], int n) {   // first n
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float pp[4] = {P[j].x, P[j].y, P[j].z, P[j].w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float t = __builtin_fmaf(pp[k], __half2float(__ushort_as_half(V[4 * j + k])), acc);
-                    acc = 4 * j + k < n ? t : acc;
-                }
-            }
-        };
-        uint16_t VA[16], VB[16];
-        float4 PA[4], PB[4];
-        ld(VA, PA, 0);
-        for (int s0 = 0; s0 < S; s0 += 32) {   // S and s0 are wave-uniform: no divergence
-            ld(VB, PB, min(s0 + 16, kH256Rows - 16));
-            if (S - s0 >= 16) mac(VA, PA);
-            else mac_part(VA, PA, S - s0);
-            ld(VA, PA, min(s0 + 32, kH256Rows - 16));
-            if (S - s0 >= 32) mac(VB, PB);
-            else if (S - s0 > 16) mac_part(VB, PB, S - s0 - 16);
-        }
-        if (valid) out[((size_t)z * H + h) * kHd + 64 * w + lane] = acc;
+        const float acc = w == 0 ? pv_head256<false>(vs + lane, pr, S)
+                                 : pv_head256<true>(vs + lane, pr, S);
+        if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
     }
 }
 
