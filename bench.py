@@ -402,6 +402,85 @@ def cpu_kernels(synth) -> list:
     return out
 
 
+def decode_breakdown(ops, synth, pos: int = 139) -> dict:
+    """The decode step's kernels at the 2B shape, rebuilt from the operator
+    ABI with 30 layers of their own (zero-coded) weights and caches, each
+    kind timed as a graph of its 30 launches (cold weights, so HBM latency
+    as in the model), then the whole chain (30 x q|k|v, attention, o_proj,
+    gate|up, down) and the LM head (final norm + tied head + argmax, its
+    finishing kernel included).  Per-launch microseconds include the launch
+    gap of a graph; the attention runs at `pos` + 1 cached positions."""
+    L = ops.lib()
+    cfg = synth.BITNET_2B
+    nl, D, F, H, Hkv, hd, V = cfg.n_layers, cfg.hidden, cfg.ffn, cfg.heads, cfg.kv_heads, 128, cfg.vocab
+    Dq, Dkv, max_seq = H * hd, Hkv * hd, 4096
+    lay = []
+    for _ in range(nl):
+        lay.append({k: ops.DeviceArray((n * kk // 4,), np.uint8, zero=True)
+                    for k, n, kk in (("qkv", Dq + 2 * Dkv, D), ("o", D, Dq), ("gu", 2 * F, D),
+                                     ("down", D, F))})
+    kvl = Hkv * max_seq * hd
+    kc = ops.DeviceArray((nl * kvl + 64 * hd,), np.uint16, zero=True)
+    vc = ops.DeviceArray((nl * kvl + 64 * hd,), np.uint16, zero=True)
+    rng = np.random.default_rng(5)
+    x = ops.DeviceArray.from_host(rng.standard_normal(D).astype(np.float32))
+    ones = ops.DeviceArray.from_host(np.ones(2 * F, np.float32))
+    ws = ops.DeviceArray.from_host(np.full(2 * F, 0.016, np.float32))
+    q, att = ops.DeviceArray((Dq,), np.float32), ops.DeviceArray((Dq,), np.float32)
+    hbuf = ops.DeviceArray((F,), np.float32)
+    cs = np.zeros(max_seq * hd, np.float32)
+    ops.check(L.oxb_rope_table(cs.ctypes.data, max_seq, hd, cfg.rope_theta), "rope")
+    rope = ops.DeviceArray.from_host(cs)
+    state = ops.DeviceArray.from_host(np.array([pos, 0, 0, 0, 1 << 20, 0, 0, 0], np.int32))
+    hist = ops.DeviceArray((1 << 20,), np.int32, zero=True)
+    E = ops.DeviceArray((L.oxb_lm_bytes(V, D),), np.uint8, zero=True)
+    logits = ops.DeviceArray((V,), np.float32)
+    stream = L.oxb_stream_create()
+    kv_b = kvl * 2
+
+    def qkv(l):
+        ops.check(L.oxb_bitlinear_qkv(lay[l]["qkv"].ptr, x.ptr, ones.ptr, 1e-5, ws.ptr, Dq, Dkv, hd, D,
+                                      q.ptr, kc.ptr + l * kv_b, vc.ptr + l * kv_b, max_seq, rope.ptr,
+                                      state.ptr, stream), "qkv")
+
+    def attn(l):
+        ops.check(L.oxb_attn_decode_head(q.ptr, kc.ptr + l * kv_b, vc.ptr + l * kv_b, state.ptr, 0, 0,
+                                         1, H, Hkv, hd, max_seq, 256, att.ptr, stream), "attention")
+
+    def o(l):
+        ops.check(L.oxb_bitlinear_gemv(lay[l]["o"].ptr, att.ptr, ones.ptr, 1e-5, ws.ptr, D, Dq, x.ptr,
+                                       1, None, None, None, stream), "o_proj")
+
+    def gu(l):
+        ops.check(L.oxb_bitlinear_gateup(lay[l]["gu"].ptr, x.ptr, ones.ptr, 1e-5, ws.ptr, 2 * F, D,
+                                         hbuf.ptr, stream), "gate|up")
+
+    def down(l):
+        ops.check(L.oxb_bitlinear_gemv(lay[l]["down"].ptr, hbuf.ptr, ones.ptr, 1e-5, ws.ptr, D, F,
+                                       x.ptr, 1, None, None, None, stream), "down")
+
+    def lm(_):   # advance 0: the position stays put across replays
+        ops.check(L.oxb_lm_head_argmax(x.ptr, ones.ptr, 1e-5, E.ptr, V, D, logits.ptr, state.ptr,
+                                       hist.ptr, 0, stream), "lm head")
+
+    out = {"positions": pos + 1}
+    for name, fn in (("qkv", qkv), ("attention", attn), ("o_proj", o), ("gate_up", gu),
+                     ("down", down)):
+        out[name + "_us"] = round(_timed(L, stream, fn, nl) * 1e3, 2)
+    out["lm_head_us"] = round(_timed(L, stream, lm, 4) * 1e3, 1)
+
+    def chain(_):
+        for l in range(nl):
+            qkv(l), attn(l), o(l), gu(l), down(l)
+        lm(0)
+    out["layers_and_lm_head_us"] = round(_timed(L, stream, chain, 1) * 1e3, 1)
+    L.oxb_stream_destroy(stream)
+    for a in [kc, vc, x, ones, ws, q, att, hbuf, rope, state, hist, E, logits] + \
+             [b for d in lay for b in d.values()]:
+        a.free()
+    return out
+
+
 def gemm_extras(ops, synth) -> dict:
     """The ternary GEMM sweep (28672x8192 and 8192x28672 at M = 8 .. 4096) and
     the 512-token prefill block."""
@@ -506,6 +585,10 @@ def main() -> int:
 
     extra = {}
     if not args.no_extra:
+        db = decode_breakdown(ops, synth)
+        log(f"decode kernels at {db['positions']} positions: " +
+            ", ".join(f"{k} {v}" for k, v in db.items() if k.endswith("_us")))
+        extra["decode_kernels"] = db
         extra.update(gemm_extras(ops, synth))
         lc = long_context(pkg, synth, path)
         log(f"long context: prefill {lc['prefill_ms']} ms")
