@@ -514,6 +514,9 @@ def main() -> int:
                          "batch sizes of --lc-batches)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the ternary GEMM sweep and the 512-token prefill block")
+    ap.add_argument("--gemm-shape", default="",
+                    help="N,K,M: time only the ternary GEMM at that shape (the command the "
+                         "GEMM rocprofv3 --pmc runs profile)")
     ap.add_argument("--lc-batches", default="1,8,32")
     ap.add_argument("--lc-steps", type=int, default=512)
     args = ap.parse_args()
@@ -529,6 +532,12 @@ def main() -> int:
     log(f"device {info['name']} CUs {info['cus']}")
     if args.gemm_only:
         print(json.dumps(gemm_extras(ops, synth)), flush=True)
+        return 0
+    if args.gemm_shape:
+        N, K, M = (int(v) for v in args.gemm_shape.split(","))
+        r = gemm_sweep(ops, synth, N, K, M, copies=2, iters=10)
+        log(f"gemm {N}x{K} M={M}: {r['us']} us {r['TOPS']} TOPS")
+        print(json.dumps({"gemm": r}), flush=True)
         return 0
     if args.roofline_only:
         roof = gemv_roofline(ops, synth, 8192, 28672, copies=16, iters=400)
