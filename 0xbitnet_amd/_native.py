@@ -110,6 +110,12 @@ SIGNATURES = {
     # model
     "oxb_model_load": (vp, [C.c_char_p, C.c_int]),
     "oxb_model_load_kv": (vp, [C.c_char_p, C.c_int, C.c_int]),
+    "oxb_tokenizer_load": (vp, [C.c_char_p]),
+    "oxb_tokenizer_free": (None, [vp]),
+    "oxb_tokenizer_encode": (C.c_int, [vp, C.c_char_p, C.c_int, vp, C.c_int]),
+    "oxb_tokenizer_decode_one": (C.c_int, [vp, C.c_int32, vp, C.c_int]),
+    "oxb_tokenizer_chat": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_int]),
+    "oxb_tokenizer_info": (C.c_int, [vp, vp]),
     "oxb_model_free": (None, [vp]),
     "oxb_model_get_info": (C.c_int, [vp, C.POINTER(ModelInfo)]),
     "oxb_model_reset": (C.c_int, [vp]),

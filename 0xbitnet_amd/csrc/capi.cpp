@@ -272,7 +272,13 @@ int32_t oxbitnet_generate(struct OxBitNet *model, const char *prompt,
         return -1;
     }
     const GenOpts o = read_opts(options);
-    generate_from_ids(model, model->tok.encode(prompt, true), o, callback, userdata);
+    // lib.rs:113: an encode error becomes an empty prompt (no tokens, no error)
+    std::vector<int32_t> ids;
+    if (!model->tok.encode(prompt, true, ids)) {
+        ids.clear();
+        clear_error();
+    }
+    generate_from_ids(model, ids, o, callback, userdata);
     return 0;
 }
 
@@ -314,10 +320,96 @@ int32_t oxbitnet_chat(struct OxBitNet *model, const struct OxBitNetChatMessage *
         return -1;
     }
     const GenOpts o = read_opts(options);
-    generate_from_ids(model, model->tok.apply_chat_template(msgs), o, callback, userdata);
+    // lib.rs:123-126: a template error becomes an empty prompt
+    std::vector<int32_t> ids;
+    if (!model->tok.apply_chat_template(msgs, ids)) {
+        ids.clear();
+        clear_error();
+    }
+    generate_from_ids(model, ids, o, callback, userdata);
     return 0;
 }
 
 const char *oxbitnet_error_message(void) { return last_error(); }
+
+}  // extern "C"
+
+struct oxb_tokenizer {
+    oxb::GgufFile *g = nullptr;
+    oxb::Tokenizer tok;
+    ~oxb_tokenizer() { delete g; }
+};
+
+extern "C" {
+
+oxb_tokenizer *oxb_tokenizer_load(const char *path) {
+    clear_error();
+    if (!path) {
+        set_error("source is NULL");
+        return nullptr;
+    }
+    oxb::GgufFile *g = oxb::gguf_open(path);
+    if (!g) return nullptr;
+    auto *t = new oxb_tokenizer();
+    t->g = g;
+    if (!t->tok.init(*g)) {
+        delete t;
+        return nullptr;
+    }
+    return t;
+}
+
+void oxb_tokenizer_free(oxb_tokenizer *t) { delete t; }
+
+static int copy_ids(const std::vector<int32_t> &v, int32_t *ids, int cap) {
+    if (ids && cap > 0) std::copy_n(v.begin(), std::min((size_t)cap, v.size()), ids);
+    return (int)v.size();
+}
+
+int oxb_tokenizer_encode(const oxb_tokenizer *t, const char *text, int add_bos, int32_t *ids,
+                         int cap) {
+    clear_error();
+    OXB_REQUIRE(t && text, "tokenizer or text is NULL");
+    std::vector<int32_t> v;
+    if (!t->tok.encode(text, add_bos != 0, v)) return -1;
+    return copy_ids(v, ids, cap);
+}
+
+int oxb_tokenizer_decode_one(const oxb_tokenizer *t, int32_t id, char *buf, int cap) {
+    clear_error();
+    OXB_REQUIRE(t, "tokenizer is NULL");
+    const std::string s = t->tok.decode_one(id);
+    if (buf && cap > 0) {
+        const size_t n = std::min((size_t)cap - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return (int)s.size();
+}
+
+int oxb_tokenizer_chat(const oxb_tokenizer *t, const char *const *roles,
+                       const char *const *contents, int n, int32_t *ids, int cap) {
+    clear_error();
+    OXB_REQUIRE(t && n >= 0 && (n == 0 || (roles && contents)), "tokenizer chat: bad arguments");
+    std::vector<oxb::ChatMsg> msgs;
+    for (int i = 0; i < n; ++i) {
+        OXB_REQUIRE(roles[i] && contents[i], "messages[%d] has a NULL field", i);
+        msgs.push_back({roles[i], contents[i]});
+    }
+    std::vector<int32_t> v;
+    if (!t->tok.apply_chat_template(msgs, v)) return -1;
+    return copy_ids(v, ids, cap);
+}
+
+int oxb_tokenizer_info(const oxb_tokenizer *t, int32_t *out) {
+    clear_error();
+    OXB_REQUIRE(t && out, "tokenizer or output is NULL");
+    out[0] = t->tok.bos();
+    out[1] = t->tok.eos();
+    out[2] = t->tok.eot();
+    out[3] = t->tok.im_end();
+    out[4] = (int32_t)t->tok.vocab_size();
+    return 0;
+}
 
 }  // extern "C"

@@ -242,6 +242,22 @@ def write_gguf(path: str, cfg: Config = BITNET_2B, seed: int = 1234) -> str:
     return path
 
 
+def write_tokenizer_gguf(path: str, tokens: list[str], merges: list[str] | None = None,
+                         bos: int = 0, eos: int = 1) -> str:
+    """A GGUF holding tokenizer metadata only (tokens, optional merges "a b",
+    bos/eos ids) and no tensors: what oxb_tokenizer_load reads."""
+    kvs = [_str("general.architecture", "bitnet-25"), _str("tokenizer.ggml.model", "gpt2"),
+           _strarr("tokenizer.ggml.tokens", tokens), _u32("tokenizer.ggml.bos_token_id", bos),
+           _u32("tokenizer.ggml.eos_token_id", eos)]
+    if merges is not None:
+        kvs.append(_strarr("tokenizer.ggml.merges", merges))
+    header = struct.pack("<IIQQ", 0x46554747, 3, 0, len(kvs)) + b"".join(kvs)
+    with open(path, "wb") as f:
+        f.write(header)
+        f.write(b"\0" * ((-len(header)) % ALIGN))
+    return path
+
+
 def cached_gguf(cfg: Config = BITNET_2B, seed: int = 1234, directory: str | None = None) -> str:
     """Path of a synthetic model file, written once per (config, seed)."""
     directory = directory or os.environ.get("OXB_MODEL_DIR", "/tmp/oxbitnet_models")

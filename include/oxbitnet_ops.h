@@ -209,6 +209,28 @@ int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vca
 int32_t oxb_sample_logits(float *logits, size_t V, float temperature, size_t top_k,
                           float repeat_penalty, const int32_t *recent, size_t n_recent, float u);
 
+/* ---- tokenizer (host) ------------------------------------------------------- */
+/* The tokenizer of a GGUF file from its metadata alone (no weights, no GPU):
+ * byte-level BPE over tokenizer.ggml.tokens / .merges as the reference builds
+ * it with HF tokenizers, the chat templates and the stop ids.  Replaces
+ * rs/tokenizer.rs:22-216 (from_gguf_metadata, encode, decode_one,
+ * apply_chat_template).  NULL / -1 on error (oxb_last_error). */
+typedef struct oxb_tokenizer oxb_tokenizer;
+oxb_tokenizer *oxb_tokenizer_load(const char *path);
+void oxb_tokenizer_free(oxb_tokenizer *t);
+/* The ids of text (BOS first when add_bos): writes min(count, cap) ids and
+ * returns count. */
+int oxb_tokenizer_encode(const oxb_tokenizer *t, const char *text, int add_bos, int32_t *ids,
+                         int cap);
+/* One token as text (UTF-8; invalid byte sequences replaced by U+FFFD):
+ * writes at most cap - 1 bytes and a NUL, returns the full length. */
+int oxb_tokenizer_decode_one(const oxb_tokenizer *t, int32_t id, char *buf, int cap);
+/* apply_chat_template over n messages: writes min(count, cap) ids, returns count. */
+int oxb_tokenizer_chat(const oxb_tokenizer *t, const char *const *roles,
+                       const char *const *contents, int n, int32_t *ids, int cap);
+/* out[0..4] = bos, eos, eot (-1 if absent), im_end (-1 if absent), vocabulary size. */
+int oxb_tokenizer_info(const oxb_tokenizer *t, int32_t *out);
+
 /* ---- embedding / LM head --------------------------------------------------- */
 /* x[t] = E[ids[t]] (f16 -> f32; out-of-range ids give zeros); ids == NULL reads
  * the decode state's token.  Replaces nn/model.rs:312-352. */

@@ -341,18 +341,22 @@ def test_loader_metadata_prefix_and_f16_norms(prefix, f16):
     assert len(_greedy_parity(path, prompt, 8)) == 9
 
 
-def _byte_decoder():
-    enc = synth._byte_alphabet()
-    return {ch: b for b, ch in enumerate(enc)}
+def _token_text(path):
+    """decode_one through the host tokenizer (pinned against HF tokenizers in
+    test_tokenizer.py): the bytes generate passes to its callback per id."""
+    L = pkg._native.lib()
+    t = L.oxb_tokenizer_load(path.encode())
+    assert t, L.oxb_last_error()
+    cache = {}
 
-
-def _decode(vocab, dec, i):
-    """tokenizer.rs decode_one for the synthetic vocabulary: byte-level
-    tokens to bytes, specials to b''."""
-    t = vocab[i]
-    if t.startswith("<|") and len(t) > 4:
-        return b""
-    return bytes(dec[c] for c in t)
+    def text(i):
+        if i not in cache:
+            n = L.oxb_tokenizer_decode_one(t, i, None, 0)
+            buf = C.create_string_buffer(n + 1)
+            L.oxb_tokenizer_decode_one(t, i, buf, n + 1)
+            cache[i] = buf.raw[:n]
+        return cache[i]
+    return text
 
 
 def _greedy_ids(path, ids, n):
@@ -415,7 +419,7 @@ def test_generate_top1_with_penalty_is_the_host_argmax_of_penalised_logits():
     h = L.oxbitnet_load(path.encode(), None)
     assert h, L.oxbitnet_error_message()
     got = []
-    vocab, dec = synth.synthetic_vocab(cfg.vocab), _byte_decoder()
+    text = _token_text(path)
     tf = pkg._native.TokenFn(lambda t, k, ud: (got.append(C.string_at(t, k)), 0)[1])
     g = L.oxbitnet_default_generate_options()
     g.max_tokens, g.top_k, g.repeat_penalty, g.temperature = n, 1, 1.1, 0.8
@@ -432,7 +436,7 @@ def test_generate_top1_with_penalty_is_the_host_argmax_of_penalised_logits():
         if t in (257, 260):
             break
         recent.append(t)
-        b = _decode(vocab, dec, t)
+        b = text(t)
         if b"\0" not in b:
             want.append(b)
         _, logits = m.forward(np.array([t], np.int32))
@@ -446,14 +450,14 @@ def test_python_binding_greedy_tokens_are_the_engines():
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
     ids = _greedy_ids(path, [256, 97, 98], 16)
-    vocab, dec = synth.synthetic_vocab(cfg.vocab), _byte_decoder()
+    text = _token_text(path)
     want = []
     for i in ids:
         if i in (257, 260):   # EOS, <|eot_id|>
             break
-        b = _decode(vocab, dec, i)
+        b = text(i)
         if b"\0" not in b:   # a token with a NUL is not passed to the callback
-            want.append(b.decode("utf-8", "replace"))
+            want.append(b.decode("utf-8"))
     bn = pkg.BitNet.load_sync(path)
     got = []
     n = bn.generate("ab", got.append, max_tokens=16, top_k=1, repeat_penalty=1.0)
