@@ -204,7 +204,12 @@ extern "C" int oxb_device_info(char *name, int len, int *cus, int *clock_khz, si
     hipDeviceProp_t prop;
     OXB_CHECK_HIP(hipGetDeviceProperties(&prop, dev));
     if (name && len > 0) {
-        snprintf(name, (size_t)len, "%s (%s)", prop.name, prop.gcnArchName);
+        // the marketing name can be empty (some drivers leave it blank): the
+        // architecture and CU count identify the part then
+        if (prop.name[0])
+            snprintf(name, (size_t)len, "%s (%s)", prop.name, prop.gcnArchName);
+        else
+            snprintf(name, (size_t)len, "%s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
     }
     if (cus) *cus = prop.multiProcessorCount;
     if (clock_khz) *clock_khz = prop.clockRate;

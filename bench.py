@@ -643,6 +643,7 @@ def main() -> int:
         **extra,
         "cpu_baseline": cpu,
         "device": info["name"],
+        "hbm_gib": round(info["hbm_bytes"] / 2**30, 1),
     }
     print(json.dumps(line), flush=True)
     return 0
