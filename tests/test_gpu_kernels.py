@@ -463,6 +463,43 @@ def test_gemm_epilogues(n):
     assert np.array_equal(R, O.add(r, yd))
 
 
+def test_prefill_block_512_tokens():
+    """The 512-token prefill block at the 2B shape, chained as the engine runs
+    it: RMSNorm (gamma ~ U(0.5, 1.5)) + absmax quantize of X [512, 2560] ~
+    N(0, 1), the fused gate|up GEMM (W [6912, 2560] each, seeded uniform
+    ternary, per-tensor scales 1/mean|w| of a N(0, 0.02) master) with
+    relu^2(gate) * up, the subln RMSNorm + requantize, the down GEMM (W [2560,
+    6912]).  Every stage equals the oracle's composition bit for bit."""
+    rng = np.random.default_rng(2512)
+    M, D, F = 512, 2560, 6912
+    wg, wu, wd = ternary(rng, F, D), ternary(rng, F, D), ternary(rng, D, F)
+    sg, su, sd = (synth.master_scale(rng) for _ in range(3))
+    g1 = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    g2 = rng.uniform(0.5, 1.5, F).astype(np.float32)
+    x = rng.standard_normal((M, D)).astype(np.float32)
+    # oracle: rs/nn/ffn.rs:60-80 on the rs/nn/bitlinear.rs:207-247 path
+    q1, s1 = O.quantize(O.rmsnorm(x, g1, 1e-5))
+    _, yg = O.gemm(synth.i2s_pack(wg), q1, sg, s1, D)
+    _, yu = O.gemm(synth.i2s_pack(wu), q1, su, s1, D)
+    h_o = O.mul(O.relu2(yg), yu)
+    q2, s2 = O.quantize(O.rmsnorm(h_o, g2, 1e-5))
+    acc_o, y_o = O.gemm(synth.i2s_pack(wd), q2, sd, s2, F)
+    # device: interleaved gate|up rows, fused epilogue, then the down GEMM
+    inter = np.empty((2 * F, D), np.int8)
+    inter[0::2], inter[1::2] = wg, wu
+    ws = np.empty(2 * F, np.float32)
+    ws[0::2], ws[1::2] = sg, su
+    _, h, sc1 = ops.gemm(ops.upload_ternary(synth.i2s_pack(inter), D), x, g1, 1e-5, ws, 2 * F, D,
+                         epilogue=2)
+    assert np.array_equal(sc1, s1)
+    assert np.array_equal(h, h_o)
+    acc, y, sc2 = ops.gemm(ops.upload_ternary(synth.i2s_pack(wd), F), h, g2, 1e-5,
+                           np.full(D, sd, np.float32), D, F)
+    assert np.array_equal(sc2, s2)
+    assert np.array_equal(acc, acc_o)
+    assert np.array_equal(y, y_o)
+
+
 def test_lm_head_argmax():
     rng = np.random.default_rng(41)
     V, D = 5003, 2560
