@@ -44,8 +44,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const int *__restrict__ pos_ptr,
     int max_seq, float scale, float *__restrict__ scores, size_t kv_stride, int pos_stride) {
     // K rows of this position block, 16 uint4 each, padded to 17 so that the
-    // 64 lanes reading one column hit different banks.
+    // 64 lanes reading one column hit different banks; the G q rows.
     __shared__ uint4 ks[kScoreP][17];
+    __shared__ __align__(16) float qs[G * kHd];
+    // all kernel arguments in SGPRs up front (a late one is a further kernarg
+    // round trip before the chain)
+    asm volatile("" ::"s"(q), "s"(kc), "s"(pos_ptr), "s"(max_seq), "s"(scale), "s"(scores),
+                 "s"(kv_stride), "s"(pos_stride));
     {   // sequence blockIdx.z of a batch: its own q, cache, position, scores
         const int z = blockIdx.z, H = gridDim.y * G;
         q += (size_t)z * H * kHd;
@@ -60,7 +65,10 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const int s0 = b * kScoreP;
     if (s0 >= S) return;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    // coalesced tile load: thread i takes uint4 i, i + 256, ... of the rows
+    // the G q rows (float4 tid mod 32G: every thread loads and stores, so no
+    // load sits under a branch), then the coalesced tile load: thread i takes
+    // uint4 i, i + 256, ... of the rows
+    const float4 q4 = ((const float4 *)(q + (size_t)hk * G * kHd))[tid & (G * 32 - 1)];
     const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
     uint4 kt[4];
 #pragma unroll
@@ -68,6 +76,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         const int i = tid + 256 * k, row = i >> 4;
         kt[k] = K4[(size_t)min(s0 + row, S - 1) * 16 + (i & 15)];
     }
+    *(float4 *)(qs + 4 * (tid & (G * 32 - 1))) = q4;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int i = tid + 256 * k;
@@ -77,27 +86,41 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
-    // this lane's K row into registers; the head's q row is wave-uniform and
-    // read with scalar loads, so each step of the chain is one v_fma_mix
-    // (q operand in an SGPR, k converted from f16 inside the instruction)
+    // this lane's K row into registers; the head's q row is read as LDS
+    // broadcasts three 8-term groups ahead (scalar loads would return out of
+    // order and force full waits inside the chain); each step of the chain is
+    // one v_fma_mix (k converted from f16 inside the instruction)
     uint4 kr16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kr16[i] = ks[lane][i];
     const int wu = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
-        const float *__restrict__ qg = q + (size_t)(hk * G + wu + 4 * h) * kHd;
+        const float *qg = qs + (wu + 4 * h) * kHd;
+        constexpr int kAhead = 3;
+        float4 qa[16], qb[16];
+        auto ld = [&](int i) {
+            qa[i] = *(const float4 *)(qg + 8 * i);
+            qb[i] = *(const float4 *)(qg + 8 * i + 4);
+        };
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) ld(i);
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (i + kAhead < 16) ld(i + kAhead);
+            __builtin_amdgcn_sched_barrier(0);
+            const float qv[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w,
+                                 qb[i].x, qb[i].y, qb[i].z, qb[i].w};
             const uint4 kr = kr16[i];
             const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
                 const float k0 = __half2float(__ushort_as_half((uint16_t)(kw[k2] & 0xffffu)));
                 const float k1 = __half2float(__ushort_as_half((uint16_t)(kw[k2] >> 16)));
-                dot = __builtin_fmaf(qg[8 * i + 2 * k2], k0, dot);
-                dot = __builtin_fmaf(qg[8 * i + 2 * k2 + 1], k1, dot);
+                dot = __builtin_fmaf(qv[2 * k2], k0, dot);
+                dot = __builtin_fmaf(qv[2 * k2 + 1], k1, dot);
             }
         }
         scores[(size_t)(hk * G + wu + 4 * h) * max_seq + s] = dot * scale;
