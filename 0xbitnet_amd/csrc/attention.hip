@@ -680,6 +680,259 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Prefill on f32 MFMA.  v_mfma_f32_16x16x1_4b (K = 1) adds one product to
+// each output element per instruction, D = A*B + C rounded once, which is
+// the fused multiply-add: a chain of them over d (or over positions) is the
+// same sequential fma chain as the shaders' loops, bit for bit, at twice the
+// VALU's fma rate.  Lane l supplies A[block l/16][row l%16] and B[block
+// l/16][col l%16]; element (block b, row i, col j) of D is in lane
+// j + 16(i/4), register 4b + i%4.
+//
+// The B operands come from f32 copies of the cache laid out for them
+// (attn_kv_tiles_kernel, one pass per call): per KV head
+//   Kt [tile of 64 positions][d/4][64 positions][4 d]
+//   Vt [position/4][128 d][4 positions]
+// zero past the last position, so a lane's 16-byte load is 4 steps of its
+// operand with no conversion, and a wave's load is 1 KB contiguous.
+//
+// One workgroup of 16 waves (four per SIMD: a dependent MFMA chain issues at
+// ~64% of the MFMA rate from one wave per SIMD, ~100% from four) per (16/G
+// consecutive queries, KV head): 16 score rows, row r = query r/G, head r%G;
+// query i attends over its position + 1 positions (causal).
+//   scores: wave w takes the 64-position tiles w, w+16, ...: per d one
+//     instruction covers the 16 rows (A = q[r][d], the same in the 4 blocks)
+//     x 64 positions (B = K[tile + l][d]), 128 of them in order of d.
+//     dot * scale goes to the row in LDS.
+//   softmax: wave_softmax_row on row w, in place; positions past the row's
+//     length become exact zeros.
+//   P.V: task = (256-position block b, half h), wave w taking tasks w, w+16:
+//     per position one instruction (A = p[r][s], B = V[s][c + 64h] for the
+//     64 columns c), in order of s from zero.  A row shorter than the block
+//     sees p = 0 steps, which add an exact zero (its sum starts at +0, so it
+//     is never -0; V is finite).  The block sums go to LDS, and each output
+//     is the in-order sum of the blocks its row reaches
+//     (sh/attention.wgsl:96-104, the oracle's 256-position blocks).
+// LDS (dynamic): q [16][132] | rows [16][Sw], Sw = the longest row rounded
+// up to 64, plus 4, so that the 16 rows one read touches start in different
+// banks; the block sums [blocks][16][128] reuse it after the last read of p.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int kPfmWaves = 16;
+constexpr int kPfmThreads = 64 * kPfmWaves;
+constexpr int kPfmQs = kHd + 4;   // q row stride (floats)
+constexpr int kPfmMaxS = 2368;    // longest row whose 16 rows fit the LDS (160 KB)
+constexpr int kPfmTasks = ((kPfmMaxS + kPvBlock - 1) / kPvBlock * 2 + kPfmWaves - 1) / kPfmWaves;
+constexpr int kTileF4 = 64 * kHd / 4;   // float4 of one 64-position tile of Kt or Vt
+
+__host__ __device__ inline int pfm_row_stride(int s_max) { return ((s_max + 63) & ~63) + 4; }
+__host__ __device__ inline size_t pfm_smem(int s_max) {
+    const size_t rows = (size_t)16 * (kPfmQs + pfm_row_stride(s_max)) * sizeof(float);
+    const size_t sums = (size_t)((s_max + kPvBlock - 1) / kPvBlock) * 16 * kHd * sizeof(float);
+    return rows > sums ? rows : sums;
+}
+
+__device__ __forceinline__ v16f mfma_f32_k1(float a, float b, const v16f &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+// Kt and Vt tiles (layouts above) of positions [64t, 64t + 64) of KV head hk
+// from the f16 caches; positions >= S are zeros.  Grid (tiles, Hkv).
+__global__ __launch_bounds__(256) void attn_kv_tiles_kernel(const uint16_t *__restrict__ kc,
+                                                            const uint16_t *__restrict__ vc,
+                                                            int max_seq, int S, int ntile_ws,
+                                                            float4 *__restrict__ Kt,
+                                                            float4 *__restrict__ Vt) {
+    __shared__ uint4 ks[64][17], vs[64][17];   // 64 rows of 16 uint4, padded
+    const int t = blockIdx.x, hk = blockIdx.y, tid = threadIdx.x;
+    const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
+    const uint4 *V4 = (const uint4 *)(vc + (size_t)hk * max_seq * kHd);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = tid + 256 * k, row = i >> 4, c = i & 15, pos = 64 * t + row;
+        uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+        if (pos < S) {
+            kv = K4[(size_t)pos * 16 + c];
+            vv = V4[(size_t)pos * 16 + c];
+        }
+        ks[row][c] = kv;
+        vs[row][c] = vv;
+    }
+    __syncthreads();
+    auto h2f = [](uint32_t h) { return __half2float(__ushort_as_half((uint16_t)h)); };
+    float4 *kt = Kt + ((size_t)hk * ntile_ws + t) * kTileF4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {   // kt[c][p]: dims 4c .. 4c+3 of position p
+        const int i = tid + 256 * k, c = i >> 6, pos = i & 63;
+        const uint4 u = ks[pos][c >> 1];
+        const uint32_t lo = (c & 1) ? u.z : u.x, hi = (c & 1) ? u.w : u.y;
+        kt[i] = make_float4(h2f(lo & 0xffff), h2f(lo >> 16), h2f(hi & 0xffff), h2f(hi >> 16));
+    }
+    float4 *vt = Vt + ((size_t)hk * ntile_ws + t) * kTileF4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {   // vt[g][d]: positions 4g .. 4g+3 of dim d
+        const int i = tid + 256 * k, g = i >> 7, d = i & 127;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 u = vs[4 * g + j][d >> 3];
+            const uint32_t wd = ((d & 7) >> 1) == 0 ? u.x : ((d & 7) >> 1) == 1 ? u.y
+                              : ((d & 7) >> 1) == 2 ? u.z : u.w;
+            v[j] = h2f((d & 1) ? wd >> 16 : wd & 0xffff);
+        }
+        vt[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
+    const float *__restrict__ q, const float4 *__restrict__ Kt, const float4 *__restrict__ Vt,
+    int ntile_ws, int pos0, int n_q, int H, float scale, float *__restrict__ out) {
+    constexpr int QB = 16 / G;   // queries per workgroup
+    extern __shared__ __align__(16) float smem[];
+    float *qs = smem, *rows = smem + 16 * kPfmQs;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform loop control
+    const int nblk = (n_q + QB - 1) / QB;
+    const int q0 = (nblk - 1 - (int)blockIdx.x) * QB, hk = blockIdx.y;   // longest rows first
+    const int Smax = pos0 + min(q0 + QB - 1, n_q - 1) + 1;
+    const int ntile = (Smax + 63) >> 6;
+    if (ntile > ntile_ws || Smax > kPfmMaxS) return;   // host checks too; never read out of range
+    const int Sw = pfm_row_stride(Smax);
+    auto row_len = [&](int r) { return pos0 + min(q0 + r / G, n_q - 1) + 1; };
+
+    for (int i = tid; i < 16 * (kHd / 4); i += kPfmThreads) {
+        const int r = i / (kHd / 4), c = i % (kHd / 4);
+        const int qi = min(q0 + r / G, n_q - 1);
+        *(float4 *)(qs + r * kPfmQs + 4 * c) =
+            *(const float4 *)(q + ((size_t)qi * H + hk * G + r % G) * kHd + 4 * c);
+    }
+    lds_barrier();
+
+    // ---- scores (sh/attention.wgsl:48-58) ----------------------------------
+    {
+        const float *qrow = qs + (lane & 15) * kPfmQs;
+        for (int t = w; t < ntile; t += kPfmWaves) {
+            const float4 *kt = Kt + ((size_t)hk * ntile_ws + t) * kTileF4 + lane;
+            v16f acc = {};
+            float4 kg[2][8];   // dims 32g .. 32g+31 of this lane's position, two groups
+#pragma unroll
+            for (int j = 0; j < 8; ++j) kg[0][j] = kt[64 * j];
+#pragma unroll
+            for (int g = 0; g < kHd / 32; ++g) {
+                if (g + 1 < kHd / 32) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) kg[(g + 1) & 1][j] = kt[64 * (8 * (g + 1) + j)];
+                }
+                __builtin_amdgcn_sched_barrier(0);   // next group's loads ahead of these MFMAs
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int c = 8 * g + j;   // dims 4c .. 4c+3
+                    const float4 qv = *(const float4 *)(qrow + 4 * c);
+                    const float4 kv = kg[g & 1][j];
+                    acc = mfma_f32_k1(qv.x, kv.x, acc);
+                    acc = mfma_f32_k1(qv.y, kv.y, acc);
+                    acc = mfma_f32_k1(qv.z, kv.z, acc);
+                    acc = mfma_f32_k1(qv.w, kv.w, acc);
+                }
+            }
+            const int r0 = 4 * (lane >> 4), p = 64 * t + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int pos = p + 16 * (r >> 2);
+                if (pos < Smax) rows[(r0 + (r & 3)) * Sw + pos] = acc[r] * scale;
+            }
+        }
+    }
+    lds_barrier();
+
+    // ---- softmax (sh/softmax.wgsl:25-80) ------------------------------------
+    for (int r = w; r < 16; r += kPfmWaves) {
+        const int S = row_len(r);
+        // wave_softmax_row for rows of up to kPfmMaxS positions (register-held row)
+        float *row = rows + r * Sw;
+        const int nj = (S + 255) >> 8;
+        if (nj <= 1) softmax_row_regs<1, true>(row, row, S, Sw, lane);
+        else if (nj <= 2) softmax_row_regs<2, true>(row, row, S, Sw, lane);
+        else if (nj <= 4) softmax_row_regs<4, true>(row, row, S, Sw, lane);
+        else if (nj <= 6) softmax_row_regs<6, true>(row, row, S, Sw, lane);
+        else if (nj <= 8) softmax_row_regs<8, true>(row, row, S, Sw, lane);
+        else softmax_row_regs<(kPfmMaxS + 255) / 256, true>(row, row, S, Sw, lane);
+        for (int s = S + lane; s < Sw; s += 64) row[s] = 0.0f;   // same wave: in order
+    }
+    lds_barrier();
+
+    // ---- P.V: task = (block b, half h): 16 rows x the 64 dims c + 64h -------
+    const int nb = (Smax + kPvBlock - 1) / kPvBlock;
+    const float *prow = rows + (lane & 15) * Sw;
+    const int s_last = 64 * ntile - 8;   // last batch start inside Vt and the rows
+    v16f part[kPfmTasks];
+#pragma unroll
+    for (int k = 0; k < kPfmTasks; ++k) {
+        const int task = w + kPfmWaves * k, b = task >> 1, h = task & 1;
+        v16f a = {};
+        if (b < nb) {
+            const float4 *vt = Vt + (size_t)hk * ntile_ws * kTileF4 + lane + 64 * h;
+            const int s0 = b * kPvBlock, e = min(s0 + kPvBlock, Smax);
+            // 8 positions per batch; the next batch's V (global) and p (LDS)
+            // are read before this batch's MFMAs (a batch past the block reads
+            // the last batch and is never used)
+            auto load = [&](float4 (&vv)[2], float4 (&pp)[2], int s) {
+                const int sb = min(s, s_last);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
+                    pp[j] = *(const float4 *)(prow + sb + 4 * j);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            auto run = [&](const float4 (&vv)[2], const float4 (&pp)[2]) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    a = mfma_f32_k1(pp[j].x, vv[j].x, a);
+                    a = mfma_f32_k1(pp[j].y, vv[j].y, a);
+                    a = mfma_f32_k1(pp[j].z, vv[j].z, a);
+                    a = mfma_f32_k1(pp[j].w, vv[j].w, a);
+                }
+            };
+            float4 va[2], vb[2], pa[2], pb[2];
+            load(va, pa, s0);
+            for (int s = s0;; s += 16) {
+                load(vb, pb, s + 8);
+                run(va, pa);
+                if (s + 8 >= e) break;
+                load(va, pa, s + 16);
+                run(vb, pb);
+                if (s + 16 >= e) break;
+            }
+        }
+        part[k] = a;
+    }
+    lds_barrier();   // every wave is done with the probabilities
+    float *sums = smem;   // [nb][16][kHd]
+#pragma unroll
+    for (int k = 0; k < kPfmTasks; ++k) {
+        const int task = w + kPfmWaves * k, b = task >> 1, h = task & 1;
+        if (b < nb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 4 * (lane >> 4) + (r & 3);
+                const int d = 16 * (r >> 2) + (lane & 15) + 64 * h;
+                sums[((size_t)b * 16 + i) * kHd + d] = part[k][r];
+            }
+        }
+    }
+    lds_barrier();
+    for (int o = tid; o < 16 * kHd; o += kPfmThreads) {
+        const int r = o / kHd, d = o % kHd;
+        const int S = row_len(r);
+        float total = sums[r * kHd + d];
+        for (int b = 1; b * kPvBlock < S; ++b) total = total + sums[((size_t)b * 16 + r) * kHd + d];
+        const int qi = q0 + r / G;
+        if (qi < n_q) out[((size_t)qi * H + hk * G + r % G) * kHd + d] = total;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode, one kernel: two 1024-thread workgroups per KV head (one per half of
 // the 128 dims) each compute the scores and softmax of its G <= 4 query
 // heads, then the P.V sums of their half of the dims, so a layer's attention
@@ -1273,15 +1526,53 @@ static int launch_prefill_g(const float *q, const uint16_t *kc, const uint16_t *
     return launch_prefill<G, 1>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
 }
 
-static int dispatch_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int pos0,
-                            int n_q, int H, int Hkv, int hd, int max_seq, int s_max, float *out,
-                            void *stream) {
+template <int G>
+static int launch_prefill_mfma(const float *q, const uint16_t *kc, const uint16_t *vc, int pos0,
+                               int n_q, int H, int Hkv, int max_seq, int s_max, void *ws,
+                               float *out, hipStream_t s) {
+    constexpr int QB = 16 / G;
+    if (allow_dynamic_lds((const void *)attn_prefill_mfma_kernel<G>)) return -1;
+    const int ntile = (s_max + 63) / 64;
+    float4 *Kt = (float4 *)ws, *Vt = Kt + (size_t)Hkv * ntile * kTileF4;
+    hipLaunchKernelGGL(attn_kv_tiles_kernel, dim3(ntile, Hkv), dim3(256), 0, s, kc, vc, max_seq,
+                       s_max, ntile, Kt, Vt);
+    OXB_CHECK_HIP(hipGetLastError());
+    const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    hipLaunchKernelGGL((attn_prefill_mfma_kernel<G>), dim3((n_q + QB - 1) / QB, Hkv),
+                       dim3(kPfmThreads), pfm_smem(s_max), s, q, Kt, Vt, ntile, pos0, n_q, H,
+                       scale, out);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+size_t attn_prefill_ws_bytes(int Hkv, int s_max) {
+    if (Hkv <= 0 || s_max <= 0 || s_max > kPfmMaxS) return 0;
+    return (size_t)2 * Hkv * ((s_max + 63) / 64) * kTileF4 * sizeof(float4);
+}
+
+// f32 MFMA kernel (with its Kt / Vt workspace) while its 16 rows fit the LDS
+// (up to kPfmMaxS positions), else the VALU kernel: the same sums in the same
+// order either way
+int attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int n_q, int pos0, int H,
+                 int Hkv, int hd, int max_seq, void *ws, size_t ws_bytes, float *out,
+                 void *stream) {
     OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
-    const int G = H / Hkv;
+    OXB_REQUIRE(n_q > 0 && pos0 >= 0 && pos0 + n_q <= max_seq, "prefill attention: bad range");
+    const int G = H / Hkv, s_max = pos0 + n_q;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t need = attn_prefill_ws_bytes(Hkv, s_max);
+    if (need && ws && ws_bytes >= need) {
+        switch (G) {
+            case 1: return launch_prefill_mfma<1>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, ws, out, s);
+            case 2: return launch_prefill_mfma<2>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, ws, out, s);
+            case 4: return launch_prefill_mfma<4>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, ws, out, s);
+            case 8: return launch_prefill_mfma<8>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, ws, out, s);
+            default: break;
+        }
+    }
     OXB_REQUIRE(prefill_smem(G, s_max) <= kPrefillLds,
                 "attention: %d heads per KV head x %d positions exceed the LDS budget", G, s_max);
-    hipStream_t s = (hipStream_t)stream;
     switch (G) {
         case 1: return launch_prefill_g<1>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
         case 2: return launch_prefill_g<2>(q, kc, vc, pos0, n_q, H, Hkv, max_seq, s_max, out, s);
@@ -1415,12 +1706,23 @@ extern "C" int oxb_attn_decode_fused(const float *q, const uint16_t *kcache,
     }
 }
 
+// The Kt / Vt workspace is stream-ordered memory of this call (allocated and
+// released on the caller's stream).
 extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                                 int n_tok, int pos0, int H, int Hkv, int hd, int max_seq,
                                 float *out, void *stream) {
     OXB_REQUIRE(n_tok > 0 && pos0 >= 0 && pos0 + n_tok <= max_seq, "prefill attention: bad range");
-    return dispatch_prefill(q, kcache, vcache, pos0, n_tok, H, Hkv, hd, max_seq, pos0 + n_tok, out,
-                            stream);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t need = attn_prefill_ws_bytes(Hkv, pos0 + n_tok);
+    void *ws = nullptr;
+    if (need) OXB_CHECK_HIP(hipMallocAsync(&ws, need, s));
+    const int rc = attn_prefill(q, kcache, vcache, n_tok, pos0, H, Hkv, hd, max_seq, ws, need, out,
+                                stream);
+    if (ws) {
+        const hipError_t e = hipFreeAsync(ws, s);
+        if (rc == 0) OXB_CHECK_HIP(e);
+    }
+    return rc;
 }
 
 extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,

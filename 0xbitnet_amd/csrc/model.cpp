@@ -626,6 +626,11 @@ int oxb_model::ensure_prefill(int n) {
 // table, state block and position (the model's own, or a batch slot's).
 int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg) {
     if (ensure_prefill(n)) return -1;
+    const size_t ws_need = oxb::attn_prefill_ws_bytes(Hkv, tg.pos + n);
+    if (ws_need > pf_ws_bytes) {   // earlier workspaces may still be in use by queued work
+        if (!(pf_ws = dalloc(ws_need))) return -1;
+        pf_ws_bytes = ws_need;
+    }
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
@@ -640,8 +645,8 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
             return -1;
         if (kv_f32 ? oxb::attn_f32(pq, (const float *)kc, (const float *)vc, nullptr, tg.pos, n, H,
                                    Hkv, hd, tg.max_seq, pattn, s)
-                   : oxb_attn_prefill(pq, (const uint16_t *)kc, (const uint16_t *)vc, n, tg.pos, H,
-                                      Hkv, hd, tg.max_seq, pattn, s))
+                   : oxb::attn_prefill(pq, (const uint16_t *)kc, (const uint16_t *)vc, n, tg.pos,
+                                       H, Hkv, hd, tg.max_seq, pf_ws, pf_ws_bytes, pattn, s))
             return -1;
         if (oxb_quantize_rows_tiled(pattn, L.attn_sub, 1e-5f, n, Dq, pX, pscale, psum, s)) return -1;
         if (oxb_gemm_i8(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1, s))

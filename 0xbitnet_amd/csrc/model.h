@@ -44,6 +44,8 @@ struct oxb_model {
 
     // prefill buffers (grown on demand)
     int pf_cap = 0;
+    void *pf_ws = nullptr;   // prefill attention's K / V copies (grows; old ones kept until unload)
+    size_t pf_ws_bytes = 0;
     float *px = nullptr, *pq = nullptr, *pattn = nullptr, *ph = nullptr, *pscale = nullptr;
     void *pX = nullptr;
     int *psum = nullptr, *pids = nullptr;

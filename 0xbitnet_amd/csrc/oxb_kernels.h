@@ -31,6 +31,14 @@ int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const in
              const float *rope_cs, void *stream);
 // Attention over an f32 cache ([Hkv][max_seq][hd]): n_q queries at positions
 // pos0 + i, or one query at *pos_ptr when pos_ptr is given (attention.hip).
+// Causal prefill attention (oxb_attn_prefill) with the caller's workspace for
+// the f32-MFMA kernel's K / V copies: attn_prefill_ws_bytes(Hkv, pos0 + n_q)
+// bytes (0: that length runs on the VALU kernel, which needs none).  A
+// smaller or null workspace selects the VALU kernel; the results are the same.
+size_t attn_prefill_ws_bytes(int Hkv, int s_max);
+int attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int n_q, int pos0, int H,
+                 int Hkv, int hd, int max_seq, void *ws, size_t ws_bytes, float *out,
+                 void *stream);
 int attn_f32(const float *q, const float *kcache, const float *vcache, const int *pos_ptr,
              int pos0, int n_q, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
 int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,

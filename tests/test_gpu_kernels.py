@@ -340,14 +340,21 @@ def test_attn_decode_fused_rejects_unsupported():
                         np.zeros((4, 8, 128), np.float16), 3, 32, 4, 128, 8, fused=True)
 
 
-# G = 4 and 8 take query pairs (an odd n leaves a lone last query); (0, 257)
-# pairs rows of 256 and 257 positions; G = 1, 2 one query per workgroup
+# Rows up to 2368 positions run on the f32-MFMA kernel (16 score rows per
+# workgroup: 16/G queries; ragged last blocks; rows that straddle a 256-position
+# P.V block; (0, 257) pairs rows of 256 and 257 positions), longer ones on the
+# VALU kernel (G = 4 and 8 take query pairs, G = 1, 2 one query per workgroup)
 @pytest.mark.parametrize("H,Hkv,S,pos0,n", [(20, 5, 256, 30, 100), (20, 5, 512, 0, 257),
                                             (16, 2, 1200, 900, 31), (8, 8, 300, 5, 40),
                                             (16, 8, 300, 100, 33), (20, 5, 2100, 2040, 9),
                                             (20, 5, 64, 0, 1),
                                             # 1001 queries over 4 P.V blocks, a lone last query
-                                            (20, 5, 1100, 50, 1001)])
+                                            (20, 5, 1100, 50, 1001),
+                                            # the longest rows the MFMA kernel takes
+                                            (20, 5, 2368, 2300, 68),
+                                            # VALU kernel: rows past 2368 positions
+                                            (20, 5, 2600, 2369, 30), (16, 8, 3000, 2900, 17),
+                                            (8, 8, 2500, 2450, 11)])
 def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
     rng = np.random.default_rng(21 + n)
     hd = 128
