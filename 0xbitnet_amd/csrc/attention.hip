@@ -184,7 +184,7 @@ __device__ __forceinline__ void softmax_row_regs(float *row, const float *__rest
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float e = oxb_expf(x[j][i] - m);
+            const float e = oxb_expf_nonpos(x[j][i] - m);   // <= 0 for the positions kept
             x[j][i] = 256 * j + 4 * lane + i < S ? e : 0.0f;
             c[i] = c[i] + x[j][i];
         }
@@ -864,7 +864,7 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
     // ---- P.V: task = (block b, half h): 16 rows x the 64 dims c + 64h -------
     const int nb = (Smax + kPvBlock - 1) / kPvBlock;
     const float *prow = rows + (lane & 15) * Sw;
-    const int s_last = 64 * ntile - 8;   // last batch start inside Vt and the rows
+    const int s_last = 64 * ntile - 16;   // last batch start inside Vt and the rows
     v16f part[kPfmTasks];
 #pragma unroll
     for (int k = 0; k < kPfmTasks; ++k) {
@@ -873,36 +873,36 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
         if (b < nb) {
             const float4 *vt = Vt + (size_t)hk * ntile_ws * kTileF4 + lane + 64 * h;
             const int s0 = b * kPvBlock, e = min(s0 + kPvBlock, Smax);
-            // 8 positions per batch; the next batch's V (global) and p (LDS)
+            // 16 positions per batch; the next batch's V (global) and p (LDS)
             // are read before this batch's MFMAs (a batch past the block reads
             // the last batch and is never used)
-            auto load = [&](float4 (&vv)[2], float4 (&pp)[2], int s) {
+            auto load = [&](float4 (&vv)[4], float4 (&pp)[4], int s) {
                 const int sb = min(s, s_last);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
                     pp[j] = *(const float4 *)(prow + sb + 4 * j);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             };
-            auto run = [&](const float4 (&vv)[2], const float4 (&pp)[2]) {
+            auto run = [&](const float4 (&vv)[4], const float4 (&pp)[4]) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     a = mfma_f32_k1(pp[j].x, vv[j].x, a);
                     a = mfma_f32_k1(pp[j].y, vv[j].y, a);
                     a = mfma_f32_k1(pp[j].z, vv[j].z, a);
                     a = mfma_f32_k1(pp[j].w, vv[j].w, a);
                 }
             };
-            float4 va[2], vb[2], pa[2], pb[2];
+            float4 va[4], vb[4], pa[4], pb[4];
             load(va, pa, s0);
-            for (int s = s0;; s += 16) {
-                load(vb, pb, s + 8);
+            for (int s = s0;; s += 32) {
+                load(vb, pb, s + 16);
                 run(va, pa);
-                if (s + 8 >= e) break;
-                load(va, pa, s + 16);
-                run(vb, pb);
                 if (s + 16 >= e) break;
+                load(va, pa, s + 32);
+                run(vb, pb);
+                if (s + 32 >= e) break;
             }
         }
         part[k] = a;

@@ -290,6 +290,25 @@ __device__ inline float oxb_expf(float x) {
     return x != x ? x : y;
 }
 
+// oxb_expf for the softmax's arguments x - max <= 0 (or NaN): the same bits
+// there, in fewer instructions (no overflow test, and NaN propagates through
+// the arithmetic).  For x > 0 the result is not oxb_expf's; the softmax only
+// evaluates x > 0 for positions it discards.
+__device__ inline float oxb_expf_nonpos(float x) {
+    const float kf = rintf(x * 1.44269502f);
+    float r = __builtin_fmaf(-kf, 0.693145751953125f, x);
+    r = __builtin_fmaf(-kf, 1.42860677e-06f, r);
+    float p = __builtin_fmaf(1.98412701e-04f, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float y = ldexpf(p, (int)fmaxf(kf, -200.0f));   // kf <= 0 for x <= 0
+    return x < -103.972084f ? 0.0f : y;
+}
+
 // sh/quantize.wgsl:59,68,71 for one value given the row absmax.
 __device__ inline int quant_one(float v, float inv) {
     int q = (int)rintf(v * inv);
