@@ -426,6 +426,7 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kTiledRows = 2;
 
+template <int NREG>   // >= D / 256 values per thread (the row's loads)
 __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     const float *__restrict__ x, const float *__restrict__ gamma, float eps, int D, int n_tok,
     uint4 *__restrict__ Xt, float *__restrict__ scales, int *__restrict__ sums) {
@@ -438,9 +439,9 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     const int row = blockIdx.x * kTiledRows + grp;
     float scale = 1.0f;
     if (row < n_tok) {
-        float v[kMaxNormReg], g[kMaxNormReg];
-        load_row<kMaxNormReg>(x + (size_t)row * D, gamma, D, v, g);
-        scale = norm_quant_regs<kMaxNormReg>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
+        float v[NREG], g[NREG];
+        load_row<NREG>(x + (size_t)row * D, gamma, D, v, g);
+        scale = norm_quant_regs<NREG>(v, g, gamma != nullptr, eps, D, q_lds, red, wq);
     } else {
         // padding rows: the group still meets the row path's barriers (one in
         // the norm's tree sum, one for the absmax)
@@ -637,8 +638,17 @@ extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float
     OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
     const int rows = (n_tok + 15) & ~15;
     const size_t sm = (size_t)kTiledRows * (((D + 15) & ~15) + 328 * 4);
-    hipLaunchKernelGGL(quantize_rows_tiled_kernel, dim3(rows / kTiledRows), dim3(256 * kTiledRows),
-                       sm, stream, x, gamma, eps, D, n_tok, (uint4 *)Xt, scales, sums);
+    // loads per thread: the row length's bucket (the model's 2560 and 6912 exactly)
+    const int nr = D / 256;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(rows / kTiledRows), dim3(256 * kTiledRows), sm, stream, x,
+                           gamma, eps, D, n_tok, (uint4 *)Xt, scales, sums);
+    };
+    if (nr <= 4) go(quantize_rows_tiled_kernel<4>);
+    else if (nr <= 10) go(quantize_rows_tiled_kernel<10>);
+    else if (nr <= 16) go(quantize_rows_tiled_kernel<16>);
+    else if (nr <= 27) go(quantize_rows_tiled_kernel<27>);
+    else go(quantize_rows_tiled_kernel<kMaxNormReg>);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
