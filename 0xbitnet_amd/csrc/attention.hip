@@ -18,6 +18,8 @@
 // pair of queries).  Cache layout: [Hkv][max_seq][128] f16 bits.
 #include <mutex>
 
+#include <cstring>
+
 #include "oxb_common.h"
 #include "oxb_kernels.h"
 
@@ -532,6 +534,128 @@ __global__ __launch_bounds__(256) void attn_pv_wide_kernel(
         }
     }
     if (ws < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Decode P.V on f32 MFMA (split path: > 256 positions, and batches).
+// v_mfma_f32_4x4x1_16b adds one product per output per instruction (one
+// rounding: the fused step, as the 16x16x1 form in the prefill kernel): lane
+// l supplies A[block l/4][row l%4] and B[block l/4][col l%4], and holds
+// D[block l/4][row r][col l%4] in register r.  Rows are the G <= 4 query
+// heads of a KV head (A = p[head][s], the same in all 16 blocks; rows past G
+// are zero probabilities), columns are dims: lane l takes dims 2l and 2l+1,
+// one dword of the f16 V row per position for two chains.  One workgroup of
+// 16 waves per (KV head, sequence): the softmax of the G rows into LDS, then
+// wave w sums the 256-position block w in order of s from zero, with three
+// 16-position batches of V rows in flight (read straight from the cache,
+// 256 B per wave per position); the block sums are added in block order
+// (sh/attention.wgsl:96-104 with the oracle's 256-position blocks).
+// LDS (dynamic): p [4][Sp] | block sums [blocks][4][128].
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kPvmWaves = 16;
+constexpr int kPvmThreads = 64 * kPvmWaves;
+constexpr int kPvmMaxBlocks = kPvmWaves;   // one block per wave: positions up to 4096
+
+__host__ __device__ inline int pvm_row_stride(int max_seq) { return ((max_seq + 15) & ~15) + 4; }
+__host__ __device__ inline size_t pvm_smem(int max_seq) {
+    return ((size_t)4 * pvm_row_stride(max_seq) +
+            (size_t)((max_seq + kPvBlock - 1) / kPvBlock) * 4 * kHd) * sizeof(float);
+}
+
+template <int G>
+__global__ __launch_bounds__(kPvmThreads) void attn_pv_mfma_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
+    int pos_stride) {
+    static_assert(G >= 1 && G <= 4, "four MFMA rows");
+    {   // sequence blockIdx.y of a batch
+        const int z = blockIdx.y, H = gridDim.x * G;
+        scores += (size_t)z * H * max_seq;
+        vc += (size_t)z * kv_stride;
+        pos_ptr += (size_t)z * pos_stride;
+        out += (size_t)z * H * kHd;
+    }
+    extern __shared__ __align__(16) float smem[];
+    const int Sp = pvm_row_stride(max_seq);
+    float *pr = smem, *sums = smem + 4 * Sp;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hk = blockIdx.x;
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1, Spad = (S + 3) & ~3;
+    const int nb = (S + kPvBlock - 1) / kPvBlock;
+    if (nb > kPvmMaxBlocks) return;   // host checks too
+    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + lane;   // dims 2l, 2l+1
+    const int s0 = w * kPvBlock, e = min(s0 + kPvBlock, S);
+
+    auto load_v = [&](uint32_t (&vv)[16], int s) {   // positions s .. s+15, clamped to the cache
+#pragma unroll
+        for (int u = 0; u < 16; ++u) vv[u] = V2[(size_t)min(s + u, S - 1) * (kHd / 2)];
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    uint32_t va[16], vb[16], vcur[16];
+    load_v(va, s0);   // the first two batches go out before the softmax
+    load_v(vb, s0 + 16);
+
+    // ---- softmax of the G score rows (sh/softmax.wgsl:25-80); rows >= G are zeros
+    if (w < G) {
+        wave_softmax_row(pr + w * Sp, scores + (size_t)(hk * G + w) * max_seq, S, Spad, lane,
+                         (max_seq & 3) == 0);
+        for (int s = Spad + lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
+    } else if (w < 4) {
+        for (int s = lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
+    }
+    lds_barrier();
+
+    // ---- P.V of block w: positions s0 .. e-1 --------------------------------------
+    // Past S (the last block's last batch) p is an exact zero and V a clamped
+    // finite row, so such a step adds +0 to a sum that started at +0 (never
+    // -0): the block sum is unchanged.
+    if (w < nb) {
+        const float *prow = pr + (lane & 3) * Sp;
+        v4f a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto run = [&](const uint32_t (&vv)[16], int s) {
+#pragma unroll
+            for (int u4 = 0; u4 < 16; u4 += 4) {
+                const float4 p = *(const float4 *)(prow + s + u4);
+                const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float2 v = __half22float2(*(const __half2 *)&vv[u4 + u]);
+                    a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.x, a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.y, a1, 0, 0, 0);
+                }
+            }
+        };
+        // batches rotate va -> vb -> vcur: the batch two ahead is in flight
+        // while one is summed (loads are clamped, never skipped)
+        for (int s = s0;; s += 48) {
+            load_v(vcur, s + 32);
+            run(va, s);
+            if (s + 16 >= e) break;
+            load_v(va, s + 48);
+            run(vb, s + 16);
+            if (s + 32 >= e) break;
+            load_v(vb, s + 64);
+            run(vcur, s + 32);
+            if (s + 48 >= e) break;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const v4f &a = h ? a1 : a0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sums[((size_t)w * 4 + r) * kHd + 2 * lane + h] = a[r];
+        }
+    }
+    lds_barrier();
+    for (int o = tid; o < G * kHd; o += kPvmThreads) {
+        const int r = o / kHd, d = o % kHd;
+        float tot = sums[r * kHd + d];
+        for (int b = 1; b < nb; ++b) tot = tot + sums[((size_t)b * 4 + r) * kHd + d];
+        out[(size_t)(hk * G + r) * kHd + d] = tot;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1607,6 +1731,24 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
     if (allow_dynamic_lds(eight ? (const void *)attn_pv_kernel<G, G == 1 ? 4 : 8>
                                 : (const void *)attn_pv_kernel<G, 4>))
         return -1;
+    // f32 MFMA P.V (the G heads as rows) for wide grids: its one workgroup per
+    // (KV head, sequence) is MFMA-bound at ~20 us for 2304 positions, the VALU
+    // kernels' chains grow with the batch (B = 1 / 4 / 8 / 32 at 2304
+    // positions, scores + P.V: VALU 13 / 20 / 32 / 57 us, MFMA 23 / 24 / 27 / 40 us).
+    // OXB_PV=valu|mfma forces either (same sums, same bits).
+    const char *pv = getenv("OXB_PV");
+    const bool force_valu = pv && !strcmp(pv, "valu"), force_mfma = pv && !strcmp(pv, "mfma");
+    if constexpr (G <= 4) {
+        if (max_seq <= kPvmMaxBlocks * kPvBlock && !force_valu &&
+            (force_mfma || (long)batch * Hkv >= 32)) {
+            if (allow_dynamic_lds((const void *)attn_pv_mfma_kernel<G>)) return -1;
+            hipLaunchKernelGGL((attn_pv_mfma_kernel<G>), dim3(Hkv, batch), dim3(kPvmThreads),
+                               pvm_smem(max_seq), s, scores, vc, pos, max_seq, out, kv_stride,
+                               pos_stride);
+            OXB_CHECK_HIP(hipGetLastError());
+            return 0;
+        }
+    }
     const dim3 grid(Hkv, kHd / pv_dims_per_wave(G), batch);
     if ((long)grid.x * grid.y * grid.z > device_cus()) {   // wide: one softmax per 16 G dims
         constexpr int DWB = pv_dims_per_wave(G) * (2 * G < 4 ? 2 * G : 4);

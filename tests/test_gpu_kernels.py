@@ -220,6 +220,15 @@ def test_attn_decode_bitexact(pos, H, Hkv, S):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+# the f32-MFMA P.V forced for one sequence (G = 4, 2, 1; 1 to 16 blocks)
+@pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (255, 20, 5, 512), (256, 20, 5, 512),
+                                         (2599, 20, 5, 2600), (4095, 20, 5, 4096),
+                                         (700, 16, 8, 1024), (300, 8, 8, 4096)])
+def test_attn_decode_mfma_pv_bitexact(pos, H, Hkv, S, monkeypatch):
+    monkeypatch.setenv("OXB_PV", "mfma")
+    test_attn_decode_bitexact(pos, H, Hkv, S)
+
+
 @pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (255, 20, 5, 512),
                                          (256, 20, 5, 512), (300, 20, 5, 408), (511, 20, 5, 512),
                                          (700, 8, 4, 1024), (1500, 20, 5, 4096),
@@ -300,11 +309,16 @@ def test_attn_decode_head_rejects_long_caches():
                         s_max=600)
 
 
+# pv: the P.V kernel the dispatch picks ("auto": f32 MFMA once batch x KV
+# heads >= 32, here B = 16, 40 and 9 x 8) or the one forced by OXB_PV
+@pytest.mark.parametrize("pv", ["auto", "valu", "mfma"])
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
-                                       (9, 8, 8, 512)])
-def test_attn_decode_batch_bitexact(B, H, Hkv, S):
-    """Batched decode attention (per-slot caches and positions; B = 16 and 40
-    take the wide P.V layout): every slot equals the oracle."""
+                                       (9, 8, 8, 512), (8, 16, 8, 2600)])
+def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
+    """Batched decode attention (per-slot caches and positions; the VALU P.V
+    takes the wide layout at B = 16 and 40): every slot equals the oracle."""
+    if pv != "auto":
+        monkeypatch.setenv("OXB_PV", pv)
     rng = np.random.default_rng(B * 13 + H)
     hd = 128
     q = rng.standard_normal((B, H * hd)).astype(np.float32)
