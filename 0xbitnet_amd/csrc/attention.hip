@@ -563,6 +563,68 @@ __host__ __device__ inline size_t pvm_smem(int max_seq) {
             (size_t)((max_seq + kPvBlock - 1) / kPvBlock) * 4 * kHd) * sizeof(float);
 }
 
+// V rows s .. s+15 of the lane's dword (dims 2l, 2l+1), clamped to the cache
+__device__ __forceinline__ void pv_load16(uint32_t (&vv)[16], const uint32_t *V2, int s, int S) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vv[u] = V2[(size_t)min(s + u, S - 1) * (kHd / 2)];
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// P.V of the 256-position block [s0, e) for the four rows at prow (the
+// lane's row lane % 4): two v_mfma_f32_4x4x1_16b chains (dims 2l and 2l+1),
+// in order of s from zero; va and vb hold the block's first two batches.
+// Past S (the last block's last batch) p is an exact zero and V a clamped
+// finite row, so such a step adds +0 to a sum that started at +0 (never -0):
+// the block sum is unchanged.
+__device__ __forceinline__ void pv_mfma_block(const float *prow, const uint32_t *V2, int s0, int e,
+                                              int S, uint32_t (&va)[16], uint32_t (&vb)[16],
+                                              v4f &a0, v4f &a1) {
+    a0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    a1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto run = [&](const uint32_t (&vv)[16], int s) {
+#pragma unroll
+        for (int u4 = 0; u4 < 16; u4 += 4) {
+            const float4 p = *(const float4 *)(prow + s + u4);
+            const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 v = __half22float2(*(const __half2 *)&vv[u4 + u]);
+                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.x, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.y, a1, 0, 0, 0);
+            }
+        }
+    };
+    // batches rotate va -> vb -> vc: the batch two ahead is in flight while
+    // one is summed (loads are clamped, never skipped)
+    uint32_t vc[16];
+    for (int s = s0;; s += 48) {
+        pv_load16(vc, V2, s + 32, S);
+        run(va, s);
+        if (s + 16 >= e) break;
+        pv_load16(va, V2, s + 48, S);
+        run(vb, s + 16);
+        if (s + 32 >= e) break;
+        pv_load16(vb, V2, s + 64, S);
+        run(vc, s + 32);
+        if (s + 48 >= e) break;
+    }
+}
+
+// Softmax of the G score rows (sh/softmax.wgsl:25-80) on waves 0 .. G-1,
+// rows G .. 3 zero-filled by waves G .. 3, into pr [4][Sp].
+template <int G>
+__device__ __forceinline__ void pv_mfma_softmax(float *pr, int Sp, const float *scores, int hk,
+                                                int max_seq, int S, int w, int lane) {
+    const int Spad = (S + 3) & ~3;
+    if (w < G) {
+        wave_softmax_row(pr + w * Sp, scores + (size_t)(hk * G + w) * max_seq, S, Spad, lane,
+                         (max_seq & 3) == 0);
+        for (int s = Spad + lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
+    } else if (w < 4) {
+        for (int s = lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
+    }
+}
+
 template <int G>
 __global__ __launch_bounds__(kPvmThreads) void attn_pv_mfma_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
@@ -584,69 +646,23 @@ __global__ __launch_bounds__(kPvmThreads) void attn_pv_mfma_kernel(
     const int hk = blockIdx.x;
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) return;
-    const int S = pos + 1, Spad = (S + 3) & ~3;
+    const int S = pos + 1;
     const int nb = (S + kPvBlock - 1) / kPvBlock;
     if (nb > kPvmMaxBlocks) return;   // host checks too
     const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + lane;   // dims 2l, 2l+1
-    const int s0 = w * kPvBlock, e = min(s0 + kPvBlock, S);
-
-    auto load_v = [&](uint32_t (&vv)[16], int s) {   // positions s .. s+15, clamped to the cache
-#pragma unroll
-        for (int u = 0; u < 16; ++u) vv[u] = V2[(size_t)min(s + u, S - 1) * (kHd / 2)];
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    uint32_t va[16], vb[16], vcur[16];
-    load_v(va, s0);   // the first two batches go out before the softmax
-    load_v(vb, s0 + 16);
-
-    // ---- softmax of the G score rows (sh/softmax.wgsl:25-80); rows >= G are zeros
-    if (w < G) {
-        wave_softmax_row(pr + w * Sp, scores + (size_t)(hk * G + w) * max_seq, S, Spad, lane,
-                         (max_seq & 3) == 0);
-        for (int s = Spad + lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
-    } else if (w < 4) {
-        for (int s = lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
-    }
+    const int s0 = w * kPvBlock;
+    uint32_t va[16], vb[16];
+    pv_load16(va, V2, s0, S);   // the first two batches go out before the softmax
+    pv_load16(vb, V2, s0 + 16, S);
+    pv_mfma_softmax<G>(pr, Sp, scores, hk, max_seq, S, w, lane);
     lds_barrier();
-
-    // ---- P.V of block w: positions s0 .. e-1 --------------------------------------
-    // Past S (the last block's last batch) p is an exact zero and V a clamped
-    // finite row, so such a step adds +0 to a sum that started at +0 (never
-    // -0): the block sum is unchanged.
-    if (w < nb) {
-        const float *prow = pr + (lane & 3) * Sp;
-        v4f a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto run = [&](const uint32_t (&vv)[16], int s) {
+    if (w < nb) {   // block w
+        v4f a0, a1;
+        pv_mfma_block(pr + (lane & 3) * Sp, V2, s0, min(s0 + kPvBlock, S), S, va, vb, a0, a1);
 #pragma unroll
-            for (int u4 = 0; u4 < 16; u4 += 4) {
-                const float4 p = *(const float4 *)(prow + s + u4);
-                const float pp[4] = {p.x, p.y, p.z, p.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float2 v = __half22float2(*(const __half2 *)&vv[u4 + u]);
-                    a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.x, a0, 0, 0, 0);
-                    a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.y, a1, 0, 0, 0);
-                }
-            }
-        };
-        // batches rotate va -> vb -> vcur: the batch two ahead is in flight
-        // while one is summed (loads are clamped, never skipped)
-        for (int s = s0;; s += 48) {
-            load_v(vcur, s + 32);
-            run(va, s);
-            if (s + 16 >= e) break;
-            load_v(va, s + 48);
-            run(vb, s + 16);
-            if (s + 32 >= e) break;
-            load_v(vb, s + 64);
-            run(vcur, s + 32);
-            if (s + 48 >= e) break;
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const v4f &a = h ? a1 : a0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sums[((size_t)w * 4 + r) * kHd + 2 * lane + h] = a[r];
+        for (int r = 0; r < 4; ++r) {
+            sums[((size_t)w * 4 + r) * kHd + 2 * lane] = a0[r];
+            sums[((size_t)w * 4 + r) * kHd + 2 * lane + 1] = a1[r];
         }
     }
     lds_barrier();
@@ -654,6 +670,71 @@ __global__ __launch_bounds__(kPvmThreads) void attn_pv_mfma_kernel(
         const int r = o / kHd, d = o % kHd;
         float tot = sums[r * kHd + d];
         for (int b = 1; b < nb; ++b) tot = tot + sums[((size_t)b * 4 + r) * kHd + d];
+        out[(size_t)(hk * G + r) * kHd + d] = tot;
+    }
+}
+
+// The same P.V over more workgroups (a workspace for the block sums): one
+// 4-wave workgroup per (KV head, kPvcBlocks blocks, sequence), each running
+// the G rows' softmax and summing its blocks (waves 0 .. kPvcBlocks-1);
+// attn_pv_combine_kernel then adds each output's block sums in block order.
+// ws: [batch][Hkv][ceil(max_seq / 256)][4][128] f32.
+constexpr int kPvcBlocks = 2;
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_pv_mfma_chunk_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ ws, size_t kv_stride,
+    int pos_stride) {
+    static_assert(G >= 1 && G <= 4, "four MFMA rows");
+    const int z = blockIdx.z, Hkv = gridDim.x, hk = blockIdx.x;
+    const int nbmax = (max_seq + kPvBlock - 1) / kPvBlock;
+    scores += (size_t)z * Hkv * G * max_seq;
+    vc += (size_t)z * kv_stride;
+    pos_ptr += (size_t)z * pos_stride;
+    ws += ((size_t)z * Hkv + hk) * nbmax * 4 * kHd;
+    extern __shared__ __align__(16) float smem[];
+    const int Sp = pvm_row_stride(max_seq);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) return;
+    const int S = pos + 1, nb = (S + kPvBlock - 1) / kPvBlock;
+    const int b = blockIdx.y * kPvcBlocks + w;   // this wave's block (waves < kPvcBlocks)
+    if (blockIdx.y * kPvcBlocks >= nb) return;  // the workgroup's blocks are past the cache
+    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + lane;
+    const int s0 = min(b, nb - 1) * kPvBlock;
+    uint32_t va[16], vb[16];
+    pv_load16(va, V2, s0, S);
+    pv_load16(vb, V2, s0 + 16, S);
+    pv_mfma_softmax<G>(smem, Sp, scores, hk, max_seq, S, w, lane);
+    lds_barrier();
+    if (w < kPvcBlocks && b < nb) {
+        v4f a0, a1;
+        pv_mfma_block(smem + (lane & 3) * Sp, V2, s0, min(s0 + kPvBlock, S), S, va, vb, a0, a1);
+#pragma unroll
+        for (int r = 0; r < G; ++r) {
+            *(float2 *)(ws + ((size_t)b * 4 + r) * kHd + 2 * lane) = make_float2(a0[r], a1[r]);
+        }
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(512) void attn_pv_combine_kernel(const float *__restrict__ ws,
+                                                              const int *__restrict__ pos_ptr,
+                                                              int max_seq, float *__restrict__ out,
+                                                              int pos_stride) {
+    const int z = blockIdx.y, Hkv = gridDim.x, hk = blockIdx.x;
+    const int nbmax = (max_seq + kPvBlock - 1) / kPvBlock;
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;
+    const int nb = (pos + kPvBlock) / kPvBlock;
+    ws += ((size_t)z * Hkv + hk) * nbmax * 4 * kHd;
+    out += (size_t)z * Hkv * G * kHd;
+    for (int o = threadIdx.x; o < G * kHd; o += 512) {
+        const int r = o / kHd, d = o % kHd;
+        float tot = ws[r * kHd + d];
+        for (int b = 1; b < nb; ++b) tot = tot + ws[((size_t)b * 4 + r) * kHd + d];
         out[(size_t)(hk * G + r) * kHd + d] = tot;
     }
 }
@@ -1715,7 +1796,8 @@ using namespace oxb;
 template <int G>
 static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                          int Hkv, int max_seq, float *scores, float *out, hipStream_t s,
-                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0) {
+                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0,
+                         float *pv_ws = nullptr) {
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipLaunchKernelGGL(attn_scores_kernel<G>,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
@@ -1736,11 +1818,28 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
     // kernels' chains grow with the batch (B = 1 / 4 / 8 / 32 at 2304
     // positions, scores + P.V: VALU 13 / 20 / 32 / 57 us, MFMA 23 / 24 / 27 / 40 us).
     // OXB_PV=valu|mfma forces either (same sums, same bits).
+    // With a workspace, the MFMA P.V spreads over kPvcBlocks-block workgroups
+    // while they fit the CUs once (OXB_PV=chunk forces it).
     const char *pv = getenv("OXB_PV");
     const bool force_valu = pv && !strcmp(pv, "valu"), force_mfma = pv && !strcmp(pv, "mfma");
+    const bool force_chunk = pv_ws && pv && !strcmp(pv, "chunk");
     if constexpr (G <= 4) {
+        const int nchunk = ((max_seq + kPvBlock - 1) / kPvBlock + kPvcBlocks - 1) / kPvcBlocks;
         if (max_seq <= kPvmMaxBlocks * kPvBlock && !force_valu &&
-            (force_mfma || (long)batch * Hkv >= 32)) {
+            (force_mfma || force_chunk || (long)batch * Hkv >= 32)) {
+            if (force_chunk ||
+                (pv_ws && !force_mfma && (long)batch * Hkv * nchunk <= device_cus())) {
+                const size_t csmem = (size_t)4 * pvm_row_stride(max_seq) * sizeof(float);
+                if (csmem > 64 * 1024 && allow_dynamic_lds((const void *)attn_pv_mfma_chunk_kernel<G>))
+                    return -1;
+                hipLaunchKernelGGL((attn_pv_mfma_chunk_kernel<G>), dim3(Hkv, nchunk, batch), dim3(256),
+                                   csmem, s, scores, vc, pos, max_seq, pv_ws, kv_stride, pos_stride);
+                OXB_CHECK_HIP(hipGetLastError());
+                hipLaunchKernelGGL((attn_pv_combine_kernel<G>), dim3(Hkv, batch), dim3(512), 0, s,
+                                   pv_ws, pos, max_seq, out, pos_stride);
+                OXB_CHECK_HIP(hipGetLastError());
+                return 0;
+            }
             if (allow_dynamic_lds((const void *)attn_pv_mfma_kernel<G>)) return -1;
             hipLaunchKernelGGL((attn_pv_mfma_kernel<G>), dim3(Hkv, batch), dim3(kPvmThreads),
                                pvm_smem(max_seq), s, scores, vc, pos, max_seq, out, kv_stride,
@@ -1784,6 +1883,37 @@ extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uin
         case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
+        default:
+            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
+            return -1;
+    }
+}
+
+extern "C" size_t oxb_attn_decode_batch_ws_bytes(int batch, int Hkv, int max_seq) {
+    if (batch < 1 || Hkv < 1 || max_seq < 1) return 0;
+    return (size_t)batch * Hkv * ((max_seq + kPvBlock - 1) / kPvBlock) * 4 * kHd * sizeof(float);
+}
+
+extern "C" int oxb_attn_decode_batch_ws(const float *q, const uint16_t *kcache,
+                                        const uint16_t *vcache, const int *pos, int pos_stride,
+                                        size_t kv_stride, int batch, int H, int Hkv, int hd,
+                                        int max_seq, float *scores, float *ws, float *out,
+                                        void *stream) {
+    OXB_REQUIRE(pos && scores && ws, "attention: pos, scores or ws is NULL");
+    OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
+    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
+                "attention: caches of a batch overlap (stride %zu)", kv_stride);
+    const int G = H / Hkv;
+    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
+                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
+    hipStream_t s = (hipStream_t)stream;
+    switch (G) {
+        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
+        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
+        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
+        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
         default:
             oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
             return -1;

@@ -156,6 +156,18 @@ int oxb_attn_decode_batch(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                           int Hkv, int hd, int max_seq, float *scores, float *out, void *stream);
 
+/* oxb_attn_decode_batch with a workspace of
+ * oxb_attn_decode_batch_ws_bytes(batch, Hkv, max_seq) bytes for the P.V block
+ * sums: wide grids (batch x Hkv >= 32) then spread each sequence's P.V over
+ * more workgroups (two 256-position blocks each) and add the block sums in a
+ * second kernel; same result bits.  Replaces nn/attention.rs:109-118 like
+ * oxb_attn_decode_batch; no counterpart of its own in the reference. */
+size_t oxb_attn_decode_batch_ws_bytes(int batch, int Hkv, int max_seq);
+int oxb_attn_decode_batch_ws(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                             const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
+                             int Hkv, int hd, int max_seq, float *scores, float *ws, float *out,
+                             void *stream);
+
 /* The same decode attention as one kernel: two 1024-thread workgroups per KV
  * head (one per half of the dims) compute scores, softmax and P.V in LDS (no
  * scores buffer), same result bits.  Faster for short caches (each KV head's

@@ -310,15 +310,18 @@ def test_attn_decode_head_rejects_long_caches():
 
 
 # pv: the P.V kernel the dispatch picks ("auto": f32 MFMA once batch x KV
-# heads >= 32, here B = 16, 40 and 9 x 8) or the one forced by OXB_PV
-@pytest.mark.parametrize("pv", ["auto", "valu", "mfma"])
+# heads >= 32, here B = 16, 40 and 9 x 8) or the one forced by OXB_PV; the
+# "ws" cases call oxb_attn_decode_batch_ws, whose MFMA P.V runs two blocks per
+# workgroup and adds the block sums in a second kernel while those workgroups
+# fit the CUs once (forced by OXB_PV=chunk)
+@pytest.mark.parametrize("pv", ["auto", "valu", "mfma", "ws", "ws_mfma", "ws_chunk"])
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
                                        (9, 8, 8, 512), (8, 16, 8, 2600)])
 def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
     """Batched decode attention (per-slot caches and positions; the VALU P.V
     takes the wide layout at B = 16 and 40): every slot equals the oracle."""
-    if pv != "auto":
-        monkeypatch.setenv("OXB_PV", pv)
+    if pv in ("valu", "mfma", "ws_mfma", "ws_chunk"):
+        monkeypatch.setenv("OXB_PV", pv.removeprefix("ws_"))
     rng = np.random.default_rng(B * 13 + H)
     hd = 128
     q = rng.standard_normal((B, H * hd)).astype(np.float32)
@@ -335,8 +338,16 @@ def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
     dst = ops.DeviceArray.from_host(st)
     sc = ops.DeviceArray((B * H * S,), np.float32)
     out = ops.DeviceArray((B, H * hd), np.float32)
-    ops.check(L.oxb_attn_decode_batch(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H, Hkv,
-                                      hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
+    if pv.startswith("ws"):
+        nws = L.oxb_attn_decode_batch_ws_bytes(B, Hkv, S)
+        assert nws == B * Hkv * ((S + 255) // 256) * 4 * hd * 4
+        ws = ops.DeviceArray((nws // 4,), np.float32)
+        ops.check(L.oxb_attn_decode_batch_ws(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B,
+                                             H, Hkv, hd, S, sc.ptr, ws.ptr, out.ptr, None),
+                  "attn_decode_batch_ws")
+    else:
+        ops.check(L.oxb_attn_decode_batch(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H,
+                                          Hkv, hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
     ops.sync()
     got = out.download()
     for z in range(B):
