@@ -423,6 +423,10 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
 // (each in the shaders' 256-thread order), so that its stores are 32-byte
 // runs of 2 tokens instead of one token's scattered 16-byte pieces (4 rows
 // per workgroup would need more than the 128 VGPRs of a 1024-thread wave).
+// The 8 workgroups of a 16-token tile are blockIdx values congruent mod 8,
+// which the dispatcher places on one XCD, so each 128-byte line of the tile
+// is completed in one L2: workgroup b runs row pair (b / 8) % 8 of tile
+// (b / 64) * 8 + b % 8 (grid: 64 per 8 tiles; those past the last tile exit).
 // ---------------------------------------------------------------------------
 constexpr int kTiledRows = 2;
 
@@ -436,7 +440,9 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     int8_t *q_lds = smem + grp * dpad;
     float *red = (float *)(smem + kTiledRows * dpad) + grp * 328;
     int *wq = (int *)(red + 324);
-    const int row = blockIdx.x * kTiledRows + grp;
+    const int b = blockIdx.x, tile = (b >> 6) * 8 + (b & 7), r0 = ((b >> 3) & 7) * kTiledRows;
+    if (tile * 16 >= n_tok) return;   // whole workgroup: past the last 16-token tile
+    const int row = tile * 16 + r0 + grp;
     float scale = 1.0f;
     if (row < n_tok) {
         float v[NREG], g[NREG];
@@ -451,7 +457,7 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
         if (tl < 4) wq[tl] = 0;
     }
     lds_barrier();
-    const int KC = D >> 6, tile = row >> 4, r0 = (blockIdx.x * kTiledRows) & 15;
+    const int KC = D >> 6;
     // unit i: row group i % 2, plane (i / 2) % 4, chunk i / 8
     for (int i = threadIdx.x; i < KC * 4 * kTiledRows; i += 256 * kTiledRows) {
         const int rr = i % kTiledRows, gp = (i / kTiledRows) & 3, kc = i / (4 * kTiledRows);
@@ -636,12 +642,12 @@ extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float
     OXB_REQUIRE(D > 0 && D % 256 == 0 && D <= 256 * kMaxNormReg,
                 "quantize_rows_tiled: D %d must be a multiple of 256 and <= %d", D, 256 * kMaxNormReg);
     OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
-    const int rows = (n_tok + 15) & ~15;
+    const int grid = (n_tok + 127) / 128 * 64;   // 8 tiles of 16 tokens per 64 workgroups
     const size_t sm = (size_t)kTiledRows * (((D + 15) & ~15) + 328 * 4);
     // loads per thread: the row length's bucket (the model's 2560 and 6912 exactly)
     const int nr = D / 256;
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(rows / kTiledRows), dim3(256 * kTiledRows), sm, stream, x,
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * kTiledRows), sm, stream, x,
                            gamma, eps, D, n_tok, (uint4 *)Xt, scales, sums);
     };
     if (nr <= 4) go(quantize_rows_tiled_kernel<4>);
