@@ -1078,17 +1078,19 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
         if (b < nb) {
             const float4 *vt = Vt + (size_t)hk * ntile_ws * kTileF4 + lane + 64 * h;
             const int s0 = b * kPvBlock, e = min(s0 + kPvBlock, Smax);
-            // 16 positions per batch; the next batch's V (global) and p (LDS)
-            // are read before this batch's MFMAs (a batch past the block reads
-            // the last batch and is never used)
-            auto load = [&](float4 (&vv)[4], float4 (&pp)[4], int s) {
+            // 16 positions per batch: V (global) two batches ahead, p (LDS)
+            // just before its batch's MFMAs (a batch past the block reads the
+            // last batch and is never used)
+            auto loadv = [&](float4 (&vv)[4], int s) {
                 const int sb = min(s, s_last);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
-                    pp[j] = *(const float4 *)(prow + sb + 4 * j);
-                }
+                for (int j = 0; j < 4; ++j) vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
                 __builtin_amdgcn_sched_barrier(0);
+            };
+            auto loadp = [&](float4 (&pp)[4], int s) {
+                const int sb = min(s, s_last);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pp[j] = *(const float4 *)(prow + sb + 4 * j);
             };
             auto run = [&](const float4 (&vv)[4], const float4 (&pp)[4]) {
 #pragma unroll
@@ -1099,15 +1101,22 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
                     a = mfma_f32_k1(pp[j].w, vv[j].w, a);
                 }
             };
-            float4 va[4], vb[4], pa[4], pb[4];
-            load(va, pa, s0);
-            for (int s = s0;; s += 32) {
-                load(vb, pb, s + 16);
-                run(va, pa);
+            float4 va[4], vb[4], vc[4], pp[4];
+            loadv(va, s0);
+            loadv(vb, s0 + 16);
+            for (int s = s0;; s += 48) {
+                loadv(vc, s + 32);
+                loadp(pp, s);
+                run(va, pp);
                 if (s + 16 >= e) break;
-                load(va, pa, s + 32);
-                run(vb, pb);
+                loadv(va, s + 48);
+                loadp(pp, s + 16);
+                run(vb, pp);
                 if (s + 32 >= e) break;
+                loadv(vb, s + 64);
+                loadp(pp, s + 32);
+                run(vc, pp);
+                if (s + 48 >= e) break;
             }
         }
         part[k] = a;
