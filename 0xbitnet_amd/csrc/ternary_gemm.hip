@@ -705,10 +705,13 @@ static int gemm_launch(const GemmParams &p, void *stream) {
         }
     }
     // LDS-staged tiles: the largest of 128x128, 128x64, 64x128, 64x64 whose
-    // grid still gives every CU a workgroup (N a multiple of the tile).
+    // grid still gives every CU a workgroup (N a multiple of the tile); the
+    // 256x128 DMA-staged tile already from 5/8 of the CUs (N = 2560 at 2048
+    // tokens, 160 workgroups: K = 6912 / 2560 take 56.3 / 29.2 us against
+    // 64.4 / 33.6 us for 320 workgroups of 128x128).
     const int cus = device_cus();
     auto blocks = [&](int ft, int tk) { return (long)(p.N / ft) * ((p.n_tok + tk - 1) / tk); };
-    if (p.N % 256 == 0 && blocks(256, 128) >= cus * 3 / 4) return dma_launch<EPI, 2, 2, 4, 3>(p, s);
+    if (p.N % 256 == 0 && blocks(256, 128) >= cus * 5 / 8) return dma_launch<EPI, 2, 2, 4, 3>(p, s);
     if (p.N % 128 == 0 && blocks(128, 128) >= cus) return lds_launch<EPI, 2, 2>(p, s);
     if (p.N % 128 == 0 && blocks(128, 64) >= cus) return lds_launch<EPI, 2, 1>(p, s);
     if (p.N % 64 == 0 && blocks(64, 128) >= cus) return lds_launch<EPI, 1, 2>(p, s);

@@ -411,8 +411,10 @@ def test_attn_prefill_causal_bitexact(H, Hkv, S, pos0, n):
                                    (16384, 512, 8), (28672, 256, 20), (8192, 1024, 16),
                                    (16384, 512, 40), (28672, 256, 64),
                                    # few tiles for the CUs: one ragged token tile over 27
-                                   # K stages; 30 and 40 256x128 tiles' worth
-                                   (2560, 6912, 65), (2560, 2560, 300), (5120, 4096, 200)])
+                                   # K stages; 30 and 40 256x128 tiles' worth; 160 of them
+                                   # (5/8 of the CUs) with a ragged last token tile
+                                   (2560, 6912, 65), (2560, 2560, 300), (5120, 4096, 200),
+                                   (2560, 2560, 2000)])
 def test_gemm_mfma_bitexact(N, K, n):
     rng = np.random.default_rng(N + n)
     w = ternary(rng, N, K)
