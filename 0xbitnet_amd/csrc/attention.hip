@@ -1993,6 +1993,11 @@ extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const ui
                                 int n_tok, int pos0, int H, int Hkv, int hd, int max_seq,
                                 float *out, void *stream) {
     OXB_REQUIRE(n_tok > 0 && pos0 >= 0 && pos0 + n_tok <= max_seq, "prefill attention: bad range");
+    // the arguments are checked before the workspace is allocated
+    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
+    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
+    OXB_REQUIRE(H / Hkv == 1 || H / Hkv == 2 || H / Hkv == 4 || H / Hkv == 8,
+                "attention: GQA group %d unsupported (1, 2, 4, 8)", H / Hkv);
     hipStream_t s = (hipStream_t)stream;
     const size_t need = attn_prefill_ws_bytes(Hkv, pos0 + n_tok);
     void *ws = nullptr;

@@ -69,6 +69,35 @@ def test_load_argument_errors():
     assert _err() == "model must not be NULL"
 
 
+def test_operator_entry_points_check_arguments_first():
+    """Host-side argument checks of the operator entry points return -1 with
+    their message before any device call (so this runs without a GPU)."""
+    L = nat.lib()
+    p = C.c_void_p(64)   # never dereferenced: every call below fails its checks first
+    assert L.oxb_attn_decode_batch_ws_bytes(0, 5, 100) == 0
+    assert L.oxb_attn_decode_batch_ws_bytes(2, 5, 300) == 2 * 5 * 2 * 4 * 128 * 4
+    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 5, 128, 300, p, None, p, None) == -1
+    assert _err() == "attention: pos, scores or ws is NULL"
+    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 5, 64, 300, p, p, p, None) == -1
+    assert _err() == "attention: head_dim 64 unsupported (128 only)"
+    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 6, 128, 300, p, p, p, None) == -1
+    assert _err() == "attention: heads 20 not a multiple of kv heads 6"
+    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 100, 2, 20, 5, 128, 300, p, p, p, None) == -1
+    assert _err().startswith("attention: caches of a batch overlap")
+    assert L.oxb_attn_prefill(p, p, p, 10, 95, 20, 5, 128, 100, p, None) == -1
+    assert _err() == "prefill attention: bad range"
+    assert L.oxb_attn_prefill(p, p, p, 10, 0, 20, 5, 64, 100, p, None) == -1
+    assert _err() == "attention: head_dim 64 unsupported (128 only)"
+    assert L.oxb_attn_prefill(p, p, p, 10, 0, 24, 8, 128, 100, p, None) == -1
+    assert _err() == "attention: GQA group 3 unsupported (1, 2, 4, 8)"
+    assert L.oxb_gemm_i8(p, p, p, p, p, 100, 256, 4, p, None, 0, None) == -1
+    assert _err() == "ternary GEMM: out_dim 100 must be a multiple of 32"
+    assert L.oxb_gemm_i8(p, p, p, p, p, 64, 300, 4, p, None, 0, None) == -1
+    assert _err() == "ternary GEMM: in_dim 300 must be a multiple of 256"
+    assert L.oxb_quantize_rows_tiled(p, p, 1e-5, 4, 100, p, p, p, None) == -1
+    assert _err().startswith("quantize_rows_tiled: D 100 must be a multiple of 256")
+
+
 def _write(tmp_path, name, data: bytes):
     p = tmp_path / name
     p.write_bytes(data)
