@@ -1708,6 +1708,138 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same design for caches of up to 512 positions: 512 threads (thread t
+// scores position t), K staged as [512][17] uint4; the V rows are loaded with
+// K and written over the K rows once every score chain is done (one more
+// barrier).  Softmax in the shader's 256-thread order: thread t < 256 forms
+// its strided partial (0 + e_t) + e_(t+256), then the same halving tree in
+// every wave.  P.V: waves 0 / 1 sum block 0 (positions 0..255, even / odd
+// dims) and waves 2 / 3 block 1 (256..511) with the head256 chains; block
+// sums added in block order.  Same arithmetic as the other forms.
+// ---------------------------------------------------------------------------
+constexpr int kH512Rows = 512;
+constexpr size_t kH512KBytes = (size_t)kH512Rows * 17 * 16;   // K rows, padded; then V rows
+constexpr size_t kH512Lds = kH512KBytes + (kHd + 512 + 512 + 256 + 128 + 8) * 4;
+static_assert((size_t)kH512Rows * kHd * 2 <= kH512KBytes, "V rows fit the K region");
+
+__global__ __launch_bounds__(512) void attn_head512_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
+    size_t kv_stride, int pos_stride) {
+    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(max_seq), "s"(scale),
+                 "s"(out), "s"(kv_stride), "s"(pos_stride));
+    extern __shared__ __align__(16) int8_t smem_h[];
+    u32x4_t (*ks)[17] = (u32x4_t (*)[17])smem_h;
+    u32x4_t *vs4 = (u32x4_t *)smem_h;                                // V [512][64] dwords (after K)
+    const uint32_t *vs = (const uint32_t *)vs4;
+    float *qs = (float *)(smem_h + kH512KBytes);                     // q [128]
+    float *pr = qs + kHd;                                            // probabilities [512]
+    float *ev = pr + 512;                                            // e [512]
+    float *red = ev + 512;                                           // partial sums [256]
+    float *bsum = red + 256;                                         // block 1 sums [128]
+    float *wmax = bsum + 128;                                        // [8]
+    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int hk = h / G;
+    const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
+    kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    const float4 q4 = ((const float4 *)qh)[tid & 31];
+    __builtin_amdgcn_sched_barrier(0);
+    const bool valid = pos >= 0 && pos < kH512Rows && pos < max_seq;
+    const int S = valid ? pos + 1 : 1;
+    u32x4_t kt[16], vt[16];
+    const u32x4_t *__restrict__ K4 = (const u32x4_t *)kc;
+    const u32x4_t *__restrict__ V4 = (const u32x4_t *)vc;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) kt[k] = K4[min(32 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vt[k] = V4[min(32 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ks[32 * k + (tid >> 4)][tid & 15] = kt[k];
+    *(float4 *)(qs + 4 * (tid & 31)) = q4;
+    lds_barrier();
+
+    // ---- score of position tid: 128 terms in order of d -----------------
+    float x;
+    {
+        constexpr int kAhead = 3;
+        u32x4_t kr[16];
+        float4 qa[16], qb[16];
+        auto ld = [&](int i) {
+            kr[i] = ks[tid][i];
+            qa[i] = *(const float4 *)(qs + 8 * i);
+            qb[i] = *(const float4 *)(qs + 8 * i + 4);
+        };
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) ld(i);
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (i + kAhead < 16) ld(i + kAhead);
+            __builtin_amdgcn_sched_barrier(0);
+            const float qv[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w,
+                                 qb[i].x, qb[i].y, qb[i].z, qb[i].w};
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const uint32_t kw = kr[i][k2];
+                const float k0 = __half2float(__ushort_as_half((uint16_t)(kw & 0xffffu)));
+                const float k1 = __half2float(__ushort_as_half((uint16_t)(kw >> 16)));
+                dot = __builtin_fmaf(qv[2 * k2], k0, dot);
+                dot = __builtin_fmaf(qv[2 * k2 + 1], k1, dot);
+            }
+        }
+        x = dot * scale;
+    }
+
+    // ---- softmax (sh/softmax.wgsl:25-80) --------------------------------------
+    float m = tid < S ? x : -3.402823e+38f;
+    m = wave_max_dpp(m);
+    if (lane == 0) wmax[w] = m;
+    lds_barrier();   // every score chain is done: the K rows are free
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vs4[tid + 512 * k] = vt[k];
+    m = fmaxf(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])),
+              fmaxf(fmaxf(wmax[4], wmax[5]), fmaxf(wmax[6], wmax[7])));
+    const float e = tid < S ? oxb_expf(x - m) : 0.0f;
+    ev[tid] = e;
+    lds_barrier();
+    if (tid < 256) red[tid] = (0.0f + ev[tid]) + ev[tid + 256];   // thread t's strided partial
+    lds_barrier();
+    float inv;
+    {   // the halving tree, in every wave (identical values)
+        const float a = red[lane & 63] + red[(lane & 63) + 128];
+        const float c = red[(lane & 63) + 64] + red[(lane & 63) + 192];
+        inv = 1.0f / wave_tree_sum(a + c);
+    }
+    pr[tid] = e * inv;   // 0 past S
+    lds_barrier();
+
+    // ---- P.V (sh/attention.wgsl:96-104): blocks of 256 positions -----------
+    if (w < 4) {
+        const int blk = w >> 1, Sb = min(S - kH256Rows * blk, kH256Rows);
+        float acc = 0.0f;
+        if (Sb > 0) {
+            const uint32_t *vcol = vs + (size_t)blk * kH256Rows * (kHd / 2) + lane;
+            acc = (w & 1) ? pv_head256<true>(vcol, pr + kH256Rows * blk, Sb)
+                          : pv_head256<false>(vcol, pr + kH256Rows * blk, Sb);
+        }
+        if (blk == 1) bsum[2 * lane + (w & 1)] = acc;
+        else red[2 * lane + (w & 1)] = acc;   // red is free after the tree
+    }
+    lds_barrier();
+    if (tid < kHd) {
+        float acc = red[tid];
+        if (S > kH256Rows) acc = acc + bsum[tid];   // block sums in block order
+        if (valid) out[((size_t)z * H + h) * kHd + tid] = acc;
+    }
+}
+
 // LDS of the prefill kernel for R score rows of up to s_max positions
 __host__ __device__ inline size_t prefill_smem(int R, int s_max) {
     return (size_t)R * (kHd + ((s_max + 3) & ~3)) * sizeof(float);
@@ -2032,9 +2164,11 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
     } else if (s_max <= 256)
         hipLaunchKernelGGL(attn_head_kernel<1>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
                            pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
-    else
-        hipLaunchKernelGGL(attn_head_kernel<2>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
-                           pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    else {
+        if (allow_dynamic_lds((const void *)attn_head512_kernel)) return -1;
+        hipLaunchKernelGGL(attn_head512_kernel, dim3(H, batch), dim3(512), kH512Lds, s, q, kcache,
+                           vcache, pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    }
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }

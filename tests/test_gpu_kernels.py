@@ -259,7 +259,8 @@ def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     (255, 20, 5, 256, 256),
     # two groups (the second P.V block on waves 2-3): 257 .. 512 positions
     (256, 20, 5, 512, 512), (300, 20, 5, 512, 512), (383, 20, 5, 384, 512),
-    (511, 20, 5, 512, 512), (10, 20, 5, 512, 512),
+    (511, 20, 5, 512, 512), (10, 20, 5, 512, 512), (400, 16, 2, 512, 512),
+    (290, 8, 8, 300, 512),
     # other GQA groups; short caches (K rows clamped to the cache extent)
     (200, 8, 8, 512, 256), (100, 16, 2, 256, 256), (40, 32, 4, 64, 256), (63, 20, 5, 64, 256),
     (20, 4, 1, 21, 256)])
