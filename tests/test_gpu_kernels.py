@@ -317,7 +317,7 @@ def test_attn_decode_head_rejects_long_caches():
 # fit the CUs once (forced by OXB_PV=chunk)
 @pytest.mark.parametrize("pv", ["auto", "valu", "mfma", "ws", "ws_mfma", "ws_chunk"])
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
-                                       (9, 8, 8, 512), (8, 16, 8, 2600)])
+                                       (9, 8, 8, 512), (8, 16, 8, 2600), (7, 20, 5, 1001)])
 def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
     """Batched decode attention (per-slot caches and positions; the VALU P.V
     takes the wide layout at B = 16 and 40): every slot equals the oracle."""
