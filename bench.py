@@ -585,7 +585,7 @@ def main() -> int:
     log(f"decode {args.steps} steps: {dt * 1e3:.1f} ms -> {tps:.1f} tok/s; prefill "
         f"{args.prompt} tok {prefill_s * 1e3:.1f} ms; first tokens {toks[:8].tolist()}")
 
-    # roofline of the ternary GEMV (the north-star shape) and the sweep
+    # roofline of the ternary GEMV (8192 x 28672, M = 1) and the sweep
     roof = gemv_roofline(ops, synth, 8192, 28672, copies=16, iters=400)
     log(f"gemv 8192x28672: {roof['us']} us, {roof['GBps']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     sweep = []
