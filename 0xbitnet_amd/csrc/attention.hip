@@ -1519,9 +1519,10 @@ __global__ __launch_bounds__(256) void attn_head_kernel(
 
 // ---------------------------------------------------------------------------
 // Decode, one workgroup per query head, caches of up to 256 positions:
-//  - the position first, then every K and V load before the first is
-//    waited for: rows below S (thread i: uint4 i + 256 k of each, coalesced,
-//    rows clamped to S - 1, so the loads are branch-free), and the q row;
+//  - the q row and the position, then every K and V load before the first
+//    is waited for: the 256 rows (thread i: uint4 i + 256 k of each,
+//    coalesced, clamped to the cache, so the loads are branch-free and do not
+//    wait for the position; rows at or past S are never used);
 //  - K staged in LDS as [256][17] uint4 (padded rows), q as [128] f32; the
 //    V loads are still landing while thread t runs the 128-step score chain
 //    of position t, q read as LDS broadcasts three 8-term groups ahead (no
@@ -1627,16 +1628,19 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     // flight); every thread loads, so no load sits under a branch
     const float4 q4 = ((const float4 *)qh)[tid & 31];
     __builtin_amdgcn_sched_barrier(0);
-    const bool valid = pos >= 0 && pos < kH256Rows && pos < max_seq;
-    const int S = valid ? pos + 1 : 1;
     u32x4_t kt[16], vt[16];
     const u32x4_t *__restrict__ K4 = (const u32x4_t *)kc;
     const u32x4_t *__restrict__ V4 = (const u32x4_t *)vc;
+    // rows clamped to the cache, not to S, so these loads do not wait for the
+    // position: rows at or past S are never used (their scores are masked,
+    // and the P.V chains stop at S)
 #pragma unroll
-    for (int k = 0; k < 16; ++k) kt[k] = K4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+    for (int k = 0; k < 16; ++k) kt[k] = K4[min(16 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vt[k] = V4[min(16 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+    for (int k = 0; k < 16; ++k) vt[k] = V4[min(16 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
     __builtin_amdgcn_sched_barrier(0);
+    const bool valid = pos >= 0 && pos < kH256Rows && pos < max_seq;
+    const int S = valid ? pos + 1 : 1;
 #pragma unroll
     for (int k = 0; k < 16; ++k) ks[16 * k + (tid >> 4)][tid & 15] = kt[k];
     // every thread stores (8 store the same float4 to each slot): a store
@@ -1749,16 +1753,18 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     const int pos = pos_ptr[(size_t)z * pos_stride];
     const float4 q4 = ((const float4 *)qh)[tid & 31];
     __builtin_amdgcn_sched_barrier(0);
-    const bool valid = pos >= 0 && pos < kH512Rows && pos < max_seq;
-    const int S = valid ? pos + 1 : 1;
     u32x4_t kt[16], vt[16];
     const u32x4_t *__restrict__ K4 = (const u32x4_t *)kc;
     const u32x4_t *__restrict__ V4 = (const u32x4_t *)vc;
+    // rows clamped to the cache, not to S: no wait for the position (rows at
+    // or past S are never used)
 #pragma unroll
-    for (int k = 0; k < 16; ++k) kt[k] = K4[min(32 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+    for (int k = 0; k < 16; ++k) kt[k] = K4[min(32 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vt[k] = V4[min(32 * k + (tid >> 4), S - 1) * 16 + (tid & 15)];
+    for (int k = 0; k < 16; ++k) vt[k] = V4[min(32 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
     __builtin_amdgcn_sched_barrier(0);
+    const bool valid = pos >= 0 && pos < kH512Rows && pos < max_seq;
+    const int S = valid ? pos + 1 : 1;
 #pragma unroll
     for (int k = 0; k < 16; ++k) ks[32 * k + (tid >> 4)][tid & 15] = kt[k];
     *(float4 *)(qs + 4 * (tid & 31)) = q4;
