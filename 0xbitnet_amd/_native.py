@@ -126,9 +126,6 @@ SIGNATURES = {
     "oxb_model_step": (C.c_int, [vp, vp]),
     "oxb_attn_decode_batch": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                         vp, vp, vp]),
-    "oxb_attn_decode_batch_ws_bytes": (C.c_size_t, [i32, i32, i32]),
-    "oxb_attn_decode_batch_ws": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32,
-                                           i32, vp, vp, vp, vp]),
     "oxb_lm_head_argmax_batch": (C.c_int, [vp, C.c_size_t, vp, f32, vp, i32, i32, vp, vp, i32,
                                            vp, i32, i32, i32, vp]),
     "oxb_batch_create": (vp, [vp, i32, i32]),

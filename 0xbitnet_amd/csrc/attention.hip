@@ -129,10 +129,6 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     }
 }
 
-// P.V association (the oracle's OXO_PV_BLOCK): positions are summed in blocks
-// of kPvBlock in order of s, and the block sums are added in block order.
-constexpr int kPvBlock = 256;  // LDS floats of the staged V slice (32 KiB, plus row padding)
-
 // The shaders' 256-thread halving tree s[t] += s[t + stride], stride
 // 128 .. 1, with s[4l + i] in component i of lane l: strides 128 .. 4 pair
 // lanes 32 .. 1 apart (shuffles, then DPP row_shl), strides 2 and 1 pair
@@ -254,14 +250,6 @@ __device__ __forceinline__ void wave_softmax_row(float *row, const float *__rest
     for (int s = S + lane; s < Spad; s += 64) row[s] = 0.0f;
 }
 
-// P.V split of the two-kernel path: a wave covers the G heads x 64/G dims of
-// its workgroup (one output per lane); the workgroup's NWV waves take the
-// kPvBlock-position blocks in turn, so a long cache is summed as
-// ceil(blocks / NWV) chains of kPvBlock steps instead of one chain of S.
-__host__ __device__ constexpr int pv_dims_per_wave(int G) { return 64 / G; }
-constexpr int kPvStage = 2048;   // f32 of V a wave stages at a time (8 KiB)
-constexpr int kWideVFloats = 8192;   // f32 of V the wide kernel stages per chunk (32 KiB)
-
 // acc + sum_{s < n} p[s] * v[s ^ sw], one fused multiply-add at a time in
 // order of s.  The LDS operands of the next 16 positions are read while the
 // current 16 are summed (p and v 16-byte aligned).  sw is a multiple of 4
@@ -317,425 +305,216 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
     return acc;
 }
 
-// Decode P.V: workgroup (KV head hk, dims d0 .. d0 + 64/G - 1, sequence z),
-// NWV waves.  Waves g < G run head g's softmax into LDS.  Then wave w sums
-// the P.V blocks w, w + NWV, ... (lane: head lane / DWW, dim d0 + lane %
-// DWW), staging each block's V slice in sub-chunks of kSub positions into its
-// own LDS region (f32, [dim][position]); the block sums go to LDS and wave 0
-// adds them in block order (sh/attention.wgsl:96-101, blocked as the oracle).
-// A wave's V sub-chunks are loaded two ahead in alternating register sets,
-// the first two before the softmax.  Rows past the cache length are clamped
-// to its last row (staged, never summed), so loads stay branch-free.
-template <int G, int NWV>
-__global__ __launch_bounds__(64 * NWV) void attn_pv_kernel(
-    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
-    int pos_stride) {
-    {   // sequence blockIdx.z of a batch
-        const int z = blockIdx.z, H = gridDim.x * G;
-        scores += (size_t)z * H * max_seq;
-        vc += (size_t)z * kv_stride;
-        pos_ptr += (size_t)z * pos_stride;
-        out += (size_t)z * H * kHd;
-    }
-    constexpr int DWW = pv_dims_per_wave(G);   // dims of the workgroup
-    constexpr int PPP = DWW / 8;               // uint4 (8 f16) per position of the slice
-    constexpr int kSub = kPvStage / DWW;       // positions per staged sub-chunk
-    constexpr int SPB = kPvBlock / kSub;       // sub-chunks per block
-    constexpr int kVS = kSub + 4;              // padded row
-    constexpr int kLd = kSub * PPP / 64;       // uint4 per lane per sub-chunk
-    static_assert(PPP >= 1 && kLd * 64 == kSub * PPP && SPB * kSub == kPvBlock, "P.V staging shape");
-    extern __shared__ __align__(16) float pr[];   // [G][Sp] probabilities | [blocks][64] block sums
-    __shared__ __align__(16) float vt[NWV][DWW * kVS];
-    const int pos = *pos_ptr;
-    if (pos < 0 || pos >= max_seq) return;
-    const int S = pos + 1;
-    const int Spad = (S + 3) & ~3;
-    const int Sp = ((Spad >> 2) | 1) << 2;      // Sp / 4 odd: head rows start in different banks
-    const int nb = (S + kPvBlock - 1) / kPvBlock;
-    const int hk = blockIdx.x, d0 = blockIdx.y * DWW;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
-    float *bsum = pr + G * Sp;
-    float *vtw = vt[w];
-
-    // sub-chunk j of this wave: block w + NWV * (j / SPB), part j % SPB
-    auto sub_start = [&](int j) { return (w + NWV * (j / SPB)) * kPvBlock + (j % SPB) * kSub; };
-    auto load_sub = [&](uint4 (&r)[kLd], int st) {
-#pragma unroll
-        for (int k = 0; k < kLd; ++k) {
-            const int i = lane + 64 * k, sl = i / PPP, h = i % PPP;
-            r[k] = *(const uint4 *)(Vh + (size_t)min(st + sl, S - 1) * kHd + 8 * h);
-        }
-    };
-    auto stage_sub = [&](const uint4 (&r)[kLd]) {
-#pragma unroll
-        for (int k = 0; k < kLd; ++k) {
-            const int i = lane + 64 * k, sl = i / PPP, h = i % PPP;
-            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 f = __half22float2(*(const __half2 *)&wv[e]);
-                vtw[(8 * h + 2 * e) * kVS + sl] = f.x;
-                vtw[(8 * h + 2 * e + 1) * kVS + sl] = f.y;
-            }
-        }
-    };
-    // loads are unconditional (a start past the cache reads its last row), so
-    // the waits before each staging count exactly the loads issued after it
-    uint4 ra[kLd], rb[kLd];
-    load_sub(ra, sub_start(0));
-    load_sub(rb, sub_start(1));
-
-    for (int g = w; g < G; g += NWV)
-        wave_softmax_row(pr + g * Sp, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
-                         (max_seq & 3) == 0);
-    lds_barrier();
-
-    const int g = lane / DWW, dd = lane % DWW;
-    const float *prg = pr + g * Sp;
-    const float *vrow = vtw + dd * kVS;
-    float part = 0.0f;
-    // one sub-chunk: stage it (the wave's own region; LDS runs a wave's
-    // accesses in order, so the chain below reads what was just written and
-    // the next staging follows this chain's reads), refill its register set
-    // two sub-chunks ahead, sum it into the block's partial
-    auto step = [&](uint4 (&r)[kLd], int j) {
-        const int st = sub_start(j);
-        stage_sub(r);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        load_sub(r, sub_start(j + 2));
-        part = pv_chain(prg + st, vrow, min(kSub, S - st), part);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if ((j + 1) % SPB == 0 || st + kSub >= S) {   // block done
-            bsum[(w + NWV * (j / SPB)) * 64 + lane] = part;
-            part = 0.0f;
-        }
-    };
-    for (int j = 0; sub_start(j) < S; j += 2) {
-        step(ra, j);
-        if (sub_start(j + 1) >= S) break;
-        step(rb, j + 1);
-    }
-    lds_barrier();
-    if (w == 0) {
-        float tot = bsum[lane];
-        for (int b = 1; b < nb; ++b) tot = tot + bsum[b * 64 + lane];
-        out[(size_t)(hk * G + g) * kHd + d0 + dd] = tot;
-    }
-}
-
-// Decode P.V for grids wider than the chip (large batches): workgroup (KV
-// head, 16 G dims, sequence), 4 waves, min(4, 2G) of them summing (one chain
-// per lane over the whole cache, blocked as above), the V slice staged for
-// the workgroup in chunks; one softmax per 16 G dims instead of per 64 / G.
-template <int G>
-__global__ __launch_bounds__(256) void attn_pv_wide_kernel(
-    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
-    int pos_stride) {
-    {   // sequence blockIdx.z of a batch
-        const int z = blockIdx.z, H = gridDim.x * G;
-        scores += (size_t)z * H * max_seq;
-        vc += (size_t)z * kv_stride;
-        pos_ptr += (size_t)z * pos_stride;
-        out += (size_t)z * H * kHd;
-    }
-    constexpr int DWW = pv_dims_per_wave(G);     // a wave: G heads x DWW dims, one per lane
-    constexpr int WPB = 2 * G < 4 ? 2 * G : 4;   // summing waves per workgroup
-    constexpr int DWB = DWW * WPB;               // dims per workgroup
-    constexpr int PPP = DWB / 8;                 // uint4 (8 f16) per position of the slice
-    constexpr int kVChunk = kWideVFloats / DWB;  // positions staged per pass
-    constexpr int kVS = kVChunk + 4;             // padded row: the rows start in different banks
-    // Staging: a wave writes 64 / PPP positions x PPP uint4 of 8 dims; the
-    // dims 8h + e of one e share a bank for every h (8 kVS = 0 mod 32 banks),
-    // so position s of dim row d is stored at s ^ swz(d / 8): 2 lanes/bank.
-    auto swz = [](int h) { return PPP >= 8 ? 4 * (h & 7) : PPP == 4 ? 16 * (h & 3) : 0; };
-    static_assert(PPP != 4 || kVChunk >= 64, "swizzle stays inside the chunk");
-    constexpr int kLoads = kWideVFloats / 8 / 256;   // uint4 per thread per chunk
-    extern __shared__ __align__(16) float pr[];   // [G][Sp] scores, then probabilities
-    __shared__ __align__(16) float vt[DWB * kVS];  // V slice, [d][s] f32
-    const int pos = *pos_ptr;
-    if (pos < 0 || pos >= max_seq) return;
-    const int S = pos + 1;
-    const int Spad = (S + 3) & ~3;
-    const int hk = blockIdx.x, d0 = blockIdx.y * DWB;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint16_t *Vh = vc + (size_t)hk * max_seq * kHd + d0;
-
-    // V slices of the first two chunks, issued before anything else.  Rows
-    // past the cache length are clamped to its last row (staged, never read),
-    // so the loads stay branch-free and the waits exact.
-    auto load_chunk = [&](uint4 (&r)[kLoads], int c0) {
-#pragma unroll
-        for (int k = 0; k < kLoads; ++k) {
-            const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
-            r[k] = *(const uint4 *)(Vh + (size_t)min(c0 + s, S - 1) * kHd + 8 * h);
-        }
-    };
-    uint4 ra[kLoads], rb[kLoads];
-    load_chunk(ra, 0);
-    load_chunk(rb, min(kVChunk, S - 1));
-
-    // each wave owns heads w, w+4: load its score rows and run their softmax.
-    // Rows are Sp floats apart, Sp / 4 odd, so that the G rows a summing wave
-    // reads at one step start in different bank groups.
-    const int Sp = ((Spad >> 2) | 1) << 2;
-    for (int g = w; g < G; g += 4)
-        wave_softmax_row(pr + g * Sp, scores + (size_t)(hk * G + g) * max_seq, S, Spad, lane,
-                         (max_seq & 3) == 0);
-
-    auto stage = [&](const uint4 (&r)[kLoads]) {
-#pragma unroll
-        for (int k = 0; k < kLoads; ++k) {
-            const int i = tid + 256 * k, s = i / PPP, h = i % PPP;
-            const uint32_t wv[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 f = __half22float2(*(const __half2 *)&wv[e]);
-                const int ss = s ^ swz(h);
-                vt[(8 * h + 2 * e) * kVS + ss] = f.x;
-                vt[(8 * h + 2 * e + 1) * kVS + ss] = f.y;
-            }
-        }
-    };
-    // sh/attention.wgsl:96-101: out[d] = sum_s p[s] * v[s][d], in order of s;
-    // waves < WPB each run 64 such chains (heads lane / DWW, dims w*DWW + lane % DWW).
-    // Chunks alternate between the two register sets: a set is refilled (two
-    // chunks ahead) as soon as it is staged, so no load is waited for early.
-    // The summing roles rotate with the block index so that workgroups sharing
-    // a CU sum on different SIMDs.
-    const int ws = (w - (int)((blockIdx.x + 3 * blockIdx.y + blockIdx.z) & 3)) & 3;
-    const int g = lane / DWW, dd = ws * DWW + lane % DWW;
-    // blocked P.V: a chunk (kVChunk divides kPvBlock) adds to the block's
-    // partial; a finished block's partial is added to the total in order
-    static_assert(kPvBlock % kVChunk == 0, "chunks tile the P.V blocks");
-    float acc = 0.0f, part = 0.0f;
-    auto chain = [&](int c) {
-        part = pv_chain(pr + g * Sp + c, vt + dd * kVS, min(kVChunk, S - c), part, swz(dd >> 3));
-        if ((c + kVChunk) % kPvBlock == 0 || c + kVChunk >= S) {
-            acc = c < kPvBlock ? part : acc + part;
-            part = 0.0f;
-        }
-    };
-    for (int c0 = 0; c0 < S; c0 += 2 * kVChunk) {
-        lds_barrier();  // probabilities ready / previous chunk consumed
-        stage(ra);
-        lds_barrier();
-        load_chunk(ra, min(c0 + 2 * kVChunk, S - 1));
-        if (ws < WPB) chain(c0);
-        const int c1 = c0 + kVChunk;
-        if (c1 < S) {
-            lds_barrier();
-            stage(rb);
-            lds_barrier();
-            load_chunk(rb, min(c1 + 2 * kVChunk, S - 1));
-            if (ws < WPB) chain(c1);
-        }
-    }
-    if (ws < WPB) out[(size_t)(hk * G + g) * kHd + d0 + dd] = acc;
-}
-
 // ---------------------------------------------------------------------------
-// Decode P.V on f32 MFMA (split path: > 256 positions, and batches).
-// v_mfma_f32_4x4x1_16b adds one product per output per instruction (one
-// rounding: the fused step, as the 16x16x1 form in the prefill kernel): lane
-// l supplies A[block l/4][row l%4] and B[block l/4][col l%4], and holds
-// D[block l/4][row r][col l%4] in register r.  Rows are the G <= 4 query
-// heads of a KV head (A = p[head][s], the same in all 16 blocks; rows past G
-// are zero probabilities), columns are dims: lane l takes dims 2l and 2l+1,
-// one dword of the f16 V row per position for two chains.  One workgroup of
-// 16 waves per (KV head, sequence): the softmax of the G rows into LDS, then
-// wave w sums the 256-position block w in order of s from zero, with three
-// 16-position batches of V rows in flight (read straight from the cache,
-// 256 B per wave per position); the block sums are added in block order
-// (sh/attention.wgsl:96-104 with the oracle's 256-position blocks).
-// LDS (dynamic): p [4][Sp] | block sums [blocks][4][128].
+// Decode P.V in the reference's association: out[d] = sum of p[s] * v[s][d]
+// in one loop over every position s (sh/attention.wgsl:96-104), one fused
+// step per position, on f32 MFMA.  v_mfma_f32_4x4x1_16b adds one product per
+// output per instruction with one rounding (the fused step, as the 16x16x1
+// form in the prefill kernel): lane l supplies A[block l/4][row l%4] and
+// B[block l/4][col l%4], and holds D[block l/4][row r][col l%4] in register
+// r.  Rows are four query heads of the KV head (A = p[head][s], the same in
+// all 16 blocks; rows past the group's heads are never stored), columns 64
+// dims: wave 0 chains the even dims 2l, wave 1 the odd dims 2l + 1, both from
+// dword l of the f16 V row (converted exactly to f32).
+// One 16-wave workgroup per (KV head, group of four heads, sequence):
+//  - softmax of row r on waves 4r .. 4r+3 (wave 4r + j, lane l playing
+//    thread 64j + l of the shader's 256-thread workgroup) into LDS rows;
+//  - the V rows stream into an LDS ring of NS slots of kPcRows rows,
+//    staged by every wave with global_load_lds_dwordx4 (four 256-byte rows
+//    per wave and slot) NS - 1 slots ahead: iteration c waits for the
+//    wave's own loads of slot c, a barrier publishes the slot (and frees slot
+//    c - 1, whose ring entry the next loads refill), and waves 0 and 1 sum
+//    slot c.  Rows past the cache length are clamped to its last row (staged,
+//    never summed), so the loads are unconditional and the waits exact; the
+//    chains stop at S.
+// LDS (dynamic): ring [NS][kPcRows][64 dwords] | p [4][Sp] | red [4][256] | wmax [16]
 // ---------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
-constexpr int kPvmWaves = 16;
-constexpr int kPvmThreads = 64 * kPvmWaves;
-constexpr int kPvmMaxBlocks = kPvmWaves;   // one block per wave: positions up to 4096
+constexpr int kPcWaves = 16;
+constexpr int kPcThreads = 64 * kPcWaves;
+constexpr int kPcRows = 4 * kPcWaves;        // V rows per ring slot (one DMA per wave)
+constexpr int kPcSlotBytes = kPcRows * kHd * 2;
+constexpr int kPcMaxSeq = 6144;               // score rows of up to 24 x 256 positions
+constexpr int kPcMaxNI = (kPcMaxSeq + 255) / 256;
 
-__host__ __device__ inline int pvm_row_stride(int max_seq) { return ((max_seq + 15) & ~15) + 4; }
-__host__ __device__ inline size_t pvm_smem(int max_seq) {
-    return ((size_t)4 * pvm_row_stride(max_seq) +
-            (size_t)((max_seq + kPvBlock - 1) / kPvBlock) * 4 * kHd) * sizeof(float);
+__host__ __device__ inline int pc_row_stride(int max_seq) { return ((max_seq + 15) & ~15) + 4; }
+__host__ __device__ inline size_t pc_smem(int slots, int max_seq) {
+    return (size_t)slots * kPcSlotBytes + ((size_t)4 * pc_row_stride(max_seq) + 4 * 256 + 16) * 4;
 }
 
-// V rows s .. s+15 of the lane's dword (dims 2l, 2l+1), clamped to the cache
-__device__ __forceinline__ void pv_load16(uint32_t (&vv)[16], const uint32_t *V2, int s, int S) {
+// Softmax of one score row by four waves (sh/softmax.wgsl:25-80): thread t =
+// 64 j + lane of the shader's workgroup sums exp(x - max) over positions
+// t + 256 i in order of i, then the halving tree; the max over the row is
+// exact in any order.  Loads are clamped to the row (branch-free).  The four
+// waves of the row exchange through wm (their maxima) and red (the 256
+// partials); every wave of the workgroup must call (two barriers).
+template <int NI>
+__device__ __forceinline__ void softmax_row_4w(float *prow, const float *__restrict__ src, int S,
+                                               bool has_row, float *wm, float *red, int j,
+                                               int lane) {
+    const int t = 64 * j + lane;
+    float x[NI];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) vv[u] = V2[(size_t)min(s + u, S - 1) * (kHd / 2)];
-    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < NI; ++i) x[i] = has_row ? src[min(t + 256 * i, S - 1)] : 0.0f;
+    float m = -3.402823e+38f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) m = t + 256 * i < S ? fmaxf(m, x[i]) : m;
+    m = wave_max_dpp(m);
+    if (lane == 0) wm[j] = m;
+    lds_barrier();
+    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        x[i] = t + 256 * i < S ? oxb_expf_nonpos(x[i] - m) : 0.0f;
+        part = part + x[i];
+    }
+    red[t] = part;
+    lds_barrier();
+    const float a = red[lane] + red[lane + 128];        // stride 128 (t = lane)
+    const float c = red[lane + 64] + red[lane + 192];   // stride 128 (t = lane + 64)
+    const float inv = 1.0f / wave_tree_sum(a + c);      // stride 64, then 32 .. 1
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        if (t + 256 * i < S) prow[t + 256 * i] = x[i] * inv;
 }
 
-// P.V of the 256-position block [s0, e) for the four rows at prow (the
-// lane's row lane % 4): two v_mfma_f32_4x4x1_16b chains (dims 2l and 2l+1),
-// in order of s from zero; va and vb hold the block's first two batches.
-// Past S (the last block's last batch) p is an exact zero and V a clamped
-// finite row, so such a step adds +0 to a sum that started at +0 (never -0):
-// the block sum is unchanged.
-__device__ __forceinline__ void pv_mfma_block(const float *prow, const uint32_t *V2, int s0, int e,
-                                              int S, uint32_t (&va)[16], uint32_t (&vb)[16],
-                                              v4f &a0, v4f &a1) {
-    a0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    a1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    auto run = [&](const uint32_t (&vv)[16], int s) {
+__device__ __forceinline__ void softmax_row_4w_any(float *prow, const float *src, int S,
+                                                   bool has_row, float *wm, float *red, int j,
+                                                   int lane) {
+    const int ni = (S + 255) >> 8;   // workgroup-uniform
+    if (ni <= 1) softmax_row_4w<1>(prow, src, S, has_row, wm, red, j, lane);
+    else if (ni <= 2) softmax_row_4w<2>(prow, src, S, has_row, wm, red, j, lane);
+    else if (ni <= 4) softmax_row_4w<4>(prow, src, S, has_row, wm, red, j, lane);
+    else if (ni <= 8) softmax_row_4w<8>(prow, src, S, has_row, wm, red, j, lane);
+    else if (ni <= 12) softmax_row_4w<12>(prow, src, S, has_row, wm, red, j, lane);
+    else if (ni <= 16) softmax_row_4w<16>(prow, src, S, has_row, wm, red, j, lane);
+    else softmax_row_4w<kPcMaxNI>(prow, src, S, has_row, wm, red, j, lane);
+}
+
+// n positions (1 .. 64) of one ring slot into the chain: vs = dword `lane` of
+// the slot's row 0 (rows 64 dwords apart), pp = the lane's p row at the
+// slot's first position.  Groups of four positions, operands read three
+// groups ahead (ring entries rotate with the group); whole groups run
+// without selects, the last partial group keeps the old sums past n.
+template <bool HI>
+__device__ __forceinline__ void pc_chain_slot(v4f &acc, const uint32_t *vs, const float *pp, int n) {
+    uint32_t V[4][4];
+    float4 P[4];
+    auto ld = [&](int b, int g) {   // group g (clamped into the slot) into entry b
+        g = min(g, kPcRows / 4 - 1);
 #pragma unroll
-        for (int u4 = 0; u4 < 16; u4 += 4) {
-            const float4 p = *(const float4 *)(prow + s + u4);
-            const float pp[4] = {p.x, p.y, p.z, p.w};
+        for (int k = 0; k < 4; ++k) V[b][k] = vs[(4 * g + k) * (kHd / 2)];
+        P[b] = *(const float4 *)(pp + 4 * g);
+    };
+    auto vf = [](uint32_t u) {
+        return __half2float(__ushort_as_half((uint16_t)(HI ? u >> 16 : u & 0xffffu)));
+    };
+    auto full = [&](const uint32_t (&v4)[4], const float4 &p4) {
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.x, vf(v4[0]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.y, vf(v4[1]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.z, vf(v4[2]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.w, vf(v4[3]), acc, 0, 0, 0);
+    };
+    auto part = [&](const uint32_t (&v4)[4], const float4 &p4, int m) {   // m < 4 positions
+        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float2 v = __half22float2(*(const __half2 *)&vv[u4 + u]);
-                a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.x, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(pp[u], v.y, a1, 0, 0, 0);
-            }
+        for (int k = 0; k < 3; ++k) {
+            const v4f r = __builtin_amdgcn_mfma_f32_4x4x1f32(pv[k], vf(v4[k]), acc, 0, 0, 0);
+            acc = k < m ? r : acc;
         }
     };
-    // batches rotate va -> vb -> vc: the batch two ahead is in flight while
-    // one is summed (loads are clamped, never skipped)
-    uint32_t vc[16];
-    for (int s = s0;; s += 48) {
-        pv_load16(vc, V2, s + 32, S);
-        run(va, s);
-        if (s + 16 >= e) break;
-        pv_load16(va, V2, s + 48, S);
-        run(vb, s + 16);
-        if (s + 32 >= e) break;
-        pv_load16(vb, V2, s + 64, S);
-        run(vc, s + 32);
-        if (s + 48 >= e) break;
+    ld(0, 0);
+    ld(1, 1);
+    ld(2, 2);
+    // 16 positions per iteration, fully unrolled (exits are wave-uniform
+    // branches): a loop's back edge would wait for every LDS read in flight.
+    // At the top of an iteration entries 0..2 hold its groups 0..2.
+    int s0 = 0;
+#pragma unroll
+    for (int it = 0; it < kPcRows / 16; ++it) {
+        if (s0 + 16 > n) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            ld((j + 3) & 3, s0 / 4 + j + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            full(V[j], P[j]);
+        }
+        s0 += 16;
+    }
+    if (s0 >= n) return;
+    ld(3, s0 / 4 + 3);   // the last n - s0 < 16 positions: entries 0..3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = n - s0 - 4 * j;
+        if (m >= 4) full(V[j], P[j]);
+        else if (m > 0) part(V[j], P[j], m);
     }
 }
 
-// Softmax of the G score rows (sh/softmax.wgsl:25-80) on waves 0 .. G-1,
-// rows G .. 3 zero-filled by waves G .. 3, into pr [4][Sp].
-template <int G>
-__device__ __forceinline__ void pv_mfma_softmax(float *pr, int Sp, const float *scores, int hk,
-                                                int max_seq, int S, int w, int lane) {
-    const int Spad = (S + 3) & ~3;
-    if (w < G) {
-        wave_softmax_row(pr + w * Sp, scores + (size_t)(hk * G + w) * max_seq, S, Spad, lane,
-                         (max_seq & 3) == 0);
-        for (int s = Spad + lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
-    } else if (w < 4) {
-        for (int s = lane; s < Sp; s += 64) pr[w * Sp + s] = 0.0f;
-    }
-}
-
-template <int G>
-__global__ __launch_bounds__(kPvmThreads) void attn_pv_mfma_kernel(
+template <int NS>
+__global__ __launch_bounds__(kPcThreads) void attn_pv_chain_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ out, size_t kv_stride,
-    int pos_stride) {
-    static_assert(G >= 1 && G <= 4, "four MFMA rows");
-    {   // sequence blockIdx.y of a batch
-        const int z = blockIdx.y, H = gridDim.x * G;
-        scores += (size_t)z * H * max_seq;
-        vc += (size_t)z * kv_stride;
-        pos_ptr += (size_t)z * pos_stride;
-        out += (size_t)z * H * kHd;
-    }
-    extern __shared__ __align__(16) float smem[];
-    const int Sp = pvm_row_stride(max_seq);
-    float *pr = smem, *sums = smem + 4 * Sp;
+    const int *__restrict__ pos_ptr, int G, int max_seq, float *__restrict__ out,
+    size_t kv_stride, int pos_stride) {
+    static_assert(NS >= 3 && NS - 2 < 64, "ring depth within vmcnt");
+    const int RG = (G + 3) >> 2;                  // groups of four heads per KV head
+    const int hk = blockIdx.x / RG, rg = blockIdx.x % RG, z = blockIdx.y;
+    const int Hkv = gridDim.x / RG, H = Hkv * G;
+    scores += (size_t)z * H * max_seq;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    out += (size_t)z * H * kHd;
+    extern __shared__ __align__(16) int8_t smem_pc[];
+    uint4 *ring = (uint4 *)smem_pc;
+    const int Sp = pc_row_stride(max_seq);
+    float *pr = (float *)(smem_pc + (size_t)NS * kPcSlotBytes);
+    float *red = pr + 4 * Sp, *wmax = red + 4 * 256;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int hk = blockIdx.x;
-    const int pos = *pos_ptr;
-    if (pos < 0 || pos >= max_seq) return;
-    const int S = pos + 1;
-    const int nb = (S + kPvBlock - 1) / kPvBlock;
-    if (nb > kPvmMaxBlocks) return;   // host checks too
-    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + lane;   // dims 2l, 2l+1
-    const int s0 = w * kPvBlock;
-    uint32_t va[16], vb[16];
-    pv_load16(va, V2, s0, S);   // the first two batches go out before the softmax
-    pv_load16(vb, V2, s0 + 16, S);
-    pv_mfma_softmax<G>(pr, Sp, scores, hk, max_seq, S, w, lane);
-    lds_barrier();
-    if (w < nb) {   // block w
-        v4f a0, a1;
-        pv_mfma_block(pr + (lane & 3) * Sp, V2, s0, min(s0 + kPvBlock, S), S, va, vb, a0, a1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sums[((size_t)w * 4 + r) * kHd + 2 * lane] = a0[r];
-            sums[((size_t)w * 4 + r) * kHd + 2 * lane + 1] = a1[r];
-        }
-    }
-    lds_barrier();
-    for (int o = tid; o < G * kHd; o += kPvmThreads) {
-        const int r = o / kHd, d = o % kHd;
-        float tot = sums[r * kHd + d];
-        for (int b = 1; b < nb; ++b) tot = tot + sums[((size_t)b * 4 + r) * kHd + d];
-        out[(size_t)(hk * G + r) * kHd + d] = tot;
-    }
-}
-
-// The same P.V over more workgroups (a workspace for the block sums): one
-// 4-wave workgroup per (KV head, kPvcBlocks blocks, sequence), each running
-// the G rows' softmax and summing its blocks (waves 0 .. kPvcBlocks-1);
-// attn_pv_combine_kernel then adds each output's block sums in block order.
-// ws: [batch][Hkv][ceil(max_seq / 256)][4][128] f32.
-constexpr int kPvcBlocks = 2;
-
-template <int G>
-__global__ __launch_bounds__(256) void attn_pv_mfma_chunk_kernel(
-    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int max_seq, float *__restrict__ ws, size_t kv_stride,
-    int pos_stride) {
-    static_assert(G >= 1 && G <= 4, "four MFMA rows");
-    const int z = blockIdx.z, Hkv = gridDim.x, hk = blockIdx.x;
-    const int nbmax = (max_seq + kPvBlock - 1) / kPvBlock;
-    scores += (size_t)z * Hkv * G * max_seq;
-    vc += (size_t)z * kv_stride;
-    pos_ptr += (size_t)z * pos_stride;
-    ws += ((size_t)z * Hkv + hk) * nbmax * 4 * kHd;
-    extern __shared__ __align__(16) float smem[];
-    const int Sp = pvm_row_stride(max_seq);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pos = *pos_ptr;
-    if (pos < 0 || pos >= max_seq) return;
-    const int S = pos + 1, nb = (S + kPvBlock - 1) / kPvBlock;
-    const int b = blockIdx.y * kPvcBlocks + w;   // this wave's block (waves < kPvcBlocks)
-    if (blockIdx.y * kPvcBlocks >= nb) return;  // the workgroup's blocks are past the cache
-    const uint32_t *V2 = (const uint32_t *)(vc + (size_t)hk * max_seq * kHd) + lane;
-    const int s0 = min(b, nb - 1) * kPvBlock;
-    uint32_t va[16], vb[16];
-    pv_load16(va, V2, s0, S);
-    pv_load16(vb, V2, s0 + 16, S);
-    pv_mfma_softmax<G>(smem, Sp, scores, hk, max_seq, S, w, lane);
-    lds_barrier();
-    if (w < kPvcBlocks && b < nb) {
-        v4f a0, a1;
-        pv_mfma_block(smem + (lane & 3) * Sp, V2, s0, min(s0 + kPvBlock, S), S, va, vb, a0, a1);
-#pragma unroll
-        for (int r = 0; r < G; ++r) {
-            *(float2 *)(ws + ((size_t)b * 4 + r) * kHd + 2 * lane) = make_float2(a0[r], a1[r]);
-        }
-    }
-}
-
-template <int G>
-__global__ __launch_bounds__(512) void attn_pv_combine_kernel(const float *__restrict__ ws,
-                                                              const int *__restrict__ pos_ptr,
-                                                              int max_seq, float *__restrict__ out,
-                                                              int pos_stride) {
-    const int z = blockIdx.y, Hkv = gridDim.x, hk = blockIdx.x;
-    const int nbmax = (max_seq + kPvBlock - 1) / kPvBlock;
     const int pos = pos_ptr[(size_t)z * pos_stride];
-    if (pos < 0 || pos >= max_seq) return;
-    const int nb = (pos + kPvBlock) / kPvBlock;
-    ws += ((size_t)z * Hkv + hk) * nbmax * 4 * kHd;
-    out += (size_t)z * Hkv * G * kHd;
-    for (int o = threadIdx.x; o < G * kHd; o += 512) {
-        const int r = o / kHd, d = o % kHd;
-        float tot = ws[r * kHd + d];
-        for (int b = 1; b < nb; ++b) tot = tot + ws[((size_t)b * 4 + r) * kHd + d];
-        out[(size_t)(hk * G + r) * kHd + d] = tot;
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1;
+    const int nslots = (S + kPcRows - 1) / kPcRows;
+
+    // this wave's share of a slot: rows 4w .. 4w+3 (lane: row 4w + lane/16,
+    // 16 bytes lane % 16), clamped to the cache length
+    const uint4 *V4 = (const uint4 *)vc;
+    auto issue = [&](int c) {
+        const int row = min(c * kPcRows + 4 * w + (lane >> 4), S - 1);
+        lds_dma16(V4 + (size_t)row * (kHd / 8) + (lane & 15),
+                  ring + ((size_t)(c % NS) * kPcRows + 4 * w) * (kHd / 8));
+    };
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+
+    // ---- softmax: row r = w / 4 (heads 4rg + r of the KV head) -------------
+    {
+        const int r = w >> 2, j = w & 3, head = 4 * rg + r;
+        const bool has_row = head < G;
+        softmax_row_4w_any(pr + r * Sp, scores + (size_t)(hk * G + min(head, G - 1)) * max_seq, S,
+                           has_row, wmax + 4 * r, red + 256 * r, j, lane);
+    }
+
+    // ---- P.V chains over the ring --------------------------------------------
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *prow = pr + (lane & 3) * Sp;
+    for (int c = 0; c < nslots; ++c) {
+        wait_vmcnt<NS - 2>();   // this wave's loads of slot c have landed
+        lds_barrier();          // ... every wave's; slot c - 1 is consumed (and p is written)
+        issue(c + NS - 1);      // into slot c - 1's ring entry (clamped past the cache)
+        if (w < 2) {
+            const uint32_t *vs = (const uint32_t *)(ring + (size_t)(c % NS) * kPcRows * (kHd / 8)) + lane;
+            const int n = min(kPcRows, S - c * kPcRows);
+            if (w == 0) pc_chain_slot<false>(acc, vs, prow + c * kPcRows, n);
+            else pc_chain_slot<true>(acc, vs, prow + c * kPcRows, n);
+        }
+    }
+    wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
+    if (w < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * rg + r < G) out[(size_t)(hk * G + 4 * rg + r) * kHd + 2 * lane + w] = acc[r];
     }
 }
 
@@ -835,47 +614,38 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
         rr[c] = tid / kHd + (kPrefillThreads / kHd) * c;
         Sc[c] = Sq[rr[c] / G];
     }
-    // blocks of kPvBlock positions: each block's sum starts at zero and is
-    // added to the row's total in block order (rows skip blocks past their end)
+    // one chain per output over its row's positions, in order of s
+    // (sh/attention.wgsl:96-104): the positions every row reaches in
+    // unrolled steps, then the longer rows' last positions
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
     const int S0 = Sq[0];   // every row attends at least this far
     constexpr int U = 16;
-    static_assert(kPvBlock % U == 0, "blocks hold whole unrolled steps");
-    for (int b0 = 0; b0 < Smax; b0 += kPvBlock) {
-        float part[NC];
+    int s = 0;
+    for (; s + U <= S0; s += U) {
+        float v[U];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) part[c] = 0.0f;
-        const int e0 = min(b0 + kPvBlock, S0), e1 = min(b0 + kPvBlock, Smax);
-        int s = b0;
-        for (; s + U <= e0; s += U) {
-            float v[U];
+        for (int u = 0; u < U; ++u) v[u] = __half2float(__ushort_as_half(Vd[(size_t)(s + u) * kHd]));
 #pragma unroll
-            for (int u = 0; u < U; ++u) v[u] = __half2float(__ushort_as_half(Vd[(size_t)(s + u) * kHd]));
+        for (int u4 = 0; u4 < U; u4 += 4) {
+            float4 pc[NC];   // probabilities of 4 positions per chain (broadcast reads)
 #pragma unroll
-            for (int u4 = 0; u4 < U; u4 += 4) {
-                float4 pc[NC];   // probabilities of 4 positions per chain (broadcast reads)
+            for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
 #pragma unroll
-                for (int c = 0; c < NC; ++c) pc[c] = *(const float4 *)(sc + rr[c] * Sw + s + u4);
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    part[c] = __builtin_fmaf(pc[c].x, v[u4], part[c]);
-                    part[c] = __builtin_fmaf(pc[c].y, v[u4 + 1], part[c]);
-                    part[c] = __builtin_fmaf(pc[c].z, v[u4 + 2], part[c]);
-                    part[c] = __builtin_fmaf(pc[c].w, v[u4 + 3], part[c]);
-                }
+            for (int c = 0; c < NC; ++c) {
+                acc[c] = __builtin_fmaf(pc[c].x, v[u4], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].y, v[u4 + 1], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].z, v[u4 + 2], acc[c]);
+                acc[c] = __builtin_fmaf(pc[c].w, v[u4 + 3], acc[c]);
             }
         }
-        for (; s < e1; ++s) {   // the last < U common positions, then the longer rows' tails
-            const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                if (s < Sc[c]) part[c] = __builtin_fmaf(sc[rr[c] * Sw + s], v, part[c]);
-        }
+    }
+    for (; s < Smax; ++s) {   // the last < U common positions, then the longer rows' tails
+        const float v = __half2float(__ushort_as_half(Vd[(size_t)s * kHd]));
 #pragma unroll
         for (int c = 0; c < NC; ++c)
-            if (b0 < Sc[c]) acc[c] = b0 == 0 ? part[c] : acc[c] + part[c];
+            if (s < Sc[c]) acc[c] = __builtin_fmaf(sc[rr[c] * Sw + s], v, acc[c]);
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -893,12 +663,12 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 // l/16][col l%16]; element (block b, row i, col j) of D is in lane
 // j + 16(i/4), register 4b + i%4.
 //
-// The B operands come from f32 copies of the cache laid out for them
+// The B operands come from copies of the cache laid out for them
 // (attn_kv_tiles_kernel, one pass per call): per KV head
-//   Kt [tile of 64 positions][d/4][64 positions][4 d]
-//   Vt [position/4][128 d][4 positions]
+//   Kt [tile of 64 positions][d/4][64 positions][4 d]           f32
+//   Vt [position/4][64 dim pairs][4 positions]    f16 pairs (dims 2j, 2j+1)
 // zero past the last position, so a lane's 16-byte load is 4 steps of its
-// operand with no conversion, and a wave's load is 1 KB contiguous.
+// operand (K with no conversion), and a wave's load is 1 KB contiguous.
 //
 // One workgroup of 16 waves (four per SIMD: a dependent MFMA chain issues at
 // ~64% of the MFMA rate from one wave per SIMD, ~100% from four) per (16/G
@@ -910,30 +680,30 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 //     dot * scale goes to the row in LDS.
 //   softmax: wave_softmax_row on row w, in place; positions past the row's
 //     length become exact zeros.
-//   P.V: task = (256-position block b, half h), wave w taking tasks w, w+16:
-//     per position one instruction (A = p[r][s], B = V[s][c + 64h] for the
-//     64 columns c), in order of s from zero.  A row shorter than the block
-//     sees p = 0 steps, which add an exact zero (its sum starts at +0, so it
-//     is never -0; V is finite).  The block sums go to LDS, and each output
-//     is the in-order sum of the blocks its row reaches
-//     (sh/attention.wgsl:96-104, the oracle's 256-position blocks).
+//   P.V (sh/attention.wgsl:96-104): one chain per output over all of its
+//     row's positions, in order of s, on v_mfma_f32_4x4x1_16b (one fused
+//     step per output per instruction; lane l supplies A[block l/4][row
+//     l%4], B[block l/4][col l%4] and holds D[block l/4][row i][col l%4] in
+//     register i).  Wave g < 4 takes rows 4g .. 4g+3 (A = p[4g + l%4][s])
+//     and all 128 dims as two chains per lane: dims 2l and 2l + 1 from one
+//     f16 pair of V.  Positions that every row of the group covers run in
+//     whole 16-position batches; the last ones keep each row's sum past its
+//     own length (a select per row).
 // LDS (dynamic): q [16][132] | rows [16][Sw], Sw = the longest row rounded
 // up to 64, plus 4, so that the 16 rows one read touches start in different
-// banks; the block sums [blocks][16][128] reuse it after the last read of p.
+// banks.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kPfmWaves = 16;
 constexpr int kPfmThreads = 64 * kPfmWaves;
 constexpr int kPfmQs = kHd + 4;   // q row stride (floats)
 constexpr int kPfmMaxS = 2368;    // longest row whose 16 rows fit the LDS (160 KB)
-constexpr int kPfmTasks = ((kPfmMaxS + kPvBlock - 1) / kPvBlock * 2 + kPfmWaves - 1) / kPfmWaves;
-constexpr int kTileF4 = 64 * kHd / 4;   // float4 of one 64-position tile of Kt or Vt
+constexpr int kTileF4 = 64 * kHd / 4;    // float4 of one 64-position tile of Kt
+constexpr int kVTileU4 = 64 * kHd / 8;   // uint4 of one 64-position tile of Vt
 
 __host__ __device__ inline int pfm_row_stride(int s_max) { return ((s_max + 63) & ~63) + 4; }
 __host__ __device__ inline size_t pfm_smem(int s_max) {
-    const size_t rows = (size_t)16 * (kPfmQs + pfm_row_stride(s_max)) * sizeof(float);
-    const size_t sums = (size_t)((s_max + kPvBlock - 1) / kPvBlock) * 16 * kHd * sizeof(float);
-    return rows > sums ? rows : sums;
+    return (size_t)16 * (kPfmQs + pfm_row_stride(s_max)) * sizeof(float);
 }
 
 __device__ __forceinline__ v16f mfma_f32_k1(float a, float b, const v16f &c) {
@@ -946,7 +716,7 @@ __global__ __launch_bounds__(256) void attn_kv_tiles_kernel(const uint16_t *__re
                                                             const uint16_t *__restrict__ vc,
                                                             int max_seq, int S, int ntile_ws,
                                                             float4 *__restrict__ Kt,
-                                                            float4 *__restrict__ Vt) {
+                                                            uint4 *__restrict__ Vt) {
     __shared__ uint4 ks[64][17], vs[64][17];   // 64 rows of 16 uint4, padded
     const int t = blockIdx.x, hk = blockIdx.y, tid = threadIdx.x;
     const uint4 *K4 = (const uint4 *)(kc + (size_t)hk * max_seq * kHd);
@@ -972,25 +742,23 @@ __global__ __launch_bounds__(256) void attn_kv_tiles_kernel(const uint16_t *__re
         const uint32_t lo = (c & 1) ? u.z : u.x, hi = (c & 1) ? u.w : u.y;
         kt[i] = make_float4(h2f(lo & 0xffff), h2f(lo >> 16), h2f(hi & 0xffff), h2f(hi >> 16));
     }
-    float4 *vt = Vt + ((size_t)hk * ntile_ws + t) * kTileF4;
+    uint4 *vt = Vt + ((size_t)hk * ntile_ws + t) * kVTileU4;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {   // vt[g][d]: positions 4g .. 4g+3 of dim d
-        const int i = tid + 256 * k, g = i >> 7, d = i & 127;
-        float v[4];
+    for (int k = 0; k < 4; ++k) {   // vt[g][j]: dword j (dims 2j, 2j+1) of positions 4g .. 4g+3
+        const int i = tid + 256 * k, g = i >> 6, j = i & 63;
+        uint32_t v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint4 u = vs[4 * g + j][d >> 3];
-            const uint32_t wd = ((d & 7) >> 1) == 0 ? u.x : ((d & 7) >> 1) == 1 ? u.y
-                              : ((d & 7) >> 1) == 2 ? u.z : u.w;
-            v[j] = h2f((d & 1) ? wd >> 16 : wd & 0xffff);
+        for (int r = 0; r < 4; ++r) {
+            const uint4 u = vs[4 * g + r][j >> 2];
+            v[r] = (j & 3) == 0 ? u.x : (j & 3) == 1 ? u.y : (j & 3) == 2 ? u.z : u.w;
         }
-        vt[i] = make_float4(v[0], v[1], v[2], v[3]);
+        vt[i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 }
 
 template <int G>
 __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
-    const float *__restrict__ q, const float4 *__restrict__ Kt, const float4 *__restrict__ Vt,
+    const float *__restrict__ q, const float4 *__restrict__ Kt, const uint4 *__restrict__ Vt,
     int ntile_ws, int pos0, int n_q, int H, float scale, float *__restrict__ out) {
     constexpr int QB = 16 / G;   // queries per workgroup
     extern __shared__ __align__(16) float smem[];
@@ -1066,83 +834,118 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
     }
     lds_barrier();
 
-    // ---- P.V: task = (block b, half h): 16 rows x the 64 dims c + 64h -------
-    const int nb = (Smax + kPvBlock - 1) / kPvBlock;
-    const float *prow = rows + (lane & 15) * Sw;
-    const int s_last = 64 * ntile - 16;   // last batch start inside Vt and the rows
-    v16f part[kPfmTasks];
+    // ---- P.V (sh/attention.wgsl:96-104): one chain per output ---------------
+    if (w < 4) {
+        const int g = w;   // rows 4g .. 4g+3 (lengths non-decreasing in the row)
+        int len[4];
 #pragma unroll
-    for (int k = 0; k < kPfmTasks; ++k) {
-        const int task = w + kPfmWaves * k, b = task >> 1, h = task & 1;
-        v16f a = {};
-        if (b < nb) {
-            const float4 *vt = Vt + (size_t)hk * ntile_ws * kTileF4 + lane + 64 * h;
-            const int s0 = b * kPvBlock, e = min(s0 + kPvBlock, Smax);
-            // 16 positions per batch: V (global) two batches ahead, p (LDS)
-            // just before its batch's MFMAs (a batch past the block reads the
-            // last batch and is never used)
-            auto loadv = [&](float4 (&vv)[4], int s) {
-                const int sb = min(s, s_last);
+        for (int i = 0; i < 4; ++i) len[i] = row_len(4 * g + i);
+        const int e = len[0] & ~15;   // whole batches every row of the group covers
+        const int s_last = 64 * ntile - 16;   // last batch start inside Vt and the rows
+        const uint4 *vt = Vt + (size_t)hk * ntile_ws * kVTileU4 + lane;
+        const float *prow = rows + (4 * g + (lane & 3)) * Sw;
+        // 16 positions per batch: V (global) two batches ahead, p (LDS) just
+        // before its batch's MFMAs (batch starts past the rows are clamped)
+        auto loadv = [&](uint4 (&vv)[4], int s) {
+            const int sb = min(s, s_last);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            auto loadp = [&](float4 (&pp)[4], int s) {
-                const int sb = min(s, s_last);
+            for (int j = 0; j < 4; ++j) vv[j] = vt[(size_t)(sb / 4 + j) * (kHd / 2)];
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto loadp = [&](float4 (&pp)[4], int s) {
+            const int sb = min(s, s_last);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) pp[j] = *(const float4 *)(prow + sb + 4 * j);
-            };
-            auto run = [&](const float4 (&vv)[4], const float4 (&pp)[4]) {
+            for (int j = 0; j < 4; ++j) pp[j] = *(const float4 *)(prow + sb + 4 * j);
+        };
+        auto lo = [](uint32_t u) { return __half2float(__ushort_as_half((uint16_t)(u & 0xffffu))); };
+        auto hi = [](uint32_t u) { return __half2float(__ushort_as_half((uint16_t)(u >> 16))); };
+        v4f a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto run = [&](const uint4 (&vv)[4], const float4 (&pp)[4]) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    a = mfma_f32_k1(pp[j].x, vv[j].x, a);
-                    a = mfma_f32_k1(pp[j].y, vv[j].y, a);
-                    a = mfma_f32_k1(pp[j].z, vv[j].z, a);
-                    a = mfma_f32_k1(pp[j].w, vv[j].w, a);
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t u[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
+                const float p[4] = {pp[j].x, pp[j].y, pp[j].z, pp[j].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], lo(u[k]), a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], hi(u[k]), a1, 0, 0, 0);
                 }
-            };
-            float4 va[4], vb[4], vc[4], pp[4];
-            loadv(va, s0);
-            loadv(vb, s0 + 16);
-            for (int s = s0;; s += 48) {
+            }
+        };
+        // the batch at st, each row's sum kept past its own length
+        auto tail = [&](const uint4 (&vv)[4], float4 (&pp)[4], int st) {
+            if (st >= len[3]) return;
+            loadp(pp, st);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t u[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
+                const float p[4] = {pp[j].x, pp[j].y, pp[j].z, pp[j].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int s = st + 4 * j + k;
+                    const v4f r0 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], lo(u[k]), a0, 0, 0, 0);
+                    const v4f r1 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], hi(u[k]), a1, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        a0[i] = s < len[i] ? r0[i] : a0[i];
+                        a1[i] = s < len[i] ? r1[i] : a1[i];
+                    }
+                }
+            }
+        };
+        // batches rotate va -> vb -> vc, each loaded two batches ahead; at the
+        // exit the next two batches (the positions past e, fewer than 19)
+        // are moved to va and vb for the one tail
+        uint4 va[4], vb[4], vc[4];
+        float4 pp[4];
+        loadv(va, 0);
+        loadv(vb, 16);
+        int s = 0;
+        if (e > 0) {
+            for (;; s += 48) {
                 loadv(vc, s + 32);
                 loadp(pp, s);
                 run(va, pp);
-                if (s + 16 >= e) break;
+                if (s + 16 >= e) {   // next: vb, vc
+                    s += 16;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        va[j] = vb[j];
+                        vb[j] = vc[j];
+                    }
+                    break;
+                }
                 loadv(va, s + 48);
                 loadp(pp, s + 16);
                 run(vb, pp);
-                if (s + 32 >= e) break;
+                if (s + 32 >= e) {   // next: vc, va
+                    s += 32;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint4 t = va[j];
+                        va[j] = vc[j];
+                        vb[j] = t;
+                    }
+                    break;
+                }
                 loadv(vb, s + 64);
                 loadp(pp, s + 32);
                 run(vc, pp);
-                if (s + 48 >= e) break;
+                if (s + 48 >= e) {   // next: va, vb
+                    s += 48;
+                    break;
+                }
             }
         }
-        part[k] = a;
-    }
-    lds_barrier();   // every wave is done with the probabilities
-    float *sums = smem;   // [nb][16][kHd]
+        tail(va, pp, s);
+        tail(vb, pp, s + 16);
 #pragma unroll
-    for (int k = 0; k < kPfmTasks; ++k) {
-        const int task = w + kPfmWaves * k, b = task >> 1, h = task & 1;
-        if (b < nb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = 4 * (lane >> 4) + (r & 3);
-                const int d = 16 * (r >> 2) + (lane & 15) + 64 * h;
-                sums[((size_t)b * 16 + i) * kHd + d] = part[k][r];
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i, qi = q0 + r / G;
+            if (qi < n_q)
+                *(float2 *)(out + ((size_t)qi * H + hk * G + r % G) * kHd + 2 * lane) =
+                    make_float2(a0[i], a1[i]);
         }
-    }
-    lds_barrier();
-    for (int o = tid; o < 16 * kHd; o += kPfmThreads) {
-        const int r = o / kHd, d = o % kHd;
-        const int S = row_len(r);
-        float total = sums[r * kHd + d];
-        for (int b = 1; b * kPvBlock < S; ++b) total = total + sums[((size_t)b * 16 + r) * kHd + d];
-        const int qi = q0 + r / G;
-        if (qi < n_q) out[((size_t)qi * H + hk * G + r % G) * kHd + d] = total;
     }
 }
 
@@ -1315,20 +1118,17 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     if (w < G) wave_softmax_row(sc + w * spad_max, sc + w * spad_max, S, Spad, lane, true);
 
     // ---- P.V: wave g < G sums head g, lane = dim 64*half + lane --------------
-    // Chunks alternate between the two register sets, each refilled (two
-    // chunks ahead) once staged.  A chunk is one P.V block: its sum starts
-    // at zero and is added to the total in block order.
-    static_assert(kFusedVC == kPvBlock, "a V chunk is one P.V block");
+    // One chain over every position (sh/attention.wgsl:96-104), continued
+    // from chunk to chunk.  Chunks alternate between the two register sets,
+    // each refilled (two chunks ahead) once staged.
     float acc = 0.0f;
     for (int c0 = 0; c0 < S; c0 += 2 * kFusedVC) {
         lds_barrier();   // softmax done / K rows or the previous V chunk consumed
         fused_stage_v(vt, va, w, lane);
         lds_barrier();
         fused_load_v(va, V2, c0 + 2 * kFusedVC, S, w, lane);
-        if (w < G) {
-            const float part = pv_chain(sc + w * spad_max + c0, vt + lane * kFusedVS, min(kFusedVC, S - c0), 0.0f);
-            acc = c0 == 0 ? part : acc + part;
-        }
+        if (w < G)
+            acc = pv_chain(sc + w * spad_max + c0, vt + lane * kFusedVS, min(kFusedVC, S - c0), acc);
         const int c1 = c0 + kFusedVC;
         if (c1 < S) {
             lds_barrier();
@@ -1336,7 +1136,7 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
             lds_barrier();
             fused_load_v(vb, V2, c1 + 2 * kFusedVC, S, w, lane);
             if (w < G)
-                acc = acc + pv_chain(sc + w * spad_max + c1, vt + lane * kFusedVS, min(kFusedVC, S - c1), 0.0f);
+                acc = pv_chain(sc + w * spad_max + c1, vt + lane * kFusedVS, min(kFusedVC, S - c1), acc);
         }
     }
     if (w < G) out[(size_t)(hk * G + w) * kHd + 64 * half + lane] = acc;
@@ -1344,34 +1144,33 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
 
 // ---------------------------------------------------------------------------
 // Decode, one workgroup per query head (grid: heads x sequences), 256
-// threads, up to 256 * NJ cached positions (NJ = 1 or 2).  Built for latency:
-//  - thread t computes the scores of positions t + 256 j from its own K rows,
+// threads, up to 256 cached positions, for caches of fewer than 256 rows
+// (the head256 kernel below stages whole 256-row blocks).  Built for latency:
+//  - thread t computes the score of position t from its own K row,
 //    loaded straight into registers at kernel start and clamped to the cache
 //    extent (rows at or past S are stale but in bounds and never used), so
 //    no load waits for the position; the head's q row is an SGPR operand of
 //    each v_fma_mix step (scalar loads), and its eight cache lines are
 //    fetched while the K rows are in flight;
 //  - the softmax runs on all four waves in the shader's order: thread t's
-//    strided partial exp(x_t - max) + exp(x_{t+256} - max), then the halving
-//    tree (strides 128 and 64 through LDS, 32 .. 1 in one wave);
-//  - P.V: wave w sums 256-position block w / 2 for dim 64 (w % 2) + lane, its
-//    V elements loaded into registers with 16-bit loads one 64-position chunk
-//    ahead (no LDS staging); the two block sums are added in block order.
+//    partial exp(x_t - max), then the halving tree (strides 128 and 64
+//    through LDS, 32 .. 1 in one wave);
+//  - P.V: waves 0 and 1 sum dim 64 w + lane over every position in order,
+//    the V elements loaded into registers with 16-bit loads one 64-position
+//    chunk ahead (no LDS staging).
 // Same arithmetic as the other decode kernels, so the same bits.
 // ---------------------------------------------------------------------------
 constexpr int kHeadChunk = 64;   // V positions per register chunk
 
-template <int NJ>
 __global__ __launch_bounds__(256) void attn_head_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
     size_t kv_stride, int pos_stride) {
-    static_assert(NJ == 1 || NJ == 2, "attn_head_kernel: up to 512 positions");
+    constexpr int NJ = 1;   // positions per thread
     __shared__ __align__(16) float pr[256 * NJ];   // probabilities
     __shared__ float red[256];
     __shared__ float wmax[4];
     __shared__ float inv_s;
-    __shared__ float bsum[kHd];                  // block 1's sums
     const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
@@ -1413,8 +1212,7 @@ __global__ __launch_bounds__(256) void attn_head_kernel(
 #pragma unroll
         for (int i = 0; i < kHeadChunk; ++i) dst[i] = vrow[i * kHd];
     };
-    // waves 2-3 have a P.V block only with two position groups
-    const bool pv_wave = NJ == 2 || blk == 0;
+    const bool pv_wave = blk == 0;   // waves 0 and 1
     uint16_t va[kHeadChunk], vb[kHeadChunk];
     load_v(va, min(b0, S - 1));   // (every wave: a conditional load would wait at the join)
 
@@ -1509,11 +1307,6 @@ __global__ __launch_bounds__(256) void attn_head_kernel(
         if (nb > 3 * kHeadChunk)
             sum_chunk(vb, b0 + 3 * kHeadChunk, nb - 3 * kHeadChunk);
     }
-    if constexpr (NJ == 2) {   // blocks added in order: total = part0 + part1
-        if (blk == 1) bsum[d] = acc;
-        lds_barrier();
-        if (blk == 0 && S > 256) acc = acc + bsum[d];
-    }
     if (blk == 0 && valid) out[((size_t)z * H + h) * kHd + d] = acc;
 }
 
@@ -1557,15 +1350,15 @@ __device__ __forceinline__ float pv4(float acc, const uint32_t (&V)[4], const fl
     return acc;
 }
 
-// P.V of one wave: lane j's chain over the S positions of dim 2j + HI;
-// vcol = the V rows' dword j (row stride 64 dwords)
-template <bool HI>
-__device__ __forceinline__ float pv_head256(const uint32_t *vcol, const float *pr, int S) {
+// P.V of one wave: lane j's chain over the S positions (S <= ROWS) of dim
+// 2j + HI, in order of s; vcol = the V rows' dword j (row stride 64 dwords)
+template <bool HI, int ROWS>
+__device__ __forceinline__ float pv_head(const uint32_t *vcol, const float *pr, int S) {
     float acc = 0.0f;
     uint32_t V[4][4];
     float4 P[4];
     auto ld = [&](int b, int s) {   // the block at s (clamped into the rows) into ring slot b
-        s = min(s, kH256Rows - 4);
+        s = min(s, ROWS - 4);
 #pragma unroll
         for (int k = 0; k < 4; ++k) V[b][k] = vcol[(s + k) * (kHd / 2)];
         P[b] = *(const float4 *)(pr + s);
@@ -1578,7 +1371,7 @@ __device__ __forceinline__ float pv_head256(const uint32_t *vcol, const float *p
     // which would drain the ring once per 16 positions
     int s0 = 0;
 #pragma unroll
-    for (int it = 0; it < kH256Rows / 16; ++it) {
+    for (int it = 0; it < ROWS / 16; ++it) {
         if (s0 + 16 > S) break;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1706,8 +1499,8 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
 
     // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
     if (w < 2) {
-        const float acc = w == 0 ? pv_head256<false>(vs + lane, pr, S)
-                                 : pv_head256<true>(vs + lane, pr, S);
+        const float acc = w == 0 ? pv_head<false, kH256Rows>(vs + lane, pr, S)
+                                 : pv_head<true, kH256Rows>(vs + lane, pr, S);
         if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
     }
 }
@@ -1718,13 +1511,12 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
 // K and written over the K rows once every score chain is done (one more
 // barrier).  Softmax in the shader's 256-thread order: thread t < 256 forms
 // its strided partial (0 + e_t) + e_(t+256), then the same halving tree in
-// every wave.  P.V: waves 0 / 1 sum block 0 (positions 0..255, even / odd
-// dims) and waves 2 / 3 block 1 (256..511) with the head256 chains; block
-// sums added in block order.  Same arithmetic as the other forms.
+// every wave.  P.V: waves 0 / 1 (even / odd dims) run the head256 chains
+// over all S positions in order.  Same arithmetic as the other forms.
 // ---------------------------------------------------------------------------
 constexpr int kH512Rows = 512;
 constexpr size_t kH512KBytes = (size_t)kH512Rows * 17 * 16;   // K rows, padded; then V rows
-constexpr size_t kH512Lds = kH512KBytes + (kHd + 512 + 512 + 256 + 128 + 8) * 4;
+constexpr size_t kH512Lds = kH512KBytes + (kHd + 512 + 512 + 256 + 8) * 4;
 static_assert((size_t)kH512Rows * kHd * 2 <= kH512KBytes, "V rows fit the K region");
 
 __global__ __launch_bounds__(512) void attn_head512_kernel(
@@ -1741,8 +1533,7 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     float *pr = qs + kHd;                                            // probabilities [512]
     float *ev = pr + 512;                                            // e [512]
     float *red = ev + 512;                                           // partial sums [256]
-    float *bsum = red + 256;                                         // block 1 sums [128]
-    float *wmax = bsum + 128;                                        // [8]
+    float *wmax = red + 256;                                         // [8]
     const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
@@ -1826,23 +1617,11 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     pr[tid] = e * inv;   // 0 past S
     lds_barrier();
 
-    // ---- P.V (sh/attention.wgsl:96-104): blocks of 256 positions -----------
-    if (w < 4) {
-        const int blk = w >> 1, Sb = min(S - kH256Rows * blk, kH256Rows);
-        float acc = 0.0f;
-        if (Sb > 0) {
-            const uint32_t *vcol = vs + (size_t)blk * kH256Rows * (kHd / 2) + lane;
-            acc = (w & 1) ? pv_head256<true>(vcol, pr + kH256Rows * blk, Sb)
-                          : pv_head256<false>(vcol, pr + kH256Rows * blk, Sb);
-        }
-        if (blk == 1) bsum[2 * lane + (w & 1)] = acc;
-        else red[2 * lane + (w & 1)] = acc;   // red is free after the tree
-    }
-    lds_barrier();
-    if (tid < kHd) {
-        float acc = red[tid];
-        if (S > kH256Rows) acc = acc + bsum[tid];   // block sums in block order
-        if (valid) out[((size_t)z * H + h) * kHd + tid] = acc;
+    // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
+    if (w < 2) {
+        const float acc = w == 0 ? pv_head<false, kH512Rows>(vs + lane, pr, S)
+                                 : pv_head<true, kH512Rows>(vs + lane, pr, S);
+        if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
     }
 }
 
@@ -1885,7 +1664,8 @@ static int launch_prefill_mfma(const float *q, const uint16_t *kc, const uint16_
     constexpr int QB = 16 / G;
     if (allow_dynamic_lds((const void *)attn_prefill_mfma_kernel<G>)) return -1;
     const int ntile = (s_max + 63) / 64;
-    float4 *Kt = (float4 *)ws, *Vt = Kt + (size_t)Hkv * ntile * kTileF4;
+    float4 *Kt = (float4 *)ws;
+    uint4 *Vt = (uint4 *)(Kt + (size_t)Hkv * ntile * kTileF4);
     hipLaunchKernelGGL(attn_kv_tiles_kernel, dim3(ntile, Hkv), dim3(256), 0, s, kc, vc, max_seq,
                        s_max, ntile, Kt, Vt);
     OXB_CHECK_HIP(hipGetLastError());
@@ -1899,8 +1679,10 @@ static int launch_prefill_mfma(const float *q, const uint16_t *kc, const uint16_
 
 size_t attn_prefill_ws_bytes(int Hkv, int s_max) {
     if (Hkv <= 0 || s_max <= 0 || s_max > kPfmMaxS) return 0;
-    return (size_t)2 * Hkv * ((s_max + 63) / 64) * kTileF4 * sizeof(float4);
+    return (size_t)Hkv * ((s_max + 63) / 64) * (kTileF4 * sizeof(float4) + kVTileU4 * sizeof(uint4));
 }
+
+size_t attn_prefill_ws_max_bytes(int Hkv) { return attn_prefill_ws_bytes(Hkv, kPfmMaxS); }
 
 // f32 MFMA kernel (with its Kt / Vt workspace) while its 16 rows fit the LDS
 // (up to kPfmMaxS positions), else the VALU kernel: the same sums in the same
@@ -1940,77 +1722,29 @@ int attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int n_q
 
 using namespace oxb;
 
+// Decode attention over the f16 cache in two launches: the scores kernel
+// (64-position blocks), then the softmax and the one-chain P.V of
+// attn_pv_chain_kernel per (KV head, group of four heads, sequence), with a
+// five-slot V ring while its LDS fits beside the score rows, else three.
 template <int G>
 static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                          int Hkv, int max_seq, float *scores, float *out, hipStream_t s,
-                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0,
-                         float *pv_ws = nullptr) {
+                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0) {
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipLaunchKernelGGL(attn_scores_kernel<G>,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
-    // LDS: the G probability rows (each padded to an odd multiple of 4) and
-    // the block sums; 8 summing waves when their staging fits beside them
-    const size_t smem = ((size_t)G * ((((max_seq + 3) & ~3) >> 2 | 1) << 2) +
-                         (size_t)((max_seq + kPvBlock - 1) / kPvBlock) * 64) * sizeof(float);
-    constexpr size_t stage8 = (size_t)8 * pv_dims_per_wave(G) * (kPvStage / pv_dims_per_wave(G) + 4) * 4;
-    // (G = 1: the 8-wave variant needs more than 256 VGPRs; 4 waves only)
-    const bool eight = G > 1 && smem + stage8 <= 160 * 1024;
-    if (allow_dynamic_lds(eight ? (const void *)attn_pv_kernel<G, G == 1 ? 4 : 8>
-                                : (const void *)attn_pv_kernel<G, 4>))
-        return -1;
-    // f32 MFMA P.V (the G heads as rows) for wide grids: its one workgroup per
-    // (KV head, sequence) is MFMA-bound at ~20 us for 2304 positions, the VALU
-    // kernels' chains grow with the batch (B = 1 / 4 / 8 / 32 at 2304
-    // positions, scores + P.V: VALU 13 / 20 / 32 / 57 us, MFMA 23 / 24 / 27 / 40 us).
-    // OXB_PV=valu|mfma forces either (same sums, same bits).
-    // With a workspace, the MFMA P.V spreads over kPvcBlocks-block workgroups
-    // while they fit the CUs once (OXB_PV=chunk forces it).
-    const char *pv = getenv("OXB_PV");
-    const bool force_valu = pv && !strcmp(pv, "valu"), force_mfma = pv && !strcmp(pv, "mfma");
-    const bool force_chunk = pv_ws && pv && !strcmp(pv, "chunk");
-    if constexpr (G <= 4) {
-        const int nchunk = ((max_seq + kPvBlock - 1) / kPvBlock + kPvcBlocks - 1) / kPvcBlocks;
-        if (max_seq <= kPvmMaxBlocks * kPvBlock && !force_valu &&
-            (force_mfma || force_chunk || (long)batch * Hkv >= 32)) {
-            if (force_chunk ||
-                (pv_ws && !force_mfma && (long)batch * Hkv * nchunk <= device_cus())) {
-                const size_t csmem = (size_t)4 * pvm_row_stride(max_seq) * sizeof(float);
-                if (csmem > 64 * 1024 && allow_dynamic_lds((const void *)attn_pv_mfma_chunk_kernel<G>))
-                    return -1;
-                hipLaunchKernelGGL((attn_pv_mfma_chunk_kernel<G>), dim3(Hkv, nchunk, batch), dim3(256),
-                                   csmem, s, scores, vc, pos, max_seq, pv_ws, kv_stride, pos_stride);
-                OXB_CHECK_HIP(hipGetLastError());
-                hipLaunchKernelGGL((attn_pv_combine_kernel<G>), dim3(Hkv, batch), dim3(512), 0, s,
-                                   pv_ws, pos, max_seq, out, pos_stride);
-                OXB_CHECK_HIP(hipGetLastError());
-                return 0;
-            }
-            if (allow_dynamic_lds((const void *)attn_pv_mfma_kernel<G>)) return -1;
-            hipLaunchKernelGGL((attn_pv_mfma_kernel<G>), dim3(Hkv, batch), dim3(kPvmThreads),
-                               pvm_smem(max_seq), s, scores, vc, pos, max_seq, out, kv_stride,
-                               pos_stride);
-            OXB_CHECK_HIP(hipGetLastError());
-            return 0;
-        }
+    const dim3 grid(Hkv * ((G + 3) / 4), batch);
+    if (pc_smem(5, max_seq) <= 160 * 1024) {
+        if (allow_dynamic_lds((const void *)attn_pv_chain_kernel<5>)) return -1;
+        hipLaunchKernelGGL(attn_pv_chain_kernel<5>, grid, dim3(kPcThreads), pc_smem(5, max_seq), s,
+                           scores, vc, pos, G, max_seq, out, kv_stride, pos_stride);
+    } else {
+        if (allow_dynamic_lds((const void *)attn_pv_chain_kernel<3>)) return -1;
+        hipLaunchKernelGGL(attn_pv_chain_kernel<3>, grid, dim3(kPcThreads), pc_smem(3, max_seq), s,
+                           scores, vc, pos, G, max_seq, out, kv_stride, pos_stride);
     }
-    const dim3 grid(Hkv, kHd / pv_dims_per_wave(G), batch);
-    if ((long)grid.x * grid.y * grid.z > device_cus()) {   // wide: one softmax per 16 G dims
-        constexpr int DWB = pv_dims_per_wave(G) * (2 * G < 4 ? 2 * G : 4);
-        const size_t wsmem = (size_t)G * (((max_seq + 3) & ~3) + 4) * sizeof(float);
-        if (allow_dynamic_lds((const void *)attn_pv_wide_kernel<G>)) return -1;
-        hipLaunchKernelGGL((attn_pv_wide_kernel<G>), dim3(Hkv, kHd / DWB, batch), dim3(256), wsmem, s,
-                           scores, vc, pos, max_seq, out, kv_stride, pos_stride);
-        OXB_CHECK_HIP(hipGetLastError());
-        return 0;
-    }
-    if (eight)
-        hipLaunchKernelGGL((attn_pv_kernel<G, G == 1 ? 4 : 8>), grid, dim3(G == 1 ? 256 : 512), smem, s,
-                           scores, vc, pos, max_seq, out, kv_stride, pos_stride);
-    else
-        hipLaunchKernelGGL((attn_pv_kernel<G, 4>), grid, dim3(256), smem, s, scores, vc, pos,
-                           max_seq, out, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -2021,48 +1755,16 @@ extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uin
     OXB_REQUIRE(pos && scores, "attention: pos or scores is NULL");
     OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
-    const int G = H / Hkv;
-    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
-                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
+    OXB_REQUIRE(max_seq >= 1 && max_seq <= kPcMaxSeq,
+                "attention: max_seq %d out of range (1..%d)", max_seq, kPcMaxSeq);
     hipStream_t s = (hipStream_t)stream;
-    switch (G) {
+    switch (H / Hkv) {
         case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s);
         default:
-            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
-            return -1;
-    }
-}
-
-extern "C" size_t oxb_attn_decode_batch_ws_bytes(int batch, int Hkv, int max_seq) {
-    if (batch < 1 || Hkv < 1 || max_seq < 1) return 0;
-    return (size_t)batch * Hkv * ((max_seq + kPvBlock - 1) / kPvBlock) * 4 * kHd * sizeof(float);
-}
-
-extern "C" int oxb_attn_decode_batch_ws(const float *q, const uint16_t *kcache,
-                                        const uint16_t *vcache, const int *pos, int pos_stride,
-                                        size_t kv_stride, int batch, int H, int Hkv, int hd,
-                                        int max_seq, float *scores, float *ws, float *out,
-                                        void *stream) {
-    OXB_REQUIRE(pos && scores && ws, "attention: pos, scores or ws is NULL");
-    OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
-    OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
-    OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
-    OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
-                "attention: caches of a batch overlap (stride %zu)", kv_stride);
-    const int G = H / Hkv;
-    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
-                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
-    hipStream_t s = (hipStream_t)stream;
-    switch (G) {
-        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
-        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
-        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
-        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, ws);
-        default:
-            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
+            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", H / Hkv);
             return -1;
     }
 }
@@ -2077,17 +1779,16 @@ extern "C" int oxb_attn_decode_batch(const float *q, const uint16_t *kcache,
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
     OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
                 "attention: caches of a batch overlap (stride %zu)", kv_stride);
-    const int G = H / Hkv;
-    OXB_REQUIRE((size_t)G * max_seq * 4 <= 96 * 1024,
-                "attention: %d heads per KV head x %d positions exceed the LDS budget", G, max_seq);
+    OXB_REQUIRE(max_seq >= 1 && max_seq <= kPcMaxSeq,
+                "attention: max_seq %d out of range (1..%d)", max_seq, kPcMaxSeq);
     hipStream_t s = (hipStream_t)stream;
-    switch (G) {
+    switch (H / Hkv) {
         case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
         case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
         case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
         case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
         default:
-            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", G);
+            oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", H / Hkv);
             return -1;
     }
 }
@@ -2168,7 +1869,7 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
         hipLaunchKernelGGL(attn_head256_kernel, dim3(H, batch), dim3(256), kH256Lds, s, q, kcache,
                            vcache, pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
     } else if (s_max <= 256)
-        hipLaunchKernelGGL(attn_head_kernel<1>, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
+        hipLaunchKernelGGL(attn_head_kernel, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
                            pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
     else {
         if (allow_dynamic_lds((const void *)attn_head512_kernel)) return -1;
@@ -2188,8 +1889,8 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
 //   scores   thread t takes positions t, t + 128, ...: 128 fused steps in
 //            order of d (q from LDS, the K row from HBM), times the scale
 //   softmax  wave 0, the 256-thread order (wave_softmax_row)
-//   P.V      thread d < 128: out[d] = blocks of kPvBlock positions summed in
-//            order of s, block sums added in block order
+//   P.V      thread d < 128: out[d] = one chain over the S positions in order
+//            of s (sh/attention.wgsl:96-104)
 // Query qi sits at position pos0 + qi (pos0 = *pos_ptr for a decode step
 // from device state) and attends over S = its position + 1 positions.
 // LDS: q [128] | scores [Sp] | probabilities [Sp], Sp = s_max rounded to 4.
@@ -2232,22 +1933,17 @@ __global__ __launch_bounds__(kF32Threads) void attn_f32_kernel(
     if (w == 0) wave_softmax_row(pr, sc, S, Spad, lane, false);
     lds_barrier();
     const int d = tid;
-    float total = 0.0f;
-    for (int b0 = 0; b0 < S; b0 += kPvBlock) {
-        const int e = min(b0 + kPvBlock, S);
-        float part = 0.0f;
-        int s = b0;
-        for (; s + 8 <= e; s += 8) {
-            float v[8];
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+        float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = V[(size_t)(s + k) * kHd + d];
+        for (int k = 0; k < 8; ++k) v[k] = V[(size_t)(s + k) * kHd + d];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) part = __builtin_fmaf(pr[s + k], v[k], part);
-        }
-        for (; s < e; ++s) part = __builtin_fmaf(pr[s], V[(size_t)s * kHd + d], part);
-        total = b0 == 0 ? part : total + part;
+        for (int k = 0; k < 8; ++k) acc = __builtin_fmaf(pr[s + k], v[k], acc);
     }
-    out[((size_t)qi * H + h) * kHd + d] = total;
+    for (; s < S; ++s) acc = __builtin_fmaf(pr[s], V[(size_t)s * kHd + d], acc);
+    out[((size_t)qi * H + h) * kHd + d] = acc;
 }
 
 namespace oxb {

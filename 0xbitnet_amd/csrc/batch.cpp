@@ -38,7 +38,6 @@ struct oxb_batch {
     float *rope = nullptr;                // [max_seq][hd/2] (cos, sin)
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
     float *scores = nullptr, *logits = nullptr, *xscale = nullptr;
-    float *pv_ws = nullptr;   // attention P.V block sums
     float *hn = nullptr;                  // [B][D] LM-head pair tables (normalised rows)
     int *xsum = nullptr;
     void *X = nullptr;                    // token-tiled int8 rows
@@ -79,8 +78,8 @@ int oxb_batch::enqueue_step() {
                           state + OXB_ST_POS, OXB_STATE_INTS, slot_kv, q, kc, vc, max_seq, rope,
                           true, s))
             return -1;
-        if (oxb_attn_decode_batch_ws(q, kc, vc, state + OXB_ST_POS, OXB_STATE_INTS, slot_kv, B,
-                                     M.H, M.Hkv, M.hd, max_seq, scores, pv_ws, attn, s))
+        if (oxb_attn_decode_batch(q, kc, vc, state + OXB_ST_POS, OXB_STATE_INTS, slot_kv, B,
+                                  M.H, M.Hkv, M.hd, max_seq, scores, attn, s))
             return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
         if (oxb_quantize_rows_tiled(attn, L.attn_sub, 1e-5f, B, Dq, X, xscale, xsum, s)) return -1;
@@ -168,14 +167,13 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
     b->attn = (float *)b->dalloc((size_t)batch * Dq * 4);
     b->h = (float *)b->dalloc((size_t)batch * F * 4);
     b->scores = (float *)b->dalloc((size_t)batch * m->H * max_seq * 4);
-    b->pv_ws = (float *)b->dalloc(oxb_attn_decode_batch_ws_bytes(batch, m->Hkv, max_seq));
     b->logits = (float *)b->dalloc((size_t)batch * m->V * 4);
     b->hn = (float *)b->dalloc((size_t)batch * D * 4);
     b->xscale = (float *)b->dalloc((size_t)rows * 4);
     b->xsum = (int *)b->dalloc((size_t)rows * 4);
     b->X = b->dalloc((size_t)rows * std::max(D, F));
     bool ok = b->kcache && b->vcache && b->state && b->tok_hist && b->rope && b->x && b->q &&
-              b->attn && b->h && b->scores && b->pv_ws && b->logits && b->hn && b->xscale &&
+              b->attn && b->h && b->scores && b->logits && b->hn && b->xscale &&
               b->xsum && b->X;
     if (ok && hipHostMalloc((void **)&b->pinned, (size_t)batch * OXB_STATE_INTS * 4,
                             hipHostMallocDefault) != hipSuccess) {

@@ -45,6 +45,16 @@ oxb_model::~oxb_model() {   // teardown: errors have no caller to go to
     delete gguf;
 }
 
+void oxb_model::dfree(void *p) {
+    for (size_t i = 0; i < allocations.size(); ++i)
+        if (allocations[i] == p) {
+            (void)hipFree(p);
+            allocations[i] = allocations.back();
+            allocations.pop_back();
+            return;
+        }
+}
+
 void *oxb_model::dalloc(size_t bytes) {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
@@ -473,7 +483,11 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
         }
     }
     m->tok_hist = (int *)m->dalloc((size_t)m->hist_cap * 4);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist)
+    // the prefill attention's K / V copies, once, for the longest rows any
+    // prefill of this model or a batch slot can hand the MFMA kernel
+    m->pf_ws_bytes = oxb::attn_prefill_ws_max_bytes(Hkv);
+    m->pf_ws = m->dalloc(m->pf_ws_bytes);
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist || !m->pf_ws)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
         hipMemset(m->vcache, 0, kv_bytes) != hipSuccess) {
@@ -603,6 +617,13 @@ int oxb_model::ensure_graphs(int p0, int p1) {
 
 int oxb_model::ensure_prefill(int n) {
     if (n <= pf_cap) return 0;
+    // the buffers of a shorter prefill: released once the work queued on them is done
+    if (pf_cap) {
+        M_CHECK(hipStreamSynchronize(stream));
+        for (void *p : {(void *)px, (void *)pq, (void *)pattn, (void *)ph, (void *)pscale, pX,
+                        (void *)psum, (void *)pids})
+            dfree(p);
+    }
     const int cap = ((n + 63) / 64) * 64;
     const int Dq = H * hd;
     const int Kmax = std::max(D, F);
@@ -626,11 +647,6 @@ int oxb_model::ensure_prefill(int n) {
 // table, state block and position (the model's own, or a batch slot's).
 int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg) {
     if (ensure_prefill(n)) return -1;
-    const size_t ws_need = oxb::attn_prefill_ws_bytes(Hkv, tg.pos + n);
-    if (ws_need > pf_ws_bytes) {   // earlier workspaces may still be in use by queued work
-        if (!(pf_ws = dalloc(ws_need))) return -1;
-        pf_ws_bytes = ws_need;
-    }
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));

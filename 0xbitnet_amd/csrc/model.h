@@ -44,7 +44,7 @@ struct oxb_model {
 
     // prefill buffers (grown on demand)
     int pf_cap = 0;
-    void *pf_ws = nullptr;   // prefill attention's K / V copies (grows; old ones kept until unload)
+    void *pf_ws = nullptr;   // prefill attention's K / V copies (sized at load)
     size_t pf_ws_bytes = 0;
     float *px = nullptr, *pq = nullptr, *pattn = nullptr, *ph = nullptr, *pscale = nullptr;
     void *pX = nullptr;
@@ -72,6 +72,7 @@ struct oxb_model {
 
     ~oxb_model();
     void *dalloc(size_t bytes);
+    void dfree(void *p);   // a dalloc allocation no queued work uses any more
     int enqueue_decode_step(AttnForm attn);
     int ensure_prefill(int n);
     // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state

@@ -309,6 +309,33 @@ __device__ inline float oxb_expf_nonpos(float x) {
     return x < -103.972084f ? 0.0f : y;
 }
 
+// Direct global -> LDS loads (global_load_lds_dwordx4): each lane's 16 B
+// land at the wave's LDS base + 16 * lane, taking no VGPRs and no LDS
+// store instructions.
+// The loads are issued from inline assembly with explicit vmcnt waits: the
+// compiler's builtin for them makes every later LDS read wait for all
+// outstanding loads, which would serialise the prefetch.  The compiler does
+// not count these loads, so its own vmcnt waits can only come out stricter.
+// The LDS base goes through m0, which the asm saves and restores itself (m0 is
+// a reserved register: declaring it clobbered is not allowed).
+__device__ __forceinline__ void lds_dma16(const void *g, const uint4 *lds_wave_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)lds_wave_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(g)
+        : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // s_waitcnt immediate: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // sh/quantize.wgsl:59,68,71 for one value given the row absmax.
 __device__ inline int quant_one(float v, float inv) {
     int q = (int)rintf(v * inv);

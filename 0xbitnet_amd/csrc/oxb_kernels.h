@@ -36,6 +36,8 @@ int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const in
 // bytes (0: that length runs on the VALU kernel, which needs none).  A
 // smaller or null workspace selects the VALU kernel; the results are the same.
 size_t attn_prefill_ws_bytes(int Hkv, int s_max);
+// the largest such workspace (rows of up to the MFMA kernel's 2368 positions)
+size_t attn_prefill_ws_max_bytes(int Hkv);
 int attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int n_q, int pos0, int H,
                  int Hkv, int hd, int max_seq, void *ws, size_t ws_bytes, float *out,
                  void *stream);

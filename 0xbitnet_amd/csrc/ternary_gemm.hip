@@ -456,29 +456,7 @@ __global__ __launch_bounds__(128 * NWF, 4 / NWF) void gemm_lds_kernel(GemmParams
 //   be in flight), barrier (every thread's stage s has landed, and every wave
 //   is done reading the buffer that stage s+NBUF-1 reuses), issue stage
 //   s+NBUF-1, multiply stage s.
-// The loads are issued from inline assembly with explicit vmcnt waits: the
-// compiler's builtin for them makes every later LDS read wait for all
-// outstanding loads, which would serialise the prefetch.  The compiler does
-// not count these loads, so its own vmcnt waits can only come out stricter.
-// The LDS base goes through m0, which the asm saves and restores itself (m0 is
-// a reserved register: declaring it clobbered is not allowed).
-__device__ __forceinline__ void lds_dma16(const void *g, const uint4 *lds_wave_base) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)lds_wave_base);
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(base), "v"(g)
-        : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    // s_waitcnt immediate: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
+// (lds_dma16 and wait_vmcnt: oxb_common.h)
 
 // workgroups per CU that the LDS of a DMA-staged tile allows (160 KB)
 __host__ __device__ constexpr int dma_occupancy(int MF, int MT, int NWF, int NBUF) {

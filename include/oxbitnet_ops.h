@@ -140,11 +140,13 @@ int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, cons
 
 /* ---- attention ------------------------------------------------------------ */
 /* Decode attention for one token over L = *pos + 1 cached positions, in the
- * reference's order for the scores and softmax, with P.V summed in blocks of
- * 256 positions whose sums are added in order (for L <= 256 the shaders' one
- * loop; f32 result identical to the oracle's arithmetic on the f16-rounded
- * cache).  q, out: [H*128] f32; scores: [H][max_seq] f32 scratch.  Replaces nn/attention.rs:109-118
- * (scores, softmax, P.V dispatches). */
+ * reference's order: scores as 128-term chains in order of d, the softmax in
+ * the shader's 256-thread order, and P.V as one chain per output over all L
+ * positions in order (sh/attention.wgsl:29-59,79-105, sh/softmax.wgsl:25-80;
+ * f32 result identical to the oracle's arithmetic on the f16-rounded cache).
+ * Two launches: scores to the buffer, then softmax and P.V.  q, out: [H*128]
+ * f32; scores: [H][max_seq] f32 scratch; max_seq <= 6144.  Replaces
+ * nn/attention.rs:109-118 (scores, softmax, P.V dispatches). */
 int oxb_attn_decode(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                     const int *pos, int H, int Hkv, int hd, int max_seq, float *scores,
                     float *out, void *stream);
@@ -156,18 +158,6 @@ int oxb_attn_decode_batch(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                           int Hkv, int hd, int max_seq, float *scores, float *out, void *stream);
 
-/* oxb_attn_decode_batch with a workspace of
- * oxb_attn_decode_batch_ws_bytes(batch, Hkv, max_seq) bytes for the P.V block
- * sums: wide grids (batch x Hkv >= 32) then spread each sequence's P.V over
- * more workgroups (two 256-position blocks each) and add the block sums in a
- * second kernel; same result bits.  Replaces nn/attention.rs:109-118 like
- * oxb_attn_decode_batch; no counterpart of its own in the reference. */
-size_t oxb_attn_decode_batch_ws_bytes(int batch, int Hkv, int max_seq);
-int oxb_attn_decode_batch_ws(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                             const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
-                             int Hkv, int hd, int max_seq, float *scores, float *ws, float *out,
-                             void *stream);
-
 /* The same decode attention as one kernel: two 1024-thread workgroups per KV
  * head (one per half of the dims) compute scores, softmax and P.V in LDS (no
  * scores buffer), same result bits.  Faster for short caches (each KV head's
@@ -178,17 +168,19 @@ int oxb_attn_decode_fused(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int H, int Hkv, int hd, int max_seq, float *out,
                           void *stream);
 
-/* The same decode attention, one 256-thread workgroup per query head and
- * sequence (grid H x batch), for caches of up to s_max <= 512 positions
- * (256 * ceil(s_max / 256) positions are supported by the launch).  Built for
- * latency: K rows load into registers before the position is known, the q
- * row is an SGPR operand of each score step, the softmax runs on four waves
- * in the shader's order and the two 256-position P.V blocks on separate
- * waves; same result bits as oxb_attn_decode.  Sequence z: q + z*H*128,
- * caches + z*kv_stride, pos[z*pos_stride], out + z*H*128.  The cache
- * allocations must extend OXB_KV_PAD_ROWS rows past the last head (V is read
- * in whole chunks).  Replaces nn/attention.rs:109-118 like oxb_attn_decode;
- * no counterpart of its own in the reference. */
+/* The same decode attention in one launch, one workgroup per query head and
+ * sequence (grid H x batch), for caches of up to s_max <= 512 positions.
+ * Built for latency: every K and V row is loaded before the position is
+ * known (clamped to the cache), each thread scores one position with q read
+ * from LDS, the softmax runs in the shader's order and waves 0 and 1 run the
+ * P.V chains (even and odd dims); same result bits as oxb_attn_decode.  Three
+ * kernels: s_max <= 256 with max_seq >= 256 (256 threads), s_max <= 256 with
+ * max_seq < 256 (256 threads; reads V in 64-row chunks past the position, so
+ * that cache allocation must extend OXB_KV_PAD_ROWS rows past its last head),
+ * and s_max <= 512 (512 threads).  Sequence z: q + z*H*128, caches +
+ * z*kv_stride, pos[z*pos_stride], out + z*H*128.  Replaces
+ * nn/attention.rs:109-118 like oxb_attn_decode; no counterpart of its own in
+ * the reference. */
 int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                          const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                          int Hkv, int hd, int max_seq, int s_max, float *out, void *stream);

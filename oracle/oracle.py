@@ -60,7 +60,7 @@ class _Model(C.Structure):
         ("eps", C.c_float), ("rope_theta", C.c_float), ("kv_f16", C.c_int),
         ("embed", _u16p), ("final_norm", _f32p), ("layers", C.POINTER(_Layer)),
         ("kcache", _f32p), ("vcache", _f32p), ("seq_len", C.c_int),
-        ("probe", ProbeFn), ("probe_ud", C.c_void_p),
+        ("probe", ProbeFn), ("probe_ud", C.c_void_p), ("pv_block", C.c_int),
     ]
 
 
@@ -85,6 +85,7 @@ def _declare(L):
         getattr(L, n).argtypes = [_f32p, _f32p, C.c_size_t, _f32p]
     L.oxo_rope.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
     L.oxo_attention.argtypes = [_f32p, _f32p, _f32p] + [C.c_int] * 5 + [_f32p]
+    L.oxo_attention_pv_blocked.argtypes = [_f32p, _f32p, _f32p] + [C.c_int] * 6 + [_f32p]
     L.oxo_softmax.argtypes = [_f32p, C.c_int, C.c_int, _f32p]
     L.oxo_embedding.argtypes = [_u32p, C.c_int, _u16p, C.c_int, C.c_int, _f32p]
     L.oxo_lm_head.argtypes = [_f32p, _u16p, C.c_int, C.c_int, _f32p]
@@ -233,10 +234,22 @@ def softmax(x):
 
 
 def attention(q, kc, vc, n_tok, S, H, Hkv, hd):
+    """sh/attention.wgsl + sh/softmax.wgsl: P.V in one loop over the positions."""
     q, kc, vc = _c(q, np.float32), _c(kc, np.float32), _c(vc, np.float32)
     out = np.zeros(n_tok * H * hd, np.float32)
     lib().oxo_attention(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p), n_tok, S, H, Hkv, hd,
                         _p(out, _f32p))
+    return out
+
+
+def attention_pv_blocked(q, kc, vc, n_tok, S, H, Hkv, hd, pv_block):
+    """The named non-reference variant: P.V summed in blocks of pv_block
+    positions, block sums added in order (identical to attention() while a
+    query has at most pv_block positions)."""
+    q, kc, vc = _c(q, np.float32), _c(kc, np.float32), _c(vc, np.float32)
+    out = np.zeros(n_tok * H * hd, np.float32)
+    lib().oxo_attention_pv_blocked(_p(q, _f32p), _p(kc, _f32p), _p(vc, _f32p), n_tok, S, H,
+                                   Hkv, hd, pv_block, _p(out, _f32p))
     return out
 
 
@@ -279,7 +292,10 @@ class Model:
     [rows, K/4], their per-tensor scales under "...weight_scale" as float,
     norms as float32, the embedding as uint16 [V, D] (f16 bits)."""
 
-    def __init__(self, cfg: dict, weights: dict, max_seq: int, kv_f16: bool = False):
+    def __init__(self, cfg: dict, weights: dict, max_seq: int, kv_f16: bool = False,
+                 pv_block: int = 0):
+        """pv_block 0: the reference's one-loop P.V; > 0: the blocked variant
+        (oxo_attention_pv_blocked), which no product path computes."""
         self.cfg = cfg
         self._keep = []
         L = cfg["n_layers"]
@@ -316,6 +332,7 @@ class Model:
         m.layers = self._layers
         m.kcache, m.vcache = _p(self.kcache, _f32p), _p(self.vcache, _f32p)
         m.seq_len = 0
+        m.pv_block = int(pv_block)
         self._m = m
 
     def _hold(self, a):

@@ -331,8 +331,9 @@ void oxo_softmax(const float *x, int rows, int D, float *y) {
 /* ------------------------------------------------------------------------ */
 /* attention (scores -> softmax -> attn_v)                                   */
 /* ------------------------------------------------------------------------ */
-void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
-                   int S, int H, int Hkv, int hd, float *out) {
+void oxo_attention_pv_blocked(const float *q, const float *kc, const float *vc,
+                              int n_tok, int S, int H, int Hkv, int hd,
+                              int pv_block, float *out) {
     float scale = 1.0f / sqrtf((float)hd); /* rs/nn/attention.rs:206 */
     int group = H / Hkv;
 #pragma omp parallel for schedule(static)
@@ -350,16 +351,15 @@ void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
             sc[kp] = causal ? -3.402823e+38f : dot * scale;
         }
         softmax_row(sc, S, pr);
-        /* sh/attention.wgsl:96-104 sums p[s] * v[s][d] over s in one loop.  Here
-         * the query's own positions (the masked ones contribute exact zeros)
-         * are summed in blocks of OXO_PV_BLOCK in order of s, and the block
-         * sums are added in block order; up to OXO_PV_BLOCK positions this is
-         * the shader's loop itself.  See the header. */
+        /* sh/attention.wgsl:96-104: one loop over s for each d.  The masked
+         * positions past the query's own (p = 0) add exact zeros and are not
+         * visited. */
         const int Sq = qp + (S - n_tok) + 1;
+        const int blk = pv_block > 0 ? pv_block : Sq;
         for (int d = 0; d < hd; d++) {
             float total = 0.0f;
-            for (int b0 = 0; b0 < Sq; b0 += OXO_PV_BLOCK) {
-                const int e = b0 + OXO_PV_BLOCK < Sq ? b0 + OXO_PV_BLOCK : Sq;
+            for (int b0 = 0; b0 < Sq; b0 += blk) {
+                const int e = b0 + blk < Sq ? b0 + blk : Sq;
                 float part = 0.0f;
                 for (int s = b0; s < e; s++) /* fused: see header */
                     part = fmaf(pr[s], vc[((size_t)s * Hkv + kvh) * hd + d], part);
@@ -370,6 +370,11 @@ void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
         free(sc);
         free(pr);
     }
+}
+
+void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
+                   int S, int H, int Hkv, int hd, float *out) {
+    oxo_attention_pv_blocked(q, kc, vc, n_tok, S, H, Hkv, hd, 0, out);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -497,7 +502,7 @@ int oxo_forward(oxo_model *m, const uint32_t *ids, int n, float *logits) {
             kc[(size_t)pos * kvd + i] = kv_k;
             vc[(size_t)pos * kvd + i] = kv_v;
         }
-        oxo_attention(qr, kc, vc, n, pos + n, H, Hkv, hd, att);
+        oxo_attention_pv_blocked(qr, kc, vc, n, pos + n, H, Hkv, hd, m->pv_block, att);
         probe(m, l, OXO_SITE_ATTN, att, f4 * (size_t)n * H * hd);
         bitlinear(m, l, OXO_SITE_O_Q8, att, n, H * hd, D, L->wo, L->so, L->attn_sub_norm, o);
         probe(m, l, OXO_SITE_O, o, f4 * nD);

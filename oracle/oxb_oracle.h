@@ -98,17 +98,21 @@ void oxo_rope(const float *x, int n_tok, int heads, int hd, int pos_offset,
  *      rs/nn/attention.rs:85-124 -------------------------------------------
  * q: [n_tok][H][hd]; K, V caches: [S][Hkv][hd] (S = positions incl. the new
  * ones); out: [n_tok][H][hd].
- * P.V association: the shader sums p[s] * v[s][d] in one loop over s.  Here
- * each query's positions are summed in blocks of OXO_PV_BLOCK = 256 in order
- * of s (one fmaf per step), and the block sums are added in block order, so
- * that the device can run the blocks of a long cache side by side instead of
- * one dependent chain per output.  For up to 256 positions this is the
- * shader's loop exactly; beyond, it is another association of the same sum,
- * whose distance from the one-loop order is pinned in the tests (far inside
- * the path's 1e-3 tolerance). */
-#define OXO_PV_BLOCK 256
+ * P.V (sh/attention.wgsl:96-104): out[d] = sum of p[s] * v[s][d] in one
+ * loop over s = 0 .. S-1, one fmaf per step (see the float conventions
+ * above); masked positions (p = 0) add exact zeros, so a query is summed over
+ * its own positions only. */
 void oxo_attention(const float *q, const float *kc, const float *vc, int n_tok,
                    int S, int H, int Hkv, int hd, float *out);
+/* The same attention with P.V summed in blocks of pv_block positions in order
+ * of s (each block from zero) and the block sums added in block order; the
+ * shader's one loop when pv_block <= 0 or pv_block >= S.  NOT the reference
+ * order past pv_block positions: a named variant kept so that the tests can
+ * show that they tell this association from the reference's (no product path
+ * computes it). */
+void oxo_attention_pv_blocked(const float *q, const float *kc, const float *vc,
+                              int n_tok, int S, int H, int Hkv, int hd,
+                              int pv_block, float *out);
 /* softmax rows in place order: sh/softmax.wgsl */
 void oxo_softmax(const float *x, int rows, int D, float *y);
 
@@ -175,6 +179,8 @@ typedef struct {
     int seq_len;
     oxo_probe_fn probe;     /* optional: intermediates, see OXO_SITE_* */
     void *probe_ud;
+    int pv_block;           /* 0: the reference's one-loop P.V; > 0: the named
+                               blocked variant (oxo_attention_pv_blocked) */
 } oxo_model;
 
 /* Forward n_tok ids at position model->seq_len; writes the last token's

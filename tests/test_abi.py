@@ -74,16 +74,16 @@ def test_operator_entry_points_check_arguments_first():
     their message before any device call (so this runs without a GPU)."""
     L = nat.lib()
     p = C.c_void_p(64)   # never dereferenced: every call below fails its checks first
-    assert L.oxb_attn_decode_batch_ws_bytes(0, 5, 100) == 0
-    assert L.oxb_attn_decode_batch_ws_bytes(2, 5, 300) == 2 * 5 * 2 * 4 * 128 * 4
-    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 5, 128, 300, p, None, p, None) == -1
-    assert _err() == "attention: pos, scores or ws is NULL"
-    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 5, 64, 300, p, p, p, None) == -1
+    assert L.oxb_attn_decode_batch(p, p, p, p, 8, 0, 1, 20, 5, 128, 300, None, p, None) == -1
+    assert _err() == "attention: pos or scores is NULL"
+    assert L.oxb_attn_decode_batch(p, p, p, p, 8, 0, 1, 20, 5, 64, 300, p, p, None) == -1
     assert _err() == "attention: head_dim 64 unsupported (128 only)"
-    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 0, 1, 20, 6, 128, 300, p, p, p, None) == -1
+    assert L.oxb_attn_decode_batch(p, p, p, p, 8, 0, 1, 20, 6, 128, 300, p, p, None) == -1
     assert _err() == "attention: heads 20 not a multiple of kv heads 6"
-    assert L.oxb_attn_decode_batch_ws(p, p, p, p, 8, 100, 2, 20, 5, 128, 300, p, p, p, None) == -1
+    assert L.oxb_attn_decode_batch(p, p, p, p, 8, 100, 2, 20, 5, 128, 300, p, p, None) == -1
     assert _err().startswith("attention: caches of a batch overlap")
+    assert L.oxb_attn_decode_batch(p, p, p, p, 8, 0, 1, 20, 5, 128, 6145, p, p, None) == -1
+    assert _err() == "attention: max_seq 6145 out of range (1..6144)"
     assert L.oxb_attn_prefill(p, p, p, 10, 95, 20, 5, 128, 100, p, None) == -1
     assert _err() == "prefill attention: bad range"
     assert L.oxb_attn_prefill(p, p, p, 10, 0, 20, 5, 64, 100, p, None) == -1

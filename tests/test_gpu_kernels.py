@@ -203,11 +203,18 @@ def _oracle_attn(q, kc16, vc16, n, S, H, Hkv, hd):
     return O.attention(q, k, v, n, S, H, Hkv, hd)
 
 
+# The two-launch decode attention (scores, then softmax and one P.V chain per
+# output over an LDS ring of 64-row V slots): first slot, slot edges (63/64,
+# 127/128), the ring wrapping (319/320 with five slots), G = 4, 2, 1 and 8 (two
+# groups of four heads per KV head), caches past 4864 rows (three slots),
+# lengths not a multiple of 4 (per-element score loads)
 @pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (64, 20, 5, 512),
-                                         (200, 20, 5, 512), (511, 20, 5, 512), (300, 8, 8, 4096),
+                                         (127, 20, 5, 512), (128, 20, 5, 512),
+                                         (200, 20, 5, 512), (319, 20, 5, 512), (320, 20, 5, 512),
+                                         (511, 20, 5, 512), (300, 8, 8, 4096),
                                          (700, 16, 8, 1024), (4095, 20, 5, 4096), (100, 16, 2, 256),
-                                         (2599, 20, 5, 2600),
-                                         # cache length not a multiple of 4: per-element score loads
+                                         (1500, 32, 4, 2048), (2599, 20, 5, 2600),
+                                         (6143, 20, 5, 6144), (4999, 16, 4, 5000),
                                          (200, 20, 5, 515), (514, 20, 5, 515)])
 def test_attn_decode_bitexact(pos, H, Hkv, S):
     rng = np.random.default_rng(pos + H)
@@ -220,13 +227,41 @@ def test_attn_decode_bitexact(pos, H, Hkv, S):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
-# the f32-MFMA P.V forced for one sequence (G = 4, 2, 1; 1 to 16 blocks)
-@pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (255, 20, 5, 512), (256, 20, 5, 512),
-                                         (2599, 20, 5, 2600), (4095, 20, 5, 4096),
-                                         (700, 16, 8, 1024), (300, 8, 8, 4096)])
-def test_attn_decode_mfma_pv_bitexact(pos, H, Hkv, S, monkeypatch):
-    monkeypatch.setenv("OXB_PV", "mfma")
-    test_attn_decode_bitexact(pos, H, Hkv, S)
+def test_attn_decode_rejects_caches_past_its_lds():
+    with pytest.raises(ops.NativeError, match="max_seq"):
+        ops.attn_decode(np.zeros(20 * 128, np.float32), np.zeros((5, 6145, 128), np.float16),
+                        np.zeros((5, 6145, 128), np.float16), 10, 20, 5, 128, 6145)
+
+
+def _nan_past(c, pos):
+    """Cache rows at and past pos + 1 filled with f16 NaN and +-Inf: no form
+    may read a value of them into a result."""
+    c = c.copy()
+    tail = c[..., pos + 1:, :]
+    pat = np.array([0x7e00, 0x7c00, 0xfc00, 0xfe01], np.uint16).view(np.float16)
+    tail[...] = np.resize(pat, tail.shape)
+    return c
+
+
+@pytest.mark.parametrize("form,pos,S", [("split", 100, 512), ("split", 300, 700),
+                                        ("head", 100, 512), ("head", 255, 512),
+                                        ("head", 300, 512), ("head", 20, 64),
+                                        ("fused", 100, 512), ("fused", 300, 600)])
+def test_attn_decode_ignores_nonfinite_rows_past_the_position(form, pos, S):
+    """Rows past the position hold NaN/Inf (stale or never-written cache rows
+    of a caller): every decode form gives the oracle's bits over the rows it
+    may use."""
+    H, Hkv, hd = 20, 5, 128
+    rng = np.random.default_rng(pos + S)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = _nan_past((rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16), pos)
+    vc = _nan_past(rng.standard_normal((Hkv, S, hd)).astype(np.float16), pos)
+    kw = {"head": dict(head=True, s_max=256 if pos < 256 else 512), "fused": dict(fused=True),
+          "split": {}}[form]
+    out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, **kw)
+    ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
+    assert np.isfinite(ref).all()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("pos,H,Hkv,S", [(0, 20, 5, 512), (63, 20, 5, 512), (255, 20, 5, 512),
@@ -257,7 +292,7 @@ def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     (0, 20, 5, 512, 256), (3, 20, 5, 512, 256), (63, 20, 5, 512, 256), (64, 20, 5, 512, 256),
     (127, 20, 5, 512, 256), (128, 20, 5, 300, 256), (139, 20, 5, 400, 256),
     (255, 20, 5, 256, 256),
-    # two groups (the second P.V block on waves 2-3): 257 .. 512 positions
+    # 257 .. 512 positions (one chain through both 256-row halves)
     (256, 20, 5, 512, 512), (300, 20, 5, 512, 512), (383, 20, 5, 384, 512),
     (511, 20, 5, 512, 512), (10, 20, 5, 512, 512), (400, 16, 2, 512, 512),
     (290, 8, 8, 300, 512),
@@ -310,19 +345,12 @@ def test_attn_decode_head_rejects_long_caches():
                         s_max=600)
 
 
-# pv: the P.V kernel the dispatch picks ("auto": f32 MFMA once batch x KV
-# heads >= 32, here B = 16, 40 and 9 x 8) or the one forced by OXB_PV; the
-# "ws" cases call oxb_attn_decode_batch_ws, whose MFMA P.V runs two blocks per
-# workgroup and adds the block sums in a second kernel while those workgroups
-# fit the CUs once (forced by OXB_PV=chunk)
-@pytest.mark.parametrize("pv", ["auto", "valu", "mfma", "ws", "ws_mfma", "ws_chunk"])
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
-                                       (9, 8, 8, 512), (8, 16, 8, 2600), (7, 20, 5, 1001)])
-def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
-    """Batched decode attention (per-slot caches and positions; the VALU P.V
-    takes the wide layout at B = 16 and 40): every slot equals the oracle."""
-    if pv in ("valu", "mfma", "ws_mfma", "ws_chunk"):
-        monkeypatch.setenv("OXB_PV", pv.removeprefix("ws_"))
+                                       (9, 8, 8, 512), (8, 16, 8, 2600), (7, 20, 5, 1001),
+                                       (32, 20, 5, 2560), (3, 32, 4, 700)])
+def test_attn_decode_batch_bitexact(B, H, Hkv, S):
+    """Batched decode attention (per-slot caches and positions): every slot
+    equals the oracle."""
     rng = np.random.default_rng(B * 13 + H)
     hd = 128
     q = rng.standard_normal((B, H * hd)).astype(np.float32)
@@ -339,16 +367,8 @@ def test_attn_decode_batch_bitexact(B, H, Hkv, S, pv, monkeypatch):
     dst = ops.DeviceArray.from_host(st)
     sc = ops.DeviceArray((B * H * S,), np.float32)
     out = ops.DeviceArray((B, H * hd), np.float32)
-    if pv.startswith("ws"):
-        nws = L.oxb_attn_decode_batch_ws_bytes(B, Hkv, S)
-        assert nws == B * Hkv * ((S + 255) // 256) * 4 * hd * 4
-        ws = ops.DeviceArray((nws // 4,), np.float32)
-        ops.check(L.oxb_attn_decode_batch_ws(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B,
-                                             H, Hkv, hd, S, sc.ptr, ws.ptr, out.ptr, None),
-                  "attn_decode_batch_ws")
-    else:
-        ops.check(L.oxb_attn_decode_batch(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H,
-                                          Hkv, hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
+    ops.check(L.oxb_attn_decode_batch(dq.ptr, dk.ptr, dv.ptr, dst.ptr, 8, Hkv * S * hd, B, H,
+                                      Hkv, hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
     ops.sync()
     got = out.download()
     for z in range(B):
@@ -367,13 +387,16 @@ def test_attn_decode_fused_rejects_unsupported():
 
 
 # Rows up to 2368 positions run on the f32-MFMA kernel (16 score rows per
-# workgroup: 16/G queries; ragged last blocks; rows that straddle a 256-position
-# P.V block; (0, 257) pairs rows of 256 and 257 positions), longer ones on the
-# VALU kernel (G = 4 and 8 take query pairs, G = 1, 2 one query per workgroup)
+# workgroup: 16/G queries, so for G = 1 and 2 the four rows of one P.V chain
+# group have different lengths; ragged last blocks; (0, 257) pairs rows of 256
+# and 257 positions; rows shorter than a 16-position batch), longer ones on
+# the VALU kernel (G = 4 and 8 take query pairs, G = 1, 2 one query per
+# workgroup)
 @pytest.mark.parametrize("H,Hkv,S,pos0,n", [(20, 5, 256, 30, 100), (20, 5, 512, 0, 257),
                                             (16, 2, 1200, 900, 31), (8, 8, 300, 5, 40),
                                             (16, 8, 300, 100, 33), (20, 5, 2100, 2040, 9),
-                                            (20, 5, 64, 0, 1),
+                                            (20, 5, 64, 0, 1), (4, 4, 64, 0, 19),
+                                            (8, 4, 200, 13, 37), (4, 4, 300, 250, 11),
                                             # 1001 queries over 4 P.V blocks, a lone last query
                                             (20, 5, 1100, 50, 1001),
                                             # the longest rows the MFMA kernel takes

@@ -212,81 +212,128 @@ def test_single_token_forward_is_decode_path():
 
 
 @pytest.mark.timeout(900)
-def test_bitnet_2b_shape_greedy_192():
-    """The 2B-shaped random-init model: 128-token prompt, 192 greedy steps
-    (positions 128..320: the one-kernel attention up to 256 positions, the
-    two-kernel form past it), logits bit-equal to the oracle at every step."""
+def test_bitnet_2b_shape_greedy_256():
+    """Config 3 end to end: the 2B-shaped random-init model, 128-token prompt,
+    256 greedy steps (positions 128..384: the one-kernel attention up to 256
+    positions, the 512-row one past it), logits bit-equal to the oracle (P.V
+    in the reference's one loop over every position) at every step."""
     path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
     prompt = np.random.default_rng(2024).integers(0, synth.BITNET_2B.vocab, 128).astype(np.int32)
-    toks = _greedy_parity(path, prompt, 192)
-    assert len(toks) == 193
+    toks = _greedy_parity(path, prompt, 256)
+    assert len(toks) == 257
 
 
-def test_bitnet_2b_shape_f32_cache_greedy_64():
-    """The 2B shape with the reference's f32 KV cache: 128-token prompt, 64
+@pytest.mark.timeout(900)
+def test_bitnet_2b_shape_f32_cache_greedy_256():
+    """Config 3 with the reference's f32 KV cache: 128-token prompt, 256
     greedy steps, logits bit-equal to the oracle's f32-cache path."""
     path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
     prompt = np.random.default_rng(2024).integers(0, synth.BITNET_2B.vocab, 128).astype(np.int32)
+    assert len(_greedy_parity(path, prompt, 256, kv_f16=False)) == 257
+
+
+@pytest.mark.timeout(900)
+def test_bitnet_2b_shape_f32_cache_300_prompt_64_steps():
+    """The 2B shape, f32 KV cache, a 300-token prompt (prefill rows past 256
+    positions) and 64 greedy steps, bit-equal to the oracle."""
+    path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
+    prompt = np.random.default_rng(2025).integers(0, synth.BITNET_2B.vocab, 300).astype(np.int32)
     assert len(_greedy_parity(path, prompt, 64, kv_f16=False)) == 65
 
 
-# ---- long context: 2048-token prefill, then batched decode (bs 8 and 32) ----
+# ---- long context: 2048-token prefill, then decode (bs 1, 8 and 32) --------
 LONG = 2048
-LONG_STEPS = 8
+LONG_STEPS = 64
 
 
 def _long_prompt(slot: int) -> np.ndarray:
     return np.random.default_rng([77, slot]).integers(0, synth.BITNET_2B.vocab, LONG).astype(np.int32)
 
 
-@pytest.fixture(scope="module")
-def long_oracle():
-    """The oracle on slot 0's 2048-token prompt: prefill logits and the
+def _oracle_long(path, slot, kv_f16=True):
+    """The oracle on slot `slot`'s 2048-token prompt: prefill logits and the
     logits after each of LONG_STEPS greedy steps."""
-    path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
     cfg, w = oracle_weights(path)
-    om = O.Model(cfg, w, max_seq=LONG + LONG_STEPS + 2, kv_f16=True)
-    out = [om.forward(_long_prompt(0).astype(np.uint32))]
+    om = O.Model(cfg, w, max_seq=LONG + LONG_STEPS + 2, kv_f16=kv_f16)
+    out = [om.forward(_long_prompt(slot).astype(np.uint32))]
     for _ in range(LONG_STEPS):
         out.append(om.forward(np.array([O.argmax(out[-1])], np.uint32)))
-    return path, out
+    return out
+
+
+@pytest.fixture(scope="module")
+def long_oracle():
+    """(path, {slot: oracle logits}) for slots 0 and 1 (f16 KV cache)."""
+    path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
+    return path, {0: _oracle_long(path, 0), 1: _oracle_long(path, 1)}
+
+
+def _long_run(m, slot):
+    """Greedy tokens and logits of slot `slot`'s prompt on model m (reset)."""
+    m.reset()
+    tok, logits = m.forward(_long_prompt(slot))
+    out, toks = [logits], [tok]
+    for _ in range(LONG_STEPS):
+        tok, logits = m.step()
+        out.append(logits)
+        toks.append(tok)
+    return toks, out
+
+
+def _long_single(path, slot, kv="f16"):
+    m = pkg.Model(path, max_seq=LONG + LONG_STEPS + 2, kv=kv)
+    try:
+        return _long_run(m, slot)
+    finally:
+        m.close()
 
 
 @pytest.mark.timeout(900)
-def test_bitnet_2b_prefill_2048_and_decode(long_oracle):
+def test_bitnet_2b_prefill_2048_and_decode_64(long_oracle):
+    """Config 4 at bs 1: 2048-token prefill, then 64 greedy steps (positions
+    2048..2112), every logit bit-equal to the oracle."""
     path, ref = long_oracle
-    m = pkg.Model(path, max_seq=LONG + LONG_STEPS + 2)
-    tok, logits = m.forward(_long_prompt(0))
-    _same(logits, ref[0], "2048-token prefill")
+    toks, out = _long_single(path, 0)
+    _same(out[0], ref[0][0], "2048-token prefill")
     for i in range(LONG_STEPS):
-        assert tok == O.argmax(ref[i])
-        tok, logits = m.step()
-        _same(logits, ref[i + 1], f"step {i} at position {LONG + i}")
-    m.close()
+        assert toks[i] == O.argmax(ref[0][i]), f"step {i}"
+        _same(out[i + 1], ref[0][i + 1], f"step {i} at position {LONG + i}")
+
+
+@pytest.mark.timeout(900)
+def test_bitnet_2b_f32_cache_prefill_2048_and_decode_64():
+    """Config 4 at bs 1 with the reference's f32 KV cache, bit-equal to the
+    oracle's f32 path."""
+    path = synth.cached_gguf(synth.BITNET_2B, seed=1234)
+    ref = _oracle_long(path, 0, kv_f16=False)
+    toks, out = _long_single(path, 0, kv="f32")
+    _same(out[0], ref[0], "2048-token prefill (f32 cache)")
+    for i in range(LONG_STEPS):
+        assert toks[i] == O.argmax(ref[i]), f"step {i}"
+        _same(out[i + 1], ref[i + 1], f"step {i} at position {LONG + i} (f32 cache)")
 
 
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("B", [8, 32])
 def test_bitnet_2b_batched_decode_after_2048(long_oracle, B):
     """B slots, each prefilled with its own 2048-token prompt, decoded
-    together: every slot's tokens and last logits equal that sequence decoded
-    alone, and slot 0 equals the oracle."""
+    together for 64 steps: slots 0 and 1 equal the oracle at every step's
+    token and at the last logits, and every slot's tokens and last logits
+    equal that sequence decoded alone."""
     path, ref = long_oracle
     m = pkg.Model(path, max_seq=LONG + LONG_STEPS + 2)
     b = pkg.Batch(m, B, 2560)
     first = [b.prefill(i, _long_prompt(i)) for i in range(B)]
     got = b.decode_greedy(LONG_STEPS)
     last = b.logits()
-    _same(last[0], ref[-1], "batched slot 0 vs oracle")
-    for i in range(B):
-        m.reset()
-        tok, _ = m.forward(_long_prompt(i), want_logits=False)
-        toks, lg = [tok], None
-        for _ in range(LONG_STEPS):
-            tok, lg = m.step()
-            toks.append(tok)
+    for z in (0, 1):
+        toks = [first[z]] + got[z].tolist()
+        assert toks == [O.argmax(r) for r in ref[z]], f"slot {z} vs oracle"
+        _same(last[z], ref[z][-1], f"batched slot {z} vs oracle")
+    for i in range(2, B):
+        toks, lg = _long_run(m, i)
         assert [first[i]] + got[i].tolist() == toks, f"slot {i}"
-        _same(last[i], lg, f"slot {i}")
+        _same(last[i], lg[-1], f"slot {i}")
     b.close()
     m.close()
 

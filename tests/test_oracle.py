@@ -10,6 +10,8 @@ import json
 import math
 import os
 
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
@@ -313,12 +315,67 @@ def test_attention_closed_forms():
     assert o.reshape(4, 4)[:, 0].tolist() == [1, 1, 2, 2]
 
 
+def _f32_round(x: Fraction) -> float:
+    """An exact rational rounded to the nearest f32 (ties to even), as an
+    IEEE single-precision fused multiply-add rounds its exact result."""
+    if x == 0:
+        return 0.0
+    neg, x = x < 0, abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    e = max(e, -126)                      # subnormals share the smallest exponent
+    m = x * Fraction(2) ** (23 - e)       # 24 significant bits above the point
+    q, r = divmod(m.numerator, m.denominator)
+    if 2 * r > m.denominator or (2 * r == m.denominator and q & 1):
+        q += 1
+    v = float(Fraction(q) * Fraction(2) ** (e - 23))
+    return -v if neg else v
+
+
+def _fma_chain(p, v):
+    """sum_s p[s] * v[s] as one f32 fused multiply-add per step, in order of s
+    (sh/attention.wgsl:96-104 with each step fused), exactly."""
+    acc = 0.0
+    for a, b in zip(p, v):
+        acc = _f32_round(Fraction(float(a)) * Fraction(float(b)) + Fraction(acc))
+    return acc
+
+
+@pytest.mark.parametrize("S", [7, 256, 300, 700])
+def test_attention_pv_is_one_fused_chain_over_all_positions(S):
+    """P.V of the reference is one loop over every position.  With all K rows
+    equal every score is the same, so p[s] = exp(0) * (1 / sum) is one known
+    f32 value; V holds values whose sum depends on the association (2^24-
+    scale terms beside small ones, cancelling across the 256-position mark).
+    The oracle's output must be the exact sequential fma chain computed here
+    from rationals, for every dim; the blocked variant (256-position blocks)
+    must differ from it once S > 256 and equal it up to 256."""
+    rng = np.random.default_rng(S)
+    hd, H, Hkv = 8, 2, 1
+    q = rng.standard_normal((1, H, hd)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, Hkv, hd)).astype(np.float32), S, axis=0)
+    v = rng.integers(-9, 10, (S, Hkv, hd)).astype(np.float32) * np.float32(0.125)
+    v[0, 0, :] = 2.0 ** 24 * S        # a large first term: later small terms round away
+    if S > 256:
+        v[256, 0, :] = -(2.0 ** 24) * S   # ... until it cancels at the 256th position
+    out = O.attention(q, k, v, 1, S, H, Hkv, hd).reshape(H, hd)
+    # p = exp(0) * (1 / sum): the row sum of S exact ones is S in any order
+    pval = np.float32(1.0) * (np.float32(1.0) / np.float32(S))
+    for d in range(hd):
+        want = _fma_chain([pval] * S, v[:, 0, d])
+        assert out[0, d] == np.float32(want) and out[1, d] == np.float32(want), d
+    blk = O.attention_pv_blocked(q, k, v, 1, S, H, Hkv, hd, 256).reshape(H, hd)
+    if S > 256:
+        assert np.any(blk != out)
+    else:
+        assert np.array_equal(blk, out)
+
+
 @pytest.mark.parametrize("S", [200, 256, 257, 700, 2304])
-def test_attention_pv_blocks_against_float64(S):
-    """P.V is summed in blocks of 256 positions, block sums added in order (up
-    to 256 positions: the shader's one loop).  Against float64 attention the
-    f32 result stays within 2e-6 of the sum of |p v| terms at every length,
-    the same accuracy as the one-loop order, and 500x inside the 1e-3 bound."""
+def test_attention_pv_against_float64(S):
+    """The one-loop P.V against float64 attention: within 2e-6 of the sum of
+    |p v| terms at every length, 500x inside the path's 1e-3 bound."""
     rng = np.random.default_rng(S)
     hd, H, Hkv = 128, 4, 1
     q = rng.standard_normal((1, H, hd)).astype(np.float32)
