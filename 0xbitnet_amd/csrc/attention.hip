@@ -308,33 +308,35 @@ __device__ inline float pv_chain(const float *p, const float *v, int n, float ac
 // ---------------------------------------------------------------------------
 // Decode P.V in the reference's association: out[d] = sum of p[s] * v[s][d]
 // in one loop over every position s (sh/attention.wgsl:96-104), one fused
-// step per position, on f32 MFMA.  v_mfma_f32_4x4x1_16b adds one product per
-// output per instruction with one rounding (the fused step, as the 16x16x1
-// form in the prefill kernel): lane l supplies A[block l/4][row l%4] and
-// B[block l/4][col l%4], and holds D[block l/4][row r][col l%4] in register
-// r.  Rows are four query heads of the KV head (A = p[head][s], the same in
-// all 16 blocks; rows past the group's heads are never stored), columns 64
-// dims: wave 0 chains the even dims 2l, wave 1 the odd dims 2l + 1, both from
-// dword l of the f16 V row (converted exactly to f32).
-// One 16-wave workgroup per (KV head, group of four heads, sequence):
+// multiply-add per position.  A sequential sum is a chain of dependent
+// steps, so what bounds it is the step latency: a dependent v_fma_mix_f32
+// (f16 V operand converted inside the instruction) issues every ~4.4 cycles
+// from one wave per SIMD, against ~12.4 for a dependent 4x4x1 f32 MFMA.
+// One 16-wave workgroup per (KV head, group of four heads, half of the dims,
+// sequence):
 //  - softmax of row r on waves 4r .. 4r+3 (wave 4r + j, lane l playing
 //    thread 64j + l of the shader's 256-thread workgroup) into LDS rows;
-//  - the V rows stream into an LDS ring of NS slots of kPcRows rows,
-//    staged by every wave with global_load_lds_dwordx4 (four 256-byte rows
-//    per wave and slot) NS - 1 slots ahead: iteration c waits for the
-//    wave's own loads of slot c, a barrier publishes the slot (and frees slot
-//    c - 1, whose ring entry the next loads refill), and waves 0 and 1 sum
-//    slot c.  Rows past the cache length are clamped to its last row (staged,
-//    never summed), so the loads are unconditional and the waits exact; the
-//    chains stop at S.
-// LDS (dynamic): ring [NS][kPcRows][64 dwords] | p [4][Sp] | red [4][256] | wmax [16]
+//  - the V rows' half (128 bytes per position) stream into an LDS ring of NS
+//    slots of kPcRows rows, staged with global_load_lds_dwordx4 by every wave
+//    (8 rows per wave and slot) NS - 1 slots ahead.  Iteration c: each wave
+//    waits for its own loads of slot c + 1, a barrier publishes slots c and
+//    c + 1 and frees slot c - 1, whose ring entry the next loads refill;
+//  - waves 0 .. 3 (one per SIMD) run the chains: wave w takes heads 2(w/2)
+//    and 2(w/2) + 1 (lanes 0-31 and 32-63) and the low (w even) or high half
+//    of dword lane % 32 of the half row, so lane l chains dim 64 h + 2 (l %
+//    32) + w % 2 of its head.  Their barriers carry no LDS fence: reads of
+//    the published slots stay in flight across them.
+// Rows past the cache length are clamped to its last row (staged, never
+// summed), so the loads are unconditional and the waits exact; the chains
+// stop at S.
+// LDS (dynamic): ring [NS][kPcRows][32 dwords] | p [4][Sp] | red [4][256] | wmax [16]
 // ---------------------------------------------------------------------------
-typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kPcWaves = 16;
 constexpr int kPcThreads = 64 * kPcWaves;
-constexpr int kPcRows = 4 * kPcWaves;        // V rows per ring slot (one DMA per wave)
-constexpr int kPcSlotBytes = kPcRows * kHd * 2;
-constexpr int kPcMaxSeq = 6144;               // score rows of up to 24 x 256 positions
+constexpr int kPcRows = 8 * kPcWaves;        // V rows per ring slot (one DMA per wave)
+constexpr int kPcRowDw = kHd / 4;            // dwords of half a V row
+constexpr int kPcSlotBytes = kPcRows * kPcRowDw * 4;
+constexpr int kPcMaxSeq = 6144;              // score rows of up to 24 x 256 positions
 constexpr int kPcMaxNI = (kPcMaxSeq + 255) / 256;
 
 __host__ __device__ inline int pc_row_stride(int max_seq) { return ((max_seq + 15) & ~15) + 4; }
@@ -392,44 +394,41 @@ __device__ __forceinline__ void softmax_row_4w_any(float *prow, const float *src
     else softmax_row_4w<kPcMaxNI>(prow, src, S, has_row, wm, red, j, lane);
 }
 
-// n positions (1 .. 64) of one ring slot into the chain: vs = dword `lane` of
-// the slot's row 0 (rows 64 dwords apart), pp = the lane's p row at the
-// slot's first position.  Groups of four positions, operands read three
-// groups ahead (ring entries rotate with the group); whole groups run
-// without selects, the last partial group keeps the old sums past n.
+// acc + sum of p[s] * v_s over the n (all 4 when FULL) positions of a group,
+// in order of s; v_s the low (HI false) or high half of dword V[s]
+template <bool HI, bool FULL>
+__device__ __forceinline__ float pv4(float acc, const uint32_t (&V)[4], const float4 &P, int n = 4) {
+    const float pp[4] = {P.x, P.y, P.z, P.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t u = V[k];
+        const float v = __half2float(__ushort_as_half((uint16_t)(HI ? u >> 16 : u & 0xffffu)));
+        const float t = __builtin_fmaf(pp[k], v, acc);
+        acc = FULL || k < n ? t : acc;
+    }
+    return acc;
+}
+
+// n positions (1 .. kPcRows) of one ring slot into a lane's chain: vs = the
+// lane's dword in the slot's row 0 (rows kPcRowDw dwords apart), pp = the
+// lane's p row at the slot's first position.  Groups of four positions,
+// operands read three groups ahead; 16 positions per unrolled iteration (a
+// loop's back edge would wait for every LDS read in flight), the last n % 16
+// from ring entries 0..3.
 template <bool HI>
-__device__ __forceinline__ void pc_chain_slot(v4f &acc, const uint32_t *vs, const float *pp, int n) {
+__device__ __forceinline__ float pc_chain_slot(float acc, const uint32_t *vs, const float *pp,
+                                               int n) {
     uint32_t V[4][4];
     float4 P[4];
     auto ld = [&](int b, int g) {   // group g (clamped into the slot) into entry b
         g = min(g, kPcRows / 4 - 1);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) V[b][k] = vs[(4 * g + k) * (kHd / 2)];
+        for (int k = 0; k < 4; ++k) V[b][k] = vs[(4 * g + k) * kPcRowDw];
         P[b] = *(const float4 *)(pp + 4 * g);
-    };
-    auto vf = [](uint32_t u) {
-        return __half2float(__ushort_as_half((uint16_t)(HI ? u >> 16 : u & 0xffffu)));
-    };
-    auto full = [&](const uint32_t (&v4)[4], const float4 &p4) {
-        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.x, vf(v4[0]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.y, vf(v4[1]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.z, vf(v4[2]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(p4.w, vf(v4[3]), acc, 0, 0, 0);
-    };
-    auto part = [&](const uint32_t (&v4)[4], const float4 &p4, int m) {   // m < 4 positions
-        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const v4f r = __builtin_amdgcn_mfma_f32_4x4x1f32(pv[k], vf(v4[k]), acc, 0, 0, 0);
-            acc = k < m ? r : acc;
-        }
     };
     ld(0, 0);
     ld(1, 1);
     ld(2, 2);
-    // 16 positions per iteration, fully unrolled (exits are wave-uniform
-    // branches): a loop's back edge would wait for every LDS read in flight.
-    // At the top of an iteration entries 0..2 hold its groups 0..2.
     int s0 = 0;
 #pragma unroll
     for (int it = 0; it < kPcRows / 16; ++it) {
@@ -439,18 +438,20 @@ __device__ __forceinline__ void pc_chain_slot(v4f &acc, const uint32_t *vs, cons
             __builtin_amdgcn_sched_barrier(0);
             ld((j + 3) & 3, s0 / 4 + j + 3);
             __builtin_amdgcn_sched_barrier(0);
-            full(V[j], P[j]);
+            acc = pv4<HI, true>(acc, V[j], P[j]);
         }
         s0 += 16;
     }
-    if (s0 >= n) return;
-    ld(3, s0 / 4 + 3);   // the last n - s0 < 16 positions: entries 0..3
+    if (s0 < n) {
+        ld(3, s0 / 4 + 3);   // entries 0..2 hold groups s0/4 .. s0/4 + 2
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = n - s0 - 4 * j;
-        if (m >= 4) full(V[j], P[j]);
-        else if (m > 0) part(V[j], P[j], m);
+        for (int j = 0; j < 4; ++j) {
+            const int m = n - s0 - 4 * j;
+            if (m >= 4) acc = pv4<HI, true>(acc, V[j], P[j]);
+            else if (m > 0) acc = pv4<HI, false>(acc, V[j], P[j], m);
+        }
     }
+    return acc;
 }
 
 template <int NS>
@@ -458,13 +459,14 @@ __global__ __launch_bounds__(kPcThreads) void attn_pv_chain_kernel(
     const float *__restrict__ scores, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int G, int max_seq, float *__restrict__ out,
     size_t kv_stride, int pos_stride) {
-    static_assert(NS >= 3 && NS - 2 < 64, "ring depth within vmcnt");
+    static_assert(NS >= 3 && NS - 3 < 64, "ring depth within vmcnt");
     const int RG = (G + 3) >> 2;                  // groups of four heads per KV head
-    const int hk = blockIdx.x / RG, rg = blockIdx.x % RG, z = blockIdx.y;
-    const int Hkv = gridDim.x / RG, H = Hkv * G;
+    const int dh = blockIdx.x & 1, hg = blockIdx.x >> 1;
+    const int hk = hg / RG, rg = hg % RG, z = blockIdx.y;
+    const int Hkv = (gridDim.x >> 1) / RG, H = Hkv * G;
     scores += (size_t)z * H * max_seq;
-    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
-    out += (size_t)z * H * kHd;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd + 64 * dh;
+    out += (size_t)z * H * kHd + 64 * dh;
     extern __shared__ __align__(16) int8_t smem_pc[];
     uint4 *ring = (uint4 *)smem_pc;
     const int Sp = pc_row_stride(max_seq);
@@ -477,45 +479,176 @@ __global__ __launch_bounds__(kPcThreads) void attn_pv_chain_kernel(
     const int S = pos + 1;
     const int nslots = (S + kPcRows - 1) / kPcRows;
 
-    // this wave's share of a slot: rows 4w .. 4w+3 (lane: row 4w + lane/16,
-    // 16 bytes lane % 16), clamped to the cache length
-    const uint4 *V4 = (const uint4 *)vc;
+    // this wave's share of a slot: rows 8w .. 8w+7 (lane: row 8w + lane/8,
+    // 16 bytes lane % 8 of the half row), clamped to the cache length
     auto issue = [&](int c) {
-        const int row = min(c * kPcRows + 4 * w + (lane >> 4), S - 1);
-        lds_dma16(V4 + (size_t)row * (kHd / 8) + (lane & 15),
-                  ring + ((size_t)(c % NS) * kPcRows + 4 * w) * (kHd / 8));
+        const int row = min(c * kPcRows + 8 * w + (lane >> 3), S - 1);
+        lds_dma16(vc + (size_t)row * kHd + 8 * (lane & 7),
+                  ring + ((size_t)(c % NS) * kPcRows + 8 * w) * (kPcRowDw / 4));
     };
 #pragma unroll
     for (int c = 0; c < NS - 1; ++c) issue(c);
 
-    // ---- softmax: row r = w / 4 (heads 4rg + r of the KV head) -------------
+    // ---- softmax: row r = w / 4 (head 4rg + r of the KV head) -------------
     {
         const int r = w >> 2, j = w & 3, head = 4 * rg + r;
-        const bool has_row = head < G;
         softmax_row_4w_any(pr + r * Sp, scores + (size_t)(hk * G + min(head, G - 1)) * max_seq, S,
-                           has_row, wmax + 4 * r, red + 256 * r, j, lane);
+                           head < G, wmax + 4 * r, red + 256 * r, j, lane);
     }
 
     // ---- P.V chains over the ring --------------------------------------------
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float *prow = pr + (lane & 3) * Sp;
+    const int r = 2 * (w >> 1) + (lane >> 5);   // the lane's row (chain waves)
+    const float *prow = pr + r * Sp;
+    float acc = 0.0f;
     for (int c = 0; c < nslots; ++c) {
-        wait_vmcnt<NS - 2>();   // this wave's loads of slot c have landed
-        lds_barrier();          // ... every wave's; slot c - 1 is consumed (and p is written)
+        wait_vmcnt<NS - 3>();   // this wave's loads of slots c and c + 1 have landed
+        if (w < 4 && c > 0) {
+            // no LDS fence: published slots may still be read in flight, and
+            // slot c - 1, which the next loads refill, was consumed (its
+            // values feed the sums computed before this point); these waves
+            // write no LDS after the softmax, whose rows the first (fenced)
+            // barrier publishes
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            lds_barrier();
+        }
         issue(c + NS - 1);      // into slot c - 1's ring entry (clamped past the cache)
-        if (w < 2) {
-            const uint32_t *vs = (const uint32_t *)(ring + (size_t)(c % NS) * kPcRows * (kHd / 8)) + lane;
+        if (w < 4) {
+            const uint32_t *vs =
+                (const uint32_t *)(ring + (size_t)(c % NS) * kPcRows * (kPcRowDw / 4)) + (lane & 31);
             const int n = min(kPcRows, S - c * kPcRows);
-            if (w == 0) pc_chain_slot<false>(acc, vs, prow + c * kPcRows, n);
-            else pc_chain_slot<true>(acc, vs, prow + c * kPcRows, n);
+            acc = (w & 1) ? pc_chain_slot<true>(acc, vs, prow + c * kPcRows, n)
+                          : pc_chain_slot<false>(acc, vs, prow + c * kPcRows, n);
         }
     }
     wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
-    if (w < 2) {
+    if (w < 4 && 4 * rg + r < G)
+        out[(size_t)(hk * G + 4 * rg + r) * kHd + 2 * (lane & 31) + (w & 1)] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// The same P.V with one chain wave per CU, for few sequences: a workgroup of
+// 4 waves per (query head, parity of the dims, sequence).  What bounds the
+// chain above is the LDS's return path: every chain wave reads 256 bytes per
+// position of V (its dword of the row) and 256 of p (a broadcast read of
+// four positions returns 16 bytes to each lane), ~4 cycles of the CU's LDS
+// per wave and position against ~4.4 for the fused step; with four chain
+// waves on a CU the LDS takes ~16.  Here wave 0 runs the CU's one chain
+// wave: lane l chains dim 2l + parity (the low or high half of dword l of
+// the full f16 row, read two positions at a time); all four waves run the
+// row's softmax (the 256-thread order) and stage the V rows through the
+// ring.  The 2G workgroups of a KV head take block indices congruent mod 8,
+// so they run on one XCD and its L2 serves their shared V rows: block b ->
+// KV head 8 (b / (16 G)) + b % 8, item (b / 8) % (2G); blocks whose KV head
+// is past the last are idle.
+// LDS (dynamic): ring [NS][kPhRows][64 dwords] | p [Sp] | red [256] | wmax [4]
+// ---------------------------------------------------------------------------
+constexpr int kPhWaves = 4;
+constexpr int kPhThreads = 64 * kPhWaves;
+constexpr int kPhRows = 64;                      // V rows per ring slot (4 DMA per wave)
+constexpr int kPhSlotBytes = kPhRows * kHd * 2;
+constexpr int kPhMaxBatch = 8;                  // sequences that take this kernel
+
+__host__ __device__ inline size_t ph_smem(int slots, int max_seq) {
+    return (size_t)slots * kPhSlotBytes + ((size_t)pc_row_stride(max_seq) + 256 + 8) * 4;
+}
+
+template <bool HI>
+__device__ __forceinline__ float ph_chain_slot(float acc, const uint32_t *vs, const float *pp, int n) {
+    uint32_t V[4][4];
+    float4 P[4];
+    auto ld = [&](int b, int g) {   // group g (clamped into the slot) into entry b
+        g = min(g, kPhRows / 4 - 1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (4 * rg + r < G) out[(size_t)(hk * G + 4 * rg + r) * kHd + 2 * lane + w] = acc[r];
+        for (int k = 0; k < 4; ++k) V[b][k] = vs[(4 * g + k) * (kHd / 2)];
+        P[b] = *(const float4 *)(pp + 4 * g);
+    };
+    ld(0, 0);
+    ld(1, 1);
+    ld(2, 2);
+    int s0 = 0;
+#pragma unroll
+    for (int it = 0; it < kPhRows / 16; ++it) {
+        if (s0 + 16 > n) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            ld((j + 3) & 3, s0 / 4 + j + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv4<HI, true>(acc, V[j], P[j]);
+        }
+        s0 += 16;
     }
+    if (s0 < n) {
+        ld(3, s0 / 4 + 3);   // entries 0..2 hold groups s0/4 .. s0/4 + 2
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = n - s0 - 4 * j;
+            if (m >= 4) acc = pv4<HI, true>(acc, V[j], P[j]);
+            else if (m > 0) acc = pv4<HI, false>(acc, V[j], P[j], m);
+        }
+    }
+    return acc;
+}
+
+template <int NS>
+__global__ __launch_bounds__(kPhThreads) void attn_pv_head_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc,
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float *__restrict__ out,
+    size_t kv_stride, int pos_stride) {
+    static_assert(NS >= 3 && 4 * (NS - 3) < 64, "ring depth within vmcnt");
+    const int b = blockIdx.x, z = blockIdx.y;
+    const int hk = 8 * (b / (16 * G)) + (b & 7), item = (b >> 3) % (2 * G);
+    if (hk >= Hkv) return;
+    const int h = hk * G + (item >> 1), parity = item & 1, H = Hkv * G;
+    scores += (size_t)z * H * max_seq + (size_t)h * max_seq;
+    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    out += (size_t)z * H * kHd + (size_t)h * kHd;
+    extern __shared__ __align__(16) int8_t smem_ph[];
+    uint4 *ring = (uint4 *)smem_ph;
+    float *pr = (float *)(smem_ph + (size_t)NS * kPhSlotBytes);
+    float *red = pr + pc_row_stride(max_seq), *wmax = red + 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1;
+    const int nslots = (S + kPhRows - 1) / kPhRows;
+
+    // this wave's share of a slot: rows 16w .. 16w+15 as four 4-row loads
+    // (lane: row + lane/16, 16 bytes lane % 16 of the row), clamped
+    const uint4 *V4 = (const uint4 *)vc;
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r0 = 16 * w + 4 * k;
+            const int row = min(c * kPhRows + r0 + (lane >> 4), S - 1);
+            lds_dma16(V4 + (size_t)row * (kHd / 8) + (lane & 15),
+                      ring + ((size_t)(c % NS) * kPhRows + r0) * (kHd / 8));
+        }
+    };
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+
+    softmax_row_4w_any(pr, scores, S, true, wmax, red, w, lane);
+
+    float acc = 0.0f;
+    for (int c = 0; c < nslots; ++c) {
+        wait_vmcnt<4 * (NS - 3)>();   // this wave's loads of slots c and c + 1 have landed
+        if (w == 0 && c > 0)
+            asm volatile("s_barrier" ::: "memory");   // reads in flight stay (see the 4-head kernel)
+        else
+            lds_barrier();
+        issue(c + NS - 1);
+        if (w == 0) {
+            const uint32_t *vs = (const uint32_t *)(ring + (size_t)(c % NS) * kPhRows * (kHd / 8)) + lane;
+            const int n = min(kPhRows, S - c * kPhRows);
+            acc = parity ? ph_chain_slot<true>(acc, vs, pr + c * kPhRows, n)
+                         : ph_chain_slot<false>(acc, vs, pr + c * kPhRows, n);
+        }
+    }
+    wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
+    if (w == 0) out[2 * lane + parity] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -694,6 +827,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 // banks.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kPfmWaves = 16;
 constexpr int kPfmThreads = 64 * kPfmWaves;
 constexpr int kPfmQs = kHd + 4;   // q row stride (floats)
@@ -1335,21 +1469,6 @@ constexpr size_t kH256KBytes = (size_t)kH256Rows * 17 * 16;   // K rows, padded
 constexpr size_t kH256VBytes = (size_t)kH256Rows * kHd * 2;   // V rows
 constexpr size_t kH256Lds = kH256KBytes + kH256VBytes + (kHd + 256 + 256 + 8) * 4;
 
-// acc + sum of p[s] * v_s over the n (all 4 when FULL) positions of a block,
-// in order of s; v_s the low (HI false) or high half of dword V[s]
-template <bool HI, bool FULL>
-__device__ __forceinline__ float pv4(float acc, const uint32_t (&V)[4], const float4 &P, int n = 4) {
-    const float pp[4] = {P.x, P.y, P.z, P.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t u = V[k];
-        const float v = __half2float(__ushort_as_half((uint16_t)(HI ? u >> 16 : u & 0xffffu)));
-        const float t = __builtin_fmaf(pp[k], v, acc);
-        acc = FULL || k < n ? t : acc;
-    }
-    return acc;
-}
-
 // P.V of one wave: lane j's chain over the S positions (S <= ROWS) of dim
 // 2j + HI, in order of s; vcol = the V rows' dword j (row stride 64 dwords)
 template <bool HI, int ROWS>
@@ -1735,7 +1854,21 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
-    const dim3 grid(Hkv * ((G + 3) / 4), batch);
+    if (batch <= kPhMaxBatch) {   // one chain wave per CU
+        const dim3 hgrid(16 * G * ((Hkv + 7) / 8), batch);
+        if (ph_smem(6, max_seq) <= 160 * 1024) {
+            if (allow_dynamic_lds((const void *)attn_pv_head_kernel<6>)) return -1;
+            hipLaunchKernelGGL(attn_pv_head_kernel<6>, hgrid, dim3(kPhThreads), ph_smem(6, max_seq),
+                               s, scores, vc, pos, G, Hkv, max_seq, out, kv_stride, pos_stride);
+        } else {
+            if (allow_dynamic_lds((const void *)attn_pv_head_kernel<4>)) return -1;
+            hipLaunchKernelGGL(attn_pv_head_kernel<4>, hgrid, dim3(kPhThreads), ph_smem(4, max_seq),
+                               s, scores, vc, pos, G, Hkv, max_seq, out, kv_stride, pos_stride);
+        }
+        OXB_CHECK_HIP(hipGetLastError());
+        return 0;
+    }
+    const dim3 grid(Hkv * ((G + 3) / 4) * 2, batch);
     if (pc_smem(5, max_seq) <= 160 * 1024) {
         if (allow_dynamic_lds((const void *)attn_pv_chain_kernel<5>)) return -1;
         hipLaunchKernelGGL(attn_pv_chain_kernel<5>, grid, dim3(kPcThreads), pc_smem(5, max_seq), s,
