@@ -99,6 +99,9 @@ SIGNATURES = {
     "oxb_attn_decode_fused": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "oxb_sample_logits": (C.c_int32, [vp, C.c_size_t, C.c_float, C.c_size_t, C.c_float, vp,
                                       C.c_size_t, C.c_float]),
+    "oxb_sample_ws_bytes": (C.c_size_t, [i32]),
+    "oxb_sample_device": (C.c_int, [vp, i32, C.c_float, C.c_size_t, C.c_float, vp, i32, vp, vp,
+                                    vp, C.c_size_t, vp]),
     "oxb_attn_decode_noalloc": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "oxb_attn_decode_head": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                        i32, vp, vp]),
@@ -124,6 +127,8 @@ SIGNATURES = {
     "oxb_model_position": (C.c_int, [vp]),
     "oxb_model_set_token": (C.c_int, [vp, i32]),
     "oxb_model_step": (C.c_int, [vp, vp]),
+    "oxb_model_set_sampling": (C.c_int, [vp, C.c_float, C.c_size_t, C.c_float, C.c_size_t, vp,
+                                         C.c_int]),
     "oxb_attn_decode_batch": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                         vp, vp, vp]),
     "oxb_lm_head_argmax_batch": (C.c_int, [vp, C.c_size_t, vp, f32, vp, i32, i32, vp, vp, i32,

@@ -160,6 +160,19 @@ class Model:
             raise NativeError(last_error())
         return tok, logits
 
+    def set_sampling(self, u=None, temperature: float = 1.0, top_k: int = 50,
+                     repeat_penalty: float = 1.1, repeat_last_n: int = 64) -> None:
+        """Draw the tokens of later forwards / steps on the device
+        (oxb_model_set_sampling); u[i] is the uniform draw of the i-th token
+        since reset.  u=None: back to the LM head's argmax."""
+        if u is None:
+            check(lib().oxb_model_set_sampling(self._m, 1.0, 0, 1.0, 0, None, 0), "sampling")
+            return
+        u = np.ascontiguousarray(u, np.float32).reshape(-1)
+        check(lib().oxb_model_set_sampling(self._m, float(temperature), int(top_k),
+                                           float(repeat_penalty), int(repeat_last_n),
+                                           u.ctypes.data, u.size), "sampling")
+
     def close(self) -> None:
         if self._m:
             lib().oxb_model_free(self._m)

@@ -30,7 +30,6 @@ struct OxBitNet {
     oxb_model *model = nullptr;
     Tokenizer tok;
     std::mt19937 rng{std::random_device{}()};
-    std::vector<float> logits;
 };
 
 namespace {
@@ -101,7 +100,7 @@ extern "C" int32_t oxb_sample_logits(float *lg, size_t V, float temperature, siz
     for (size_t i = 0; i < V; ++i) mx = std::max(mx, lg[i]);
     float sum = 0.0f;
     for (size_t i = 0; i < V; ++i) {
-        lg[i] = std::exp(lg[i] - mx);
+        lg[i] = oxb_expf(lg[i] - mx);   // the device sampler's exp, bit for bit
         sum += lg[i];
     }
     const float r = u * sum;
@@ -111,14 +110,6 @@ extern "C" int32_t oxb_sample_logits(float *lg, size_t V, float temperature, siz
         if (cum >= r) return (int32_t)i;
     }
     return (int32_t)(V - 1);
-}
-
-static int32_t sample_token(std::vector<float> &lg, float temperature, size_t top_k,
-                            float repeat_penalty, const int32_t *recent, size_t n_recent,
-                            std::mt19937 &rng) {
-    const float u = std::uniform_real_distribution<float>(0.0f, 1.0f)(rng);
-    return oxb_sample_logits(lg.data(), lg.size(), temperature, top_k, repeat_penalty, recent,
-                             n_recent, u);
 }
 
 struct GenOpts {
@@ -142,43 +133,58 @@ static GenOpts read_opts(const OxBitNetGenerateOptions *o) {
 }
 
 // lib.rs:130-189.  Errors inside the loop end generation silently (:155-158).
+// The tokens are drawn on the device right after each LM head (the
+// sampler of sampling.rs:4-80 with this handle's uniform draws, one per
+// token, uploaded before the prefill), so the host never reads logits: it
+// queues the next step before handing the current token to the callback
+// and reads that step's token back when it is done.  top_k == 1 with a
+// positive temperature and no penalty keeps the LM head's argmax (the
+// top-1 draw); with a penalty the first token (empty window) still does.
 static void generate_from_ids(OxBitNet *h, const std::vector<int32_t> &ids, const GenOpts &o,
                               OxBitNetTokenFn cb, void *ud) {
     oxb_model *m = h->model;
     if (ids.empty() || oxb_model_reset(m)) return;
-    const bool greedy = o.top_k == 1 && o.temperature > 0.0f;
-    std::vector<int32_t> recent;
-    int32_t tok = oxb_model_forward(m, ids.data(), (int)ids.size(), nullptr);
-    if (tok < 0) return;
-    h->logits.resize((size_t)m->V);
+    const bool top1 = o.top_k == 1 && o.temperature > 0.0f;
+    const bool greedy = top1 && o.repeat_penalty == 1.0f;
+    const size_t n_draw = std::min(o.max_tokens, (size_t)m->hist_cap);
+    std::vector<float> u;
+    if (!greedy) {
+        u.resize(std::max<size_t>(n_draw, 1));
+        std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+        for (float &x : u) x = dist(h->rng);
+    }
+    auto sample_on = [&]() {
+        return oxb_model_set_sampling(m, o.temperature, o.top_k, o.repeat_penalty,
+                                      o.repeat_last_n, u.data(), (int)u.size());
+    };
+    // first token: sampled unless it is a top-1 draw over an empty window
+    if (oxb_model_set_sampling(m, 0, 0, 0, 0, nullptr, 0)) return;
+    if (!top1 && sample_on()) return;
+    int32_t cur = oxb_model_forward(m, ids.data(), (int)ids.size(), nullptr);
+    if (cur < 0) return;
+    if (top1 && !greedy && sample_on()) return;
+    const int last = std::min(m->pos + (int)std::min(o.max_tokens, (size_t)m->max_seq), m->max_seq);
+    if (m->ensure_graphs(m->pos, last)) return;   // no capture between queued steps
     for (size_t i = 0; i < o.max_tokens; ++i) {
-        size_t start = 0;
-        if (o.repeat_last_n > 0 && recent.size() > o.repeat_last_n)
-            start = recent.size() - o.repeat_last_n;
-        const size_t nwin = recent.size() - start;
-        int32_t next;
-        if (greedy && (o.repeat_penalty == 1.0f || nwin == 0)) {
-            next = tok;  // the device argmax is the top-1 sample
-        } else {
-            if (hipMemcpy(h->logits.data(), m->logits, h->logits.size() * 4,
-                          hipMemcpyDeviceToHost) != hipSuccess)
-                return;
-            next = sample_token(h->logits, o.temperature, o.top_k, o.repeat_penalty,
-                                recent.data() + start, nwin, h->rng);
+        const bool stop = cur == h->tok.eos() || cur == h->tok.eot() || cur == h->tok.im_end();
+        const bool more = !stop && i + 1 < o.max_tokens && m->pos + 1 <= m->max_seq;
+        if (more) {
+            if (m->step_async()) break;
         }
-        if (next == h->tok.eos() || next == h->tok.eot() || next == h->tok.im_end()) break;
-        recent.push_back(next);
+        if (stop) break;
         if (cb) {
-            const std::string s = h->tok.decode_one(next);
+            const std::string s = h->tok.decode_one(cur);
             if (s.find('\0') == std::string::npos) {  // CString::new fails -> skipped
                 if (cb(s.c_str(), (uintptr_t)s.size(), ud) != 0) break;
             }
         }
-        if (i + 1 == o.max_tokens) break;
-        if (m->pos + 1 > m->max_seq) break;
-        tok = oxb_model_forward(m, &next, 1, nullptr);
-        if (tok < 0) break;
+        if (!more) break;
+        cur = m->step_wait();
+        if (cur < 0) break;
     }
+    // a step queued for a token the caller no longer wants still completes
+    (void)hipStreamSynchronize(m->stream);
+    (void)oxb_model_set_sampling(m, 0, 0, 0, 0, nullptr, 0);
 }
 
 extern "C" {

@@ -37,8 +37,11 @@ using namespace oxb;
 
 oxb_model::~oxb_model() {   // teardown: errors have no caller to go to
     if (stream) (void)hipStreamSynchronize(stream);
-    for (hipGraphExec_t g : graphs)
-        if (g) (void)hipGraphExecDestroy(g);
+    for (auto &row : graphs)
+        for (hipGraphExec_t g : row)
+            if (g) (void)hipGraphExecDestroy(g);
+    for (hipEvent_t e : tok_ev)
+        if (e) (void)hipEventDestroy(e);
     for (void *p : allocations) (void)hipFree(p);
     if (pinned) (void)hipHostFree(pinned);
     if (stream) (void)hipStreamDestroy(stream);
@@ -397,6 +400,11 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
         set_error("hipHostMalloc failed");
         return nullptr;
     }
+    for (hipEvent_t &e : m->tok_ev)
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            set_error("hipEventCreate failed");
+            return nullptr;
+        }
 
     const size_t staging_bytes = (size_t)std::max(Dq + 2 * Dkv, 2 * F) * std::max(D, F) / 4;
     void *staging = m->dalloc(staging_bytes);
@@ -487,7 +495,13 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
     // prefill of this model or a batch slot can hand the MFMA kernel
     m->pf_ws_bytes = oxb::attn_prefill_ws_max_bytes(Hkv);
     m->pf_ws = m->dalloc(m->pf_ws_bytes);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores || !m->logits || !m->state || !m->tok_hist || !m->pf_ws)
+    m->samp_ctl = (oxb::SampleCtl *)m->dalloc(sizeof(oxb::SampleCtl));
+    m->samp_u = (float *)m->dalloc((size_t)m->hist_cap * 4);
+    m->samp_ws_bytes = oxb::sample_ws_bytes(m->V);
+    m->samp_ws = m->dalloc(m->samp_ws_bytes);
+    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores ||
+        !m->logits || !m->state || !m->tok_hist || !m->pf_ws || !m->samp_ctl || !m->samp_u ||
+        !m->samp_ws)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
         hipMemset(m->vcache, 0, kv_bytes) != hipSuccess) {
@@ -525,7 +539,12 @@ oxb_model::AttnForm oxb_model::attn_form(int S) const {
     return ATTN_SPLIT;
 }
 
-int oxb_model::enqueue_decode_step(AttnForm attn) {
+int oxb_model::enqueue_sample() {
+    return oxb::sample_enqueue(logits, V, samp_ctl, oxb::SampleCtl{}, tok_hist, 0, state,
+                               tok_hist, samp_u, nullptr, samp_ws, samp_ws_bytes, stream);
+}
+
+int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     int *posp = state + OXB_ST_POS;
@@ -569,12 +588,13 @@ int oxb_model::enqueue_decode_step(AttnForm attn) {
                                nullptr, s))
             return -1;
     }
-    return oxb_lm_head_argmax(x, final_norm, eps, embed_lm, V, D, logits, state, tok_hist,
-                              1, s);
+    if (oxb_lm_head_argmax(x, final_norm, eps, embed_lm, V, D, logits, state, tok_hist, 1, s))
+        return -1;
+    return sample ? enqueue_sample() : 0;
 }
 
-int oxb_model::capture_graph(AttnForm attn) {
-    hipGraphExec_t &slot = graphs[attn];
+int oxb_model::capture_graph(AttnForm attn, bool sample) {
+    hipGraphExec_t &slot = graphs[sample][attn];
     if (slot) return 0;
     hipGraph_t g = nullptr;
     // Capture only on an idle stream: no replay of another step graph may
@@ -583,7 +603,7 @@ int oxb_model::capture_graph(AttnForm attn) {
     // this handle in flight.
     M_CHECK(hipStreamSynchronize(stream));
     M_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_decode_step(attn);
+    int rc = enqueue_decode_step(attn, sample);
     hipError_t e = hipStreamEndCapture(stream, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -609,7 +629,7 @@ int oxb_model::capture_graph(AttnForm attn) {
 int oxb_model::ensure_graphs(int p0, int p1) {
     for (int p = p0; p < p1;) {
         const AttnForm f = attn_form(p + 1);
-        if (capture_graph(f)) return -1;
+        if (capture_graph(f, sampling)) return -1;
         while (p < p1 && attn_form(p + 1) == f) ++p;   // the run of positions with this form
     }
     return 0;
@@ -763,6 +783,7 @@ static int write_state(oxb_model *m) {
 
 extern "C" int oxb_model_reset(oxb_model *m) {
     OXB_REQUIRE(m, "model is NULL");
+    m->tok_issued = m->tok_read = 0;   // write_state waits for every queued step
     m->pos = 0;
     m->ngen = 0;
     m->pinned[OXB_ST_TOKEN] = 0;
@@ -812,9 +833,55 @@ extern "C" int oxb_model_forward(oxb_model *m, const int32_t *ids, int n, float 
         return oxb_model_step(m, logits_host);
     }
     if (m->enqueue_prefill(ids, n)) return -1;
+    if (m->sampling && m->enqueue_sample()) return -1;
     m->pos += n;
     m->ngen += 1;
     return read_token(m, logits_host);
+}
+
+extern "C" int oxb_model_set_sampling(oxb_model *m, float temperature, size_t top_k,
+                                      float repeat_penalty, size_t repeat_last_n, const float *u,
+                                      int n_u) {
+    clear_error();
+    OXB_REQUIRE(m, "model is NULL");
+    if (!u) {
+        m->sampling = false;
+        return 0;
+    }
+    OXB_REQUIRE(n_u >= 0 && n_u <= m->hist_cap, "sampling: %d draws (at most %d)", n_u,
+                m->hist_cap);
+    oxb::SampleCtl c{temperature, (top_k > 0 && top_k < (size_t)m->V) ? (int)top_k : 0,
+                     repeat_penalty,
+                     repeat_last_n > (size_t)0x7fffffff ? 0x7fffffff : (int)repeat_last_n};
+    // the kernels of queued steps may still read the old options and draws
+    M_CHECK(hipStreamSynchronize(m->stream));
+    M_CHECK(hipMemcpy(m->samp_ctl, &c, sizeof c, hipMemcpyHostToDevice));
+    if (n_u) M_CHECK(hipMemcpy(m->samp_u, u, (size_t)n_u * 4, hipMemcpyHostToDevice));
+    m->sampling = true;
+    return 0;
+}
+
+int oxb_model::step_async() {
+    OXB_REQUIRE(tok_issued - tok_read < 2, "two steps already queued");
+    OXB_REQUIRE(pos + 1 <= max_seq, "KV cache full: position %d of %d", pos, max_seq);
+    if (ensure_graphs(pos, pos + 1)) return -1;
+    M_CHECK(hipGraphLaunch(step_graph(pos), stream));
+    const int k = tok_issued & 1;
+    M_CHECK(hipMemcpyAsync(pinned + kTokSlot + k, state + OXB_ST_TOKEN, 4, hipMemcpyDeviceToHost,
+                           stream));
+    M_CHECK(hipEventRecord(tok_ev[k], stream));
+    ++tok_issued;
+    pos += 1;
+    ngen += 1;
+    return 0;
+}
+
+int oxb_model::step_wait() {
+    OXB_REQUIRE(tok_read < tok_issued, "no step queued");
+    const int k = tok_read & 1;
+    M_CHECK(hipEventSynchronize(tok_ev[k]));
+    ++tok_read;
+    return pinned[kTokSlot + k];
 }
 
 extern "C" int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *tokens_out) {

@@ -57,7 +57,8 @@ struct oxb_model {
     //   ATTN_FUSED: two workgroups per KV head, S <= 256
     //   ATTN_SPLIT: scores kernel + P.V kernel, any S
     enum AttnForm { ATTN_HEAD1 = 0, ATTN_HEAD2, ATTN_FUSED, ATTN_SPLIT, ATTN_FORMS };
-    hipGraphExec_t graphs[ATTN_FORMS] = {};
+    // step graphs by [sampling on][attention form]
+    hipGraphExec_t graphs[2][ATTN_FORMS] = {};
     // which forms the model uses: 0 per-head kernels up to 512 positions
     // (default), 1 the fused kernel up to 256, 2 the split kernels only
     // (OXB_ATTN=head|fused|split when the model loads; all give the same bits)
@@ -67,13 +68,27 @@ struct oxb_model {
     int pos = 0;                // host mirror of state[OXB_ST_POS]
     int ngen = 0;               // host mirror of state[OXB_ST_NGEN]
 
+    // device sampling (oxb_model_set_sampling): options and draws in device
+    // memory, read by the sampler kernels of every forward and step graph
+    bool sampling = false;
+    oxb::SampleCtl *samp_ctl = nullptr;   // device
+    float *samp_u = nullptr;              // device [hist_cap] draws by token index
+    void *samp_ws = nullptr;
+    size_t samp_ws_bytes = 0;
+    // steps queued ahead of the host (step_async / step_wait): each one's
+    // token is copied to pinned[kTokSlot + i % 2] and marked by tok_ev[i % 2]
+    static constexpr int kTokSlot = 32;
+    hipEvent_t tok_ev[2] = {};
+    int tok_issued = 0, tok_read = 0;
+
     std::vector<void *> allocations;
     oxb::GgufFile *gguf = nullptr;  // kept for the tokenizer metadata
 
     ~oxb_model();
     void *dalloc(size_t bytes);
     void dfree(void *p);   // a dalloc allocation no queued work uses any more
-    int enqueue_decode_step(AttnForm attn);
+    int enqueue_decode_step(AttnForm attn, bool sample);
+    int enqueue_sample();   // the sampler over logits (state, history, draws)
     int ensure_prefill(int n);
     // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state
     // block, token history and position
@@ -86,12 +101,17 @@ struct oxb_model {
     };
     int enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &t);
     int enqueue_prefill(const int32_t *ids, int n);
-    int capture_graph(AttnForm attn);
+    int capture_graph(AttnForm attn, bool sample);
     // capture the graphs of every step at positions [p0, p1) (on an idle
     // stream, before any of them is replayed)
     int ensure_graphs(int p0, int p1);
     // the graph for a step whose token sits at position p (after ensure_graphs)
-    hipGraphExec_t step_graph(int p) const { return graphs[attn_form(p + 1)]; }
+    hipGraphExec_t step_graph(int p) const { return graphs[sampling][attn_form(p + 1)]; }
+    // One step queued behind the ones already queued (graphs captured by
+    // ensure_graphs beforehand), its token read back later by step_wait, at
+    // most two ahead.  step_wait returns the oldest queued step's token.
+    int step_async();
+    int step_wait();
 };
 
 namespace oxb {

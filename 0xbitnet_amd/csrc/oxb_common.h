@@ -10,6 +10,7 @@
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -63,6 +64,33 @@ constexpr int kChunkBytes = 16; // one lane load: 64 ternary weights
 // A wave load of lane l -> (r = l%16, kc = kc0 + l/16) reads 1 KiB contiguous.
 __host__ __device__ inline size_t tiled_offset16(int row, int kc, int KC) {
     return ((size_t)(row >> 4) * KC + kc) * 16 + (row & 15);
+}
+
+// exp(x) for the softmaxes and the sampler, fixed so that host and device give
+// the same bits:
+// Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2 plus the tail),
+// degree-7 Taylor polynomial of e^r by Horner, ldexp by k.  Every step after
+// the first product is an explicit fused multiply-add (one IEEE rounding,
+// the same on the host's fmaf); ~1 ulp.
+// Branch-free: the polynomial path runs for every x and the special cases
+// are selected afterwards (NaN last), which gives the same value as testing
+// them first and lets many independent exps interleave.
+__host__ __device__ inline float oxb_expf(float x) {
+    const float kf = rintf(x * 1.44269502f);
+    float r = __builtin_fmaf(-kf, 0.693145751953125f, x);
+    r = __builtin_fmaf(-kf, 1.42860677e-06f, r);
+    float p = __builtin_fmaf(1.98412701e-04f, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    // |k| <= 150 in range; the clamp keeps the conversion defined elsewhere
+    float y = ldexpf(p, (int)fminf(fmaxf(kf, -200.0f), 200.0f));
+    y = x > 88.7228394f ? __builtin_inff() : y;
+    y = x < -103.972084f ? 0.0f : y;
+    return x != x ? x : y;
 }
 
 }  // namespace oxb
@@ -262,32 +290,6 @@ __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
     return v;
-}
-
-// exp(x) for the softmax, fixed so that host and device give the same bits:
-// Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2 plus the tail),
-// degree-7 Taylor polynomial of e^r by Horner, ldexp by k.  Every step after
-// the first product is an explicit fused multiply-add (one IEEE rounding,
-// the same on the host's fmaf); ~1 ulp.
-// Branch-free: the polynomial path runs for every x and the special cases
-// are selected afterwards (NaN last), which gives the same value as testing
-// them first and lets many independent exps interleave.
-__device__ inline float oxb_expf(float x) {
-    const float kf = rintf(x * 1.44269502f);
-    float r = __builtin_fmaf(-kf, 0.693145751953125f, x);
-    r = __builtin_fmaf(-kf, 1.42860677e-06f, r);
-    float p = __builtin_fmaf(1.98412701e-04f, r, 1.38888892e-03f);
-    p = __builtin_fmaf(p, r, 8.33333377e-03f);
-    p = __builtin_fmaf(p, r, 4.16666679e-02f);
-    p = __builtin_fmaf(p, r, 1.66666672e-01f);
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    // |k| <= 150 in range; the clamp keeps the conversion defined elsewhere
-    float y = ldexpf(p, (int)fminf(fmaxf(kf, -200.0f), 200.0f));
-    y = x > 88.7228394f ? __builtin_inff() : y;
-    y = x < -103.972084f ? 0.0f : y;
-    return x != x ? x : y;
 }
 
 // oxb_expf for the softmax's arguments x - max <= 0 (or NaN): the same bits

@@ -50,4 +50,21 @@ int lm_head_argmax_rows(const float *x, size_t x_stride, const float *gamma, flo
                         const void *E, int V, int D, float *logits, int *state, int state_stride,
                         int *tok_hist, int hist_stride, int n_rows, int advance, float *hn,
                         void *stream);
+// Device sampling (sampling.hip).  SampleCtl holds the options of one
+// generation; top_k is the one in effect (0: keep all, else 0 < top_k < V).
+struct SampleCtl {
+    float temperature;
+    int top_k;
+    float penalty;
+    int last_n;   // window: the last last_n tokens before the current one, 0: all
+};
+size_t sample_ws_bytes(int V);
+// Draws one token from logits[V].  The options come from *ctl_dev when it is
+// given (read when the kernels run), else from ctl.  With state: the window
+// is win[...] (the token history) from state NGEN and last_n, the draw is
+// u[NGEN - 1], and the token goes to state TOKEN and win[NGEN - 1] (hist);
+// without: window win[0..nwin), draw u[0], token to *out.
+int sample_enqueue(const float *logits, int V, const SampleCtl *ctl_dev, SampleCtl ctl,
+                   const int *win, int nwin, int *state, int *hist, const float *u, int *out,
+                   void *ws, size_t ws_bytes, void *stream);
 }  // namespace oxb

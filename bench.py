@@ -500,6 +500,66 @@ def gemm_extras(ops, synth) -> dict:
     return {"gemm_sweep": gs, "prefill_block": pb}
 
 
+def generate_surface(pkg, model, path: str, max_tokens: int = 128) -> dict:
+    """Tokens/s of the C ABI's streaming generate (oxbitnet_generate,
+    rs/lib.rs:130-189) on the same file, as a user of include/oxbitnet.h sees
+    it: greedy options (top_k 1, penalty 1: the LM head's argmax) and the
+    reference's defaults (top_k 50, T 1, penalty 1.1 over the last 64 tokens:
+    drawn on the device).  One warm-up call (graph capture), then one timed
+    call each; the rate is taken between the first and the last token the
+    callback receives (the decode steps), the call's wall time is reported
+    beside it (prefill and tokenizer included).  The ids-level greedy decode
+    (oxb_model_decode_greedy) over the same positions is timed for the
+    ratio."""
+    import ctypes as C
+    nat = pkg._native
+    L = nat.lib()
+    h = L.oxbitnet_load(path.encode(), None)
+    if not h:
+        raise RuntimeError(L.oxbitnet_error_message())
+    prompt = b"The quick brown fox jumps over the lazy dog; generate some more text."
+    out = {}
+    try:
+        for name, (top_k, penalty) in (("greedy", (1, 1.0)), ("reference_defaults", (50, 1.1))):
+            g = L.oxbitnet_default_generate_options()
+            g.max_tokens, g.top_k, g.repeat_penalty = max_tokens, top_k, penalty
+            stamps = []
+            tf = nat.TokenFn(lambda t, n, ud: (stamps.append(time.perf_counter()), 0)[1])
+            if L.oxbitnet_generate(h, prompt, C.byref(g), tf, None) != 0:
+                raise RuntimeError(L.oxbitnet_error_message())
+            stamps.clear()
+            t0 = time.perf_counter()
+            if L.oxbitnet_generate(h, prompt, C.byref(g), tf, None) != 0:
+                raise RuntimeError(L.oxbitnet_error_message())
+            wall = time.perf_counter() - t0
+            n = len(stamps)
+            rate = (n - 1) / (stamps[-1] - stamps[0]) if n > 2 else None
+            out[name] = {"tokens": n, "tok_s": round(rate, 2) if rate else None,
+                         "call_ms": round(wall * 1e3, 2), "top_k": top_k,
+                         "repeat_penalty": penalty, "temperature": 1.0, "repeat_last_n": 64}
+    finally:
+        L.oxbitnet_free(h)
+    # the same positions through the ids-level engine: a prompt of the same
+    # length, then max_tokens - 1 greedy steps as one run of graph replays
+    tok = L.oxb_tokenizer_load(path.encode())
+    n_prompt = L.oxb_tokenizer_encode(tok, prompt, 1, None, 0)
+    L.oxb_tokenizer_free(tok)
+    ids = np.random.default_rng(5).integers(0, model.vocab, n_prompt).astype(np.int32)
+    model.reset()
+    model.forward(ids, want_logits=False)
+    model.decode_greedy(max_tokens - 1)
+    model.reset()
+    model.forward(ids, want_logits=False)
+    t0 = time.perf_counter()
+    model.decode_greedy(max_tokens - 1)
+    ref = (max_tokens - 1) / (time.perf_counter() - t0)
+    for v in out.values():
+        v["decode_greedy_tok_s"] = round(ref, 2)
+        v["vs_decode_greedy"] = round(v["tok_s"] / ref, 4) if v["tok_s"] else None
+    out["prompt_tokens"] = n_prompt
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -521,6 +581,9 @@ def main() -> int:
     ap.add_argument("--gemm-shape", default="",
                     help="N,K,M: time only the ternary GEMM at that shape (the command the "
                          "GEMM rocprofv3 --pmc runs profile)")
+    ap.add_argument("--no-generate", action="store_true",
+                    help="skip the oxbitnet_generate (C ABI streaming) timing")
+    ap.add_argument("--gen-tokens", type=int, default=128)
     ap.add_argument("--lc-batches", default="1,8,32")
     ap.add_argument("--lc-steps", type=int, default=512)
     args = ap.parse_args()
@@ -585,6 +648,14 @@ def main() -> int:
     log(f"decode {args.steps} steps: {dt * 1e3:.1f} ms -> {tps:.1f} tok/s; prefill "
         f"{args.prompt} tok {prefill_s * 1e3:.1f} ms; first tokens {toks[:8].tolist()}")
 
+    gen = None
+    if not args.no_generate:
+        gen = generate_surface(pkg, model, path, args.gen_tokens)
+        for k in ("greedy", "reference_defaults"):
+            v = gen[k]
+            log(f"oxbitnet_generate {k}: {v['tokens']} tokens, {v['tok_s']} tok/s "
+                f"({v['call_ms']} ms per call); decode_greedy {v['decode_greedy_tok_s']} tok/s")
+
     # roofline of the ternary GEMV (8192 x 28672, M = 1) and the sweep
     roof = gemv_roofline(ops, synth, 8192, 28672, copies=16, iters=400)
     log(f"gemv 8192x28672: {roof['us']} us, {roof['GBps']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
@@ -639,6 +710,7 @@ def main() -> int:
         "decode_step_GBps": round(step_bytes * tps / 1e9, 1),
         "decode_step_frac": round(step_bytes * tps / 1e9 / HBM_PEAK_GBS, 4),
         "prefill_ms": round(prefill_s * 1e3, 2),
+        "generate": gen,
         "roofline": {"bound": "hbm", "achieved": roof["GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": roof["frac"], "traffic": measured_traffic(),
                      "kernel": "gemv_kernel<PRO_INT8,EPI_STORE> N=8192 K=28672 M=1",

@@ -201,17 +201,31 @@ int oxb_attn_decode_noalloc(const float *q, const uint16_t *kcache, const uint16
 int oxb_attn_prefill(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_tok,
                      int pos0, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
 
-/* ---- sampling (host) -------------------------------------------------------- */
+/* ---- sampling ---------------------------------------------------------------- */
 /* One draw of rs/sampling.rs:4-80 over logits[V] (modified in place):
  * repetition penalty over recent[n_recent] (positive logits divided, others
  * multiplied, once per occurrence), temperature (logits * 1/T when T != 1),
  * top-k (values below the k-th largest become -inf; k == 0 or >= V keeps all),
  * softmax, then the first index whose running sum reaches u * sum for the
- * uniform draw u in [0, 1) (V - 1 if none does).  The C ABI's generate passes
- * u from its own generator; top_k == 1 without a penalty is the device argmax.
+ * uniform draw u in [0, 1) (V - 1 if none does).  exp is the library's
+ * fixed exp (Cody-Waite + degree-7 polynomial, ~1 ulp; the reference's Rust
+ * f32::exp is the platform libm's), so the device sampler gives the same
+ * token.  The C ABI's generate passes u from its own generator to the device
+ * sampler; top_k == 1 without a penalty is the LM head's argmax.
  * Host code, no GPU. */
 int32_t oxb_sample_logits(float *logits, size_t V, float temperature, size_t top_k,
                           float repeat_penalty, const int32_t *recent, size_t n_recent, float u);
+
+/* The same draw on the device (sampling.hip): logits[V], recent[n_recent],
+ * u (one float) and token (one int) are device pointers; ws is a device
+ * workspace of oxb_sample_ws_bytes(V) bytes.  Gives oxb_sample_logits's token
+ * for the same logits and u (exp is oxb_expf on both sides) and leaves the
+ * logits unchanged.  Replaces the host readback + sample_token of
+ * rs/lib.rs:151-167 per generated token. */
+size_t oxb_sample_ws_bytes(int V);
+int oxb_sample_device(const float *logits, int V, float temperature, size_t top_k,
+                      float repeat_penalty, const int32_t *recent, int n_recent, const float *u,
+                      int32_t *token, void *ws, size_t ws_bytes, void *stream);
 
 /* ---- tokenizer (host) ------------------------------------------------------- */
 /* The tokenizer of a GGUF file from its metadata alone (no weights, no GPU):
@@ -298,10 +312,12 @@ int oxb_model_get_info(const oxb_model *m, oxb_model_info *out);
 int oxb_model_reset(oxb_model *m);
 /* forward(ids): prefill n >= 1 tokens at the current position; writes the
  * last token's logits to logits_host (nullable) and returns the greedy
- * token (>= 0) or -1.  nn/model.rs:193-298. */
+ * token (the sampled one when oxb_model_set_sampling is on; >= 0) or -1.
+ * nn/model.rs:193-298. */
 int oxb_model_forward(oxb_model *m, const int32_t *ids, int n, float *logits_host);
 /* n_steps greedy decode steps from the current token, each one replay of a
- * captured hipGraph; tokens_out[n_steps] (host).  Returns 0 / -1. */
+ * captured hipGraph; tokens_out[n_steps] (host).  Returns 0 / -1.  With
+ * oxb_model_set_sampling on, each step's token is sampled instead. */
 int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *tokens_out);
 /* Current KV length. */
 int oxb_model_position(const oxb_model *m);
@@ -309,6 +325,15 @@ int oxb_model_position(const oxb_model *m);
 int oxb_model_set_token(oxb_model *m, int32_t tok);
 /* One decode step from the current token, logits to host (nullable). */
 int oxb_model_step(oxb_model *m, float *logits_host);
+/* Sampling on the device for the following forwards and steps: after each
+ * LM head the token is drawn from the logits as oxb_sample_device does
+ * (penalty over the last repeat_last_n tokens of the history since reset,
+ * 0: all of them), with u[i] as the draw of the i-th token since reset
+ * (n_u <= max_seq + 16), and becomes the current token and history entry.
+ * u == NULL turns it off (the LM head's argmax is the token).  The logits
+ * (oxb_model_forward / oxb_model_step) stay the model's.  0 / -1. */
+int oxb_model_set_sampling(oxb_model *m, float temperature, size_t top_k, float repeat_penalty,
+                           size_t repeat_last_n, const float *u, int n_u);
 
 /* ---- batched greedy decode (no counterpart in the reference) --------------
  * B independent sequences (slots) on one loaded model, each with its own KV
