@@ -75,9 +75,10 @@ def test_small_model_f32_cache_oracle():
 
 
 @pytest.mark.parametrize("n_prompt", [1, 255, 300])
-def test_small_model_f32_cache_across_pv_blocks(n_prompt):
-    """Prompts that end before, at and past the first 256-position P.V block,
-    then decode across block boundaries (positions up to 560)."""
+def test_small_model_f32_cache_long_rows(n_prompt):
+    """Prompts that end before, at and past 256 positions, then decode to
+    position 560: the P.V chains run over every cached position in one loop
+    (the f32 cache's attention), bit-equal to the oracle throughout."""
     cfg = synth.small_config()
     path = synth.cached_gguf(cfg, seed=7)
     prompt = np.random.default_rng([3, n_prompt]).integers(0, cfg.vocab, n_prompt).astype(np.int32)
