@@ -1276,6 +1276,17 @@ __global__ __launch_bounds__(1024) void attn_fused_kernel(
     if (w < G) out[(size_t)(hk * G + w) * kHd + 64 * half + lane] = acc;
 }
 
+// Grids of the per-head decode kernels: workgroups go to the 8 XCDs in turn,
+// so the G workgroups of a KV head take block indices congruent mod 8 and
+// run on one XCD, whose L2 then serves the K/V rows they share.  Block x ->
+// KV head 8 (x / 8G) + x % 8, head G * (KV head) + (x / 8) % G; blocks past
+// the last KV head have no head (-1) and return at once.
+__host__ __device__ inline int head_grid_blocks(int G, int Hkv) { return 8 * G * ((Hkv + 7) / 8); }
+__device__ inline int head_of_block(int x, int G, int Hkv) {
+    const int hk = 8 * (x / (8 * G)) + x % 8;
+    return hk < Hkv ? hk * G + (x / 8) % G : -1;
+}
+
 // ---------------------------------------------------------------------------
 // Decode, one workgroup per query head (grid: heads x sequences), 256
 // threads, up to 256 cached positions, for caches of fewer than 256 rows
@@ -1298,14 +1309,15 @@ constexpr int kHeadChunk = 64;   // V positions per register chunk
 
 __global__ __launch_bounds__(256) void attn_head_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
-    size_t kv_stride, int pos_stride) {
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float scale,
+    float *__restrict__ out, size_t kv_stride, int pos_stride) {
     constexpr int NJ = 1;   // positions per thread
     __shared__ __align__(16) float pr[256 * NJ];   // probabilities
     __shared__ float red[256];
     __shared__ float wmax[4];
     __shared__ float inv_s;
-    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int h = head_of_block(blockIdx.x, G, Hkv), z = blockIdx.y, H = G * Hkv;
+    if (h < 0) return;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
     kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
@@ -1514,12 +1526,12 @@ __device__ __forceinline__ float pv_head(const uint32_t *vcol, const float *pr, 
 
 __global__ __launch_bounds__(256) void attn_head256_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
-    size_t kv_stride, int pos_stride) {
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float scale,
+    float *__restrict__ out, size_t kv_stride, int pos_stride) {
     // all kernel arguments in SGPRs up front: read where they are used, the
     // late ones are further kernarg round trips before the position's load
-    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(max_seq), "s"(scale),
-                 "s"(out), "s"(kv_stride), "s"(pos_stride));
+    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(Hkv), "s"(max_seq),
+                 "s"(scale), "s"(out), "s"(kv_stride), "s"(pos_stride));
     extern __shared__ __align__(16) int8_t smem_h[];
     u32x4_t (*ks)[17] = (u32x4_t (*)[17])smem_h;
     u32x4_t *vs4 = (u32x4_t *)(smem_h + kH256KBytes);              // V [256][64] dwords
@@ -1528,7 +1540,8 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     float *pr = qs + kHd;                                           // probabilities [256]
     float *red = pr + 256;                                          // partial sums [256]
     float *wmax = red + 256;                                        // [4]
-    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int h = head_of_block(blockIdx.x, G, Hkv), z = blockIdx.y, H = G * Hkv;
+    if (h < 0) return;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
     kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
@@ -1640,10 +1653,10 @@ static_assert((size_t)kH512Rows * kHd * 2 <= kH512KBytes, "V rows fit the K regi
 
 __global__ __launch_bounds__(512) void attn_head512_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-    const int *__restrict__ pos_ptr, int G, int max_seq, float scale, float *__restrict__ out,
-    size_t kv_stride, int pos_stride) {
-    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(max_seq), "s"(scale),
-                 "s"(out), "s"(kv_stride), "s"(pos_stride));
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float scale,
+    float *__restrict__ out, size_t kv_stride, int pos_stride) {
+    asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(Hkv), "s"(max_seq),
+                 "s"(scale), "s"(out), "s"(kv_stride), "s"(pos_stride));
     extern __shared__ __align__(16) int8_t smem_h[];
     u32x4_t (*ks)[17] = (u32x4_t (*)[17])smem_h;
     u32x4_t *vs4 = (u32x4_t *)smem_h;                                // V [512][64] dwords (after K)
@@ -1653,7 +1666,8 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     float *ev = pr + 512;                                            // e [512]
     float *red = ev + 512;                                           // partial sums [256]
     float *wmax = red + 256;                                         // [8]
-    const int h = blockIdx.x, z = blockIdx.y, H = gridDim.x;
+    const int h = head_of_block(blockIdx.x, G, Hkv), z = blockIdx.y, H = G * Hkv;
+    if (h < 0) return;
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
     kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
@@ -1997,17 +2011,19 @@ extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, cons
                 "per-head decode attention: s_max %d out of range (1..512)", s_max);
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipStream_t s = (hipStream_t)stream;
+    const int G = H / Hkv;
+    const dim3 grid(head_grid_blocks(G, Hkv), batch);
     if (s_max <= 256 && max_seq >= kH256Rows) {
         if (allow_dynamic_lds((const void *)attn_head256_kernel)) return -1;
-        hipLaunchKernelGGL(attn_head256_kernel, dim3(H, batch), dim3(256), kH256Lds, s, q, kcache,
-                           vcache, pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+        hipLaunchKernelGGL(attn_head256_kernel, grid, dim3(256), kH256Lds, s, q, kcache, vcache,
+                           pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride);
     } else if (s_max <= 256)
-        hipLaunchKernelGGL(attn_head_kernel, dim3(H, batch), dim3(256), 0, s, q, kcache, vcache,
-                           pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+        hipLaunchKernelGGL(attn_head_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos, G, Hkv,
+                           max_seq, scale, out, kv_stride, pos_stride);
     else {
         if (allow_dynamic_lds((const void *)attn_head512_kernel)) return -1;
-        hipLaunchKernelGGL(attn_head512_kernel, dim3(H, batch), dim3(512), kH512Lds, s, q, kcache,
-                           vcache, pos, H / Hkv, max_seq, scale, out, kv_stride, pos_stride);
+        hipLaunchKernelGGL(attn_head512_kernel, grid, dim3(512), kH512Lds, s, q, kcache, vcache,
+                           pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride);
     }
     OXB_CHECK_HIP(hipGetLastError());
     return 0;

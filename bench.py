@@ -581,6 +581,9 @@ def main() -> int:
     ap.add_argument("--gemm-shape", default="",
                     help="N,K,M: time only the ternary GEMM at that shape (the command the "
                          "GEMM rocprofv3 --pmc runs profile)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="stop after the decode measurement (the command the decode counter "
+                         "profiles run), logging each phase")
     ap.add_argument("--no-generate", action="store_true",
                     help="skip the oxbitnet_generate (C ABI streaming) timing")
     ap.add_argument("--gen-tokens", type=int, default=128)
@@ -634,7 +637,11 @@ def main() -> int:
     # warm-up run (graph capture, caches), then the timed run from a fresh cache
     model.reset()
     model.forward(prompt, want_logits=False)
+    if args.decode_only:
+        log("warm-up prefill done")
     model.decode_greedy(args.warmup)
+    if args.decode_only:
+        log(f"warm-up decode ({args.warmup} steps) done")
     model.reset()
     t0 = time.perf_counter()
     model.forward(prompt, want_logits=False)
@@ -647,6 +654,10 @@ def main() -> int:
     tps = args.steps / dt
     log(f"decode {args.steps} steps: {dt * 1e3:.1f} ms -> {tps:.1f} tok/s; prefill "
         f"{args.prompt} tok {prefill_s * 1e3:.1f} ms; first tokens {toks[:8].tolist()}")
+    if args.decode_only:
+        print(json.dumps({"decode_tok_s": round(tps, 2), "steps": args.steps,
+                          "prompt": args.prompt}), flush=True)
+        return 0
 
     gen = None
     if not args.no_generate:
