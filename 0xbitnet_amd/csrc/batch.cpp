@@ -247,7 +247,8 @@ extern "C" int oxb_batch_decode_greedy(oxb_batch *b, int n_steps, int32_t *token
     }
     if (b->capture()) return -1;
     hipStream_t s = b->m->stream;
-    for (int i = 0; i < n_steps; ++i) B_CHECK(hipGraphLaunch(b->graph, s));
+    for (int i = 0; i < n_steps; ++i)
+        if (b->m->launch_replay(b->graph, i)) return -1;
     for (int i = 0; i < b->B && n_steps > 0; ++i)
         B_CHECK(hipMemcpyAsync(tokens_out + (size_t)i * n_steps,
                                b->tok_hist + (size_t)i * b->hist_cap + b->ngen[i],

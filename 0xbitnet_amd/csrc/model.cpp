@@ -42,6 +42,8 @@ oxb_model::~oxb_model() {   // teardown: errors have no caller to go to
             if (g) (void)hipGraphExecDestroy(g);
     for (hipEvent_t e : tok_ev)
         if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : replay_ev)
+        if (e) (void)hipEventDestroy(e);
     for (void *p : allocations) (void)hipFree(p);
     if (pinned) (void)hipHostFree(pinned);
     if (stream) (void)hipStreamDestroy(stream);
@@ -400,6 +402,11 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
         set_error("hipHostMalloc failed");
         return nullptr;
     }
+    for (hipEvent_t &e : m->replay_ev)
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            set_error("hipEventCreate failed");
+            return nullptr;
+        }
     for (hipEvent_t &e : m->tok_ev)
         if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
             set_error("hipEventCreate failed");
@@ -861,6 +868,14 @@ extern "C" int oxb_model_set_sampling(oxb_model *m, float temperature, size_t to
     return 0;
 }
 
+int oxb_model::launch_replay(hipGraphExec_t g, int i) {
+    const int grp = i / kReplayGroup;
+    if (i % kReplayGroup == 0 && grp >= 2) M_CHECK(hipEventSynchronize(replay_ev[(grp - 2) % 3]));
+    M_CHECK(hipGraphLaunch(g, stream));
+    if (i % kReplayGroup == kReplayGroup - 1) M_CHECK(hipEventRecord(replay_ev[grp % 3], stream));
+    return 0;
+}
+
 int oxb_model::step_async() {
     OXB_REQUIRE(tok_issued - tok_read < 2, "two steps already queued");
     OXB_REQUIRE(pos + 1 <= max_seq, "KV cache full: position %d of %d", pos, max_seq);
@@ -893,7 +908,8 @@ extern "C" int oxb_model_decode_greedy(oxb_model *m, int n_steps, int32_t *token
     OXB_REQUIRE(m->ngen + n_steps <= m->hist_cap, "token history full");
     const int first = m->ngen;
     if (m->ensure_graphs(m->pos, m->pos + n_steps)) return -1;
-    for (int i = 0; i < n_steps; ++i) M_CHECK(hipGraphLaunch(m->step_graph(m->pos + i), m->stream));
+    for (int i = 0; i < n_steps; ++i)
+        if (m->launch_replay(m->step_graph(m->pos + i), i)) return -1;
     m->pos += n_steps;
     m->ngen += n_steps;
     if (n_steps)

@@ -80,6 +80,12 @@ struct oxb_model {
     static constexpr int kTokSlot = 32;
     hipEvent_t tok_ev[2] = {};
     int tok_issued = 0, tok_read = 0;
+    // A run of graph replays (decode_greedy, batch decode) keeps at most
+    // 2 * kReplayGroup of them queued: an event marks the end of every group
+    // of kReplayGroup, and group g waits for group g - 2 before it is queued.
+    static constexpr int kReplayGroup = 4;
+    hipEvent_t replay_ev[3] = {};
+    int launch_replay(hipGraphExec_t g, int i);   // i: the replay's index in its run
 
     std::vector<void *> allocations;
     oxb::GgufFile *gguf = nullptr;  // kept for the tokenizer metadata
