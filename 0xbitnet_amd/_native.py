@@ -131,6 +131,8 @@ SIGNATURES = {
                                          C.c_int]),
     "oxb_attn_decode_batch": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                         vp, vp, vp]),
+    "oxb_attn_decode_batch_v8": (C.c_int, [vp, vp, vp, vp, vp, i32, C.c_size_t, C.c_size_t, i32,
+                                           i32, i32, i32, i32, vp, vp, vp]),
     "oxb_lm_head_argmax_batch": (C.c_int, [vp, C.c_size_t, vp, f32, vp, i32, i32, vp, vp, i32,
                                            vp, i32, i32, i32, vp]),
     "oxb_batch_create": (vp, [vp, i32, i32]),

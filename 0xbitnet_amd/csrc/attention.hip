@@ -652,6 +652,147 @@ __global__ __launch_bounds__(kPhThreads) void attn_pv_head_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// The same P.V over the cache's V copy in position octets (v8_index: per KV
+// head, one dim's 8 consecutive positions in 16 bytes).  In the row-major
+// cache a lane's dim sits 256 bytes apart from one position to the next, so
+// the chain wave above reads four dwords (using half of each) and a
+// probability broadcast per 4 positions; here one 16-byte read gives the
+// lane its dim's next 8 positions, plus two broadcasts of their
+// probabilities.  Workgroup per (query head, half of the dims, sequence):
+// lane l chains dim 64 half + l, and the ring stages only that half, in
+// slots of kPoRows positions (16 octets x 64 lanes x 16 bytes); each wave
+// issues four of a slot's 1 KB DMA loads.  Octets past the cache length are
+// clamped to its last octet (staged, never summed).  Same block -> (KV head,
+// item) mapping and the same ring protocol as attn_pv_head_kernel.
+// LDS (dynamic): ring [NS][16][64][16 B] | p [Sp] | red [256] | wmax [4]
+// ---------------------------------------------------------------------------
+constexpr int kPoRows = 128;                              // positions per ring slot
+constexpr int kPoOcts = kPoRows / 8;                      // octets per slot
+constexpr int kPoSlotBytes = kPoOcts * 64 * 16;
+
+__host__ __device__ inline size_t po_smem(int slots, int max_seq) {
+    return (size_t)slots * kPoSlotBytes + ((size_t)pc_row_stride(max_seq) + 256 + 8) * 4;
+}
+
+// acc + sum of p[s] * v_s over the n (all 8 when FULL) positions of one
+// octet, in order of s (v_s: half s % 2 of dword s / 2 of V)
+template <bool FULL>
+__device__ __forceinline__ float pv8(float acc, const uint4 &V, const float4 &Pa, const float4 &Pb,
+                                     int n = 8) {
+    const uint32_t u[4] = {V.x, V.y, V.z, V.w};
+    const float pp[8] = {Pa.x, Pa.y, Pa.z, Pa.w, Pb.x, Pb.y, Pb.z, Pb.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t w = u[k >> 1];
+        const float v = __half2float(__ushort_as_half((uint16_t)((k & 1) ? w >> 16 : w & 0xffffu)));
+        const float t = __builtin_fmaf(pp[k], v, acc);
+        acc = FULL || k < n ? t : acc;
+    }
+    return acc;
+}
+
+// n positions (1 .. kPoRows) of one ring slot into a lane's chain: vs = the
+// lane's 16 bytes of the slot's octet 0 (octets 64 uint4 apart), pp = the p
+// row at the slot's first position.  Octet o in entry o % 4, read three
+// octets ahead; four octets per iteration, whose entries are constants (a
+// rotating index would put the entries in scratch), the rest from entries
+// 0..3 after the loop.
+__device__ __forceinline__ float po_chain_slot(float acc, const uint4 *vs, const float *pp, int n) {
+    uint4 V[4];
+    float4 Pa[4], Pb[4];
+    auto ld = [&](int b, int o) {   // octet o (clamped into the slot) into entry b
+        o = min(o, kPoOcts - 1);
+        V[b] = vs[o * 64];
+        Pa[b] = *(const float4 *)(pp + 8 * o);
+        Pb[b] = *(const float4 *)(pp + 8 * o + 4);
+    };
+    ld(0, 0);
+    ld(1, 1);
+    ld(2, 2);
+    int o0 = 0;
+#pragma unroll
+    for (int it = 0; it < kPoOcts / 4; ++it) {
+        if (8 * (o0 + 4) > n) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            ld((j + 3) & 3, o0 + j + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv8<true>(acc, V[j], Pa[j], Pb[j]);
+        }
+        o0 += 4;
+    }
+    if (8 * o0 < n) {
+        ld(3, o0 + 3);   // entries 0..2 hold octets o0 .. o0 + 2
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = n - 8 * (o0 + j);
+            if (m >= 8) acc = pv8<true>(acc, V[j], Pa[j], Pb[j]);
+            else if (m > 0) acc = pv8<false>(acc, V[j], Pa[j], Pb[j], m);
+        }
+    }
+    return acc;
+}
+
+template <int NS>
+__global__ __launch_bounds__(kPhThreads) void attn_pv_oct_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc8,
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float *__restrict__ out,
+    size_t kv8_stride, int pos_stride) {
+    static_assert(NS >= 3 && 4 * (NS - 3) < 64, "ring depth within vmcnt");
+    const int b = blockIdx.x, z = blockIdx.y;
+    const int hk = 8 * (b / (16 * G)) + (b & 7), item = (b >> 3) % (2 * G);
+    if (hk >= Hkv) return;
+    const int h = hk * G + (item >> 1), half = item & 1, H = Hkv * G;
+    scores += (size_t)z * H * max_seq + (size_t)h * max_seq;
+    vc8 += (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd);
+    out += (size_t)z * H * kHd + (size_t)h * kHd;
+    extern __shared__ __align__(16) int8_t smem_po[];
+    uint4 *ring = (uint4 *)smem_po;
+    float *pr = (float *)(smem_po + (size_t)NS * kPoSlotBytes);
+    float *red = pr + pc_row_stride(max_seq), *wmax = red + 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1;
+    const int nslots = (S + kPoRows - 1) / kPoRows;
+    const int last_oct = (S - 1) >> 3;
+
+    // this wave's share of a slot: octets 4w .. 4w+3, each one 1 KB load
+    // (lane l: the 16 bytes of dim 64 half + l), clamped to the last octet
+    const uint4 *V8 = (const uint4 *)vc8 + 64 * half + lane;
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int o = c * kPoOcts + 4 * w + k;
+            lds_dma16(V8 + (size_t)min(o, last_oct) * kHd,
+                      ring + ((size_t)(c % NS) * kPoOcts + 4 * w + k) * 64);
+        }
+    };
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+
+    softmax_row_4w_any(pr, scores, S, true, wmax, red, w, lane);
+
+    float acc = 0.0f;
+    for (int c = 0; c < nslots; ++c) {
+        wait_vmcnt<4 * (NS - 3)>();   // this wave's loads of slots c and c + 1 have landed
+        if (w == 0 && c > 0)
+            asm volatile("s_barrier" ::: "memory");   // reads in flight stay (see the 4-head kernel)
+        else
+            lds_barrier();
+        issue(c + NS - 1);
+        if (w == 0) {
+            const uint4 *vs = ring + (size_t)(c % NS) * kPoOcts * 64 + lane;
+            acc = po_chain_slot(acc, vs, pr + c * kPoRows, min(kPoRows, S - c * kPoRows));
+        }
+    }
+    wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
+    if (w == 0) out[64 * half + lane] = acc;
+}
+
+// ---------------------------------------------------------------------------
 // Prefill: one workgroup per (Q consecutive queries, KV head); query i of
 // the block sits at position pos0 + q0 + i and attends over S_i = its
 // position + 1 cached positions (causal).  Each K row is read once for the
@@ -1862,12 +2003,27 @@ using namespace oxb;
 template <int G>
 static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc, const int *pos,
                          int Hkv, int max_seq, float *scores, float *out, hipStream_t s,
-                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0) {
+                         int batch = 1, size_t kv_stride = 0, int pos_stride = 0,
+                         const uint16_t *vc8 = nullptr, size_t kv8_stride = 0) {
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipLaunchKernelGGL(attn_scores_kernel<G>,
                        dim3((max_seq + kScoreP - 1) / kScoreP, Hkv, batch), dim3(256), 0, s, q,
                        kc, pos, max_seq, scale, scores, kv_stride, pos_stride);
     OXB_CHECK_HIP(hipGetLastError());
+    if (vc8 && batch <= kPhMaxBatch) {   // one chain wave per CU, V in position octets
+        const dim3 hgrid(16 * G * ((Hkv + 7) / 8), batch);
+        if (po_smem(6, max_seq) <= 160 * 1024) {
+            if (allow_dynamic_lds((const void *)attn_pv_oct_kernel<6>)) return -1;
+            hipLaunchKernelGGL(attn_pv_oct_kernel<6>, hgrid, dim3(kPhThreads), po_smem(6, max_seq),
+                               s, scores, vc8, pos, G, Hkv, max_seq, out, kv8_stride, pos_stride);
+        } else {
+            if (allow_dynamic_lds((const void *)attn_pv_oct_kernel<4>)) return -1;
+            hipLaunchKernelGGL(attn_pv_oct_kernel<4>, hgrid, dim3(kPhThreads), po_smem(4, max_seq),
+                               s, scores, vc8, pos, G, Hkv, max_seq, out, kv8_stride, pos_stride);
+        }
+        OXB_CHECK_HIP(hipGetLastError());
+        return 0;
+    }
     if (batch <= kPhMaxBatch) {   // one chain wave per CU
         const dim3 hgrid(16 * G * ((Hkv + 7) / 8), batch);
         if (ph_smem(6, max_seq) <= 160 * 1024) {
@@ -1916,28 +2072,48 @@ extern "C" int oxb_attn_decode(const float *q, const uint16_t *kcache, const uin
     }
 }
 
-extern "C" int oxb_attn_decode_batch(const float *q, const uint16_t *kcache,
-                                     const uint16_t *vcache, const int *pos, int pos_stride,
-                                     size_t kv_stride, int batch, int H, int Hkv, int hd,
-                                     int max_seq, float *scores, float *out, void *stream) {
+static int decode_batch(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                        const uint16_t *vcache8, const int *pos, int pos_stride, size_t kv_stride,
+                        size_t kv8_stride, int batch, int H, int Hkv, int hd, int max_seq,
+                        float *scores, float *out, void *stream) {
     OXB_REQUIRE(pos && scores, "attention: pos or scores is NULL");
     OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
     OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
     OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
                 "attention: caches of a batch overlap (stride %zu)", kv_stride);
+    OXB_REQUIRE(!vcache8 || batch == 1 || kv8_stride >= (size_t)Hkv * v8_head_elems(max_seq, hd),
+                "attention: octet caches of a batch overlap (stride %zu)", kv8_stride);
     OXB_REQUIRE(max_seq >= 1 && max_seq <= kPcMaxSeq,
                 "attention: max_seq %d out of range (1..%d)", max_seq, kPcMaxSeq);
     hipStream_t s = (hipStream_t)stream;
     switch (H / Hkv) {
-        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
-        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
-        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
-        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride);
+        case 1: return launch_decode<1>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, vcache8, kv8_stride);
+        case 2: return launch_decode<2>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, vcache8, kv8_stride);
+        case 4: return launch_decode<4>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, vcache8, kv8_stride);
+        case 8: return launch_decode<8>(q, kcache, vcache, pos, Hkv, max_seq, scores, out, s, batch, kv_stride, pos_stride, vcache8, kv8_stride);
         default:
             oxb::set_error("attention: GQA group %d unsupported (1, 2, 4, 8)", H / Hkv);
             return -1;
     }
+}
+
+extern "C" int oxb_attn_decode_batch(const float *q, const uint16_t *kcache,
+                                     const uint16_t *vcache, const int *pos, int pos_stride,
+                                     size_t kv_stride, int batch, int H, int Hkv, int hd,
+                                     int max_seq, float *scores, float *out, void *stream) {
+    return decode_batch(q, kcache, vcache, nullptr, pos, pos_stride, kv_stride, 0, batch, H, Hkv,
+                        hd, max_seq, scores, out, stream);
+}
+
+extern "C" int oxb_attn_decode_batch_v8(const float *q, const uint16_t *kcache,
+                                        const uint16_t *vcache, const uint16_t *vcache8,
+                                        const int *pos, int pos_stride, size_t kv_stride,
+                                        size_t kv8_stride, int batch, int H, int Hkv, int hd,
+                                        int max_seq, float *scores, float *out, void *stream) {
+    OXB_REQUIRE(vcache8, "attention: vcache8 is NULL");
+    return decode_batch(q, kcache, vcache, vcache8, pos, pos_stride, kv_stride, kv8_stride, batch,
+                        H, Hkv, hd, max_seq, scores, out, stream);
 }
 
 template <int G>

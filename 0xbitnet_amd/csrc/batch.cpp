@@ -32,7 +32,8 @@ struct oxb_batch {
     oxb_model *m = nullptr;
     int B = 0, max_seq = 0, hist_cap = 0;
     size_t layer_kv = 0, slot_kv = 0;     // elements: one layer of one slot, one slot
-    uint16_t *kcache = nullptr, *vcache = nullptr;
+    size_t layer_kv8 = 0, slot_kv8 = 0;   // the same for the octet copy of V
+    uint16_t *kcache = nullptr, *vcache = nullptr, *vcache8 = nullptr;
     int *state = nullptr;                 // [B][OXB_STATE_INTS]
     int *tok_hist = nullptr;              // [B][hist_cap]
     float *rope = nullptr;                // [max_seq][hd/2] (cos, sin)
@@ -73,13 +74,14 @@ int oxb_batch::enqueue_step() {
     for (int l = 0; l < M.n_layers; ++l) {
         const oxb_model::Layer &L = M.layers[l];
         uint16_t *kc = kcache + l * layer_kv, *vc = vcache + l * layer_kv;
+        uint16_t *vc8 = vcache8 + l * layer_kv8;
         if (oxb_quantize_rows_tiled(x, L.attn_norm, M.eps, B, D, X, xscale, xsum, s)) return -1;
         if (gemm_qkv_rows(L.wqkv, (const int8_t *)X, xscale, xsum, L.sqkv, Dq, Dkv, M.hd, D, B,
                           state + OXB_ST_POS, OXB_STATE_INTS, slot_kv, q, kc, vc, max_seq, rope,
-                          true, s))
+                          true, s, vc8, slot_kv8))
             return -1;
-        if (oxb_attn_decode_batch(q, kc, vc, state + OXB_ST_POS, OXB_STATE_INTS, slot_kv, B,
-                                  M.H, M.Hkv, M.hd, max_seq, scores, attn, s))
+        if (oxb_attn_decode_batch_v8(q, kc, vc, vc8, state + OXB_ST_POS, OXB_STATE_INTS, slot_kv,
+                                     slot_kv8, B, M.H, M.Hkv, M.hd, max_seq, scores, attn, s))
             return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
         if (oxb_quantize_rows_tiled(attn, L.attn_sub, 1e-5f, B, Dq, X, xscale, xsum, s)) return -1;
@@ -154,11 +156,14 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
     b->hist_cap = max_seq + 16;
     b->layer_kv = (size_t)m->Hkv * max_seq * m->hd;
     b->slot_kv = b->layer_kv * m->n_layers;
+    b->layer_kv8 = (size_t)m->Hkv * v8_head_elems(max_seq, m->hd);
+    b->slot_kv8 = b->layer_kv8 * m->n_layers;
     const int D = m->D, F = m->F, Dq = m->H * m->hd;
     const int rows = (batch + 15) & ~15;
     const size_t pad = (size_t)OXB_KV_PAD_ROWS * m->hd;   // per-head attention reads whole V chunks
     b->kcache = (uint16_t *)b->dalloc((b->slot_kv * batch + pad) * 2);
     b->vcache = (uint16_t *)b->dalloc((b->slot_kv * batch + pad) * 2);
+    b->vcache8 = (uint16_t *)b->dalloc(b->slot_kv8 * batch * 2);
     b->state = (int *)b->dalloc((size_t)batch * OXB_STATE_INTS * 4);
     b->tok_hist = (int *)b->dalloc((size_t)batch * b->hist_cap * 4);
     b->rope = (float *)b->dalloc((size_t)max_seq * m->hd * 4);
@@ -172,7 +177,7 @@ extern "C" oxb_batch *oxb_batch_create(oxb_model *m, int batch, int max_seq) {
     b->xscale = (float *)b->dalloc((size_t)rows * 4);
     b->xsum = (int *)b->dalloc((size_t)rows * 4);
     b->X = b->dalloc((size_t)rows * std::max(D, F));
-    bool ok = b->kcache && b->vcache && b->state && b->tok_hist && b->rope && b->x && b->q &&
+    bool ok = b->kcache && b->vcache && b->vcache8 && b->state && b->tok_hist && b->rope && b->x && b->q &&
               b->attn && b->h && b->scores && b->logits && b->hn && b->xscale &&
               b->xsum && b->X;
     if (ok && hipHostMalloc((void **)&b->pinned, (size_t)batch * OXB_STATE_INTS * 4,
@@ -225,7 +230,7 @@ extern "C" int oxb_batch_prefill(oxb_batch *b, int slot, const int32_t *ids, int
     oxb_model &M = *b->m;
     int *st = b->state + (size_t)slot * OXB_STATE_INTS;
     const oxb_model::SeqTarget tg{b->kcache + slot * b->slot_kv, b->vcache + slot * b->slot_kv,
-                                  b->max_seq, b->rope, st,
+                                  b->vcache8 + slot * b->slot_kv8, b->max_seq, b->rope, st,
                                   b->tok_hist + (size_t)slot * b->hist_cap, b->pos[slot]};
     if (M.enqueue_prefill_to(ids, n, tg)) return -1;
     B_CHECK(hipMemcpyAsync(b->pinned, st, OXB_STATE_INTS * 4, hipMemcpyDeviceToHost, M.stream));

@@ -480,6 +480,8 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
     const size_t kv_bytes = kv_elems * m->kv_elem_bytes();
     m->kcache = m->dalloc(kv_bytes);
     m->vcache = m->dalloc(kv_bytes);
+    const size_t kv8_bytes = m->kv_f32 ? 0 : (size_t)m->n_layers * Hkv * v8_head_elems(m->max_seq, hd) * 2;
+    if (kv8_bytes) m->vcache8 = (uint16_t *)m->dalloc(kv8_bytes);
     m->x = (float *)m->dalloc((size_t)D * 4);
     m->q = (float *)m->dalloc((size_t)Dq * 4);
     m->attn = (float *)m->dalloc((size_t)Dq * 4);
@@ -506,12 +508,14 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
     m->samp_u = (float *)m->dalloc((size_t)m->hist_cap * 4);
     m->samp_ws_bytes = oxb::sample_ws_bytes(m->V);
     m->samp_ws = m->dalloc(m->samp_ws_bytes);
-    if (!m->kcache || !m->vcache || !m->x || !m->q || !m->attn || !m->h || !m->scores ||
+    if (!m->kcache || !m->vcache || (kv8_bytes && !m->vcache8) || !m->x || !m->q || !m->attn ||
+        !m->h || !m->scores ||
         !m->logits || !m->state || !m->tok_hist || !m->pf_ws || !m->samp_ctl || !m->samp_u ||
         !m->samp_ws)
         return nullptr;
     if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
-        hipMemset(m->vcache, 0, kv_bytes) != hipSuccess) {
+        hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
+        (kv8_bytes && hipMemset(m->vcache8, 0, kv8_bytes) != hipSuccess)) {
         set_error("hipMemset failed");
         return nullptr;
     }
@@ -561,8 +565,9 @@ int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
         const Layer &L = layers[l];
         void *kv_k = (char *)kcache + l * kv_layer, *kv_v = (char *)vcache + l * kv_layer;
         uint16_t *kc = (uint16_t *)kv_k, *vc = (uint16_t *)kv_v;
+        uint16_t *vc8 = vcache8 ? vcache8 + l * (size_t)Hkv * v8_head_elems(max_seq, hd) : nullptr;
         if (oxb::bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kv_k, kv_v,
-                               kv_f32, max_seq, rope, posp, s))
+                               kv_f32, max_seq, rope, posp, s, vc8))
             return -1;
         int rc;
         if (kv_f32)
@@ -578,7 +583,8 @@ int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
                 rc = oxb_attn_decode_fused(q, kc, vc, posp, H, Hkv, hd, max_seq, this->attn, s);
                 break;
             default:
-                rc = oxb_attn_decode(q, kc, vc, posp, H, Hkv, hd, max_seq, scores, this->attn, s);
+                rc = oxb_attn_decode_batch_v8(q, kc, vc, vc8, posp, 0, 0, 0, 1, H, Hkv, hd,
+                                              max_seq, scores, this->attn, s);
         }
         if (rc) return -1;
         // o_proj with attn_sub_norm (eps 1e-5 fixed, nn/bitlinear.rs:112) + residual
@@ -682,9 +688,11 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];
         void *kc = (char *)tg.kcache + l * kv_layer, *vc = (char *)tg.vcache + l * kv_layer;
+        uint16_t *vc8 =
+            tg.vcache8 ? tg.vcache8 + l * (size_t)Hkv * v8_head_elems(tg.max_seq, hd) : nullptr;
         if (oxb_quantize_rows_tiled(px, L.attn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
         if (oxb::gemm_qkv(L.wqkv, (const int8_t *)pX, pscale, psum, L.sqkv, Dq, Dkv, hd, D, n,
-                          tg.pos, pq, kc, vc, kv_f32, tg.max_seq, tg.rope, s))
+                          tg.pos, pq, kc, vc, kv_f32, tg.max_seq, tg.rope, s, vc8))
             return -1;
         if (kv_f32 ? oxb::attn_f32(pq, (const float *)kc, (const float *)vc, nullptr, tg.pos, n, H,
                                    Hkv, hd, tg.max_seq, pattn, s)
@@ -710,7 +718,8 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
 }
 
 int oxb_model::enqueue_prefill(const int32_t *ids, int n) {
-    return enqueue_prefill_to(ids, n, SeqTarget{kcache, vcache, max_seq, rope, state, tok_hist, pos});
+    return enqueue_prefill_to(ids, n,
+                              SeqTarget{kcache, vcache, vcache8, max_seq, rope, state, tok_hist, pos});
 }
 
 // ---------------------------------------------------------------------------

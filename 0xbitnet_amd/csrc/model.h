@@ -33,6 +33,9 @@ struct oxb_model {
     // [L][Hkv][max_seq][hd]: f16 bits, or f32 when kv_f32 (the reference's
     // cache type, nn/attention.rs:23-48; a parity mode of the engine)
     void *kcache = nullptr, *vcache = nullptr;
+    // f16 cache: V again in position octets (v8_index), per layer
+    // [Hkv][round8(max_seq) x hd]: the long-context decode P.V reads it
+    uint16_t *vcache8 = nullptr;
     bool kv_f32 = false;
     size_t kv_elem_bytes() const { return kv_f32 ? 4 : 2; }
 
@@ -100,6 +103,7 @@ struct oxb_model {
     // block, token history and position
     struct SeqTarget {
         void *kcache, *vcache;   // element type as the model's (kv_f32)
+        uint16_t *vcache8;       // the octet copy of V (f16 cache), or null
         int max_seq;
         const float *rope;
         int *state, *tok_hist;

@@ -66,6 +66,18 @@ __host__ __device__ inline size_t tiled_offset16(int row, int kc, int KC) {
     return ((size_t)(row >> 4) * KC + kc) * 16 + (row & 15);
 }
 
+// The decode V copy in position octets (per KV head of a layer): element
+// (position s, dim d) of a head of hd dims at ((s / 8) * hd + d) * 8 + s % 8,
+// so one 16-byte load gives one dim's 8 consecutive positions and a wave's
+// 64 lanes (64 consecutive dims) read 1 KB contiguous.  A head holds
+// max_seq rounded up to 8 positions.
+__host__ __device__ inline size_t v8_head_elems(int max_seq, int hd) {
+    return (size_t)((max_seq + 7) & ~7) * hd;
+}
+__host__ __device__ inline size_t v8_index(int s, int d, int hd) {
+    return ((size_t)(s >> 3) * hd + d) * 8 + (s & 7);
+}
+
 // exp(x) for the softmaxes and the sampler, fixed so that host and device give
 // the same bits:
 // Cody-Waite reduction x = k*ln2 + r (15-bit head of ln2 plus the tail),

@@ -17,18 +17,21 @@ int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int
                   const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok,
                   const int *tok_pos, int tok_pos_stride, size_t kv_tok_stride, float *q_out,
                   uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
-                  bool gemv_order, void *stream);
+                  bool gemv_order, void *stream, uint16_t *vcache8 = nullptr,
+                  size_t kv8_tok_stride = 0);
 // QKV projections that store K/V as f16 bits or, with kv_f32, as f32 (the
 // reference's cache type): one token (GEMV, ternary_gemv.hip) or a prefill
 // block (GEMM, ternary_gemm.hip).
+// vcache8 (optional, f16 cache only): V also written in position octets
+// (v8_index), the layout of the long-context decode P.V (attn_decode_v8).
 int bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float eps,
                   const float *wscale, int Dq, int Dkv, int hd, int K, float *q_out, void *kcache,
                   void *vcache, bool kv_f32, int max_seq, const float *rope_cs, const int *pos,
-                  void *stream);
+                  void *stream, uint16_t *vcache8 = nullptr);
 int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
              const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
              float *q_out, void *kcache, void *vcache, bool kv_f32, int max_seq,
-             const float *rope_cs, void *stream);
+             const float *rope_cs, void *stream, uint16_t *vcache8 = nullptr);
 // Attention over an f32 cache ([Hkv][max_seq][hd]): n_q queries at positions
 // pos0 + i, or one query at *pos_ptr when pos_ptr is given (attention.hip).
 // Causal prefill attention (oxb_attn_prefill) with the caller's workspace for

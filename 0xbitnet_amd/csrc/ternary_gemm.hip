@@ -43,6 +43,8 @@ struct GemmParams {
     // QKV
     float *q_out;          // [n_tok][Dq]
     void *kcache, *vcache;     // f16 bits, or f32 when kv_f32
+    uint16_t *vcache8;         // optional (f16): V also in position octets (v8_index)
+    size_t kv8_tok_stride;     // tok_pos: elements between consecutive tokens' octet caches
     int kv_f32;
     const float2 *rope;
     int Dq, Dkv, hd, max_seq, pos0;
@@ -168,8 +170,15 @@ __device__ inline void gemm_store(const GemmParams &p, const v4i &c, int t, int 
                 *(float4 *)((float *)cache + at) = make_float4(o[0], o[1], o[2], o[3]);
             } else {
                 uint16_t *dst = (uint16_t *)cache + at;
+                uint16_t bits[4];
 #pragma unroll
-                for (int v = 0; v < 4; ++v) dst[v] = __half_as_ushort(__float2half_rn(o[v]));
+                for (int v = 0; v < 4; ++v) dst[v] = bits[v] = __half_as_ushort(__float2half_rn(o[v]));
+                if (n0 >= Dk && p.vcache8) {
+                    uint16_t *d8 = p.vcache8 + (p.tok_pos ? t * p.kv8_tok_stride : 0) +
+                                   (size_t)head * v8_head_elems(p.max_seq, p.hd);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) d8[v8_index(pos, d + v, p.hd)] = bits[v];
+                }
             }
         }
     }
@@ -736,7 +745,7 @@ namespace oxb {
 int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
              const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
              float *q_out, void *kcache, void *vcache, bool kv_f32, int max_seq,
-             const float *rope_cs, void *stream) {
+             const float *rope_cs, void *stream, uint16_t *vcache8) {
     const int N = Dq + 2 * Dkv;
     if (gemm_check(N, K, n_tok)) return -1;
     OXB_REQUIRE(Dq % 32 == 0 && Dkv % 32 == 0 && hd % 16 == 0, "gemm qkv: bad head split");
@@ -760,6 +769,7 @@ int gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const in
     p.max_seq = max_seq;
     p.pos0 = pos0;
     p.kv_f32 = kv_f32 ? 1 : 0;
+    p.vcache8 = kv_f32 ? nullptr : vcache8;
     return gemm_launch<GE_QKV>(p, stream);
 }
 
@@ -790,7 +800,7 @@ int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int
                   const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok,
                   const int *tok_pos, int tok_pos_stride, size_t kv_tok_stride, float *q_out,
                   uint16_t *kcache, uint16_t *vcache, int max_seq, const float *rope_cs,
-                  bool gemv_order, void *stream) {
+                  bool gemv_order, void *stream, uint16_t *vcache8, size_t kv8_tok_stride) {
     const int N = Dq + 2 * Dkv;
     if (gemm_check(N, K, n_tok)) return -1;
     OXB_REQUIRE(Dq % 32 == 0 && Dkv % 32 == 0 && hd % 16 == 0, "gemm qkv: bad head split");
@@ -814,6 +824,8 @@ int gemm_qkv_rows(const void *W, const int8_t *X, const float *xscale, const int
     p.tok_pos = tok_pos;
     p.tok_pos_stride = tok_pos_stride;
     p.kv_tok_stride = kv_tok_stride;
+    p.vcache8 = vcache8;
+    p.kv8_tok_stride = kv8_tok_stride;
     p.gemv_order = gemv_order ? 1 : 0;
     return gemm_launch<GE_QKV>(p, stream);
 }

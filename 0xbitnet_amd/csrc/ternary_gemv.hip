@@ -47,6 +47,7 @@ struct GemvParams {
     // QKV
     float *q_out;          // [Dq]
     void *kcache, *vcache;  // [Hkv][max_seq][hd] f16 bits (EPI_QKV) or f32 (EPI_QKV32)
+    uint16_t *vcache8;      // optional (EPI_QKV): V also in position octets (v8_index)
     const float2 *rope;    // [max_seq][hd/2] (cos, sin)
     const int *pos;        // device position
     int Dq, Dkv, hd, max_seq;
@@ -382,10 +383,15 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
             const int head = j / p.hd, d = j % p.hd;
             const size_t at = ((size_t)head * p.max_seq + pos) * p.hd + d;
             void *cache = n < Dk ? p.kcache : p.vcache;
-            if constexpr (EPI == EPI_QKV32)
+            if constexpr (EPI == EPI_QKV32) {
                 ((float *)cache)[at] = outv;
-            else
-                ((uint16_t *)cache)[at] = f32_to_f16_bits(outv);
+            } else {
+                const uint16_t bits = f32_to_f16_bits(outv);
+                ((uint16_t *)cache)[at] = bits;
+                if (n >= Dk && p.vcache8)
+                    p.vcache8[(size_t)head * v8_head_elems(p.max_seq, p.hd) +
+                              v8_index(pos, d, p.hd)] = bits;
+            }
         }
     }
 }
@@ -587,7 +593,7 @@ namespace oxb {
 int bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float eps,
                   const float *wscale, int Dq, int Dkv, int hd, int K, float *q_out, void *kcache,
                   void *vcache, bool kv_f32, int max_seq, const float *rope_cs, const int *pos,
-                  void *stream_) {
+                  void *stream_, uint16_t *vcache8) {
     OXB_STREAM;
     const int N = Dq + 2 * Dkv;
     if (check_shape(N, K, true)) return -1;
@@ -604,6 +610,7 @@ int bitlinear_qkv(const void *W_tiled, const float *x, const float *gamma, float
     p.q_out = q_out;
     p.kcache = kcache;
     p.vcache = vcache;
+    p.vcache8 = kv_f32 ? nullptr : vcache8;
     p.rope = (const float2 *)rope_cs;
     p.pos = pos;
     p.Dq = Dq;

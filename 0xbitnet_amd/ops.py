@@ -200,6 +200,19 @@ def _padded_cache(c: np.ndarray, hd: int) -> DeviceArray:
     return DeviceArray.from_host(np.concatenate([flat, np.zeros(KV_PAD_ROWS * hd, np.uint16)]))
 
 
+def v_octets(vc: np.ndarray) -> np.ndarray:
+    """V cache rows [..., Hkv, S, hd] (f16) in the decode P.V's octet layout:
+    per head round8(S) x hd elements, (position s, dim d) at ((s // 8) * hd +
+    d) * 8 + s % 8 (positions past S zero)."""
+    vc = np.asarray(vc, np.float16)
+    *lead, hkv, S, hd = vc.shape
+    S8 = (S + 7) // 8 * 8
+    pad = np.zeros((*lead, hkv, S8, hd), np.float16)
+    pad[..., :S, :] = vc
+    o = pad.reshape(*lead, hkv, S8 // 8, 8, hd).swapaxes(-1, -2)   # [.., oct, hd, 8]
+    return np.ascontiguousarray(o).view(np.uint16).reshape(*lead, hkv * S8 * hd)
+
+
 def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, H: int, Hkv: int,
                 hd: int, max_seq: int, fused: bool = False, head: bool = False, s_max: int = 0):
     """q [H*hd] f32; caches [Hkv][max_seq][hd] f16; attends over pos+1 positions.

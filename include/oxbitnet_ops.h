@@ -158,6 +158,19 @@ int oxb_attn_decode_batch(const float *q, const uint16_t *kcache, const uint16_t
                           const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                           int Hkv, int hd, int max_seq, float *scores, float *out, void *stream);
 
+/* The same, with the V cache also held in position octets (vcache8, a copy
+ * the q|k|v projections keep beside the row-major cache in the model): per
+ * KV head of a sequence round8(max_seq) x 128 f16, element (position s, dim
+ * d) at ((s / 8) * 128 + d) * 8 + s % 8; sequence z's copy at vcache8 +
+ * z*kv8_stride.  One 16-byte read gives a P.V chain its dim's next 8
+ * positions (the row-major rows hold them 256 bytes apart), for batches of
+ * up to 8; larger batches read vcache.  Same result bits.  No counterpart in
+ * the reference (its cache is [max_seq][Hkv][hd] f32, nn/attention.rs:23-48). */
+int oxb_attn_decode_batch_v8(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                             const uint16_t *vcache8, const int *pos, int pos_stride,
+                             size_t kv_stride, size_t kv8_stride, int batch, int H, int Hkv,
+                             int hd, int max_seq, float *scores, float *out, void *stream);
+
 /* The same decode attention as one kernel: two 1024-thread workgroups per KV
  * head (one per half of the dims) compute scores, softmax and P.V in LDS (no
  * scores buffer), same result bits.  Faster for short caches (each KV head's

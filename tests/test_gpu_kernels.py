@@ -371,9 +371,53 @@ def test_attn_decode_batch_bitexact(B, H, Hkv, S):
                                       Hkv, hd, S, sc.ptr, out.ptr, None), "attn_decode_batch")
     ops.sync()
     got = out.download()
+    # the same with the octet copy of V (read by batches of up to 8)
+    v8 = ops.v_octets(vc)
+    dv8 = ops.DeviceArray.from_host(v8)
+    out8 = ops.DeviceArray((B, H * hd), np.float32)
+    ops.check(L.oxb_attn_decode_batch_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dst.ptr, 8,
+                                         Hkv * S * hd, v8.shape[-1], B, H, Hkv, hd, S, sc.ptr,
+                                         out8.ptr, None), "attn_decode_batch_v8")
+    ops.sync()
+    got8 = out8.download()
     for z in range(B):
         ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(pos[z]) + 1, H, Hkv, hd)
         assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"slot {z}"
+        assert np.array_equal(got8[z].view(np.uint32), ref.view(np.uint32)), f"octets, slot {z}"
+
+
+@pytest.mark.parametrize("S,pos", [(8, 0), (8, 7), (9, 8), (16, 9), (128, 127), (129, 128),
+                                   (300, 255), (300, 256), (1000, 999), (2560, 2303),
+                                   (4099, 4098), (6144, 6143), (6144, 130)])
+def test_attn_decode_octets_ring_edges(S, pos):
+    """The octet P.V kernel at the edges of its octets (8 positions) and ring
+    slots (128), a cache not a multiple of 8 long and the longest cache:
+    bit-equal to the oracle; its entry point also rejects a missing copy."""
+    rng = np.random.default_rng(S + 7 * pos)
+    H, Hkv, hd = 20, 5, 128
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
+    L = ops.lib()
+    dq = ops.DeviceArray.from_host(q)
+    dk = ops.DeviceArray.from_host(kc.view(np.uint16))
+    dv = ops.DeviceArray.from_host(vc.view(np.uint16))
+    v8 = ops.v_octets(vc)
+    # positions past pos in the copy hold NaN: they must never be summed
+    o = v8.view(np.float16).reshape(Hkv, -1, hd, 8)
+    for s in range(pos + 1, (S + 7) // 8 * 8):
+        o[:, s // 8, :, s % 8] = np.nan
+    dv8 = ops.DeviceArray.from_host(v8)
+    dpos = ops.DeviceArray.from_host(np.array([pos], np.int32))
+    sc = ops.DeviceArray((H * S,), np.float32)
+    out = ops.DeviceArray((H * hd,), np.float32)
+    ops.check(L.oxb_attn_decode_batch_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dpos.ptr, 0, 0, 0, 1, H,
+                                         Hkv, hd, S, sc.ptr, out.ptr, None), "attn v8")
+    ops.sync()
+    ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
+    assert np.array_equal(out.download().view(np.uint32), ref.view(np.uint32))
+    assert L.oxb_attn_decode_batch_v8(dq.ptr, dk.ptr, dv.ptr, None, dpos.ptr, 0, 0, 0, 1, H, Hkv,
+                                      hd, S, sc.ptr, out.ptr, None) == -1
 
 
 def test_attn_decode_fused_rejects_unsupported():
