@@ -792,6 +792,76 @@ __global__ __launch_bounds__(kPhThreads) void attn_pv_oct_kernel(
     if (w == 0) out[64 * half + lane] = acc;
 }
 
+// The 16-wave P.V above over the octet copy of V (larger batches): wave w
+// stages octet w of each 128-position slot of this workgroup's half of the
+// dims, and chain wave w < 4 sums row w (head 4 rg + w), lane l chaining dim
+// 64 dh + l with one 16-byte read per 8 positions (po_chain_slot).  Same
+// grid, ring protocol and LDS sizes (pc_smem) as attn_pv_chain_kernel.
+template <int NS>
+__global__ __launch_bounds__(kPcThreads) void attn_pv_chain_oct_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc8,
+    const int *__restrict__ pos_ptr, int G, int max_seq, float *__restrict__ out,
+    size_t kv8_stride, int pos_stride) {
+    static_assert(NS >= 3 && NS - 3 < 64, "ring depth within vmcnt");
+    static_assert(kPcRows == kPoRows && kPcSlotBytes == kPoSlotBytes && kPcWaves == kPoOcts,
+                  "one octet load per wave and slot");
+    const int RG = (G + 3) >> 2;                  // groups of four heads per KV head
+    const int dh = blockIdx.x & 1, hg = blockIdx.x >> 1;
+    const int hk = hg / RG, rg = hg % RG, z = blockIdx.y;
+    const int Hkv = (gridDim.x >> 1) / RG, H = Hkv * G;
+    scores += (size_t)z * H * max_seq;
+    vc8 += (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd);
+    out += (size_t)z * H * kHd + 64 * dh;
+    extern __shared__ __align__(16) int8_t smem_pco[];
+    uint4 *ring = (uint4 *)smem_pco;
+    const int Sp = pc_row_stride(max_seq);
+    float *pr = (float *)(smem_pco + (size_t)NS * kPcSlotBytes);
+    float *red = pr + 4 * Sp, *wmax = red + 4 * 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1;
+    const int nslots = (S + kPoRows - 1) / kPoRows;
+    const int last_oct = (S - 1) >> 3;
+
+    // this wave's share of a slot: octet w, one 1 KB load (lane l: dim
+    // 64 dh + l), clamped to the last octet
+    const uint4 *V8 = (const uint4 *)vc8 + 64 * dh + lane;
+    auto issue = [&](int c) {
+        const int o = c * kPoOcts + w;
+        lds_dma16(V8 + (size_t)min(o, last_oct) * kHd,
+                  ring + ((size_t)(c % NS) * kPoOcts + w) * 64);
+    };
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+
+    // ---- softmax: row r = w / 4 (head 4rg + r of the KV head) -------------
+    {
+        const int r = w >> 2, j = w & 3, head = 4 * rg + r;
+        softmax_row_4w_any(pr + r * Sp, scores + (size_t)(hk * G + min(head, G - 1)) * max_seq, S,
+                           head < G, wmax + 4 * r, red + 256 * r, j, lane);
+    }
+
+    // ---- P.V chains over the ring: wave w < 4 sums row w -------------------
+    const float *prow = pr + (w & 3) * Sp;
+    float acc = 0.0f;
+    for (int c = 0; c < nslots; ++c) {
+        wait_vmcnt<NS - 3>();   // this wave's loads of slots c and c + 1 have landed
+        if (w < 4 && c > 0)
+            asm volatile("s_barrier" ::: "memory");   // reads in flight stay (see above)
+        else
+            lds_barrier();
+        issue(c + NS - 1);      // into slot c - 1's ring entry (clamped past the cache)
+        if (w < 4) {
+            const uint4 *vs = ring + (size_t)(c % NS) * kPoOcts * 64 + lane;
+            acc = po_chain_slot(acc, vs, prow + c * kPoRows, min(kPoRows, S - c * kPoRows));
+        }
+    }
+    wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
+    if (w < 4 && 4 * rg + w < G) out[(size_t)(hk * G + 4 * rg + w) * kHd + lane] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Prefill: one workgroup per (Q consecutive queries, KV head); query i of
 // the block sits at position pos0 + q0 + i and attends over S_i = its
@@ -2039,6 +2109,21 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
         return 0;
     }
     const dim3 grid(Hkv * ((G + 3) / 4) * 2, batch);
+    if (vc8) {
+        if (pc_smem(5, max_seq) <= 160 * 1024) {
+            if (allow_dynamic_lds((const void *)attn_pv_chain_oct_kernel<5>)) return -1;
+            hipLaunchKernelGGL(attn_pv_chain_oct_kernel<5>, grid, dim3(kPcThreads),
+                               pc_smem(5, max_seq), s, scores, vc8, pos, G, max_seq, out,
+                               kv8_stride, pos_stride);
+        } else {
+            if (allow_dynamic_lds((const void *)attn_pv_chain_oct_kernel<3>)) return -1;
+            hipLaunchKernelGGL(attn_pv_chain_oct_kernel<3>, grid, dim3(kPcThreads),
+                               pc_smem(3, max_seq), s, scores, vc8, pos, G, max_seq, out,
+                               kv8_stride, pos_stride);
+        }
+        OXB_CHECK_HIP(hipGetLastError());
+        return 0;
+    }
     if (pc_smem(5, max_seq) <= 160 * 1024) {
         if (allow_dynamic_lds((const void *)attn_pv_chain_kernel<5>)) return -1;
         hipLaunchKernelGGL(attn_pv_chain_kernel<5>, grid, dim3(kPcThreads), pc_smem(5, max_seq), s,

@@ -347,7 +347,8 @@ def test_attn_decode_head_rejects_long_caches():
 
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
                                        (9, 8, 8, 512), (8, 16, 8, 2600), (7, 20, 5, 1001),
-                                       (32, 20, 5, 2560), (3, 32, 4, 700)])
+                                       (32, 20, 5, 2560), (3, 32, 4, 700), (12, 64, 8, 1500),
+                                       (10, 16, 8, 300)])
 def test_attn_decode_batch_bitexact(B, H, Hkv, S):
     """Batched decode attention (per-slot caches and positions): every slot
     equals the oracle."""
