@@ -103,6 +103,8 @@ SIGNATURES = {
     "oxb_sample_device": (C.c_int, [vp, i32, C.c_float, C.c_size_t, C.c_float, vp, i32, vp, vp,
                                     vp, C.c_size_t, vp]),
     "oxb_attn_decode_noalloc": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "oxb_attn_decode_head_v8": (C.c_int, [vp, vp, vp, vp, vp, i32, C.c_size_t, C.c_size_t, i32,
+                                          i32, i32, i32, i32, i32, vp, vp]),
     "oxb_attn_decode_head": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                        i32, vp, vp]),
     "oxb_attn_prefill": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),

@@ -1735,10 +1735,57 @@ __device__ __forceinline__ float pv_head(const uint32_t *vcol, const float *pr, 
     return acc;
 }
 
+// P.V of one wave over the octet copy staged in LDS (vo: the lane's uint4 of
+// octet 0; octets kHd uint4 apart): one chain over S <= ROWS positions in
+// order of s, 8 positions per 16-byte read, octets read three ahead, fully
+// unrolled with wave-uniform exits (as pv_head).
+template <int ROWS>
+__device__ __forceinline__ float pv_head_oct(const uint4 *vo, const float *pr, int S) {
+    constexpr int NO = ROWS / 8;
+    float acc = 0.0f;
+    uint4 V[4];
+    float4 Pa[4], Pb[4];
+    auto ld = [&](int b, int o) {   // octet o (clamped into the rows) into entry b
+        o = min(o, NO - 1);
+        V[b] = vo[o * kHd];
+        Pa[b] = *(const float4 *)(pr + 8 * o);
+        Pb[b] = *(const float4 *)(pr + 8 * o + 4);
+    };
+    ld(0, 0);
+    ld(1, 1);
+    ld(2, 2);
+    int o0 = 0;
+#pragma unroll
+    for (int it = 0; it < NO / 4; ++it) {
+        if (8 * (o0 + 4) > S) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            ld((j + 3) & 3, o0 + j + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv8<true>(acc, V[j], Pa[j], Pb[j]);
+        }
+        o0 += 4;
+    }
+    // the last S - 8 o0 < 32 positions: entries 0..2 hold octets o0 .. o0 + 2
+    ld(3, o0 + 3);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = S - 8 * (o0 + j);
+        if (n >= 8) acc = pv8<true>(acc, V[j], Pa[j], Pb[j]);
+        else if (n > 0) acc = pv8<false>(acc, V[j], Pa[j], Pb[j], n);
+    }
+    return acc;
+}
+
+// OCT: vc is the octet copy of V (v8_index; sequence z at vc + z * kv8_stride),
+// staged as it is and summed 8 positions per read (pv_head_oct), wave w taking
+// dims 64 w .. 64 w + 63.
+template <bool OCT>
 __global__ __launch_bounds__(256) void attn_head256_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float scale,
-    float *__restrict__ out, size_t kv_stride, int pos_stride) {
+    float *__restrict__ out, size_t kv_stride, int pos_stride, size_t kv8_stride) {
     // all kernel arguments in SGPRs up front: read where they are used, the
     // late ones are further kernarg round trips before the position's load
     asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(Hkv), "s"(max_seq),
@@ -1756,7 +1803,8 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
     kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
-    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    vc += OCT ? (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd)
+              : (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
     const int pos = pos_ptr[(size_t)z * pos_stride];
@@ -1772,8 +1820,14 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
     // and the P.V chains stop at S)
 #pragma unroll
     for (int k = 0; k < 16; ++k) kt[k] = K4[min(16 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+    if constexpr (OCT) {   // the first 32 octets (max_seq >= 256: all in the copy)
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vt[k] = V4[min(16 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+        for (int k = 0; k < 16; ++k) vt[k] = V4[256 * k + tid];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            vt[k] = V4[min(16 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+    }
     __builtin_amdgcn_sched_barrier(0);
     const bool valid = pos >= 0 && pos < kH256Rows && pos < max_seq;
     const int S = valid ? pos + 1 : 1;
@@ -1842,9 +1896,15 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
 
     // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
     if (w < 2) {
-        const float acc = w == 0 ? pv_head<false, kH256Rows>(vs + lane, pr, S)
-                                 : pv_head<true, kH256Rows>(vs + lane, pr, S);
-        if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
+        if constexpr (OCT) {
+            const float acc =
+                pv_head_oct<kH256Rows>((const uint4 *)vs4 + 64 * w + lane, pr, S);
+            if (valid) out[((size_t)z * H + h) * kHd + 64 * w + lane] = acc;
+        } else {
+            const float acc = w == 0 ? pv_head<false, kH256Rows>(vs + lane, pr, S)
+                                     : pv_head<true, kH256Rows>(vs + lane, pr, S);
+            if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
+        }
     }
 }
 
@@ -1862,10 +1922,12 @@ constexpr size_t kH512KBytes = (size_t)kH512Rows * 17 * 16;   // K rows, padded;
 constexpr size_t kH512Lds = kH512KBytes + (kHd + 512 + 512 + 256 + 8) * 4;
 static_assert((size_t)kH512Rows * kHd * 2 <= kH512KBytes, "V rows fit the K region");
 
+// OCT: vc is the octet copy of V, as in attn_head256_kernel.
+template <bool OCT>
 __global__ __launch_bounds__(512) void attn_head512_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
     const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float scale,
-    float *__restrict__ out, size_t kv_stride, int pos_stride) {
+    float *__restrict__ out, size_t kv_stride, int pos_stride, size_t kv8_stride) {
     asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(pos_ptr), "s"(G), "s"(Hkv), "s"(max_seq),
                  "s"(scale), "s"(out), "s"(kv_stride), "s"(pos_stride));
     extern __shared__ __align__(16) int8_t smem_h[];
@@ -1882,7 +1944,8 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     const int hk = h / G;
     const float *__restrict__ qh = q + ((size_t)z * H + h) * kHd;
     kc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
-    vc += (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
+    vc += OCT ? (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd)
+              : (size_t)z * kv_stride + (size_t)hk * max_seq * kHd;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
     const int pos = pos_ptr[(size_t)z * pos_stride];
@@ -1895,8 +1958,15 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
     // or past S are never used)
 #pragma unroll
     for (int k = 0; k < 16; ++k) kt[k] = K4[min(32 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+    if constexpr (OCT) {   // the first 64 octets, clamped to the copy (never summed past S)
+        const int last = (int)(v8_head_elems(max_seq, kHd) / 8) - 1;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vt[k] = V4[min(32 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+        for (int k = 0; k < 16; ++k) vt[k] = V4[min(512 * k + tid, last)];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            vt[k] = V4[min(32 * k + (tid >> 4), max_seq - 1) * 16 + (tid & 15)];
+    }
     __builtin_amdgcn_sched_barrier(0);
     const bool valid = pos >= 0 && pos < kH512Rows && pos < max_seq;
     const int S = valid ? pos + 1 : 1;
@@ -1963,9 +2033,15 @@ __global__ __launch_bounds__(512) void attn_head512_kernel(
 
     // ---- P.V (sh/attention.wgsl:96-104) on waves 0 and 1 ----------------------
     if (w < 2) {
-        const float acc = w == 0 ? pv_head<false, kH512Rows>(vs + lane, pr, S)
-                                 : pv_head<true, kH512Rows>(vs + lane, pr, S);
-        if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
+        if constexpr (OCT) {
+            const float acc =
+                pv_head_oct<kH512Rows>((const uint4 *)vs4 + 64 * w + lane, pr, S);
+            if (valid) out[((size_t)z * H + h) * kHd + 64 * w + lane] = acc;
+        } else {
+            const float acc = w == 0 ? pv_head<false, kH512Rows>(vs + lane, pr, S)
+                                     : pv_head<true, kH512Rows>(vs + lane, pr, S);
+            if (valid) out[((size_t)z * H + h) * kHd + 2 * lane + w] = acc;
+        }
     }
 }
 
@@ -2258,36 +2334,68 @@ extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const ui
     return rc;
 }
 
-extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                                    const int *pos, int pos_stride, size_t kv_stride, int batch,
-                                    int H, int Hkv, int hd, int max_seq, int s_max, float *out,
-                                    void *stream) {
+static int decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                       const uint16_t *vcache8, const int *pos, int pos_stride, size_t kv_stride,
+                       size_t kv8_stride, int batch, int H, int Hkv, int hd, int max_seq,
+                       int s_max, float *out, void *stream) {
     OXB_REQUIRE(pos, "attention: pos is NULL");
     OXB_REQUIRE(hd == kHd, "attention: head_dim %d unsupported (128 only)", hd);
     OXB_REQUIRE(Hkv > 0 && H % Hkv == 0, "attention: heads %d not a multiple of kv heads %d", H, Hkv);
     OXB_REQUIRE(batch >= 1 && batch <= 65535, "attention: batch %d", batch);
     OXB_REQUIRE(batch == 1 || kv_stride >= (size_t)Hkv * max_seq * hd,
                 "attention: caches of a batch overlap (stride %zu)", kv_stride);
+    OXB_REQUIRE(!vcache8 || batch == 1 || kv8_stride >= (size_t)Hkv * v8_head_elems(max_seq, hd),
+                "attention: octet caches of a batch overlap (stride %zu)", kv8_stride);
     OXB_REQUIRE(s_max >= 1 && s_max <= 512,
                 "per-head decode attention: s_max %d out of range (1..512)", s_max);
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
     hipStream_t s = (hipStream_t)stream;
     const int G = H / Hkv;
     const dim3 grid(head_grid_blocks(G, Hkv), batch);
-    if (s_max <= 256 && max_seq >= kH256Rows) {
-        if (allow_dynamic_lds((const void *)attn_head256_kernel)) return -1;
-        hipLaunchKernelGGL(attn_head256_kernel, grid, dim3(256), kH256Lds, s, q, kcache, vcache,
-                           pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    if (s_max <= 256 && max_seq >= kH256Rows && vcache8) {
+        if (allow_dynamic_lds((const void *)attn_head256_kernel<true>)) return -1;
+        hipLaunchKernelGGL(attn_head256_kernel<true>, grid, dim3(256), kH256Lds, s, q, kcache,
+                           vcache8, pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride,
+                           kv8_stride);
+    } else if (s_max <= 256 && max_seq >= kH256Rows) {
+        if (allow_dynamic_lds((const void *)attn_head256_kernel<false>)) return -1;
+        hipLaunchKernelGGL(attn_head256_kernel<false>, grid, dim3(256), kH256Lds, s, q, kcache,
+                           vcache, pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride,
+                           (size_t)0);
     } else if (s_max <= 256)
         hipLaunchKernelGGL(attn_head_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos, G, Hkv,
                            max_seq, scale, out, kv_stride, pos_stride);
-    else {
-        if (allow_dynamic_lds((const void *)attn_head512_kernel)) return -1;
-        hipLaunchKernelGGL(attn_head512_kernel, grid, dim3(512), kH512Lds, s, q, kcache, vcache,
-                           pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride);
+    else if (vcache8) {
+        if (allow_dynamic_lds((const void *)attn_head512_kernel<true>)) return -1;
+        hipLaunchKernelGGL(attn_head512_kernel<true>, grid, dim3(512), kH512Lds, s, q, kcache,
+                           vcache8, pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride,
+                           kv8_stride);
+    } else {
+        if (allow_dynamic_lds((const void *)attn_head512_kernel<false>)) return -1;
+        hipLaunchKernelGGL(attn_head512_kernel<false>, grid, dim3(512), kH512Lds, s, q, kcache,
+                           vcache, pos, G, Hkv, max_seq, scale, out, kv_stride, pos_stride,
+                           (size_t)0);
     }
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
+}
+
+extern "C" int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                    const int *pos, int pos_stride, size_t kv_stride, int batch,
+                                    int H, int Hkv, int hd, int max_seq, int s_max, float *out,
+                                    void *stream) {
+    return decode_head(q, kcache, vcache, nullptr, pos, pos_stride, kv_stride, 0, batch, H, Hkv,
+                       hd, max_seq, s_max, out, stream);
+}
+
+extern "C" int oxb_attn_decode_head_v8(const float *q, const uint16_t *kcache,
+                                       const uint16_t *vcache, const uint16_t *vcache8,
+                                       const int *pos, int pos_stride, size_t kv_stride,
+                                       size_t kv8_stride, int batch, int H, int Hkv, int hd,
+                                       int max_seq, int s_max, float *out, void *stream) {
+    OXB_REQUIRE(vcache8, "attention: vcache8 is NULL");
+    return decode_head(q, kcache, vcache, vcache8, pos, pos_stride, kv_stride, kv8_stride, batch,
+                       H, Hkv, hd, max_seq, s_max, out, stream);
 }
 
 // ---------------------------------------------------------------------------

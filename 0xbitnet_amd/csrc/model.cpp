@@ -576,8 +576,9 @@ int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
         else switch (attn) {
             case ATTN_HEAD1:
             case ATTN_HEAD2:
-                rc = oxb_attn_decode_head(q, kc, vc, posp, 0, 0, 1, H, Hkv, hd, max_seq,
-                                          attn == ATTN_HEAD1 ? 256 : 512, this->attn, s);
+                rc = oxb_attn_decode_head_v8(q, kc, vc, vc8, posp, 0, 0, 0, 1, H, Hkv, hd,
+                                             max_seq, attn == ATTN_HEAD1 ? 256 : 512, this->attn,
+                                             s);
                 break;
             case ATTN_FUSED:
                 rc = oxb_attn_decode_fused(q, kc, vc, posp, H, Hkv, hd, max_seq, this->attn, s);

@@ -214,19 +214,32 @@ def v_octets(vc: np.ndarray) -> np.ndarray:
 
 
 def attn_decode(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, H: int, Hkv: int,
-                hd: int, max_seq: int, fused: bool = False, head: bool = False, s_max: int = 0):
+                hd: int, max_seq: int, fused: bool = False, head: bool = False, s_max: int = 0,
+                octets: bool = False):
     """q [H*hd] f32; caches [Hkv][max_seq][hd] f16; attends over pos+1 positions.
     fused: the one-kernel variant (oxb_attn_decode_fused); head: one workgroup
-    per query head (oxb_attn_decode_head, caches padded as it requires)."""
+    per query head (oxb_attn_decode_head, caches padded as it requires);
+    octets: with the octet copy of V as well (oxb_attn_decode_head_v8 /
+    oxb_attn_decode_batch_v8)."""
     dq = DeviceArray.from_host(np.ascontiguousarray(q, np.float32))
     dk = _padded_cache(kcache, hd)
     dv = _padded_cache(vcache, hd)
     dpos = DeviceArray.from_host(np.array([pos], np.int32))
     out = DeviceArray((H * hd,), np.float32)
-    if head:
+    dv8 = DeviceArray.from_host(v_octets(vcache)) if octets else None
+    if head and octets:
+        check(lib().oxb_attn_decode_head_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dpos.ptr, 0, 0, 0, 1,
+                                            H, Hkv, hd, max_seq, s_max or pos + 1, out.ptr, None),
+              "attn_decode_head_v8")
+    elif head:
         check(lib().oxb_attn_decode_head(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, 0, 0, 1, H, Hkv, hd,
                                          max_seq, s_max or pos + 1, out.ptr, None),
               "attn_decode_head")
+    elif octets:
+        sc = DeviceArray((H * max_seq,), np.float32)
+        check(lib().oxb_attn_decode_batch_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dpos.ptr, 0, 0, 0, 1,
+                                             H, Hkv, hd, max_seq, sc.ptr, out.ptr, None),
+              "attn_decode_batch_v8")
     elif fused:
         check(lib().oxb_attn_decode_fused(dq.ptr, dk.ptr, dv.ptr, dpos.ptr, H, Hkv, hd, max_seq,
                                           out.ptr, None), "attn_decode_fused")

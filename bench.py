@@ -426,6 +426,8 @@ def decode_breakdown(ops, synth, pos: int = 139) -> dict:
     kvl = Hkv * max_seq * hd
     kc = ops.DeviceArray((nl * kvl + 64 * hd,), np.uint16, zero=True)
     vc = ops.DeviceArray((nl * kvl + 64 * hd,), np.uint16, zero=True)
+    kvl8 = Hkv * ((max_seq + 7) // 8 * 8) * hd   # the octet copy of V the model's attention reads
+    vc8 = ops.DeviceArray((nl * kvl8,), np.uint16, zero=True)
     rng = np.random.default_rng(5)
     x = ops.DeviceArray.from_host(rng.standard_normal(D).astype(np.float32))
     ones = ops.DeviceArray.from_host(np.ones(2 * F, np.float32))
@@ -448,8 +450,9 @@ def decode_breakdown(ops, synth, pos: int = 139) -> dict:
                                       state.ptr, stream), "qkv")
 
     def attn(l):
-        ops.check(L.oxb_attn_decode_head(q.ptr, kc.ptr + l * kv_b, vc.ptr + l * kv_b, state.ptr, 0, 0,
-                                         1, H, Hkv, hd, max_seq, 256, att.ptr, stream), "attention")
+        ops.check(L.oxb_attn_decode_head_v8(q.ptr, kc.ptr + l * kv_b, vc.ptr + l * kv_b,
+                                            vc8.ptr + l * kvl8 * 2, state.ptr, 0, 0, 0, 1, H, Hkv,
+                                            hd, max_seq, 256, att.ptr, stream), "attention")
 
     def o(l):
         ops.check(L.oxb_bitlinear_gemv(lay[l]["o"].ptr, att.ptr, ones.ptr, 1e-5, ws.ptr, D, Dq, x.ptr,
@@ -479,7 +482,7 @@ def decode_breakdown(ops, synth, pos: int = 139) -> dict:
         lm(0)
     out["layers_and_lm_head_us"] = round(_timed(L, stream, chain, 1) * 1e3, 1)
     L.oxb_stream_destroy(stream)
-    for a in [kc, vc, x, ones, ws, q, att, hbuf, rope, state, hist, E, logits] + \
+    for a in [kc, vc, vc8, x, ones, ws, q, att, hbuf, rope, state, hist, E, logits] + \
              [b for d in lay for b in d.values()]:
         a.free()
     return out

@@ -197,6 +197,14 @@ int oxb_attn_decode_fused(const float *q, const uint16_t *kcache, const uint16_t
 int oxb_attn_decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                          const int *pos, int pos_stride, size_t kv_stride, int batch, int H,
                          int Hkv, int hd, int max_seq, int s_max, float *out, void *stream);
+/* The same with the octet copy of V (as oxb_attn_decode_batch_v8): the
+ * 256-position kernel stages the copy's first 32 octets and sums 8 positions
+ * per 16-byte read (waves 0 and 1: dims 0-63 and 64-127); the other two
+ * kernels read vcache.  Same result bits.  No counterpart in the reference. */
+int oxb_attn_decode_head_v8(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                            const uint16_t *vcache8, const int *pos, int pos_stride,
+                            size_t kv_stride, size_t kv8_stride, int batch, int H, int Hkv,
+                            int hd, int max_seq, int s_max, float *out, void *stream);
 
 /* oxb_attn_decode without the scores buffer and without allocating: the
  * scores live in a static device array of the library (one per device, 1 MiB:

@@ -246,7 +246,10 @@ def _nan_past(c, pos):
 @pytest.mark.parametrize("form,pos,S", [("split", 100, 512), ("split", 300, 700),
                                         ("head", 100, 512), ("head", 255, 512),
                                         ("head", 300, 512), ("head", 20, 64),
-                                        ("fused", 100, 512), ("fused", 300, 600)])
+                                        ("fused", 100, 512), ("fused", 300, 600),
+                                        ("head8", 100, 512), ("head8", 250, 300),
+                                        ("head8", 300, 512), ("head8", 400, 404),
+                                        ("split8", 100, 512), ("split8", 1000, 1100)])
 def test_attn_decode_ignores_nonfinite_rows_past_the_position(form, pos, S):
     """Rows past the position hold NaN/Inf (stale or never-written cache rows
     of a caller): every decode form gives the oracle's bits over the rows it
@@ -257,7 +260,8 @@ def test_attn_decode_ignores_nonfinite_rows_past_the_position(form, pos, S):
     kc = _nan_past((rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16), pos)
     vc = _nan_past(rng.standard_normal((Hkv, S, hd)).astype(np.float16), pos)
     kw = {"head": dict(head=True, s_max=256 if pos < 256 else 512), "fused": dict(fused=True),
-          "split": {}}[form]
+          "split": {}, "head8": dict(head=True, s_max=256 if pos < 256 else 512, octets=True),
+          "split8": dict(octets=True)}[form]
     out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, **kw)
     ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
     assert np.isfinite(ref).all()
@@ -299,14 +303,16 @@ def test_attn_decode_fused_bitexact(pos, H, Hkv, S):
     # other GQA groups; short caches (K rows clamped to the cache extent)
     (200, 8, 8, 512, 256), (100, 16, 2, 256, 256), (40, 32, 4, 64, 256), (63, 20, 5, 64, 256),
     (20, 4, 1, 21, 256)])
-def test_attn_decode_head_bitexact(pos, H, Hkv, S, s_max):
-    """Per-query-head decode attention: same bits as the oracle."""
+@pytest.mark.parametrize("octets", [False, True])
+def test_attn_decode_head_bitexact(pos, H, Hkv, S, s_max, octets):
+    """Per-query-head decode attention: same bits as the oracle, with the
+    row-major V and with its octet copy."""
     rng = np.random.default_rng(pos * 11 + H + s_max)
     hd = 128
     q = rng.standard_normal(H * hd).astype(np.float32)
     kc = (rng.standard_normal((Hkv, S, hd)) * 0.7).astype(np.float16)
     vc = rng.standard_normal((Hkv, S, hd)).astype(np.float16)
-    out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, head=True, s_max=s_max)
+    out = ops.attn_decode(q, kc, vc, pos, H, Hkv, hd, S, head=True, s_max=s_max, octets=octets)
     ref = _oracle_attn(q, kc, vc, 1, pos + 1, H, Hkv, hd)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
@@ -336,6 +342,19 @@ def test_attn_decode_head_batch_bitexact():
     for z in range(B):
         ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(pos[z]) + 1, H, Hkv, hd)
         assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"slot {z}"
+    # the 256-position kernel over the octet copy (positions below 256)
+    v8 = ops.v_octets(vc)
+    dv8 = ops.DeviceArray.from_host(v8)
+    st[:, 0] = np.array([255, 0, 254, 128, 100], np.int32)
+    dst.upload(st)
+    ops.check(L.oxb_attn_decode_head_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dst.ptr, 8, Hkv * S * hd,
+                                        v8.shape[-1], B, H, Hkv, hd, S, 256, out.ptr, None),
+              "attn_decode_head_v8")
+    ops.sync()
+    got = out.download()
+    for z in range(B):
+        ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(st[z, 0]) + 1, H, Hkv, hd)
+        assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"octets, slot {z}"
 
 
 def test_attn_decode_head_rejects_long_caches():
