@@ -105,6 +105,8 @@ SIGNATURES = {
     "oxb_attn_decode_noalloc": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "oxb_attn_decode_head_v8": (C.c_int, [vp, vp, vp, vp, vp, i32, C.c_size_t, C.c_size_t, i32,
                                           i32, i32, i32, i32, i32, vp, vp]),
+    "oxb_qkv_attn_decode": (C.c_int, [vp, vp, vp, vp, f32, vp, vp, vp, vp, vp, vp, vp, i32, i32,
+                                      i32, i32, i32, vp, vp]),
     "oxb_attn_decode_head": (C.c_int, [vp, vp, vp, vp, i32, C.c_size_t, i32, i32, i32, i32, i32,
                                        i32, vp, vp]),
     "oxb_attn_prefill": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),

@@ -1909,6 +1909,363 @@ __global__ __launch_bounds__(256) void attn_head256_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// A decode step's q|k|v BitLinear and the attention in one launch, for caches
+// of 256+ rows with the query below position 256.  The grid is the q|k|v
+// GEMV's: one 16-row tile of the fused weights per workgroup (512 threads):
+//  - waves 0-3: the tile's GEMV as the GEMV kernel computes it (attn_norm
+//    RMSNorm, int8 quantize, ternary dot, RoPE on q and k, f16 K / V append
+//    with the V octet copy), the rows stored to q_out and the caches;
+//  - arrival: each tile counts itself, on an agent-scope counter per query
+//    head, for the heads its rows feed (a q tile: its head; a k or v tile:
+//    the G query heads of its KV head), 24 tiles per head; the workgroup that
+//    brings a head's count to 24 resets it to 0 and computes that head's
+//    attention (nobody waits: the last one to finish does the work);
+//  - the candidate: the workgroup of each head's last q tile is launched
+//    last (the k and v tiles first) and its waves 4-7 load the head's K rows
+//    and V octets of positions 0..255 into LDS while waves 0-3 run the GEMV,
+//    so that when it completes the head, as it mostly does, only q and row
+//    pos are still to read; any other workgroup that completes a head loads
+//    K and V itself first.  The candidates of one KV head share block
+//    indices mod 8 (one XCD, one L2).
+//  - the attention: as attn_head256_kernel<true> (thread t scores position
+//    t; softmax; P.V over the octets on waves 0 and 1), with row pos of K and
+//    V read back from the caches.  K row t's chunk i sits in LDS slot
+//    (i + t) % 16 of the row, so the score chains do not meet in one bank.
+// Same bits as bitlinear_qkv followed by attn_head256_kernel<true>.
+// LDS (dynamic): K [256][16] uint4 | V octets [32][128] uint4 | xq [K] |
+// red [256] | wpart [256] | q [128] | p [256] | wmax [8] | wq [4] | win [8]
+// ---------------------------------------------------------------------------
+constexpr int kQaThreads = 512;
+constexpr int kQaArrivals = 3 * (kHd / 16);   // the q, k and v tiles of a head
+
+struct QkvAttnParams {
+    const uint4 *W;          // the layer's q|k|v weights, tiled I2_S [Dq + 2 Dkv][K]
+    const float *wscale;     // [Dq + 2 Dkv]
+    const float *x;          // residual stream [K]
+    const float *gamma;      // attn_norm weight [K]
+    float eps;
+    const float2 *rope;      // [max_seq][64] (cos, sin)
+    const int *pos;          // decode state position
+    float *q;                // q rows [H * 128]
+    uint16_t *kcache, *vcache, *vcache8;   // this layer's caches (f16)
+    int *cnt;                // [H] arrival counters, 0 between launches
+    float *out;              // [H * 128]
+    float scale;
+    int G, Hkv, max_seq;
+};
+
+__host__ __device__ inline size_t qa_smem(int K) {
+    return (size_t)2 * 256 * 16 * 16 + K + (256 + 256 + kHd + 256 + 8 + 4 + 8) * 4;
+}
+
+// blocks: the k and v tiles (16 Hkv), the q tiles 0-6 of each head (7 H),
+// then the candidates (head_grid_blocks(G, Hkv), some idle)
+__host__ __device__ inline int qa_grid_blocks(int G, int Hkv) {
+    return 16 * Hkv + 7 * G * Hkv + head_grid_blocks(G, Hkv);
+}
+
+// K rows 0..255 (clamped to the cache) and V octets 0..31 of one KV head
+// into LDS: 128 loads of 1 KB, nw waves from wave w0 issuing 128 / nw each.
+// Lane l of load m fills K slot l % 16 of row 4m + l / 16 with chunk
+// (slot - row) % 16.
+__device__ inline void qa_stage_kv(const uint4 *K4, const uint4 *V8, int max_seq, uint4 *ks,
+                                   uint4 *vs4, int w, int nw, int lane) {
+    for (int m = w; m < 64; m += nw) {
+        const int row = 4 * m + (lane >> 4);
+        const int chunk = ((lane & 15) - row) & 15;
+        lds_dma16(K4 + (size_t)min(row, max_seq - 1) * 16 + chunk, ks + (size_t)m * 64);
+        lds_dma16(V8 + (size_t)m * 64 + lane, vs4 + (size_t)m * 64);
+    }
+}
+
+template <int NREG>
+__global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(QkvAttnParams p) {
+    constexpr int K = 256 * NREG, KC = K / 64, CPL = (KC + 15) / 16;
+    extern __shared__ __align__(16) int8_t smem_qa[];
+    uint4 *ks = (uint4 *)smem_qa;                              // [256 rows][16 slots]
+    uint4 *vs4 = ks + 256 * 16;                                // octets [32][128 dims]
+    int8_t *xq = (int8_t *)(vs4 + 256 * 16);                   // [K]
+    float *red = (float *)(xq + K);                            // [256]
+    int *wpart = (int *)(red + 256);                           // [256]
+    float *qs = (float *)(wpart + 256);                        // [128]
+    float *pr = qs + kHd;                                      // [256]
+    float *wmax = pr + 256;                                    // [8]
+    int *wq = (int *)(wmax + 8);                               // [4]
+    int *win = wq + 4;                                         // [8]
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int G = p.G, Hkv = p.Hkv, H = G * Hkv, max_seq = p.max_seq;
+    // this workgroup's tile (rows 16 tile ..): q tiles 0 .. 8H-1, then k, then v
+    int b = blockIdx.x, tile, qhead = -1;
+    bool cand = false;
+    if (b < 16 * Hkv) {
+        tile = 8 * H + b;
+    } else if ((b -= 16 * Hkv) < 7 * H) {
+        qhead = b / 7;
+        tile = 8 * qhead + b % 7;
+    } else {
+        qhead = head_of_block(b - 7 * H, G, Hkv);
+        if (qhead < 0) return;   // an idle slot of the candidates' grid
+        tile = 8 * qhead + 7;
+        cand = true;
+    }
+    const int Dq = H * kHd, Dkv = Hkv * kHd;
+    const int pos = p.pos[opaque_zero()];
+    const bool store = pos >= 0 && pos < max_seq;
+    const bool valid = store && pos < kH256Rows;
+    const int S = valid ? pos + 1 : 1;
+    const int n_ep = tile * 16 + (tid & 15);   // the row this thread may finish
+
+    // ---- loads (waves 0-3): the epilogue's scale, the row, the weights, the
+    // RoPE pair; waves 4-7 of a candidate: its head's K and V into LDS
+    float ws_ep = 0.0f;
+    float2 cs = make_float2(1.0f, 0.0f);
+    float v[NREG], g[NREG];
+    uint4 A[CPL];
+    if (w < 4) {
+        ws_ep = p.wscale[n_ep];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NREG; ++j) {
+            v[j] = p.x[tid + 256 * j];
+            g[j] = p.gamma[tid + 256 * j];
+        }
+        const uint4 *tw = p.W + (size_t)tile * KC * 16;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const int kc = 16 * u + 4 * w + (lane >> 4);
+            A[u] = load_nt(tw + (size_t)min(kc, KC - 1) * 16 + (lane & 15));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (n_ep < Dq + Dkv) {
+            const int d = (n_ep < Dq ? n_ep : n_ep - Dq) & (kHd - 1);
+            const int pc = min(max(pos, 0), max_seq - 1);
+            cs = p.rope[(size_t)pc * (kHd / 2) + (d >> 1)];
+        }
+    } else if (cand) {
+        const int hk = qhead / G;
+        qa_stage_kv((const uint4 *)(p.kcache + (size_t)hk * max_seq * kHd),
+                    (const uint4 *)(p.vcache8 + (size_t)hk * v8_head_elems(max_seq, kHd)),
+                    max_seq, ks, vs4, w - 4, 4, lane);
+    }
+
+    // ---- prologue: RMSNorm + absmax quantize (waves 0-3, the GEMV's order) ---
+    if (w < 4) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NREG; ++j) {
+            float sq = v[j] * v[j];
+            ss = ss + sq;
+        }
+        red[tid] = ss;
+    }
+    lds_barrier();
+    if (w < 4) {
+        const float sum = block256_tree_fold(red);
+        const float rms = 1.0f / sqrtf(sum / (float)K + p.eps);  // inverseSqrt
+        float am = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NREG; ++j) {
+            float a = v[j] * rms;
+            v[j] = a * g[j];
+            am = fmaxf(am, fabsf(v[j]));
+        }
+        am = wave_nonneg_max_dpp(am);
+        if (lane == 0) wmax[w] = am;
+    }
+    lds_barrier();
+    const float am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float in_scale = am == 0.0f ? 1.0f : am / 127.0f;   // sh/quantize.wgsl:59
+    if (w < 4) {
+        const float inv = am == 0.0f ? 0.0f : 127.0f / am;    // :68
+        int sq = 0;
+#pragma unroll
+        for (int j = 0; j < NREG; ++j) {
+            const int qv = quant_one(v[j], inv);
+            xq[tid + 256 * j] = (int8_t)qv;
+            sq += qv;
+        }
+        sq = wave_isum_dpp(sq);
+        if (lane == 0) wq[w] = sq;
+    }
+    lds_barrier();   // the int8 vector is complete
+
+    // ---- dot products (waves 0-3): chunks past K multiply zero codes ---------
+    if (w < 4) {
+        CodeAcc acc;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const int kc = 16 * u + 4 * w + (lane >> 4);
+            const int kcl = min(kc, KC - 1);
+            const int xo = (kcl >> 1) * 128 + (kcl & 1) * 16;
+            const int4 x0 = *(const int4 *)(xq + xo);
+            const int4 x1 = *(const int4 *)(xq + xo + 32);
+            const int4 x2 = *(const int4 *)(xq + xo + 64);
+            const int4 x3 = *(const int4 *)(xq + xo + 96);
+            const uint4 wv = kc < KC ? A[u] : make_uint4(0, 0, 0, 0);
+            acc.add(wv.x, x0.x, x1.x, x2.x, x3.x);
+            acc.add(wv.y, x0.y, x1.y, x2.y, x3.y);
+            acc.add(wv.z, x0.z, x1.z, x2.z, x3.z);
+            acc.add(wv.w, x0.w, x1.w, x2.w, x3.w);
+        }
+        wpart[tid] = acc.codes();   // lane (row r, column c) of wave w: 16 (4w + c) + r
+    }
+    lds_barrier();
+
+    // ---- epilogue (lanes 0-15 of wave 0): sh/ternary_gemv.wgsl:94-95, RoPE,
+    // the rows to q_out and the caches
+    if (w == 0) {
+        const int r = lane & 15;
+        int a = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) a += wpart[k * 16 + r];
+        a -= (wq[0] + wq[1]) + (wq[2] + wq[3]);
+        float yv = (float)a * ws_ep;
+        yv = yv * in_scale;
+        const float other = __shfl_xor(yv, 1, 64);
+        const int n = n_ep;
+        float outv = yv;
+        if (n < Dq + Dkv) {   // q or k: RoPE on the interleaved pair (2i, 2i + 1)
+            if ((n & 1) == 0) {
+                float a0 = yv * cs.x, a1 = other * cs.y;
+                outv = a0 - a1;
+            } else {
+                float a0 = other * cs.y, a1 = yv * cs.x;
+                outv = a0 + a1;
+            }
+        }
+        // the rows other workgroups read in this launch: agent-scope stores
+        if (lane < 16 && store) {
+            if (n < Dq) {
+                __hip_atomic_store(p.q + n, outv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                const int j = n < Dq + Dkv ? n - Dq : n - Dq - Dkv;
+                const int hk = j >> 7, d = j & (kHd - 1);
+                const size_t at = ((size_t)hk * max_seq + pos) * kHd + d;
+                const uint16_t bits = __half_as_ushort(__float2half_rn(outv));
+                if (n < Dq + Dkv) {
+                    __hip_atomic_store(p.kcache + at, bits, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    __hip_atomic_store(p.vcache + at, bits, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    p.vcache8[(size_t)hk * v8_head_elems(max_seq, kHd) + v8_index(pos, d, kHd)] =
+                        bits;
+                }
+            }
+        }
+    }
+
+    // ---- arrival (wave 0) --------------------------------------------------
+    // Agent-scope stores are visible to every XCD once complete, so waiting
+    // for them orders them before the count; a release fence would also
+    // write back the whole L2, in every workgroup.
+    const bool qt = tile < 8 * H;
+    const int n_arr = qt ? 1 : G;
+    if (w == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane < n_arr) {
+            const int h = qt ? tile >> 3 : ((tile - 8 * H) % (8 * Hkv) >> 3) * G + lane;
+            const int old = __hip_atomic_fetch_add(p.cnt + h, 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = old == kQaArrivals - 1;
+            if (last) __hip_atomic_store(p.cnt + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            win[lane] = last ? h : -1;
+        }
+    }
+    if (w >= 4) wait_vmcnt<0>();   // a candidate's K / V have landed in LDS
+    lds_barrier();
+
+    for (int i = 0; i < n_arr; ++i) {
+        const int h = win[i];
+        if (h < 0) continue;
+        const int hk = h / G;
+        if (!cand) {
+            qa_stage_kv((const uint4 *)(p.kcache + (size_t)hk * max_seq * kHd),
+                        (const uint4 *)(p.vcache8 + (size_t)hk * v8_head_elems(max_seq, kHd)),
+                        max_seq, ks, vs4, w, 8, lane);
+            wait_vmcnt<0>();
+            lds_barrier();
+        }
+        // q, and row pos of K and V over what the stage read before it was
+        // written (agent-scope loads: the values the other tiles stored)
+        if (tid < kHd) {
+            qs[tid] = __hip_atomic_load(p.q + (size_t)h * kHd + tid, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        } else if (tid < 2 * kHd && valid) {
+            const int d = tid - kHd;
+            const uint16_t kb = __hip_atomic_load(p.kcache + ((size_t)hk * max_seq + pos) * kHd + d,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ((uint16_t *)(ks + (size_t)pos * 16 + (((d >> 3) + pos) & 15)))[d & 7] = kb;
+        } else if (tid < 3 * kHd && valid) {
+            const int d = tid - 2 * kHd;
+            ((uint16_t *)vs4)[v8_index(pos, d, kHd)] =
+                __hip_atomic_load(p.vcache + ((size_t)hk * max_seq + pos) * kHd + d,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        lds_barrier();
+
+        // scores (waves 0-3: thread t, position t), 128 terms in order of d
+        float x = 0.0f;
+        if (w < 4) {
+            const u32x4_t *kv4 = (const u32x4_t *)ks + (size_t)tid * 16;
+            constexpr int kAhead = 3;
+            u32x4_t kr[16];
+            float4 qa[16], qb[16];
+            auto ld = [&](int i2) {
+                kr[i2] = kv4[(i2 + tid) & 15];
+                qa[i2] = *(const float4 *)(qs + 8 * i2);
+                qb[i2] = *(const float4 *)(qs + 8 * i2 + 4);
+            };
+#pragma unroll
+            for (int i2 = 0; i2 < kAhead; ++i2) ld(i2);
+            float dot = 0.0f;
+#pragma unroll
+            for (int i2 = 0; i2 < 16; ++i2) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (i2 + kAhead < 16) ld(i2 + kAhead);
+                __builtin_amdgcn_sched_barrier(0);
+                const float qv[8] = {qa[i2].x, qa[i2].y, qa[i2].z, qa[i2].w,
+                                     qb[i2].x, qb[i2].y, qb[i2].z, qb[i2].w};
+#pragma unroll
+                for (int k2 = 0; k2 < 4; ++k2) {
+                    const uint32_t kw = kr[i2][k2];
+                    const float k0 = __half2float(__ushort_as_half((uint16_t)(kw & 0xffffu)));
+                    const float k1 = __half2float(__ushort_as_half((uint16_t)(kw >> 16)));
+                    dot = __builtin_fmaf(qv[2 * k2], k0, dot);
+                    dot = __builtin_fmaf(qv[2 * k2 + 1], k1, dot);
+                }
+            }
+            x = dot * p.scale;
+        }
+        // softmax (sh/softmax.wgsl:25-80) on waves 0-3
+        float m = tid < S ? x : -3.402823e+38f;
+        if (w < 4) {
+            m = wave_max_dpp(m);
+            if (lane == 0) wmax[w] = m;
+        }
+        lds_barrier();
+        m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        const float e = tid < S ? oxb_expf(x - m) : 0.0f;
+        if (w < 4) red[tid] = e;   // thread t's strided partial: one position (0 + e = e)
+        lds_barrier();
+        if (w < 4) {
+            const float a = red[lane] + red[lane + 128];
+            const float c = red[lane + 64] + red[lane + 192];
+            const float inv = 1.0f / wave_tree_sum(a + c);
+            pr[tid] = e * inv;   // 0 past S
+        }
+        lds_barrier();
+        // P.V (sh/attention.wgsl:96-104) on waves 0 and 1 over the octets
+        if (w < 2) {
+            const float acc = pv_head_oct<kH256Rows>(vs4 + 64 * w + lane, pr, S);
+            if (valid) p.out[(size_t)h * kHd + 64 * w + lane] = acc;
+        }
+        lds_barrier();   // LDS is staged again for the next head
+    }
+}
+
+// ---------------------------------------------------------------------------
 // The same design for caches of up to 512 positions: 512 threads (thread t
 // scores position t), K staged as [512][17] uint4; the V rows are loaded with
 // K and written over the K rows once every score chain is done (one more
@@ -2332,6 +2689,65 @@ extern "C" int oxb_attn_prefill(const float *q, const uint16_t *kcache, const ui
         if (rc == 0) OXB_CHECK_HIP(e);
     }
     return rc;
+}
+
+namespace oxb {
+bool qkv_attn_supported(int D, int H, int Hkv, int hd, int max_seq) {
+    return hd == kHd && (D == 512 || D == 2560) && Hkv > 0 && H % Hkv == 0 &&
+           max_seq >= kH256Rows && max_seq <= 65536;
+}
+
+int qkv_attn_decode(const void *W, const float *wscale, const float *x, const float *gamma,
+                    float eps, const float *rope, const int *pos, float *q_out, uint16_t *kcache,
+                    uint16_t *vcache, uint16_t *vcache8, int *counters, int H, int Hkv, int D,
+                    int max_seq, float *out, void *stream) {
+    OXB_REQUIRE(W && wscale && x && gamma && rope && pos && q_out && kcache && vcache && vcache8 &&
+                    counters && out,
+                "qkv attention: null argument");
+    OXB_REQUIRE(qkv_attn_supported(D, H, Hkv, kHd, max_seq),
+                "qkv attention: unsupported shape (hidden %d, heads %d/%d, max_seq %d)", D, H, Hkv,
+                max_seq);
+    QkvAttnParams p{};
+    p.W = (const uint4 *)W;
+    p.wscale = wscale;
+    p.x = x;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.rope = (const float2 *)rope;
+    p.pos = pos;
+    p.q = q_out;
+    p.kcache = kcache;
+    p.vcache = vcache;
+    p.vcache8 = vcache8;
+    p.cnt = counters;
+    p.out = out;
+    p.scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
+    p.G = H / Hkv;
+    p.Hkv = Hkv;
+    p.max_seq = max_seq;
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(qa_grid_blocks(p.G, Hkv));
+    if (D == 2560) {
+        if (allow_dynamic_lds((const void *)qkv_attn_kernel<10>)) return -1;
+        hipLaunchKernelGGL(qkv_attn_kernel<10>, grid, dim3(kQaThreads), qa_smem(D), s, p);
+    } else {
+        if (allow_dynamic_lds((const void *)qkv_attn_kernel<2>)) return -1;
+        hipLaunchKernelGGL(qkv_attn_kernel<2>, grid, dim3(kQaThreads), qa_smem(D), s, p);
+    }
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+}  // namespace oxb
+
+extern "C" int oxb_qkv_attn_decode(const void *W_tiled, const float *wscale, const float *x,
+                                   const float *gamma, float eps, const float *rope_cs,
+                                   const int *pos, float *q_out, uint16_t *kcache,
+                                   uint16_t *vcache, uint16_t *vcache8, int *counters, int H,
+                                   int Hkv, int hd, int D, int max_seq, float *out, void *stream) {
+    oxb::clear_error();
+    OXB_REQUIRE(hd == kHd, "qkv attention: head_dim %d unsupported (128 only)", hd);
+    return oxb::qkv_attn_decode(W_tiled, wscale, x, gamma, eps, rope_cs, pos, q_out, kcache,
+                                vcache, vcache8, counters, H, Hkv, D, max_seq, out, stream);
 }
 
 static int decode_head(const float *q, const uint16_t *kcache, const uint16_t *vcache,

@@ -490,6 +490,14 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
     m->logits = (float *)m->dalloc((size_t)m->V * 4);
     m->state = (int *)m->dalloc(OXB_STATE_INTS * 4);
     m->hist_cap = m->max_seq + 16;
+    // OXB_QKV_ATTN=1: steps of up to 256 positions run q|k|v + attention as
+    // the one launch of oxb_qkv_attn_decode (same bits; slower on MI355X than
+    // the two launches, its cross-workgroup hand-off costs more than a launch)
+    const char *qa_env = getenv("OXB_QKV_ATTN");
+    m->qkv_attn = qa_env && !strcmp(qa_env, "1") &&
+                  oxb::qkv_attn_supported(D, H, Hkv, hd, m->max_seq) && m->vcache8;
+    // its arrival counters: zero here, zero again after every launch
+    if (m->qkv_attn) m->qa_cnt = (int *)m->dalloc((size_t)H * 4);
     if (const char *env = getenv("OXB_ATTN")) {
         if (!strcmp(env, "head")) m->attn_mode = 0;
         else if (!strcmp(env, "fused")) m->attn_mode = 1;
@@ -511,9 +519,10 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
     if (!m->kcache || !m->vcache || (kv8_bytes && !m->vcache8) || !m->x || !m->q || !m->attn ||
         !m->h || !m->scores ||
         !m->logits || !m->state || !m->tok_hist || !m->pf_ws || !m->samp_ctl || !m->samp_u ||
-        !m->samp_ws)
+        !m->samp_ws || (m->qkv_attn && !m->qa_cnt))
         return nullptr;
-    if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
+    if ((m->qa_cnt && hipMemset(m->qa_cnt, 0, (size_t)H * 4) != hipSuccess) ||
+        hipMemset(m->kcache, 0, kv_bytes) != hipSuccess ||
         hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
         (kv8_bytes && hipMemset(m->vcache8, 0, kv8_bytes) != hipSuccess)) {
         set_error("hipMemset failed");
@@ -566,11 +575,15 @@ int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
         void *kv_k = (char *)kcache + l * kv_layer, *kv_v = (char *)vcache + l * kv_layer;
         uint16_t *kc = (uint16_t *)kv_k, *vc = (uint16_t *)kv_v;
         uint16_t *vc8 = vcache8 ? vcache8 + l * (size_t)Hkv * v8_head_elems(max_seq, hd) : nullptr;
-        if (oxb::bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kv_k, kv_v,
-                               kv_f32, max_seq, rope, posp, s, vc8))
-            return -1;
         int rc;
-        if (kv_f32)
+        if (attn == ATTN_HEAD1 && qkv_attn && vc8 && L.attn_norm) {
+            // q|k|v BitLinear and the attention in one launch
+            rc = oxb::qkv_attn_decode(L.wqkv, L.sqkv, x, L.attn_norm, eps, rope, posp, q, kc, vc,
+                                      vc8, qa_cnt, H, Hkv, D, max_seq, this->attn, s);
+        } else if (oxb::bitlinear_qkv(L.wqkv, x, L.attn_norm, eps, L.sqkv, Dq, Dkv, hd, D, q, kv_k,
+                                      kv_v, kv_f32, max_seq, rope, posp, s, vc8)) {
+            return -1;
+        } else if (kv_f32)
             rc = oxb::attn_f32(q, (const float *)kv_k, (const float *)kv_v, posp, 0, 1, H, Hkv, hd,
                                max_seq, this->attn, s);
         else switch (attn) {

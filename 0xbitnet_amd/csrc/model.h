@@ -66,6 +66,8 @@ struct oxb_model {
     // (default), 1 the fused kernel up to 256, 2 the split kernels only
     // (OXB_ATTN=head|fused|split when the model loads; all give the same bits)
     int attn_mode = 0;
+    bool qkv_attn = false;   // ATTN_HEAD1 steps as one q|k|v + attention launch
+    int *qa_cnt = nullptr;   // its per-head arrival counters [H]
     AttnForm attn_form(int S) const;
     int *pinned = nullptr;      // host-pinned scratch for small readbacks
     int pos = 0;                // host mirror of state[OXB_ST_POS]

@@ -241,13 +241,12 @@ __device__ inline float block256_tree_sum_fast(float part, float *red) {
 //   u[j] = (s[j] + s[j+128]) + (s[j+64] + s[j+192]),
 // so lane i of every 16-lane row reads its 16 leaves from LDS and folds them
 // in that order; DPP row_shl:8,4,2,1 (lane l takes lane l+k of its row) does
-// strides 8..1 and lane 0 holds the shader's sum.  red >= 256 floats; all
-// 256 threads must call; result to all threads.
-__device__ inline float block256_tree_sum_1b(float part, float *red) {
-    const int t = threadIdx.x & 255;   // a 256-thread group, red its own 256 slots
-    red[t] = part;
-    lds_barrier();
-    const int i = t & 15;
+// strides 8..1 and lane 0 holds the shader's sum.  red >= 256 floats.
+// block256_tree_fold: the fold once the 256 partials are in red (a barrier
+// published them), by one whole wave, result to every lane;
+// block256_tree_sum_1b: store, barrier and fold, all 256 threads must call.
+__device__ inline float block256_tree_fold(const float *red) {
+    const int i = threadIdx.x & 15;
     float u[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -260,6 +259,13 @@ __device__ inline float block256_tree_sum_1b(float part, float *red) {
     s = s + __int_as_float(dpp0<0x102, 0xf>(__float_as_int(s)));
     s = s + __int_as_float(dpp0<0x101, 0xf>(__float_as_int(s)));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+}
+
+__device__ inline float block256_tree_sum_1b(float part, float *red) {
+    const int t = threadIdx.x & 255;   // a 256-thread group, red its own 256 slots
+    red[t] = part;
+    lds_barrier();
+    return block256_tree_fold(red);
 }
 
 // Max over the wave of finite floats (lanes without a DPP source keep their

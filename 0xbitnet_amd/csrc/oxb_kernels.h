@@ -53,6 +53,13 @@ int lm_head_argmax_rows(const float *x, size_t x_stride, const float *gamma, flo
                         const void *E, int V, int D, float *logits, int *state, int state_stride,
                         int *tok_hist, int hist_stride, int n_rows, int advance, float *hn,
                         void *stream);
+// The fused decode q|k|v BitLinear + attention (attention.hip,
+// oxb_qkv_attn_decode) and the shapes it takes.
+bool qkv_attn_supported(int D, int H, int Hkv, int hd, int max_seq);
+int qkv_attn_decode(const void *W, const float *wscale, const float *x, const float *gamma,
+                    float eps, const float *rope, const int *pos, float *q_out, uint16_t *kcache,
+                    uint16_t *vcache, uint16_t *vcache8, int *counters, int H, int Hkv, int D,
+                    int max_seq, float *out, void *stream);
 // Device sampling (sampling.hip).  SampleCtl holds the options of one
 // generation; top_k is the one in effect (0: keep all, else 0 < top_k < V).
 struct SampleCtl {

@@ -206,6 +206,28 @@ int oxb_attn_decode_head_v8(const float *q, const uint16_t *kcache, const uint16
                             size_t kv_stride, size_t kv8_stride, int batch, int H, int Hkv,
                             int hd, int max_seq, int s_max, float *out, void *stream);
 
+/* A decode step's q|k|v BitLinear (as oxb_bitlinear_qkv: attn_norm RMSNorm,
+ * int8 quantize, ternary GEMV, RoPE, q to q_out, f16 K/V append at *pos, the
+ * V octet copy too) and its attention (as oxb_attn_decode_head_v8 with s_max
+ * 256) in one launch.  The workgroups are the GEMV's 16-row tiles; each counts
+ * itself on counters[h] for the query heads its rows feed, and the one that
+ * completes a head (24 tiles) computes that head's attention, having loaded
+ * its K rows and V octets while it ran its tile when it is the head's
+ * designated last q tile.  x, gamma: [D] f32 (D 512 or 2560); rope_cs as
+ * oxb_bitlinear_qkv; q_out [H*128] f32; caches [Hkv][max_seq][128] f16
+ * (max_seq >= 256) and the octet copy; counters [H] ints, zero before the
+ * first call and zero again after each call completes (calls on one counter
+ * array must not overlap); out [H*128] f32.  Same q, cache contents and
+ * result bits as the two calls for *pos < 256; a position from 256 to
+ * max_seq - 1 is appended to the caches and out is left as it was.  Replaces
+ * nn/attention.rs:97-118 (projections, RoPE, cache copies, attention) for one
+ * token; no single counterpart in the reference. */
+int oxb_qkv_attn_decode(const void *W_tiled, const float *wscale, const float *x,
+                        const float *gamma, float eps, const float *rope_cs, const int *pos,
+                        float *q_out, uint16_t *kcache, uint16_t *vcache, uint16_t *vcache8,
+                        int *counters, int H, int Hkv, int hd, int D, int max_seq, float *out,
+                        void *stream);
+
 /* oxb_attn_decode without the scores buffer and without allocating: the
  * scores live in a static device array of the library (one per device, 1 MiB:
  * H * max_seq <= 262144; larger shapes are rejected), whose address is looked

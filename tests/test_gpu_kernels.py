@@ -440,6 +440,83 @@ def test_attn_decode_octets_ring_edges(S, pos):
                                       hd, S, sc.ptr, out.ptr, None) == -1
 
 
+# The one-launch q|k|v + attention step against the two launches it replaces
+# (oxb_bitlinear_qkv, then oxb_attn_decode_head_v8 over the octet copy):
+# hidden 512 and 2560, 1 to 4 query heads per KV head, KV heads not a multiple
+# of 8 (idle workgroups), first position, octet edges (7 / 8), the last of 256
+# positions, caches longer than 256 rows, and a position past 256 (append
+# only).  Rows past the position hold NaN / Inf.
+@pytest.mark.parametrize("D,H,Hkv,max_seq,pos", [(512, 4, 1, 256, 0), (512, 4, 1, 256, 7),
+                                                 (512, 4, 1, 300, 8), (512, 8, 2, 256, 255),
+                                                 (512, 9, 9, 256, 50), (2560, 20, 5, 256, 0),
+                                                 (2560, 20, 5, 512, 100), (2560, 20, 5, 300, 37),
+                                                 (2560, 20, 5, 4096, 255), (2560, 32, 8, 256, 200),
+                                                 (2560, 20, 5, 300, 280)])
+def test_qkv_attn_decode_matches_two_launches(D, H, Hkv, max_seq, pos):
+    rng = np.random.default_rng(D + 31 * pos + H)
+    hd = 128
+    Dq, Dkv = H * hd, Hkv * hd
+    N = Dq + 2 * Dkv
+    W = ternary(rng, N, D)
+    ws = rng.uniform(0.01, 0.03, N).astype(np.float32)
+    x = rng.standard_normal(D).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    kc = (rng.standard_normal((Hkv, max_seq, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((Hkv, max_seq, hd)).astype(np.float16)
+    kc, vc = _nan_past(kc, pos - 1), _nan_past(vc, pos - 1)   # rows pos.. stale
+    L = ops.lib()
+    Wt = ops.upload_ternary(synth.i2s_pack(W), D)
+    dx, dg, dws = (ops.DeviceArray.from_host(a) for a in (x, g, ws))
+    rope = ops.DeviceArray.from_host(rope_table(max_seq, hd, 500000.0))
+    dpos = ops.DeviceArray.from_host(np.array([pos], np.int32))
+
+    # the two launches
+    dq = ops.DeviceArray((Dq,), np.float32)
+    rk = ops.DeviceArray.from_host(kc.view(np.uint16))
+    rv = ops.DeviceArray.from_host(vc.view(np.uint16))
+    ops.check(L.oxb_bitlinear_qkv(Wt.ptr, dx.ptr, dg.ptr, 1e-5, dws.ptr, Dq, Dkv, hd, D, dq.ptr,
+                                  rk.ptr, rv.ptr, max_seq, rope.ptr, dpos.ptr, None), "qkv")
+    ops.sync()
+    kc1 = rk.download().view(np.float16).reshape(Hkv, max_seq, hd)
+    vc1 = rv.download().view(np.float16).reshape(Hkv, max_seq, hd)
+    if pos < 256:
+        want = ops.attn_decode(dq.download(), kc1, vc1, pos, H, Hkv, hd, max_seq, head=True,
+                               s_max=256, octets=True)
+        ref = _oracle_attn(dq.download(), kc1, vc1, 1, pos + 1, H, Hkv, hd)
+        assert np.array_equal(want.view(np.uint32), ref.view(np.uint32))
+    else:
+        want = np.full(H * hd, 7.5, np.float32)   # the output is left as it was
+
+    # the one launch, twice (its counters are zero again after each)
+    cnt = ops.DeviceArray((H,), np.int32, zero=True)
+    for rep in range(2):
+        fk = ops.DeviceArray.from_host(kc.view(np.uint16))
+        fv = ops.DeviceArray.from_host(vc.view(np.uint16))
+        fv8 = ops.DeviceArray.from_host(ops.v_octets(vc))
+        fq = ops.DeviceArray((Dq,), np.float32)
+        out = ops.DeviceArray.from_host(np.full(H * hd, 7.5, np.float32))
+        ops.check(L.oxb_qkv_attn_decode(Wt.ptr, dws.ptr, dx.ptr, dg.ptr, 1e-5, rope.ptr, dpos.ptr,
+                                        fq.ptr, fk.ptr, fv.ptr, fv8.ptr, cnt.ptr, H, Hkv, hd, D,
+                                        max_seq, out.ptr, None), "qkv_attn")
+        ops.sync()
+        assert not cnt.download().any()
+        assert np.array_equal(fq.download().view(np.uint32), dq.download().view(np.uint32))
+        assert np.array_equal(out.download().view(np.uint32), want.view(np.uint32)), rep
+    assert np.array_equal(fk.download().reshape(-1), kc1.view(np.uint16).reshape(-1))
+    assert np.array_equal(fv.download().reshape(-1), vc1.view(np.uint16).reshape(-1))
+    assert np.array_equal(fv8.download(), ops.v_octets(vc1))
+
+
+def test_qkv_attn_decode_rejects_unsupported():
+    L = ops.lib()
+    for D, H, Hkv, hd, max_seq in ((1024, 8, 2, 128, 256), (2560, 20, 5, 128, 255),
+                                   (2560, 20, 5, 64, 256), (2560, 20, 6, 128, 256)):
+        rc = L.oxb_qkv_attn_decode(8, 8, 8, 8, 1e-5, 8, 8, 8, 8, 8, 8, 8, H, Hkv, hd, D, max_seq,
+                                   8, None)
+        assert rc == -1
+        assert b"unsupported" in L.oxb_last_error() or b"head_dim" in L.oxb_last_error()
+
+
 def test_attn_decode_fused_rejects_unsupported():
     L = ops.lib()
     assert not L.oxb_attn_decode_fused_supported(32, 4, 128, 512)     # 8 heads per KV head

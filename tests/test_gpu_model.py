@@ -163,17 +163,17 @@ def test_graph_decode_matches_stepwise():
     m.close()
 
 
-def _decode_logits(path, prompt, steps, max_seq, attn):
+def _decode_logits(path, prompt, steps, max_seq, attn, var="OXB_ATTN"):
     import os
-    old = os.environ.get("OXB_ATTN")
-    os.environ["OXB_ATTN"] = attn   # read when the model loads
+    old = os.environ.get(var)
+    os.environ[var] = attn   # read when the model loads
     try:
         m = pkg.Model(path, max_seq=max_seq)
     finally:
         if old is None:
-            del os.environ["OXB_ATTN"]
+            del os.environ[var]
         else:
-            os.environ["OXB_ATTN"] = old
+            os.environ[var] = old
     tok, logits = m.forward(prompt)
     out = [logits]
     toks = [tok]
@@ -198,6 +198,21 @@ def test_decode_attention_forms_identical():
     assert t_split == t_fused == t_head
     assert np.array_equal(l_split.view(np.uint32), l_fused.view(np.uint32))
     assert np.array_equal(l_split.view(np.uint32), l_head.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", ["small", "2b"])
+def test_fused_qkv_attention_steps_identical(shape):
+    """OXB_QKV_ATTN=1 (q|k|v and the attention of steps up to 256 positions
+    as one launch, oxb_qkv_attn_decode) gives the default path's tokens and
+    logits bits, across position 256 where the steps switch back."""
+    cfg = synth.small_config() if shape == "small" else synth.BITNET_2B
+    path = synth.cached_gguf(cfg, seed=7 if shape == "small" else 1234)
+    n_prompt, steps = (200, 80) if shape == "small" else (230, 40)
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    t0, l0 = _decode_logits(path, prompt, steps, 320, "0", "OXB_QKV_ATTN")
+    t1, l1 = _decode_logits(path, prompt, steps, 320, "1", "OXB_QKV_ATTN")
+    assert t0 == t1
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
 
 
 def test_single_token_forward_is_decode_path():
