@@ -1010,14 +1010,15 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 // The B operands come from copies of the cache laid out for them
 // (attn_kv_tiles_kernel, one pass per call): per KV head
 //   Kt [tile of 64 positions][d/4][64 positions][4 d]           f32
-//   Vt [position/4][64 dim pairs][4 positions]    f16 pairs (dims 2j, 2j+1)
+//   Vt [position/4][128 dims][4 positions]         f16
 // zero past the last position, so a lane's 16-byte load is 4 steps of its
 // operand (K with no conversion), and a wave's load is 1 KB contiguous.
 //
 // One workgroup of 16 waves (four per SIMD: a dependent MFMA chain issues at
 // ~64% of the MFMA rate from one wave per SIMD, ~100% from four) per (16/G
 // consecutive queries, KV head): 16 score rows, row r = query r/G, head r%G;
-// query i attends over its position + 1 positions (causal).
+// query i attends over its position + 1 positions (causal).  The workgroups
+// of one XCD share the K / V copies of at most two KV heads (mapping below).
 //   scores: wave w takes the 64-position tiles w, w+16, ...: per d one
 //     instruction covers the 16 rows (A = q[r][d], the same in the 4 blocks)
 //     x 64 positions (B = K[tile + l][d]), 128 of them in order of d.
@@ -1028,11 +1029,13 @@ __global__ __launch_bounds__(kPrefillThreads) void attn_prefill_kernel(
 //     row's positions, in order of s, on v_mfma_f32_4x4x1_16b (one fused
 //     step per output per instruction; lane l supplies A[block l/4][row
 //     l%4], B[block l/4][col l%4] and holds D[block l/4][row i][col l%4] in
-//     register i).  Wave g < 4 takes rows 4g .. 4g+3 (A = p[4g + l%4][s])
-//     and all 128 dims as two chains per lane: dims 2l and 2l + 1 from one
-//     f16 pair of V.  Positions that every row of the group covers run in
-//     whole 16-position batches; the last ones keep each row's sum past its
-//     own length (a select per row).
+//     register i).  Wave w < 4 takes rows 8(w%2) .. +7 as two groups of
+//     four (A = p[row][s], two chains per lane) and dims 64(w/2) .. +63 (B =
+//     V[s][64(w/2) + l], one f16 operand for both groups), so the four
+//     waves load each V element twice, 8 bytes per lane per 4 positions, and
+//     hold kPvAhead 16-position batches of it in flight.  Positions that
+//     every row of a wave covers run in whole batches; the last ones keep
+//     each row's sum past its own length (a select per row).
 // LDS (dynamic): q [16][132] | rows [16][Sw], Sw = the longest row rounded
 // up to 64, plus 4, so that the 16 rows one read touches start in different
 // banks.
@@ -1045,6 +1048,7 @@ constexpr int kPfmQs = kHd + 4;   // q row stride (floats)
 constexpr int kPfmMaxS = 2368;    // longest row whose 16 rows fit the LDS (160 KB)
 constexpr int kTileF4 = 64 * kHd / 4;    // float4 of one 64-position tile of Kt
 constexpr int kVTileU4 = 64 * kHd / 8;   // uint4 of one 64-position tile of Vt
+constexpr int kPvAhead = 3;              // P.V: V batches in flight per wave
 
 __host__ __device__ inline int pfm_row_stride(int s_max) { return ((s_max + 63) & ~63) + 4; }
 __host__ __device__ inline size_t pfm_smem(int s_max) {
@@ -1087,17 +1091,14 @@ __global__ __launch_bounds__(256) void attn_kv_tiles_kernel(const uint16_t *__re
         const uint32_t lo = (c & 1) ? u.z : u.x, hi = (c & 1) ? u.w : u.y;
         kt[i] = make_float4(h2f(lo & 0xffff), h2f(lo >> 16), h2f(hi & 0xffff), h2f(hi >> 16));
     }
-    uint4 *vt = Vt + ((size_t)hk * ntile_ws + t) * kVTileU4;
+    uint2 *vt = (uint2 *)(Vt + ((size_t)hk * ntile_ws + t) * kVTileU4);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // vt[g][j]: dword j (dims 2j, 2j+1) of positions 4g .. 4g+3
-        const int i = tid + 256 * k, g = i >> 6, j = i & 63;
+    for (int k = 0; k < 8; ++k) {   // vt[g][d]: dim d of positions 4g .. 4g+3
+        const int i = tid + 256 * k, g = i >> 7, d = i & (kHd - 1);
         uint32_t v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint4 u = vs[4 * g + r][j >> 2];
-            v[r] = (j & 3) == 0 ? u.x : (j & 3) == 1 ? u.y : (j & 3) == 2 ? u.z : u.w;
-        }
-        vt[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        for (int r = 0; r < 4; ++r) v[r] = ((const uint16_t *)&vs[4 * g + r][0])[d];
+        vt[i] = make_uint2(v[0] | (v[1] << 16), v[2] | (v[3] << 16));
     }
 }
 
@@ -1110,8 +1111,17 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
     float *qs = smem, *rows = smem + 16 * kPfmQs;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform loop control
-    const int nblk = (n_q + QB - 1) / QB;
-    const int q0 = (nblk - 1 - (int)blockIdx.x) * QB, hk = blockIdx.y;   // longest rows first
+    const int nblk = (n_q + QB - 1) / QB, Hkv = H / G;
+    // Block b runs on XCD b % 8.  A KV head's query blocks j (longest rows
+    // first) form 8 stripes j % 8 of equal work; XCD x takes stripes Hkv x ..
+    // Hkv x + Hkv - 1 (in KV-head-major order: two KV heads at most, so its L2
+    // holds their K / V copies), and its k-th block is stripe k % Hkv's block
+    // k / Hkv, so each XCD still starts the longest rows first.
+    const int x = (int)blockIdx.x & 7, k = (int)blockIdx.x >> 3;
+    const int st = Hkv * x + k % Hkv, hk = st >> 3;
+    const int j = (k / Hkv) * 8 + (st & 7);
+    if (j >= nblk) return;   // the whole workgroup, before any barrier
+    const int q0 = (nblk - 1 - j) * QB;
     const int Smax = pos0 + min(q0 + QB - 1, n_q - 1) + 1;
     const int ntile = (Smax + 63) >> 6;
     if (ntile > ntile_ws || Smax > kPfmMaxS) return;   // host checks too; never read out of range
@@ -1181,115 +1191,118 @@ __global__ __launch_bounds__(kPfmThreads) void attn_prefill_mfma_kernel(
 
     // ---- P.V (sh/attention.wgsl:96-104): one chain per output ---------------
     if (w < 4) {
-        const int g = w;   // rows 4g .. 4g+3 (lengths non-decreasing in the row)
-        int len[4];
+        // wave w: rows 8(w&1) .. +7 as two groups of four (chains a and b,
+        // one V operand for both) x dims 64(w>>1) .. +63; lane l: dim d
+        const int r0 = 8 * (w & 1), d = 64 * (w >> 1) + lane;
+        int len[8];   // lengths non-decreasing in the row
 #pragma unroll
-        for (int i = 0; i < 4; ++i) len[i] = row_len(4 * g + i);
-        const int e = len[0] & ~15;   // whole batches every row of the group covers
+        for (int i = 0; i < 8; ++i) len[i] = row_len(r0 + i);
+        const int e = len[0] & ~15;   // whole batches every row of the wave covers
+        const int s_end = len[7];
         const int s_last = 64 * ntile - 16;   // last batch start inside Vt and the rows
-        const uint4 *vt = Vt + (size_t)hk * ntile_ws * kVTileU4 + lane;
-        const float *prow = rows + (4 * g + (lane & 3)) * Sw;
-        // 16 positions per batch: V (global) two batches ahead, p (LDS) just
-        // before its batch's MFMAs (batch starts past the rows are clamped)
-        auto loadv = [&](uint4 (&vv)[4], int s) {
+        const uint2 *vt = (const uint2 *)(Vt + (size_t)hk * ntile_ws * kVTileU4) + d;
+        const float *pa = rows + (r0 + (lane & 3)) * Sw, *pb = pa + 4 * Sw;
+        // 16 positions per batch: V (global) kPvAhead batches ahead in a ring
+        // of registers, p (LDS) at its batch (batch starts past the rows are
+        // clamped)
+        constexpr int NV = kPvAhead + 1;
+        uint2 vr[NV][4];
+        float4 qa[4], qb[4];
+        auto loadv = [&](uint2 (&vv)[4], int s) {
             const int sb = min(s, s_last);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) vv[j] = vt[(size_t)(sb / 4 + j) * (kHd / 2)];
+            for (int j = 0; j < 4; ++j) vv[j] = vt[(size_t)(sb / 4 + j) * kHd];
             __builtin_amdgcn_sched_barrier(0);
         };
-        auto loadp = [&](float4 (&pp)[4], int s) {
+        auto loadp = [&](int s) {
             const int sb = min(s, s_last);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pp[j] = *(const float4 *)(prow + sb + 4 * j);
+            for (int j = 0; j < 4; ++j) {
+                qa[j] = *(const float4 *)(pa + sb + 4 * j);
+                qb[j] = *(const float4 *)(pb + sb + 4 * j);
+            }
         };
-        auto lo = [](uint32_t u) { return __half2float(__ushort_as_half((uint16_t)(u & 0xffffu))); };
-        auto hi = [](uint32_t u) { return __half2float(__ushort_as_half((uint16_t)(u >> 16))); };
-        v4f a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto run = [&](const uint4 (&vv)[4], const float4 (&pp)[4]) {
+        auto vk = [](const uint2 &u, int k) {   // position k of the lane's quad
+            const uint32_t wd = k < 2 ? u.x : u.y;
+            return __half2float(__ushort_as_half((uint16_t)((k & 1) ? wd >> 16 : wd & 0xffffu)));
+        };
+        v4f a = {0.0f, 0.0f, 0.0f, 0.0f}, b = {0.0f, 0.0f, 0.0f, 0.0f};
+        // the batch's 16 V values converted first (while its p reads land),
+        // then its 32 steps back to back
+        auto run = [&](const uint2 (&vv)[4]) {
+            float vf[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) vf[i] = vk(vv[i >> 2], i & 3);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t u[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
-                const float p[4] = {pp[j].x, pp[j].y, pp[j].z, pp[j].w};
+                const float pa4[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                const float pb4[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    a0 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], lo(u[k]), a0, 0, 0, 0);
-                    a1 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], hi(u[k]), a1, 0, 0, 0);
+                    a = __builtin_amdgcn_mfma_f32_4x4x1f32(pa4[k], vf[4 * j + k], a, 0, 0, 0);
+                    b = __builtin_amdgcn_mfma_f32_4x4x1f32(pb4[k], vf[4 * j + k], b, 0, 0, 0);
                 }
             }
         };
         // the batch at st, each row's sum kept past its own length
-        auto tail = [&](const uint4 (&vv)[4], float4 (&pp)[4], int st) {
-            if (st >= len[3]) return;
-            loadp(pp, st);
+        auto tail = [&](const uint2 (&vv)[4], int st) {
+            if (st >= s_end) return;
+            loadp(st);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t u[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
-                const float p[4] = {pp[j].x, pp[j].y, pp[j].z, pp[j].w};
+                const float pa4[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                const float pb4[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int s = st + 4 * j + k;
-                    const v4f r0 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], lo(u[k]), a0, 0, 0, 0);
-                    const v4f r1 = __builtin_amdgcn_mfma_f32_4x4x1f32(p[k], hi(u[k]), a1, 0, 0, 0);
+                    const float v = vk(vv[j], k);
+                    const v4f ra = __builtin_amdgcn_mfma_f32_4x4x1f32(pa4[k], v, a, 0, 0, 0);
+                    const v4f rb = __builtin_amdgcn_mfma_f32_4x4x1f32(pb4[k], v, b, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        a0[i] = s < len[i] ? r0[i] : a0[i];
-                        a1[i] = s < len[i] ? r1[i] : a1[i];
+                        a[i] = s < len[i] ? ra[i] : a[i];
+                        b[i] = s < len[4 + i] ? rb[i] : b[i];
                     }
                 }
             }
         };
-        // batches rotate va -> vb -> vc, each loaded two batches ahead; at the
-        // exit the next two batches (the positions past e, fewer than 19)
-        // are moved to va and vb for the one tail
-        uint4 va[4], vb[4], vc[4];
-        float4 pp[4];
-        loadv(va, 0);
-        loadv(vb, 16);
-        int s = 0;
-        if (e > 0) {
-            for (;; s += 48) {
-                loadv(vc, s + 32);
-                loadp(pp, s);
-                run(va, pp);
-                if (s + 16 >= e) {   // next: vb, vc
-                    s += 16;
+        // batch n sits in vr[n % NV].  Passes of NV batches with no branch
+        // inside (ring indices are constants, and the loads stay in flight
+        // across batches), then the r < NV whole batches left, then the
+        // tails: batches r and r + 1 (the positions past e, fewer than 32)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        va[j] = vb[j];
-                        vb[j] = vc[j];
-                    }
-                    break;
-                }
-                loadv(va, s + 48);
-                loadp(pp, s + 16);
-                run(vb, pp);
-                if (s + 32 >= e) {   // next: vc, va
-                    s += 32;
+        for (int i = 0; i < NV - 1; ++i) loadv(vr[i], 16 * i);
+        int s0 = 0;
+        for (; s0 + 16 * NV <= e; s0 += 16 * NV) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint4 t = va[j];
-                        va[j] = vc[j];
-                        vb[j] = t;
-                    }
-                    break;
-                }
-                loadv(vb, s + 64);
-                loadp(pp, s + 32);
-                run(vc, pp);
-                if (s + 48 >= e) {   // next: va, vb
-                    s += 48;
-                    break;
-                }
+            for (int i = 0; i < NV; ++i) {
+                loadv(vr[(i + NV - 1) % NV], s0 + 16 * (i + NV - 1));
+                loadp(s0 + 16 * i);
+                run(vr[i]);
             }
         }
-        tail(va, pp, s);
-        tail(vb, pp, s + 16);
+        const int r = (e - s0) >> 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 4 * g + i, qi = q0 + r / G;
-            if (qi < n_q)
-                *(float2 *)(out + ((size_t)qi * H + hk * G + r % G) * kHd + 2 * lane) =
-                    make_float2(a0[i], a1[i]);
+        for (int i = 0; i < NV - 1; ++i) {
+            if (i < r) {
+                loadv(vr[(i + NV - 1) % NV], s0 + 16 * (i + NV - 1));
+                loadp(s0 + 16 * i);
+                run(vr[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if (i == r) {
+                tail(vr[i], s0 + 16 * i);
+                tail(vr[(i + 1) % NV], s0 + 16 * (i + 1));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = r0 + i, qi = q0 + r / G;
+            if (qi < n_q) out[((size_t)qi * H + hk * G + r % G) * kHd + d] = i < 4 ? a[i] : b[i - 4];
         }
     }
 }
@@ -2447,7 +2460,7 @@ static int launch_prefill_mfma(const float *q, const uint16_t *kc, const uint16_
                        s_max, ntile, Kt, Vt);
     OXB_CHECK_HIP(hipGetLastError());
     const float scale = 1.0f / sqrtf((float)kHd);  // nn/attention.rs:206
-    hipLaunchKernelGGL((attn_prefill_mfma_kernel<G>), dim3((n_q + QB - 1) / QB, Hkv),
+    hipLaunchKernelGGL((attn_prefill_mfma_kernel<G>), dim3(8 * Hkv * ((n_q + QB * 8 - 1) / (QB * 8))),
                        dim3(kPfmThreads), pfm_smem(s_max), s, q, Kt, Vt, ntile, pos0, n_q, H,
                        scale, out);
     OXB_CHECK_HIP(hipGetLastError());
