@@ -69,7 +69,7 @@ int oxb_batch::enqueue_step() {
     oxb_model &M = *m;
     void *s = (void *)M.stream;
     const int D = M.D, F = M.F, Dq = M.H * M.hd, Dkv = M.Hkv * M.hd;
-    if (embedding_strided(M.embed, M.V, D, state + OXB_ST_TOKEN, OXB_STATE_INTS, B, x, s))
+    if (embedding_lm(M.embed_lm, M.V, D, state + OXB_ST_TOKEN, OXB_STATE_INTS, nullptr, B, x, s))
         return -1;
     for (int l = 0; l < M.n_layers; ++l) {
         const oxb_model::Layer &L = M.layers[l];

@@ -329,6 +329,31 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t *__restri
             (id >= 0 && id < V) ? __half2float(__ushort_as_half(E[(size_t)id * D + d])) : 0.0f;
 }
 
+// The same rows read from the LM head's lm-tiled copy of the table (the
+// model keeps no other): element d of row `id` is half d % 2 of dword d / 2
+// = t + 256 j, which sits in uint4 (tile NQ + u / 4) * 64 + id % 64,
+// component u % 4, u = i NJ + j, where t is the bit-reversal image of i
+// (the map is its own inverse).
+__global__ __launch_bounds__(256) void embedding_lm_kernel(const uint32_t *__restrict__ E_lm,
+                                                           int V, int D, const int *__restrict__ ids,
+                                                           int ids_stride,
+                                                           const int *__restrict__ state,
+                                                           float *__restrict__ x) {
+    const int t_row = blockIdx.x;
+    const int id = ids ? ids[(size_t)t_row * ids_stride] : state[OXB_ST_TOKEN];
+    const int NJ = D / 512, NQ = 64 * NJ;
+    const bool in = id >= 0 && id < V;
+    const size_t base = in ? ((size_t)(id >> 6) * NQ * 64 + (id & 63)) * 4 : 0;
+    for (int d = threadIdx.x; d < D; d += 256) {
+        const int dh = d >> 1, t = dh & 255, j = dh >> 8;
+        const int i = (bitrev4(t & 15) << 4) | bitrev4(t >> 4);
+        const int u = i * NJ + j;
+        const uint32_t w = in ? E_lm[base + (size_t)(u >> 2) * 64 * 4 + (u & 3)] : 0u;
+        x[(size_t)t_row * D + d] =
+            in ? __half2float(__ushort_as_half((uint16_t)((d & 1) ? w >> 16 : w & 0xffffu))) : 0.0f;
+    }
+}
+
 // Natural f16 embedding [V][D] -> the LM head's lm-tiled layout (above).
 __global__ void repack_lm_kernel(const uint32_t *__restrict__ E, uint4 *__restrict__ dst, int V,
                                  int D) {
@@ -487,16 +512,18 @@ extern "C" int oxb_embedding(const uint16_t *E, int V, int D, const int *ids, in
 }
 
 namespace oxb {
-// Rows t = 0..n_tok-1 from ids[t * ids_stride] (e.g. the token fields of a
-// batch's state blocks).
-int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
-                      float *x, void *stream) {
-    OXB_REQUIRE(n_tok > 0 && D > 0 && ids, "embedding: bad shape");
-    hipLaunchKernelGGL(embedding_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream, E, V, D,
-                       ids, ids_stride, nullptr, x);
+// Rows from the lm-tiled table: ids[t * ids_stride] for t < n_tok, or the
+// decode state's token when ids is null (n_tok 1).
+int embedding_lm(const void *E_lm, int V, int D, const int *ids, int ids_stride, const int *state,
+                 int n_tok, float *x, void *stream) {
+    OXB_REQUIRE(n_tok > 0 && D % 512 == 0 && D <= 5 * 512 && (ids || (state && n_tok == 1)),
+                "embedding: bad shape");
+    hipLaunchKernelGGL(embedding_lm_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)stream,
+                       (const uint32_t *)E_lm, V, D, ids, ids_stride, state, x);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
+
 }  // namespace oxb
 
 extern "C" int oxb_repack_i2s_tiled(const void *natural, void *tiled, int N, int K,

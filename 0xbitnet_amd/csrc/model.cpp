@@ -435,17 +435,26 @@ oxb_model *model_load(const char *path, int max_seq, LoadHook hook, void *ud, in
         }
         if (hook) hook(2, (uint64_t)i + 1, total, ud);
     }
-    // embedding (kept f16, model/loader.rs:139-141) and final norm
-    m->embed = (uint16_t *)m->dalloc((size_t)m->V * D * 2);
-    if (!m->embed) return nullptr;
-    if (hipMemcpy(m->embed, g->base + g->data_offset + te->offset, (size_t)m->V * D * 2,
-                  hipMemcpyHostToDevice) != hipSuccess) {
-        set_error("embedding upload failed");
-        return nullptr;
+    // embedding (kept f16, model/loader.rs:139-141) and final norm: the tied
+    // table is kept once, in the LM head's layout (the embedding gathers its
+    // rows from there); the natural copy is staging only
+    {
+        uint16_t *natural = (uint16_t *)m->dalloc((size_t)m->V * D * 2);
+        if (!natural) return nullptr;
+        if (hipMemcpy(natural, g->base + g->data_offset + te->offset, (size_t)m->V * D * 2,
+                      hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("embedding upload failed");
+            return nullptr;
+        }
+        m->embed_lm = m->dalloc(oxb_lm_bytes(m->V, D));
+        if (!m->embed_lm || oxb_repack_lm(natural, m->embed_lm, m->V, D, nullptr)) return nullptr;
+        if (hipDeviceSynchronize() != hipSuccess) {
+            set_error("embedding repack failed");
+            return nullptr;
+        }
+        m->dfree(natural);
+        m->weight_bytes += oxb_lm_bytes(m->V, D);
     }
-    m->weight_bytes += (size_t)m->V * D * 2;
-    m->embed_lm = m->dalloc(oxb_lm_bytes(m->V, D));
-    if (!m->embed_lm || oxb_repack_lm(m->embed, m->embed_lm, m->V, D, nullptr)) return nullptr;
     {
         std::vector<float> w;
         if (!tensor_to_f32(*g, *tn, w) || upload_f32(m.get(), w, &m->final_norm)) return nullptr;
@@ -568,7 +577,7 @@ int oxb_model::enqueue_decode_step(AttnForm attn, bool sample) {
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     int *posp = state + OXB_ST_POS;
-    if (oxb_embedding(embed, V, D, nullptr, 1, state, x, s)) return -1;
+    if (oxb::embedding_lm(embed_lm, V, D, nullptr, 0, state, 1, x, s)) return -1;
     const size_t kv_layer = (size_t)Hkv * max_seq * hd * kv_elem_bytes();
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];
@@ -697,7 +706,7 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
-    if (oxb_embedding(embed, V, D, pids, n, tg.state, px, s)) return -1;
+    if (oxb::embedding_lm(embed_lm, V, D, pids, 1, nullptr, n, px, s)) return -1;
     const size_t kv_layer = (size_t)Hkv * tg.max_seq * hd * kv_elem_bytes();
     for (int l = 0; l < n_layers; ++l) {
         const Layer &L = layers[l];

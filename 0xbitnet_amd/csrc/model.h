@@ -26,8 +26,7 @@ struct oxb_model {
         float *attn_sub = nullptr, *ffn_sub = nullptr;  // may be null
     };
     std::vector<Layer> layers;
-    uint16_t *embed = nullptr;   // [V][D] f16 (token embedding)
-    void *embed_lm = nullptr;    // the same table in the LM head's layout
+    void *embed_lm = nullptr;    // the tied f16 table [V][D], in the LM head's layout
     float *final_norm = nullptr;
     float *rope = nullptr;       // [max_seq][hd/2] (cos, sin)
     // [L][Hkv][max_seq][hd]: f16 bits, or f32 when kv_f32 (the reference's

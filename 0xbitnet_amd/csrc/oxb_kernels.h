@@ -46,8 +46,11 @@ int attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int n_q
                  void *stream);
 int attn_f32(const float *q, const float *kcache, const float *vcache, const int *pos_ptr,
              int pos0, int n_q, int H, int Hkv, int hd, int max_seq, float *out, void *stream);
-int embedding_strided(const uint16_t *E, int V, int D, const int *ids, int ids_stride, int n_tok,
-                      float *x, void *stream);
+// The token embedding from the LM head's lm-tiled copy of the tied table
+// (oxb_repack_lm's layout): rows ids[t * ids_stride], or the decode state's
+// token when ids is null (lm_head.hip).
+int embedding_lm(const void *E_lm, int V, int D, const int *ids, int ids_stride, const int *state,
+                 int n_tok, float *x, void *stream);
 // Batched LM head with a workspace of n_rows * D floats (lm_head.hip).
 int lm_head_argmax_rows(const float *x, size_t x_stride, const float *gamma, float eps,
                         const void *E, int V, int D, float *logits, int *state, int state_stride,
