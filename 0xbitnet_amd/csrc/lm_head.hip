@@ -39,9 +39,6 @@ struct LmParams {
 // fold it left to right: 8-leaf subtrees in registers, pairs of them into
 // the 16 sums of 16 leaves, then the tree over those 16.  Result: the
 // shader's exact f32 value.
-__host__ __device__ inline int bitrev4(int x) {
-    return ((x & 1) << 3) | ((x & 2) << 1) | ((x & 4) >> 1) | ((x & 8) >> 3);
-}
 
 // (value, index) -> u64 whose unsigned maximum is the largest value with the
 // lowest index on ties (rs/sampling.rs argmax semantics); -0 counts as +0,
@@ -330,10 +327,8 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t *__restri
 }
 
 // The same rows read from the LM head's lm-tiled copy of the table (the
-// model keeps no other): element d of row `id` is half d % 2 of dword d / 2
-// = t + 256 j, which sits in uint4 (tile NQ + u / 4) * 64 + id % 64,
-// component u % 4, u = i NJ + j, where t is the bit-reversal image of i
-// (the map is its own inverse).
+// model keeps no other): element d of row `id` is half d % 2 of dword
+// lm_dword(id, d / 2).
 __global__ __launch_bounds__(256) void embedding_lm_kernel(const uint32_t *__restrict__ E_lm,
                                                            int V, int D, const int *__restrict__ ids,
                                                            int ids_stride,
@@ -341,14 +336,10 @@ __global__ __launch_bounds__(256) void embedding_lm_kernel(const uint32_t *__res
                                                            float *__restrict__ x) {
     const int t_row = blockIdx.x;
     const int id = ids ? ids[(size_t)t_row * ids_stride] : state[OXB_ST_TOKEN];
-    const int NJ = D / 512, NQ = 64 * NJ;
+    const int NJ = D / 512;
     const bool in = id >= 0 && id < V;
-    const size_t base = in ? ((size_t)(id >> 6) * NQ * 64 + (id & 63)) * 4 : 0;
     for (int d = threadIdx.x; d < D; d += 256) {
-        const int dh = d >> 1, t = dh & 255, j = dh >> 8;
-        const int i = (bitrev4(t & 15) << 4) | bitrev4(t >> 4);
-        const int u = i * NJ + j;
-        const uint32_t w = in ? E_lm[base + (size_t)(u >> 2) * 64 * 4 + (u & 3)] : 0u;
+        const uint32_t w = in ? E_lm[lm_dword(id, d >> 1, NJ)] : 0u;
         x[(size_t)t_row * D + d] =
             in ? __half2float(__ushort_as_half((uint16_t)((d & 1) ? w >> 16 : w & 0xffffu))) : 0.0f;
     }

@@ -107,6 +107,23 @@ __host__ __device__ inline float oxb_expf(float x) {
 
 }  // namespace oxb
 
+namespace oxb {
+// The LM head's lm-tiled layout of the tied f16 table [V][D] (oxb_repack_lm,
+// NJ = D / 512): 64-row tiles; within a tile, row r's dwords in uint4 u / 4
+// (component u % 4) of lane slot r, where dword dh = t + 256 j of the row has
+// u = i NJ + j and t is the bit-reversal image of i (its own inverse).
+__host__ __device__ inline int bitrev4(int x) {
+    return ((x & 1) << 3) | ((x & 2) << 1) | ((x & 4) >> 1) | ((x & 8) >> 3);
+}
+// the dword holding elements 2 dh and 2 dh + 1 of row `row`
+__host__ __device__ inline size_t lm_dword(int row, int dh, int NJ) {
+    const int t = dh & 255, j = dh >> 8;
+    const int i = (bitrev4(t & 15) << 4) | bitrev4(t >> 4);
+    const int u = i * NJ + j;
+    return (((size_t)(row >> 6) * 64 * NJ + (u >> 2)) * 64 + (row & 63)) * 4 + (u & 3);
+}
+}  // namespace oxb
+
 #ifdef __HIPCC__
 namespace oxb {
 
