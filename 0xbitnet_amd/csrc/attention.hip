@@ -350,14 +350,21 @@ __host__ __device__ inline size_t pc_smem(int slots, int max_seq) {
 // exact in any order.  Loads are clamped to the row (branch-free).  The four
 // waves of the row exchange through wm (their maxima) and red (the 256
 // partials); every wave of the workgroup must call (two barriers).
-template <int NI>
+struct NoLoads {
+    __device__ void operator()() const {}
+};
+
+// after_loads() runs once the row's loads are issued, before their first
+// wait (a caller's own loads there do not delay the softmax's).
+template <int NI, typename F = NoLoads>
 __device__ __forceinline__ void softmax_row_4w(float *prow, const float *__restrict__ src, int S,
                                                bool has_row, float *wm, float *red, int j,
-                                               int lane) {
+                                               int lane, const F &after_loads = F()) {
     const int t = 64 * j + lane;
     float x[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) x[i] = has_row ? src[min(t + 256 * i, S - 1)] : 0.0f;
+    after_loads();
     float m = -3.402823e+38f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) m = t + 256 * i < S ? fmaxf(m, x[i]) : m;
@@ -381,17 +388,18 @@ __device__ __forceinline__ void softmax_row_4w(float *prow, const float *__restr
         if (t + 256 * i < S) prow[t + 256 * i] = x[i] * inv;
 }
 
+template <typename F = NoLoads>
 __device__ __forceinline__ void softmax_row_4w_any(float *prow, const float *src, int S,
                                                    bool has_row, float *wm, float *red, int j,
-                                                   int lane) {
+                                                   int lane, const F &after_loads = F()) {
     const int ni = (S + 255) >> 8;   // workgroup-uniform
-    if (ni <= 1) softmax_row_4w<1>(prow, src, S, has_row, wm, red, j, lane);
-    else if (ni <= 2) softmax_row_4w<2>(prow, src, S, has_row, wm, red, j, lane);
-    else if (ni <= 4) softmax_row_4w<4>(prow, src, S, has_row, wm, red, j, lane);
-    else if (ni <= 8) softmax_row_4w<8>(prow, src, S, has_row, wm, red, j, lane);
-    else if (ni <= 12) softmax_row_4w<12>(prow, src, S, has_row, wm, red, j, lane);
-    else if (ni <= 16) softmax_row_4w<16>(prow, src, S, has_row, wm, red, j, lane);
-    else softmax_row_4w<kPcMaxNI>(prow, src, S, has_row, wm, red, j, lane);
+    if (ni <= 1) softmax_row_4w<1>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else if (ni <= 2) softmax_row_4w<2>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else if (ni <= 4) softmax_row_4w<4>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else if (ni <= 8) softmax_row_4w<8>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else if (ni <= 12) softmax_row_4w<12>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else if (ni <= 16) softmax_row_4w<16>(prow, src, S, has_row, wm, red, j, lane, after_loads);
+    else softmax_row_4w<kPcMaxNI>(prow, src, S, has_row, wm, red, j, lane, after_loads);
 }
 
 // acc + sum of p[s] * v_s over the n (all 4 when FULL) positions of a group,
@@ -790,6 +798,99 @@ __global__ __launch_bounds__(kPhThreads) void attn_pv_oct_kernel(
     }
     wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
     if (w == 0) out[64 * half + lane] = acc;
+}
+
+// The same P.V with V streamed from the octet copy into registers: the
+// chain wave's lanes load their dim's octets straight from global memory
+// (one 1 KB wave load per 8 positions) kPoReg - 1 octets ahead in a ring of
+// registers, so the LDS carries only the probability broadcasts and no
+// barrier paces the chain; the other three waves only help with the
+// softmax.  The first loads go out right after the softmax's score loads.
+// Same grid, block -> (KV head, item) mapping and result bits as
+// attn_pv_oct_kernel.  LDS (dynamic): p [Sp] | red [256] | wmax [4]
+constexpr int kPoReg = 16;   // octets in the chain wave's register ring
+
+__host__ __device__ inline size_t pr_smem(int max_seq) {
+    return ((size_t)pc_row_stride(max_seq) + 256 + 8) * 4;
+}
+
+// acc over positions 0 .. S-1 of a lane's dim: octet o's V at V8[o * kHd]
+// (clamped to the last octet), its p at pr[8o .. 8o+7] (read three octets
+// ahead).  Passes of kPoReg octets keep the ring indices constants; then the
+// whole octets left, then the last S % 8 positions.
+__device__ __forceinline__ float po_chain_reg(const uint4 *__restrict__ V8, const float *pr, int S,
+                                              uint4 (&vr)[kPoReg]) {
+    constexpr int NB = kPoReg;
+    const int last = (S - 1) >> 3, nfull = S >> 3;
+    float4 pa[4], pb[4];
+    auto ldv = [&](int b, int o) { vr[b] = V8[(size_t)min(o, last) * kHd]; };
+    auto ldp = [&](int b, int o) {
+        o = min(o, last);
+        pa[b] = *(const float4 *)(pr + 8 * o);
+        pb[b] = *(const float4 *)(pr + 8 * o + 4);
+    };
+    float acc = 0.0f;
+    ldp(0, 0);
+    ldp(1, 1);
+    ldp(2, 2);
+    int o0 = 0;
+    for (; o0 + NB <= nfull; o0 += NB) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            __builtin_amdgcn_sched_barrier(0);
+            ldv((i + NB - 1) % NB, o0 + i + NB - 1);
+            ldp((i + 3) & 3, o0 + i + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv8<true>(acc, vr[i], pa[i & 3], pb[i & 3]);
+        }
+    }
+    const int r = nfull - o0;   // whole octets left (< NB), then the partial one
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (i < r) {
+            __builtin_amdgcn_sched_barrier(0);
+            ldv((i + NB - 1) % NB, o0 + i + NB - 1);
+            ldp((i + 3) & 3, o0 + i + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv8<true>(acc, vr[i], pa[i & 3], pb[i & 3]);
+        } else if (i == r && (S & 7)) {
+            acc = pv8<false>(acc, vr[i], pa[i & 3], pb[i & 3], S & 7);
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(kPhThreads) void attn_pv_oreg_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc8,
+    const int *__restrict__ pos_ptr, int G, int Hkv, int max_seq, float *__restrict__ out,
+    size_t kv8_stride, int pos_stride) {
+    const int b = blockIdx.x, z = blockIdx.y;
+    const int hk = 8 * (b / (16 * G)) + (b & 7), item = (b >> 3) % (2 * G);
+    if (hk >= Hkv) return;
+    const int h = hk * G + (item >> 1), half = item & 1, H = Hkv * G;
+    scores += (size_t)z * H * max_seq + (size_t)h * max_seq;
+    vc8 += (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd);
+    out += (size_t)z * H * kHd + (size_t)h * kHd;
+    extern __shared__ __align__(16) int8_t smem_pr[];
+    float *pr = (float *)smem_pr;
+    float *red = pr + pc_row_stride(max_seq), *wmax = red + 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1, last = (S - 1) >> 3;
+    const uint4 *V8 = (const uint4 *)vc8 + 64 * half + lane;
+    uint4 vr[kPoReg];
+    // wave 0's ring: octets 0 .. kPoReg - 2, issued behind its score loads
+    auto first_v = [&]() {
+        if (w == 0) {
+#pragma unroll
+            for (int i = 0; i < kPoReg - 1; ++i) vr[i] = V8[(size_t)min(i, last) * kHd];
+        }
+    };
+    softmax_row_4w_any(pr, scores, S, true, wmax, red, w, lane, first_v);
+    lds_barrier();   // every wave's probabilities are in pr
+    if (w == 0) out[64 * half + lane] = po_chain_reg(V8, pr, S, vr);
 }
 
 // The 16-wave P.V above over the octet copy of V (larger batches): wave w
@@ -2528,7 +2629,14 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
     OXB_CHECK_HIP(hipGetLastError());
     if (vc8 && batch <= kPhMaxBatch) {   // one chain wave per CU, V in position octets
         const dim3 hgrid(16 * G * ((Hkv + 7) / 8), batch);
-        if (po_smem(6, max_seq) <= 160 * 1024) {
+        // 1-2 sequences: V staged through the LDS ring (19.7 against 20.9 us
+        // per layer at 2304 positions); more: V streamed into registers (27.0
+        // against 40.2 us for 8 sequences)
+        if (batch >= 3) {
+            if (allow_dynamic_lds((const void *)attn_pv_oreg_kernel)) return -1;
+            hipLaunchKernelGGL(attn_pv_oreg_kernel, hgrid, dim3(kPhThreads), pr_smem(max_seq), s,
+                               scores, vc8, pos, G, Hkv, max_seq, out, kv8_stride, pos_stride);
+        } else if (po_smem(6, max_seq) <= 160 * 1024) {
             if (allow_dynamic_lds((const void *)attn_pv_oct_kernel<6>)) return -1;
             hipLaunchKernelGGL(attn_pv_oct_kernel<6>, hgrid, dim3(kPhThreads), po_smem(6, max_seq),
                                s, scores, vc8, pos, G, Hkv, max_seq, out, kv8_stride, pos_stride);

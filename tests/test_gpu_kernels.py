@@ -406,6 +406,44 @@ def test_attn_decode_batch_bitexact(B, H, Hkv, S):
         assert np.array_equal(got8[z].view(np.uint32), ref.view(np.uint32)), f"octets, slot {z}"
 
 
+@pytest.mark.parametrize("poss", [[0, 127, 128, 2303], [7, 8, 136, 255], [1023, 1024, 129, 15],
+                                  [2559, 2047, 2048, 1]])
+def test_attn_decode_octets_register_stream_edges(poss):
+    """Three or more sequences read V straight into registers (a ring of 16
+    octets): every slot at the edges of an octet and of the ring (128
+    positions), the first position and the longest cache, bit-equal to the
+    oracle."""
+    B, H, Hkv, hd, S = len(poss), 20, 5, 128, 2560
+    rng = np.random.default_rng(sum(poss))
+    q = rng.standard_normal((B, H * hd)).astype(np.float32)
+    kc = (rng.standard_normal((B, Hkv, S, hd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((B, Hkv, S, hd)).astype(np.float16)
+    pos = np.array(poss, np.int32)
+    st = np.zeros((B, 8), np.int32)
+    st[:, 0] = pos
+    v8 = ops.v_octets(vc)
+    o = v8.reshape(B, Hkv, -1, hd, 8).view(np.float16)
+    for z in range(B):   # positions past each slot's own: NaN (never summed)
+        for s_ in range(int(pos[z]) + 1, S):
+            o[z, :, s_ // 8, :, s_ % 8] = np.nan
+    L = ops.lib()
+    dq = ops.DeviceArray.from_host(q)
+    dk = ops.DeviceArray.from_host(kc.view(np.uint16))
+    dv = ops.DeviceArray.from_host(vc.view(np.uint16))
+    dv8 = ops.DeviceArray.from_host(v8)
+    dst = ops.DeviceArray.from_host(st)
+    sc = ops.DeviceArray((B * H * S,), np.float32)
+    out = ops.DeviceArray((B, H * hd), np.float32)
+    ops.check(L.oxb_attn_decode_batch_v8(dq.ptr, dk.ptr, dv.ptr, dv8.ptr, dst.ptr, 8, Hkv * S * hd,
+                                         v8.shape[-1], B, H, Hkv, hd, S, sc.ptr, out.ptr, None),
+              "attn_decode_batch_v8")
+    ops.sync()
+    got = out.download()
+    for z in range(B):
+        ref = _oracle_attn(q[z], kc[z], vc[z], 1, int(pos[z]) + 1, H, Hkv, hd)
+        assert np.array_equal(got[z].view(np.uint32), ref.view(np.uint32)), f"slot {z}"
+
+
 @pytest.mark.parametrize("S,pos", [(8, 0), (8, 7), (9, 8), (16, 9), (128, 127), (129, 128),
                                    (300, 255), (300, 256), (1000, 999), (2560, 2303),
                                    (4099, 4098), (6144, 6143), (6144, 130)])
