@@ -699,18 +699,20 @@ __device__ __forceinline__ float pv8(float acc, const uint4 &V, const float4 &Pa
     return acc;
 }
 
-// n positions (1 .. kPoRows) of one ring slot into a lane's chain: vs = the
-// lane's 16 bytes of the slot's octet 0 (octets 64 uint4 apart), pp = the p
-// row at the slot's first position.  Octet o in entry o % 4, read three
+// n positions (1 .. 8 NOCT) of one ring slot into a lane's chain: vs = the
+// lane's 16 bytes of the slot's octet 0 (octets STRIDE uint4 apart), pp = the
+// p row at the slot's first position.  Octet o in entry o % 4, read three
 // octets ahead; four octets per iteration, whose entries are constants (a
 // rotating index would put the entries in scratch), the rest from entries
 // 0..3 after the loop.
+template <int NOCT = kPoOcts, int STRIDE = 64>
 __device__ __forceinline__ float po_chain_slot(float acc, const uint4 *vs, const float *pp, int n) {
+    static_assert(NOCT % 4 == 0, "whole groups of four octets");
     uint4 V[4];
     float4 Pa[4], Pb[4];
     auto ld = [&](int b, int o) {   // octet o (clamped into the slot) into entry b
-        o = min(o, kPoOcts - 1);
-        V[b] = vs[o * 64];
+        o = min(o, NOCT - 1);
+        V[b] = vs[o * STRIDE];
         Pa[b] = *(const float4 *)(pp + 8 * o);
         Pb[b] = *(const float4 *)(pp + 8 * o + 4);
     };
@@ -719,7 +721,7 @@ __device__ __forceinline__ float po_chain_slot(float acc, const uint4 *vs, const
     ld(2, 2);
     int o0 = 0;
 #pragma unroll
-    for (int it = 0; it < kPoOcts / 4; ++it) {
+    for (int it = 0; it < NOCT / 4; ++it) {
         if (8 * (o0 + 4) > n) break;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -961,6 +963,88 @@ __global__ __launch_bounds__(kPcThreads) void attn_pv_chain_oct_kernel(
     }
     wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
     if (w < 4 && 4 * rg + w < G) out[(size_t)(hk * G + 4 * rg + w) * kHd + lane] = acc;
+}
+
+// The same P.V with both halves of the dims in one workgroup per (KV head,
+// group of four heads, sequence): half as many workgroups (160 for 32
+// sequences of the 2B shape, one round over the CUs where the per-half
+// grid needs two), each staging whole V octets (both halves) in ring slots
+// of kPmRows positions: wave w loads octet w % 8 of a slot, half w / 8 (one
+// 1 KB load).  Chain wave w < 8 sums head 4 rg + w % 4, lane l dim
+// 64 (w / 4) + l.  Softmax and result bits as attn_pv_chain_oct_kernel.
+// LDS (dynamic): ring [NS][8 octets][2 halves][64 lanes] uint4 | p [4][Sp] |
+// red [4][256] | wmax [16]
+constexpr int kPmRows = 64;                    // positions per ring slot
+constexpr int kPmOcts = kPmRows / 8;
+constexpr int kPmSlotBytes = kPmOcts * 2 * 64 * 16;
+
+__host__ __device__ inline size_t pm_smem(int slots, int max_seq) {
+    return (size_t)slots * kPmSlotBytes + ((size_t)4 * pc_row_stride(max_seq) + 4 * 256 + 16) * 4;
+}
+
+template <int NS>
+__global__ __launch_bounds__(kPcThreads) void attn_pv_chain_oct2_kernel(
+    const float *__restrict__ scores, const uint16_t *__restrict__ vc8,
+    const int *__restrict__ pos_ptr, int G, int max_seq, float *__restrict__ out,
+    size_t kv8_stride, int pos_stride) {
+    static_assert(NS >= 3 && NS - 3 < 64, "ring depth within vmcnt");
+    static_assert(kPcWaves == 2 * kPmOcts, "one octet half per wave and slot");
+    const int RG = (G + 3) >> 2;                  // groups of four heads per KV head
+    const int hg = blockIdx.x, hk = hg / RG, rg = hg % RG, z = blockIdx.y;
+    const int Hkv = gridDim.x / RG, H = Hkv * G;
+    scores += (size_t)z * H * max_seq;
+    vc8 += (size_t)z * kv8_stride + (size_t)hk * v8_head_elems(max_seq, kHd);
+    out += (size_t)z * H * kHd;
+    extern __shared__ __align__(16) int8_t smem_pm[];
+    uint4 *ring = (uint4 *)smem_pm;
+    const int Sp = pc_row_stride(max_seq);
+    float *pr = (float *)(smem_pm + (size_t)NS * kPmSlotBytes);
+    float *red = pr + 4 * Sp, *wmax = red + 4 * 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = pos_ptr[(size_t)z * pos_stride];
+    if (pos < 0 || pos >= max_seq) return;   // uniform: before any barrier
+    const int S = pos + 1;
+    const int nslots = (S + kPmRows - 1) / kPmRows;
+    const int last_oct = (S - 1) >> 3;
+
+    // this wave's share of a slot: octet w % 8, half w / 8 (lane l: dim
+    // 64 (w / 8) + l), clamped to the last octet
+    const uint4 *V8 = (const uint4 *)vc8 + 64 * (w >> 3) + lane;
+    auto issue = [&](int c) {
+        const int o = c * kPmOcts + (w & 7);
+        lds_dma16(V8 + (size_t)min(o, last_oct) * kHd,
+                  ring + (((size_t)(c % NS) * kPmOcts + (w & 7)) * 2 + (w >> 3)) * 64);
+    };
+#pragma unroll
+    for (int c = 0; c < NS - 1; ++c) issue(c);
+
+    // ---- softmax: row r = w / 4 (head 4rg + r of the KV head) -------------
+    {
+        const int r = w >> 2, j = w & 3, head = 4 * rg + r;
+        softmax_row_4w_any(pr + r * Sp, scores + (size_t)(hk * G + min(head, G - 1)) * max_seq, S,
+                           head < G, wmax + 4 * r, red + 256 * r, j, lane);
+    }
+
+    // ---- P.V chains over the ring: wave w < 8 sums row w % 4, half w / 4 ---
+    const float *prow = pr + (w & 3) * Sp;
+    float acc = 0.0f;
+    for (int c = 0; c < nslots; ++c) {
+        wait_vmcnt<NS - 3>();   // this wave's loads of slots c and c + 1 have landed
+        if (w < 8 && c > 0)
+            asm volatile("s_barrier" ::: "memory");   // reads in flight stay (see above)
+        else
+            lds_barrier();
+        issue(c + NS - 1);      // into slot c - 1's ring entry (clamped past the cache)
+        if (w < 8) {
+            const uint4 *vs = ring + (size_t)(c % NS) * kPmOcts * 128 + 64 * (w >> 2) + lane;
+            acc = po_chain_slot<kPmOcts, 128>(acc, vs, prow + c * kPmRows,
+                                              min(kPmRows, S - c * kPmRows));
+        }
+    }
+    wait_vmcnt<0>();   // no LDS load in flight when the workgroup ends
+    if (w < 8 && 4 * rg + (w & 3) < G)
+        out[(size_t)(hk * G + 4 * rg + (w & 3)) * kHd + 64 * (w >> 2) + lane] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -2663,6 +2747,18 @@ static int launch_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
         return 0;
     }
     const dim3 grid(Hkv * ((G + 3) / 4) * 2, batch);
+    // both halves per workgroup once the per-half grid needs more than one
+    // round over the CUs (32 sequences: 53.0 against 57.2 us per layer at 2304
+    // positions; 16 sequences stay per half: 31.2 against 42.7)
+    if (vc8 && (int)(grid.x * grid.y) > device_cus() && pm_smem(6, max_seq) <= 160 * 1024) {
+        const dim3 grid2(Hkv * ((G + 3) / 4), batch);
+        if (allow_dynamic_lds((const void *)attn_pv_chain_oct2_kernel<6>)) return -1;
+        hipLaunchKernelGGL(attn_pv_chain_oct2_kernel<6>, grid2, dim3(kPcThreads),
+                           pm_smem(6, max_seq), s, scores, vc8, pos, G, max_seq, out, kv8_stride,
+                           pos_stride);
+        OXB_CHECK_HIP(hipGetLastError());
+        return 0;
+    }
     if (vc8) {
         if (pc_smem(5, max_seq) <= 160 * 1024) {
             if (allow_dynamic_lds((const void *)attn_pv_chain_oct_kernel<5>)) return -1;
