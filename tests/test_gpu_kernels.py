@@ -364,10 +364,12 @@ def test_attn_decode_head_rejects_long_caches():
                         s_max=600)
 
 
+# (28, 20, 5, 3800): both halves per workgroup with its LDS nearly full;
+# (28, 20, 5, 3840): one row more than that LDS holds (the per-half kernel)
 @pytest.mark.parametrize("B,H,Hkv,S", [(2, 20, 5, 512), (16, 20, 5, 1024), (40, 16, 4, 256),
                                        (9, 8, 8, 512), (8, 16, 8, 2600), (7, 20, 5, 1001),
                                        (32, 20, 5, 2560), (3, 32, 4, 700), (12, 64, 8, 1500),
-                                       (10, 16, 8, 300)])
+                                       (10, 16, 8, 300), (28, 20, 5, 3800), (28, 20, 5, 3840)])
 def test_attn_decode_batch_bitexact(B, H, Hkv, S):
     """Batched decode attention (per-slot caches and positions): every slot
     equals the oracle."""
