@@ -92,6 +92,9 @@ SIGNATURES = {
     "oxb_norm_quant_rows": (C.c_int, [vp, vp, f32, i32, i32, vp, vp, vp, vp]),
     "oxb_quantize_rows_tiled": (C.c_int, [vp, vp, f32, i32, i32, vp, vp, vp, vp]),
     "oxb_gemm_i8": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, vp]),
+    "oxb_gemm_ws_bytes": (C.c_size_t, [i32, i32, i32]),
+    "oxb_gemm_i8_ws": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, vp, C.c_size_t,
+                                 vp]),
     "oxb_gemm_qkv": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32,
                                vp, vp]),
     "oxb_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]),

@@ -544,6 +544,150 @@ __global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void g
 }
 
 // ---------------------------------------------------------------------------
+// Split-K of the DMA-staged tiles, for deep K and too few output tiles to
+// fill the CUs (8192 x 28672 at 512 tokens: 128 tiles of 256 x 128 for 256
+// CUs).  Each tile's K stages are cut into P equal pieces, one workgroup per
+// piece (grid tiles * P, tile-major).  Every workgroup stores its int32
+// accumulators into its slot of the workspace (agent-scope stores, visible
+// to every XCD once complete), waits for them, and counts in on the tile's
+// counter; the last of the P to arrive adds the others' accumulators to its
+// own and runs the epilogue.  Integer sums do not depend on their order, so
+// the result is the unsplit kernel's bit for bit.  No workgroup waits for
+// another (no co-residency is assumed), and the last arrival puts the
+// counter back to zero, so a workspace stays ready for the next call.
+// ---------------------------------------------------------------------------
+struct SplitParams {
+    int P;           // pieces per tile
+    int tiles_f;     // feature tiles per row of token tiles
+    int *cnt;        // [tiles] arrival counters, zero between launches
+    int32_t *part;   // [tiles * P][FT * TK], slot g = workgroup g's piece
+};
+
+template <int EPI, int MF, int MT, int NWF, int NBUF>
+__global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void gemm_split_kernel(
+    GemmParams p, SplitParams sp) {
+    constexpr int NTH = 128 * NWF;
+    constexpr int NF = NWF * MF, NT = 2 * MT;
+    constexpr int FT = 32 * NF, TK = 32 * NT;
+    constexpr int WU = FT * 4, XU = TK * 16;
+    constexpr int WPT = WU / NTH, XPT = XU / NTH, LPT = WPT + XPT;
+    constexpr int NPAIR = MF * MT * 8;   // 8-byte accumulator pairs per thread
+    static_assert(WPT * NTH == WU && XPT * NTH == XU, "stage units must split evenly");
+    static_assert(NBUF >= 3 && (NBUF - 2) * LPT < 64, "vmcnt holds the loads in flight");
+    __shared__ uint4 sw[NBUF][WU];
+    __shared__ uint4 sx[NBUF][XU];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = blockIdx.x;
+    const int KC = p.K >> 6, S = p.K >> 8;
+    const int t = g / sp.P, piece = g - t * sp.P;
+    const int s0 = piece * S / sp.P, steps = (piece + 1) * S / sp.P - s0;
+    const int ftile0 = (t % sp.tiles_f) * (FT / 16), ttile0 = (t / sp.tiles_f) * (TK / 16);
+    const int ntt = (p.n_tok + 15) >> 4;
+    const int wf = (w % NWF) * MF, wt = (w / NWF) * MT;
+
+    // global sources of this thread's LDS slots i = tid + NTH*k at stage s0,
+    // as in gemm_lds_kernel
+    const uint4 *wsrc[WPT], *xsrc[XPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int cp = blk / NF, fp = blk % NF, h = u >> 5, ft = 2 * fp + ((u >> 4) & 1);
+        wsrc[k] = p.W + ((size_t)(ftile0 + ft) * KC + 2 * cp + h) * 16 + (u & 15) + (size_t)s0 * 64;
+    }
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        const int i = tid + NTH * k, u = i & 63, blk = i >> 6;
+        const int tp = blk % NT, gc = blk / NT, cp = gc & 1, gg = gc >> 1, h = u >> 5;
+        const int tt = min(ttile0 + 2 * tp + ((u >> 4) & 1), ntt - 1);
+        xsrc[k] = p.X + (size_t)tt * KC * 64 + gg * 64 + (2 * cp + h) * 16 + (u & 15) +
+                  (size_t)s0 * 256;
+    }
+    auto issue = [&](int st, int b) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) lds_dma16(wsrc[k] + (size_t)st * 64, sw[b] + NTH * k + 64 * w);
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) lds_dma16(xsrc[k] + (size_t)st * 256, sx[b] + NTH * k + 64 * w);
+    };
+    v16i acc[MF][MT];
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    // the DMA kernel's pipeline over this piece's stages
+    for (int st = 0; st < NBUF - 1; ++st)
+        if (st < steps) issue(st, st);
+    int b = 0;
+    for (int s = 0; s < steps; ++s) {
+        const int later = min(NBUF - 2, steps - 1 - s);
+        if constexpr (NBUF == 3) {
+            if (later == 1) wait_vmcnt<LPT>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= NBUF - 2) wait_vmcnt<(NBUF - 2) * LPT>();
+            else if (later == 2) wait_vmcnt<2 * LPT>();
+            else if (later == 1) wait_vmcnt<LPT>();
+            else wait_vmcnt<0>();
+        }
+        lds_barrier();
+        if (s + NBUF - 1 < steps) issue(s + NBUF - 1, b == 0 ? NBUF - 1 : b - 1);
+        gemm_mma_stage<MF, MT, NF, NT>(acc, sw[b], sx[b], wf, wt, l);
+        b = b == NBUF - 1 ? 0 : b + 1;
+    }
+
+    // hand-off: element (pair e, thread tid) of a slot holds this thread's
+    // registers 2(e%8), 2(e%8)+1 of tile (e/8/MT, e/8%MT); every piece of a
+    // tile has the same register layout
+    uint64_t *const mine = (uint64_t *)(sp.part + (size_t)g * FT * TK);
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                const uint64_t pr = (uint64_t)(uint32_t)acc[i][j][2 * v] |
+                                    ((uint64_t)(uint32_t)acc[i][j][2 * v + 1] << 32);
+                __hip_atomic_store(mine + ((i * MT + j) * 8 + v) * NTH + tid, pr, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // every thread's stores are complete; every LDS read is done
+    // the last-arrival flag, in a stage buffer word that no wave reads any
+    // more (an LDS word of its own would take the 64x64 tile's second
+    // workgroup per CU)
+    int *const s_last = (int *)&sw[0][0];
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(sp.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool fin = old == sp.P - 1;
+        if (fin) __hip_atomic_store(sp.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_last = fin;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    for (int o = t * sp.P; o < (t + 1) * sp.P; ++o) {
+        if (o == g) continue;
+        const uint64_t *src = (const uint64_t *)(sp.part + (size_t)o * FT * TK);
+        uint64_t v8[NPAIR];
+#pragma unroll
+        for (int e = 0; e < NPAIR; ++e)
+            v8[e] = __hip_atomic_load(src + (size_t)e * NTH + tid, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const uint64_t pr = v8[(i * MT + j) * 8 + v];
+                    acc[i][j][2 * v] += (int)(uint32_t)pr;
+                    acc[i][j][2 * v + 1] += (int)(uint32_t)(pr >> 32);
+                }
+    }
+    gemm_lds_epilogue<EPI, MF, MT>(p, acc, ftile0, ttile0, wf, wt, l);
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM for n_tok <= 64 (batched decode, small-M sweeps): the GEMV's
 // decomposition with MFMA inside.  A workgroup owns TF 16-row feature tiles
 // and all TT = ceil(n_tok/16) token tiles; its 4 waves split K (in 4-chunk
@@ -665,12 +809,56 @@ static int lds_launch(const GemmParams &p, hipStream_t s) {
     return 0;
 }
 
+// Split-K plan for the 256x128 DMA-staged tile: pieces per tile, 0 for none.
+// It pays where those tiles leave CUs idle and every piece keeps >= 8 stages
+// (a piece's hand-off costs about what 2-3 stages do): each tile in as many
+// equal pieces as the CUs take.  At 512 tokens, 8192 x 28672 (128 tiles in 2
+// pieces) takes 115 us against 151 for the unsplit 128x128 tiles; 2560 x
+// 6912 in 6 pieces of 4.5 stages 35 us against 22 unsplit.
+static int split_pieces(int N, int K, int n_tok) {
+    if (n_tok <= 64 || N % 256) return 0;
+    const int cus = device_cus();
+    const long tiles = (long)(N / 256) * ((n_tok + 127) / 128);
+    const long pieces = std::min<long>(cus / tiles, (K / 256) / 8);
+    if (pieces < 2 || tiles * pieces < (long)cus * 5 / 8) return 0;
+    return (int)pieces;
+}
+
+// workspace: the tiles' counters (rounded up to 256 B), then one 128 KB slot
+// of accumulators per piece
+static size_t split_ws_bytes(int N, int n_tok, int pieces) {
+    if (!pieces) return 0;
+    const size_t tiles = (size_t)(N / 256) * ((n_tok + 127) / 128);
+    return (tiles * 4 + 255) / 256 * 256 + tiles * pieces * 256 * 128 * 4;
+}
+
+template <int EPI>
+static int split_launch(const GemmParams &p, int pieces, void *ws, hipStream_t s) {
+    SplitParams sp{};
+    sp.P = pieces;
+    sp.tiles_f = p.N / 256;
+    const size_t tiles = (size_t)sp.tiles_f * ((p.n_tok + 127) / 128);
+    sp.cnt = (int *)ws;
+    sp.part = (int32_t *)((char *)ws + (tiles * 4 + 255) / 256 * 256);
+    hipLaunchKernelGGL((gemm_split_kernel<EPI, 2, 2, 4, 3>), dim3((unsigned)(tiles * pieces)),
+                       dim3(512), 0, s, p, sp);
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
 // n_tok <= 64: skinny kernel (2 feature tiles per workgroup once there are
 // 3+ token tiles and enough rows, to halve the activation re-reads); else
+// the split-K kernel when it pays and the caller's workspace holds it, else
 // the LDS-staged kernel (the 64x64 register-tiled kernel for N % 64 != 0).
 template <int EPI>
-static int gemm_launch(const GemmParams &p, void *stream) {
+static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
+                       size_t ws_bytes = 0) {
     hipStream_t s = (hipStream_t)stream;
+    if (ws) {
+        const int pieces = split_pieces(p.N, p.K, p.n_tok);
+        if (pieces && ws_bytes >= split_ws_bytes(p.N, p.n_tok, pieces))
+            return split_launch<EPI>(p, pieces, ws, s);
+    }
     if (p.n_tok <= 64) {
         const int tt = (p.n_tok + 15) >> 4;
         const bool two = tt >= 3 && p.N % 32 == 0 && p.N / 32 >= 256;
@@ -709,9 +897,22 @@ static int gemm_launch(const GemmParams &p, void *stream) {
     return 0;
 }
 
+extern "C" size_t oxb_gemm_ws_bytes(int N, int K, int n_tok) {
+    if (N <= 0 || K <= 0 || n_tok <= 0) return 0;
+    return split_ws_bytes(N, n_tok, split_pieces(N, K, n_tok));
+}
+
 extern "C" int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale,
                            const int *xsum, const float *wscale, int N, int K, int n_tok,
                            float *Y, int32_t *acc_out, int epilogue, void *stream) {
+    return oxb_gemm_i8_ws(W_tiled, X, xscale, xsum, wscale, N, K, n_tok, Y, acc_out, epilogue,
+                          nullptr, 0, stream);
+}
+
+extern "C" int oxb_gemm_i8_ws(const void *W_tiled, const int8_t *X, const float *xscale,
+                              const int *xsum, const float *wscale, int N, int K, int n_tok,
+                              float *Y, int32_t *acc_out, int epilogue, void *ws, size_t ws_bytes,
+                              void *stream) {
     if (gemm_check(N, K, n_tok)) return -1;
     GemmParams p{};
     p.W = (const uint4 *)W_tiled;
@@ -725,9 +926,9 @@ extern "C" int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xs
     p.Y = Y;
     p.acc_out = acc_out;
     switch (epilogue) {
-        case GE_STORE: return gemm_launch<GE_STORE>(p, stream);
-        case GE_RESID: return gemm_launch<GE_RESID>(p, stream);
-        case GE_GATEUP: return gemm_launch<GE_GATEUP>(p, stream);
+        case GE_STORE: return gemm_launch<GE_STORE>(p, stream, ws, ws_bytes);
+        case GE_RESID: return gemm_launch<GE_RESID>(p, stream, ws, ws_bytes);
+        case GE_GATEUP: return gemm_launch<GE_GATEUP>(p, stream, ws, ws_bytes);
         default: oxb::set_error("ternary GEMM: epilogue %d unsupported here", epilogue); return -1;
     }
 }

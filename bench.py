@@ -195,13 +195,17 @@ def gemm_sweep(ops, synth, N: int, K: int, M: int, copies: int, iters: int) -> d
     Xt, sc, sm = (ops.DeviceArray.from_host(a) for a in (ht, hs, hm))
     dw = ops.DeviceArray.from_host(np.full(N, 0.016, np.float32))
     Y = ops.DeviceArray((M, N), np.float32)
+    # the split-K workspace where the shape splits (counters zero-filled)
+    wsb = L.oxb_gemm_ws_bytes(N, K, M)
+    work = ops.DeviceArray((wsb,), np.uint8, zero=True) if wsb else None
 
     def run(i):
-        ops.check(L.oxb_gemm_i8(Ws[i % copies].ptr, Xt.ptr, sc.ptr, sm.ptr, dw.ptr, N, K, M,
-                                Y.ptr, None, 0, stream), "gemm")
+        ops.check(L.oxb_gemm_i8_ws(Ws[i % copies].ptr, Xt.ptr, sc.ptr, sm.ptr, dw.ptr, N, K, M,
+                                   Y.ptr, None, 0, work.ptr if work else None, wsb, stream),
+                  "gemm")
     ms = _timed(L, stream, run, iters)
     L.oxb_stream_destroy(stream)
-    for b in Ws + [Xt, sc, sm, dw, Y]:
+    for b in Ws + [Xt, sc, sm, dw, Y] + ([work] if work else []):
         b.free()
     ops_n = 2.0 * M * N * K
     algo = N * K // 4 + M * K + 4 * M * N + 4
@@ -209,7 +213,8 @@ def gemm_sweep(ops, synth, N: int, K: int, M: int, copies: int, iters: int) -> d
     gbs = algo / (ms * 1e-3) / 1e9
     return {"N": N, "K": K, "M": M, "us": round(ms * 1e3, 2), "TOPS": round(tops, 2),
             "frac_mfma": round(tops / MFMA_I8_PEAK_TOPS, 4), "GBps": round(gbs, 1),
-            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": algo, "copies": copies}
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": algo, "copies": copies,
+            "split_k_ws_bytes": wsb}
 
 
 def prefill_block(ops, synth, M: int = 512, iters: int = 20) -> dict:
@@ -238,19 +243,23 @@ def prefill_block(ops, synth, M: int = 512, iters: int = 20) -> dict:
     sm = ops.DeviceArray((mpad,), np.int32)
     h = ops.DeviceArray((M, F), np.float32)
     y = ops.DeviceArray((M, D), np.float32)
+    # the split-K workspaces (none of the block's shapes splits at 512 tokens)
+    wb1, wb2 = L.oxb_gemm_ws_bytes(2 * F, D, M), L.oxb_gemm_ws_bytes(D, F, M)
+    work = ops.DeviceArray((max(wb1, wb2),), np.uint8, zero=True) if max(wb1, wb2) else None
+    wp = work.ptr if work else None
 
     def run(_):
         ops.check(L.oxb_quantize_rows_tiled(x.ptr, g1.ptr, 1e-5, M, D, X1.ptr, sc.ptr, sm.ptr,
                                             stream), "q1")
-        ops.check(L.oxb_gemm_i8(Wgu.ptr, X1.ptr, sc.ptr, sm.ptr, s1.ptr, 2 * F, D, M, h.ptr,
-                                None, 2, stream), "gateup")
+        ops.check(L.oxb_gemm_i8_ws(Wgu.ptr, X1.ptr, sc.ptr, sm.ptr, s1.ptr, 2 * F, D, M, h.ptr,
+                                   None, 2, wp, wb1, stream), "gateup")
         ops.check(L.oxb_quantize_rows_tiled(h.ptr, g2.ptr, 1e-5, M, F, X2.ptr, sc.ptr, sm.ptr,
                                             stream), "q2")
-        ops.check(L.oxb_gemm_i8(Wd.ptr, X2.ptr, sc.ptr, sm.ptr, s2.ptr, D, F, M, y.ptr, None, 0,
-                                stream), "down")
+        ops.check(L.oxb_gemm_i8_ws(Wd.ptr, X2.ptr, sc.ptr, sm.ptr, s2.ptr, D, F, M, y.ptr, None,
+                                   0, wp, wb2, stream), "down")
     ms = _timed(L, stream, run, iters)
     L.oxb_stream_destroy(stream)
-    for b in (Wgu, Wd, g1, g2, s1, s2, x, X1, X2, sc, sm, h, y):
+    for b in (Wgu, Wd, g1, g2, s1, s2, x, X1, X2, sc, sm, h, y) + ((work,) if work else ()):
         b.free()
     ops_n = 2.0 * M * (2 * F) * D + 2.0 * M * D * F
     tops = ops_n / (ms * 1e-3) / 1e12

@@ -133,6 +133,20 @@ int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_row
 int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
                 const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,
                 int epilogue, void *stream);
+/* The same GEMM with a workspace, which lets shapes whose output tiles leave
+ * CUs idle run split over K (stream-K: every CU takes an equal share of the
+ * tiles' 256-k stages; a tile cut between workgroups has its int32 partial
+ * sums added by the last one to finish, so the result bits are the same).
+ * oxb_gemm_ws_bytes gives the workspace a shape needs (0: the shape runs
+ * unsplit, and ws may be NULL); with a smaller or NULL workspace the call runs
+ * as oxb_gemm_i8.  The workspace's arrival counters must be zero before its
+ * first use (a zero-filled allocation) and every call leaves them zero; calls
+ * that share a workspace must not run concurrently.  No counterpart in the
+ * reference (nn/bitlinear.rs:207-247 dispatches one workgroup per tile). */
+size_t oxb_gemm_ws_bytes(int N, int K, int n_tok);
+int oxb_gemm_i8_ws(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
+                   const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,
+                   int epilogue, void *ws, size_t ws_bytes, void *stream);
 int oxb_gemm_qkv(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
                  const float *wscale, int Dq, int Dkv, int hd, int K, int n_tok, int pos0,
                  float *q_out, uint16_t *kcache, uint16_t *vcache, int max_seq,

@@ -636,6 +636,24 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
+def _tiled_rows(q, s, n, K):
+    """The oracle's int8 rows on the device in the GEMM's token-tiled layout
+    [n/16][K/256][4 planes][4 chunks][16 tokens][16 B], k = stage*256 +
+    (c//2)*128 + g*32 + (c%2)*16 + j (rows this long exceed the fused
+    quantizer, D <= 7168); a partial token tile is padded with zero rows
+    (scale 1, sum 0), as the device quantizer pads it.  Returns (X, scales,
+    sums) device arrays."""
+    n16 = (n + 15) // 16 * 16
+    qp = np.zeros((n16, K), np.int8)
+    qp[:n] = q
+    sp = np.ones(n16, np.float32)
+    sp[:n] = s
+    tiles = qp.reshape(n16 // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
+    return (ops.DeviceArray.from_host(np.ascontiguousarray(tiles).reshape(-1)),
+            ops.DeviceArray.from_host(sp),
+            ops.DeviceArray.from_host(qp.astype(np.int64).sum(axis=1).astype(np.int32)))
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("N,K,n", [(28672, 8192, 8), (28672, 8192, 64), (8192, 28672, 8),
                                    (8192, 28672, 64), (28672, 8192, 512), (8192, 28672, 512),
@@ -644,7 +662,9 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     """The ternary matmul sweep at full size: the skinny kernel (8 and 64
     tokens), the 128x128 LDS-staged or 256x128 DMA-staged kernels (512 and 4096
     tokens, 32 and 112 K stages): int32 accumulators and outputs equal the
-    oracle's."""
+    oracle's.  Where the shape splits over K with a workspace (8192 x 28672 at
+    512 tokens: 128 tiles in 2 pieces), the split runs too, twice on one
+    workspace, with the same results and its counters back at zero."""
     rng = np.random.default_rng(N + K + n)
     w = ternary(rng, N, K)
     Wn = synth.i2s_pack(w)
@@ -652,22 +672,9 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     ws = np.full(N, 0.0131, np.float32)
     q, s = O.quantize(x)
     acc_o, Y_o = O.gemm(Wn, q, ws, s, K)
-    # rows this long exceed the fused quantizer (D <= 7168): tile the oracle's
-    # int8 rows on the host into the GEMM's layout [n/16][K/256][4 planes]
-    # [4 chunks][16 tokens][16 B], k = stage*256 + (c//2)*128 + g*32 + (c%2)*16 + j;
-    # a partial token tile is padded with zero rows (scale 1, sum 0), as the
-    # device quantizer pads it
-    n16 = (n + 15) // 16 * 16
-    qp = np.zeros((n16, K), np.int8)
-    qp[:n] = q
-    sp = np.ones(n16, np.float32)
-    sp[:n] = s
-    tiles = qp.reshape(n16 // 16, 16, K // 256, 2, 4, 2, 16).transpose(0, 2, 4, 3, 5, 1, 6)
     L = ops.lib()
     Wt = ops.upload_ternary(Wn, K)
-    dX = ops.DeviceArray.from_host(np.ascontiguousarray(tiles).reshape(-1))
-    dsc = ops.DeviceArray.from_host(sp)
-    dsm = ops.DeviceArray.from_host(qp.astype(np.int64).sum(axis=1).astype(np.int32))
+    dX, dsc, dsm = _tiled_rows(q, s, n, K)
     dws = ops.DeviceArray.from_host(ws)
     Y = ops.DeviceArray((n, N), np.float32)
     acc = ops.DeviceArray((n, N), np.int32)
@@ -676,6 +683,59 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     ops.sync()
     assert np.array_equal(acc.download(), acc_o)
     assert np.array_equal(Y.download(), Y_o)
+    wsb = L.oxb_gemm_ws_bytes(N, K, n)
+    assert (wsb > 0) == ((N, K, n) == (8192, 28672, 512))
+    if wsb:
+        work = ops.DeviceArray((wsb,), np.uint8, zero=True)
+        for _ in range(2):
+            Y2 = ops.DeviceArray((n, N), np.float32)
+            acc2 = ops.DeviceArray((n, N), np.int32)
+            ops.check(L.oxb_gemm_i8_ws(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n, Y2.ptr,
+                                       acc2.ptr, 0, work.ptr, wsb, None), "gemm_i8_ws")
+            ops.sync()
+            assert np.array_equal(acc2.download(), acc_o)
+            assert np.array_equal(Y2.download(), Y_o)
+            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any()
+
+
+@pytest.mark.parametrize("n", [130, 256])
+def test_gemm_split_k_epilogues(n):
+    """The split-K kernel (5120 x 8192: 40 or 80 tiles of 256 x 128 tokens,
+    each in 4 or 3 pieces of 8 to 11 K stages) with the store, residual and
+    gate|up epilogues, a ragged token count (130: a token tile of 2 real rows)
+    included: each equals the oracle bit for bit, on two calls sharing one
+    workspace, and the arrival counters are zero after each call.  Calls
+    with a workspace too small, or none, run unsplit with the same bits."""
+    rng = np.random.default_rng(5120 + n)
+    N, K = 5120, 8192
+    L = ops.lib()
+    wsb = L.oxb_gemm_ws_bytes(N, K, n)
+    assert wsb > 0
+    w = ternary(rng, N, K)
+    Wn = synth.i2s_pack(w)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    wsc = rng.uniform(0.01, 0.02, N).astype(np.float32)
+    q, s = O.quantize(x)
+    acc_o, Y_o = O.gemm(Wn, q, wsc, s, K)
+    r = rng.standard_normal((n, N)).astype(np.float32)
+    want = {0: Y_o, 1: O.add(r, Y_o),
+            2: O.mul(O.relu2(Y_o[:, 0::2]), Y_o[:, 1::2])}
+    Wt = ops.upload_ternary(Wn, K)
+    dX, dsc, dsm = _tiled_rows(q, s, n, K)
+    dws = ops.DeviceArray.from_host(wsc)
+    work = ops.DeviceArray((wsb,), np.uint8, zero=True)
+    for epi in (0, 1, 2):
+        for call, (buf, nb) in enumerate([(work, wsb), (work, wsb), (work, wsb - 1), (None, 0)]):
+            Y = ops.DeviceArray.from_host(r) if epi == 1 else \
+                ops.DeviceArray((n, N // 2 if epi == 2 else N), np.float32)
+            acc = ops.DeviceArray((n, N), np.int32)
+            ops.check(L.oxb_gemm_i8_ws(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n, Y.ptr,
+                                       acc.ptr, epi, buf.ptr if buf else None, nb, None),
+                      "gemm_i8_ws")
+            ops.sync()
+            assert np.array_equal(acc.download(), acc_o), (epi, call)
+            assert np.array_equal(Y.download(), want[epi]), (epi, call)
+            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any(), (epi, call)
 
 
 @pytest.mark.parametrize("n", [40, 41, 130, 600])   # skinny (41: a real and a padding row share a workgroup of the quantizer), 128x64 LDS-staged, 256x128 DMA-staged
