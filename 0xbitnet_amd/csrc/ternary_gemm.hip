@@ -813,7 +813,7 @@ static int lds_launch(const GemmParams &p, hipStream_t s) {
 // It pays where those tiles leave CUs idle and every piece keeps >= 8 stages
 // (a piece's hand-off costs about what 2-3 stages do): each tile in as many
 // equal pieces as the CUs take.  At 512 tokens, 8192 x 28672 (128 tiles in 2
-// pieces) takes 115 us against 151 for the unsplit 128x128 tiles; 2560 x
+// pieces) takes 110 us against 128 for the unsplit 128x128 tiles; 2560 x
 // 6912 in 6 pieces of 4.5 stages 35 us against 22 unsplit.
 static int split_pieces(int N, int K, int n_tok) {
     if (n_tok <= 64 || N % 256) return 0;
