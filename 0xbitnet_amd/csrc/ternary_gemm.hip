@@ -654,8 +654,7 @@ __global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void g
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();   // every thread's stores are complete; every LDS read is done
     // the last-arrival flag, in a stage buffer word that no wave reads any
-    // more (an LDS word of its own would take the 64x64 tile's second
-    // workgroup per CU)
+    // more (every stage load has landed and every wave is past its MFMAs)
     int *const s_last = (int *)&sw[0][0];
     if (tid == 0) {
         const int old = __hip_atomic_fetch_add(sp.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
