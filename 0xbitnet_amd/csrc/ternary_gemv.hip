@@ -425,16 +425,20 @@ __global__ __launch_bounds__(256) void norm_quant_rows_kernel(
 // [ceil16(n_tok)/16][K/256 stages][4 planes g][4 chunks c][16 tokens][16 B],
 // the 16 B of (g, chunk kc = 4*stage + c) holding k = (kc/2)*128 + g*32 +
 // (kc%2)*16 + 0..15.  Rows past n_tok (padding to 16) are zeros with scale 1
-// and sum 0.  A workgroup takes 2 consecutive rows, one per 256-thread group
-// (each in the shaders' 256-thread order), so that its stores are 32-byte
-// runs of 2 tokens instead of one token's scattered 16-byte pieces (4 rows
-// per workgroup would need more than the 128 VGPRs of a 1024-thread wave).
-// The 8 workgroups of a 16-token tile are blockIdx values congruent mod 8,
-// which the dispatcher places on one XCD, so each 128-byte line of the tile
-// is completed in one L2: workgroup b runs row pair (b / 8) % 8 of tile
-// (b / 64) * 8 + b % 8 (grid: 64 per 8 tiles; those past the last tile exit).
+// and sum 0.  A workgroup takes kTiledRows consecutive rows, one per
+// 256-thread group (each in the shaders' 256-thread order).  One row per
+// workgroup: a row of 6912 holds 127 VGPRs per thread, so four one-row
+// workgroups fit on a CU where one two-row workgroup did (two rows made the
+// stores 32-byte runs of 2 tokens, but 2048 x 6912 took 22.0 against 17.1
+// us, 2048 x 2560 7.2 against 6.9).  The 16 / kTiledRows workgroups of a
+// 16-token tile are blockIdx values congruent mod 8, which the dispatcher
+// places on one XCD, so each 128-byte line of the tile is completed in one
+// L2: workgroup b runs row group (b / 8) % WPT of tile (b / (8 WPT)) * 8 +
+// b % 8, WPT = 16 / kTiledRows (grid: 8 WPT per 8 tiles; those past the
+// last tile exit).
 // ---------------------------------------------------------------------------
-constexpr int kTiledRows = 2;
+constexpr int kTiledRows = 1;
+constexpr int kTiledWpt = 16 / kTiledRows;   // workgroups per 16-token tile
 
 template <int NREG>   // >= D / 256 values per thread (the row's loads)
 __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
@@ -446,7 +450,8 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     int8_t *q_lds = smem + grp * dpad;
     float *red = (float *)(smem + kTiledRows * dpad) + grp * 328;
     int *wq = (int *)(red + 324);
-    const int b = blockIdx.x, tile = (b >> 6) * 8 + (b & 7), r0 = ((b >> 3) & 7) * kTiledRows;
+    const int b = blockIdx.x, tile = b / (8 * kTiledWpt) * 8 + (b & 7);
+    const int r0 = (b >> 3) % kTiledWpt * kTiledRows;
     if (tile * 16 >= n_tok) return;   // whole workgroup: past the last 16-token tile
     const int row = tile * 16 + r0 + grp;
     float scale = 1.0f;
@@ -464,7 +469,8 @@ __global__ __launch_bounds__(256 * kTiledRows) void quantize_rows_tiled_kernel(
     }
     lds_barrier();
     const int KC = D >> 6;
-    // unit i: row group i % 2, plane (i / 2) % 4, chunk i / 8
+    // unit i: row group i % kTiledRows, plane (i / kTiledRows) % 4, chunk
+    // i / (4 kTiledRows)
     for (int i = threadIdx.x; i < KC * 4 * kTiledRows; i += 256 * kTiledRows) {
         const int rr = i % kTiledRows, gp = (i / kTiledRows) & 3, kc = i / (4 * kTiledRows);
         const int src = (kc >> 1) * 128 + gp * 32 + (kc & 1) * 16;
@@ -649,7 +655,7 @@ extern "C" int oxb_quantize_rows_tiled(const float *x, const float *gamma, float
     OXB_REQUIRE(D > 0 && D % 256 == 0 && D <= 256 * kMaxNormReg,
                 "quantize_rows_tiled: D %d must be a multiple of 256 and <= %d", D, 256 * kMaxNormReg);
     OXB_REQUIRE(n_tok > 0, "quantize_rows_tiled: n_tok %d", n_tok);
-    const int grid = (n_tok + 127) / 128 * 64;   // 8 tiles of 16 tokens per 64 workgroups
+    const int grid = (n_tok + 127) / 128 * 8 * kTiledWpt;   // 8 tiles of 16 tokens per 8 WPT
     const size_t sm = (size_t)kTiledRows * (((D + 15) & ~15) + 328 * 4);
     // loads per thread: the row length's bucket (the model's 2560 and 6912 exactly)
     const int nr = D / 256;
