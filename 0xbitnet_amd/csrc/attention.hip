@@ -88,22 +88,23 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     const int s = s0 + lane;
     if (w >= G || s >= S) return;
     constexpr int HPW = G > 4 ? G / 4 : 1;   // heads per wave
-    // this lane's K row into registers; the head's q row is read as LDS
-    // broadcasts three 8-term groups ahead (scalar loads would return out of
-    // order and force full waits inside the chain); each step of the chain is
-    // one v_fma_mix (k converted from f16 inside the instruction)
-    uint4 kr16[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) kr16[i] = ks[lane][i];
+    // this lane's K row and the head's q row (LDS broadcasts) are read three
+    // 8-term groups ahead of the chain (scalar loads of q would return out of
+    // order and force full waits inside it); a ring instead of the whole K row
+    // in registers keeps the kernel near 50 VGPRs, so twice the workgroups fit
+    // on a CU; each step of the chain is one v_fma_mix (k converted from f16
+    // inside the instruction)
     const int wu = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
         const float *qg = qs + (wu + 4 * h) * kHd;
         constexpr int kAhead = 3;
         float4 qa[16], qb[16];
+        uint4 kr16[16];
         auto ld = [&](int i) {
             qa[i] = *(const float4 *)(qg + 8 * i);
             qb[i] = *(const float4 *)(qg + 8 * i + 4);
+            kr16[i] = ks[lane][i];
         };
 #pragma unroll
         for (int i = 0; i < kAhead; ++i) ld(i);
