@@ -694,15 +694,23 @@ __global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void g
 // (int32, exact) and runs the epilogue.  N/16/TF workgroups keep the chip
 // busy where the 64x64 tiling launches too few.
 // ---------------------------------------------------------------------------
-template <int EPI, int TT, int TF>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
+// SPLIT: the K stages are cut into sp.P equal pieces over blockIdx.y (long
+// rows: fewer, wider feature groups, so each group re-reads less of X); each
+// workgroup stores its summed tiles to its workspace slot and counts in on
+// its feature group's counter, and the last of the P to arrive adds the
+// other slots (int32, exact) and runs the epilogue, as gemm_split_kernel.
+template <int EPI, int TT, int TF, bool SPLIT = false>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p, SplitParams sp) {
     constexpr int NT = TF * TT;   // 16x16 tiles per wave
     __shared__ v4i red[4][NT][64];
+    __shared__ int s_last;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, q = lane >> 4;
-    const int KC = p.K >> 6, steps = KC >> 2;
+    const int KC = p.K >> 6, steps_all = KC >> 2;
+    const int P = SPLIT ? sp.P : 1, piece = SPLIT ? (int)blockIdx.y : 0;
+    const int k0 = piece * steps_all / P, steps = (piece + 1) * steps_all / P - k0;
     const int per = (steps + 3) >> 2;
-    const int s0 = min(w * per, steps), s1 = min(steps, s0 + per);
+    const int s0 = k0 + min(w * per, steps), s1 = k0 + min(steps, w * per + per);
     const int ftile0 = blockIdx.x * TF;
 
     v4i acc[TF][TT];
@@ -760,10 +768,48 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p) {
         for (int t = 0; t < TT; ++t) red[w][f * TT + t][lane] = acc[f][t];
     lds_barrier();
     const int ntok = p.n_tok;
+    if constexpr (SPLIT) {   // hand the summed tiles over; the last piece finishes
+        uint64_t *mine = (uint64_t *)(sp.part + ((size_t)blockIdx.x * P + piece) * NT * 64 * 4);
+        for (int i = w; i < NT; i += 4) {
+            v4i c = red[0][i][lane];
+#pragma unroll
+            for (int k = 1; k < 4; ++k) c += red[k][i][lane];
+            const size_t at = ((size_t)i * 64 + lane) * 2;
+            __hip_atomic_store(mine + at, (uint64_t)(uint32_t)c[0] | ((uint64_t)(uint32_t)c[1] << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(mine + at + 1, (uint64_t)(uint32_t)c[2] | ((uint64_t)(uint32_t)c[3] << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(sp.cnt + blockIdx.x, 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            const bool fin = old == P - 1;
+            if (fin) __hip_atomic_store(sp.cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = fin;
+        }
+        __syncthreads();
+        if (!s_last) return;
+    }
     for (int i = w; i < NT; i += 4) {
         v4i c = red[0][i][lane];
 #pragma unroll
         for (int k = 1; k < 4; ++k) c += red[k][i][lane];
+        if constexpr (SPLIT) {
+            for (int o = 0; o < P; ++o) {
+                if (o == piece) continue;
+                const uint64_t *src =
+                    (const uint64_t *)(sp.part + ((size_t)blockIdx.x * P + o) * NT * 64 * 4) +
+                    ((size_t)i * 64 + lane) * 2;
+                const uint64_t lo = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t hi = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                c[0] += (int)(uint32_t)lo;
+                c[1] += (int)(uint32_t)(lo >> 32);
+                c[2] += (int)(uint32_t)hi;
+                c[3] += (int)(uint32_t)(hi >> 32);
+            }
+        }
         const int f = i / TT, t = (i % TT) * 16 + r, n0 = (ftile0 + f) * 16 + 4 * q;
         const EpiTok e = epi_tok<EPI>(p, t);
         const float4 ws = *(const float4 *)(p.wscale + n0);
@@ -785,7 +831,38 @@ static int gemm_check(int N, int K, int n_tok) {
 
 template <int EPI, int TT, int TF>
 static int skinny_launch(const GemmParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, TT, TF>), dim3(p.N / (16 * TF)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, TT, TF>), dim3(p.N / (16 * TF)), dim3(256), 0, s, p,
+                       SplitParams{});
+    OXB_CHECK_HIP(hipGetLastError());
+    return 0;
+}
+
+// The skinny kernel split over K (<= 64 tokens, long rows): 4 feature tiles
+// per workgroup, each group's K in P pieces.  Workspace: the groups'
+// counters (rounded up to 256 B), then one slot of TT * 4 tiles of 16x16
+// int32 per (group, piece).
+static int skinny_split_pieces(int N, int K, int n_tok) {
+    if (n_tok > 64 || N % 64 || K < 8192) return 0;
+    const int groups = N / 64;
+    const int pieces = std::min(device_cus() / groups, K / 1024);
+    return pieces >= 2 ? pieces : 0;
+}
+
+static size_t skinny_split_ws_bytes(int N, int n_tok, int pieces) {
+    if (!pieces) return 0;
+    const size_t groups = (size_t)N / 64, tt = (n_tok + 15) / 16;
+    return (groups * 4 + 255) / 256 * 256 + groups * pieces * tt * 4 * 64 * 16;
+}
+
+template <int EPI, int TT>
+static int skinny_split_launch(const GemmParams &p, int pieces, void *ws, hipStream_t s) {
+    SplitParams sp{};
+    sp.P = pieces;
+    const size_t groups = (size_t)p.N / 64;
+    sp.cnt = (int *)ws;
+    sp.part = (int32_t *)((char *)ws + (groups * 4 + 255) / 256 * 256);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, TT, 4, true>), dim3((unsigned)groups, pieces),
+                       dim3(256), 0, s, p, sp);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
@@ -857,6 +934,15 @@ static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
         const int pieces = split_pieces(p.N, p.K, p.n_tok);
         if (pieces && ws_bytes >= split_ws_bytes(p.N, p.n_tok, pieces))
             return split_launch<EPI>(p, pieces, ws, s);
+        const int sk = skinny_split_pieces(p.N, p.K, p.n_tok);
+        if (sk && ws_bytes >= skinny_split_ws_bytes(p.N, p.n_tok, sk)) {
+            switch ((p.n_tok + 15) >> 4) {
+                case 1: return skinny_split_launch<EPI, 1>(p, sk, ws, s);
+                case 2: return skinny_split_launch<EPI, 2>(p, sk, ws, s);
+                case 3: return skinny_split_launch<EPI, 3>(p, sk, ws, s);
+                default: return skinny_split_launch<EPI, 4>(p, sk, ws, s);
+            }
+        }
     }
     if (p.n_tok <= 64) {
         const int tt = (p.n_tok + 15) >> 4;
@@ -898,7 +984,9 @@ static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
 
 extern "C" size_t oxb_gemm_ws_bytes(int N, int K, int n_tok) {
     if (N <= 0 || K <= 0 || n_tok <= 0) return 0;
-    return split_ws_bytes(N, n_tok, split_pieces(N, K, n_tok));
+    const int pieces = split_pieces(N, K, n_tok);
+    if (pieces) return split_ws_bytes(N, n_tok, pieces);
+    return skinny_split_ws_bytes(N, n_tok, skinny_split_pieces(N, K, n_tok));
 }
 
 extern "C" int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale,

@@ -133,10 +133,13 @@ int oxb_norm_quant_rows(const float *x, const float *gamma, float eps, int n_row
 int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
                 const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,
                 int epilogue, void *stream);
-/* The same GEMM with a workspace, which lets shapes whose output tiles leave
- * CUs idle run split over K (stream-K: every CU takes an equal share of the
- * tiles' 256-k stages; a tile cut between workgroups has its int32 partial
- * sums added by the last one to finish, so the result bits are the same).
+/* The same GEMM with a workspace, which lets long-K shapes run split over K:
+ * more than 64 tokens whose 256 x 128 output tiles leave CUs idle, and up to
+ * 64 tokens with K >= 8192, where the split gives each workgroup wider
+ * feature groups and so fewer re-reads of the activations.  Each tile's (or
+ * feature group's) K stages are cut into equal pieces, one workgroup each;
+ * the last piece to finish adds the others' int32 partial sums, so the
+ * result bits are the same.
  * oxb_gemm_ws_bytes gives the workspace a shape needs (0: the shape runs
  * unsplit, and ws may be NULL); with a smaller or NULL workspace the call runs
  * as oxb_gemm_i8.  The workspace's arrival counters must be zero before its

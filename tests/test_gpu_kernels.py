@@ -662,9 +662,10 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     """The ternary matmul sweep at full size: the skinny kernel (8 and 64
     tokens), the 128x128 LDS-staged or 256x128 DMA-staged kernels (512 and 4096
     tokens, 32 and 112 K stages): int32 accumulators and outputs equal the
-    oracle's.  Where the shape splits over K with a workspace (8192 x 28672 at
-    512 tokens: 128 tiles in 2 pieces), the split runs too, twice on one
-    workspace, with the same results and its counters back at zero."""
+    oracle's.  Where the shape splits over K with a workspace (8192 x 28672:
+    at 512 tokens 128 tiles in 2 pieces; at 8 and 64 tokens the skinny
+    kernel's 128 feature groups in 2 pieces), the split runs too, twice on
+    one workspace, with the same results and its counters back at zero."""
     rng = np.random.default_rng(N + K + n)
     w = ternary(rng, N, K)
     Wn = synth.i2s_pack(w)
@@ -684,7 +685,7 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
     assert np.array_equal(acc.download(), acc_o)
     assert np.array_equal(Y.download(), Y_o)
     wsb = L.oxb_gemm_ws_bytes(N, K, n)
-    assert (wsb > 0) == ((N, K, n) == (8192, 28672, 512))
+    assert (wsb > 0) == ((N, K) == (8192, 28672) and n <= 512)
     if wsb:
         work = ops.DeviceArray((wsb,), np.uint8, zero=True)
         for _ in range(2):
@@ -698,14 +699,16 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
             assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any()
 
 
-@pytest.mark.parametrize("n", [130, 256])
+@pytest.mark.parametrize("n", [130, 256, 40, 64])
 def test_gemm_split_k_epilogues(n):
-    """The split-K kernel (5120 x 8192: 40 or 80 tiles of 256 x 128 tokens,
-    each in 4 or 3 pieces of 8 to 11 K stages) with the store, residual and
-    gate|up epilogues, a ragged token count (130: a token tile of 2 real rows)
-    included: each equals the oracle bit for bit, on two calls sharing one
-    workspace, and the arrival counters are zero after each call.  Calls
-    with a workspace too small, or none, run unsplit with the same bits."""
+    """The split-K kernels on 5120 x 8192 with the store, residual and
+    gate|up epilogues: 130 and 256 tokens on the 256 x 128 tiles (40 or 80
+    tiles, each in 4 or 3 pieces of 8 to 11 K stages), 40 and 64 tokens on
+    the skinny kernel (80 feature groups of 64 rows, each in 3 pieces); ragged
+    token counts (130: a token tile of 2 real rows; 40: of 8) included.  Each
+    equals the oracle bit for bit, on two calls sharing one workspace, and
+    the arrival counters are zero after each call.  Calls with a workspace
+    too small, or none, run unsplit with the same bits."""
     rng = np.random.default_rng(5120 + n)
     N, K = 5120, 8192
     L = ops.lib()
