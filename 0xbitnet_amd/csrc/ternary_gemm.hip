@@ -983,7 +983,7 @@ static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
 }
 
 extern "C" size_t oxb_gemm_ws_bytes(int N, int K, int n_tok) {
-    if (N <= 0 || K <= 0 || n_tok <= 0) return 0;
+    if (N <= 0 || N % 32 || K <= 0 || K % 256 || n_tok <= 0) return 0;   // shapes the GEMM rejects
     const int pieces = split_pieces(N, K, n_tok);
     if (pieces) return split_ws_bytes(N, n_tok, pieces);
     return skinny_split_ws_bytes(N, n_tok, skinny_split_pieces(N, K, n_tok));

@@ -94,6 +94,8 @@ def test_operator_entry_points_check_arguments_first():
     assert _err() == "ternary GEMM: out_dim 100 must be a multiple of 32"
     assert L.oxb_gemm_i8(p, p, p, p, p, 64, 300, 4, p, None, 0, None) == -1
     assert _err() == "ternary GEMM: in_dim 300 must be a multiple of 256"
+    assert L.oxb_gemm_i8_ws(p, p, p, p, p, 64, 300, 4, p, None, 0, None, 0, None) == -1
+    assert _err() == "ternary GEMM: in_dim 300 must be a multiple of 256"
     assert L.oxb_quantize_rows_tiled(p, p, 1e-5, 4, 100, p, p, p, None) == -1
     assert _err().startswith("quantize_rows_tiled: D 100 must be a multiple of 256")
 
@@ -237,3 +239,18 @@ def test_built_kernels_have_no_private_segment():
             n += 1
             assert "ScratchSize [bytes/lane]=0" in line and "VGPRs Spill=0" in line, line
     assert n >= 20
+
+
+def test_gemm_workspace_sizes():
+    """oxb_gemm_ws_bytes (a host computation; 256 CUs assumed without a GPU):
+    the split shapes need a workspace (counters, then one int32 slot per
+    piece), every other shape and every shape the GEMM rejects none."""
+    L = nat.lib()
+    # 8192 x 28672: 128 tiles of 256 x 128 in 2 pieces at 512 tokens; the
+    # skinny kernel's 128 feature groups of 64 rows in 2 pieces at <= 64 tokens
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 512) == 512 + 128 * 2 * 256 * 128 * 4
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 8) == 512 + 128 * 2 * 1 * 4 * 64 * 16
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 64) == 512 + 128 * 2 * 4 * 4 * 64 * 16
+    for shape in [(2560, 6912, 512), (13824, 2560, 512), (28672, 8192, 64), (8192, 28672, 4096),
+                  (2560, 2560, 8), (0, 256, 4), (100, 8192, 4), (64, 8200, 4), (8192, 28672, 0)]:
+        assert L.oxb_gemm_ws_bytes(*shape) == 0, shape
