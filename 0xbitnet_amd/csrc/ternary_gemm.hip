@@ -922,10 +922,12 @@ static int split_launch(const GemmParams &p, int pieces, void *ws, hipStream_t s
     return 0;
 }
 
-// n_tok <= 64: skinny kernel (2 feature tiles per workgroup once there are
-// 3+ token tiles and enough rows, to halve the activation re-reads); else
-// the split-K kernel when it pays and the caller's workspace holds it, else
-// the LDS-staged kernel (the 64x64 register-tiled kernel for N % 64 != 0).
+// With a workspace that holds it, a split over K where it pays (the 256x128
+// tiles above 64 tokens, the skinny kernel's 64-row groups at up to 64).
+// Otherwise n_tok <= 64: skinny kernel (2 feature tiles per workgroup once
+// there are 3+ token tiles and enough rows, to halve the activation
+// re-reads); else the LDS-staged kernel (the 64x64 register-tiled kernel for
+// N % 64 != 0).
 template <int EPI>
 static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
                        size_t ws_bytes = 0) {
