@@ -741,6 +741,57 @@ def test_gemm_split_k_epilogues(n):
             assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any(), (epi, call)
 
 
+@pytest.mark.parametrize("n", [512, 8])
+def test_gemm_split_k_graph_replays(n):
+    """The K splits (8192 x 28672: the 256 x 128 tiles at 512 tokens, the
+    skinny kernel at 8) captured in a graph of three calls on one workspace
+    and replayed four times, with eager calls and synchronisations between
+    the replays: every replay gives the unsplit kernel's bits (each call's
+    last arrival puts its counters back to zero, so no clearing node is
+    needed in the graph)."""
+    rng = np.random.default_rng(9000 + n)
+    N, K = 8192, 28672
+    L = ops.lib()
+    wsb = L.oxb_gemm_ws_bytes(N, K, n)
+    assert wsb > 0
+    Wn = synth.i2s_pack(ternary(rng, N, K))
+    q, s_ = O.quantize(rng.standard_normal((n, K)).astype(np.float32))
+    Wt = ops.upload_ternary(Wn, K)
+    dX, dsc, dsm = _tiled_rows(q, s_, n, K)
+    dws = ops.DeviceArray.from_host(rng.uniform(0.01, 0.02, N).astype(np.float32))
+    work = ops.DeviceArray((wsb,), np.uint8, zero=True)
+    ref = ops.DeviceArray((n, N), np.float32)
+    ops.check(L.oxb_gemm_i8(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n, ref.ptr, None, 0,
+                            None), "gemm_i8")
+    ops.sync()
+    want = ref.download()
+    outs = [ops.DeviceArray((n, N), np.float32) for _ in range(3)]
+    stream = L.oxb_stream_create()
+    ops.check(L.oxb_stream_begin_capture(stream), "capture")
+    for o in outs:
+        ops.check(L.oxb_gemm_i8_ws(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n, o.ptr, None,
+                                   0, work.ptr, wsb, stream), "gemm_i8_ws")
+    graph = L.oxb_stream_end_capture(stream)
+    assert graph
+    try:
+        for rep in range(4):
+            for o in outs:
+                ops.check(L.oxb_memset_d(o.ptr, 0, n * N * 4, stream), "clear")
+            ops.check(L.oxb_graph_launch(graph, stream), "replay")
+            ops.check(L.oxb_stream_sync(stream), "sync")
+            for o in outs:
+                assert np.array_equal(o.download(), want), rep
+            # an eager split call between the replays, on the same workspace
+            ops.check(L.oxb_gemm_i8_ws(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, n,
+                                       outs[0].ptr, None, 0, work.ptr, wsb, stream), "gemm_i8_ws")
+            ops.check(L.oxb_stream_sync(stream), "sync")
+            assert np.array_equal(outs[0].download(), want), rep
+            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any(), rep
+    finally:
+        L.oxb_graph_destroy(graph)
+        L.oxb_stream_destroy(stream)
+
+
 @pytest.mark.parametrize("n", [40, 41, 130, 600])   # skinny (41: a real and a padding row share a workgroup of the quantizer), 128x64 LDS-staged, 256x128 DMA-staged
 def test_gemm_epilogues(n):
     rng = np.random.default_rng(31 + n)
