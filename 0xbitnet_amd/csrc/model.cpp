@@ -697,12 +697,35 @@ int oxb_model::ensure_prefill(int n) {
     return 0;
 }
 
+// The workspace that lets the prefill's o_proj, gate|up and down GEMMs over n
+// tokens run split over K where that pays (e.g. the 2560 x 6912 down
+// projection over 65-384 tokens); zero-filled when it grows, and every GEMM
+// call leaves its counters zero again.
+int oxb_model::ensure_gemm_ws(int n) {
+    const int Dq = H * hd;
+    const size_t need = std::max({oxb_gemm_ws_bytes(D, Dq, n), oxb_gemm_ws_bytes(2 * F, D, n),
+                                  oxb_gemm_ws_bytes(D, F, n)});
+    if (need <= gemm_ws_bytes) return 0;
+    if (gemm_ws) {   // released once the work queued on it is done
+        M_CHECK(hipStreamSynchronize(stream));
+        dfree(gemm_ws);
+        gemm_ws = nullptr;
+        gemm_ws_bytes = 0;
+    }
+    void *w = dalloc(need);
+    if (!w) return -1;
+    M_CHECK(hipMemsetAsync(w, 0, need, stream));
+    gemm_ws = w;
+    gemm_ws_bytes = need;
+    return 0;
+}
+
 // Prefill n tokens (nn/model.rs:193-266 with n > 1): per-row norm+quantize,
 // MFMA GEMMs with fused epilogues, causal attention, then the LM head on the
 // last row (advance = n).  The target names the sequence's caches, RoPE
 // table, state block and position (the model's own, or a batch slot's).
 int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg) {
-    if (ensure_prefill(n)) return -1;
+    if (ensure_prefill(n) || ensure_gemm_ws(n)) return -1;
     void *s = (void *)stream;
     const int Dq = H * hd, Dkv = Hkv * hd;
     M_CHECK(hipMemcpyAsync(pids, ids, (size_t)n * 4, hipMemcpyHostToDevice, stream));
@@ -723,17 +746,20 @@ int oxb_model::enqueue_prefill_to(const int32_t *ids, int n, const SeqTarget &tg
                                        H, Hkv, hd, tg.max_seq, pf_ws, pf_ws_bytes, pattn, s))
             return -1;
         if (oxb_quantize_rows_tiled(pattn, L.attn_sub, 1e-5f, n, Dq, pX, pscale, psum, s)) return -1;
-        if (oxb_gemm_i8(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1, s))
+        if (oxb_gemm_i8_ws(L.wo, (const int8_t *)pX, pscale, psum, L.so, D, Dq, n, px, nullptr, 1,
+                           gemm_ws, gemm_ws_bytes, s))
             return -1;
         if (oxb_quantize_rows_tiled(px, L.ffn_norm, eps, n, D, pX, pscale, psum, s)) return -1;
         if (!relu2) {
             set_error("unsupported activation: SiLU gate (arch %s)", arch.c_str());
             return -1;
         }
-        if (oxb_gemm_i8(L.wgu, (const int8_t *)pX, pscale, psum, L.sgu, 2 * F, D, n, ph, nullptr, 2, s))
+        if (oxb_gemm_i8_ws(L.wgu, (const int8_t *)pX, pscale, psum, L.sgu, 2 * F, D, n, ph, nullptr,
+                           2, gemm_ws, gemm_ws_bytes, s))
             return -1;
         if (oxb_quantize_rows_tiled(ph, L.ffn_sub, 1e-5f, n, F, pX, pscale, psum, s)) return -1;
-        if (oxb_gemm_i8(L.wd, (const int8_t *)pX, pscale, psum, L.sd, D, F, n, px, nullptr, 1, s))
+        if (oxb_gemm_i8_ws(L.wd, (const int8_t *)pX, pscale, psum, L.sd, D, F, n, px, nullptr, 1,
+                           gemm_ws, gemm_ws_bytes, s))
             return -1;
     }
     return oxb_lm_head_argmax(px + (size_t)(n - 1) * D, final_norm, eps, embed_lm, V, D, logits,

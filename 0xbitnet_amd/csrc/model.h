@@ -48,6 +48,10 @@ struct oxb_model {
     int pf_cap = 0;
     void *pf_ws = nullptr;   // prefill attention's K / V copies (sized at load)
     size_t pf_ws_bytes = 0;
+    // the prefill GEMMs' split-K workspace (grown to the largest need met so
+    // far; its arrival counters are zero between calls)
+    void *gemm_ws = nullptr;
+    size_t gemm_ws_bytes = 0;
     float *px = nullptr, *pq = nullptr, *pattn = nullptr, *ph = nullptr, *pscale = nullptr;
     void *pX = nullptr;
     int *psum = nullptr, *pids = nullptr;
@@ -100,6 +104,7 @@ struct oxb_model {
     int enqueue_decode_step(AttnForm attn, bool sample);
     int enqueue_sample();   // the sampler over logits (state, history, draws)
     int ensure_prefill(int n);
+    int ensure_gemm_ws(int n);
     // one sequence's caches ([L][Hkv][max_seq][hd] each), RoPE table, state
     // block, token history and position
     struct SeqTarget {

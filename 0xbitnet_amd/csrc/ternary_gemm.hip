@@ -563,6 +563,13 @@ struct SplitParams {
     int32_t *part;   // [tiles * P][FT * TK], slot g = workgroup g's piece
 };
 
+// Every split form keeps its arrival counters in one fixed area at the start
+// of the workspace and its slots after it, so one workspace can serve calls of
+// any shapes in turn: a call leaves every counter it used at zero, and no
+// form's slots overlap another form's counters.
+constexpr int kSplitCounters = 4096;
+constexpr size_t kSplitCounterBytes = kSplitCounters * sizeof(int);
+
 template <int EPI, int MF, int MT, int NWF, int NBUF>
 __global__ __launch_bounds__(128 * NWF, dma_occupancy(MF, MT, NWF, NBUF)) void gemm_split_kernel(
     GemmParams p, SplitParams sp) {
@@ -838,11 +845,10 @@ static int skinny_launch(const GemmParams &p, hipStream_t s) {
 }
 
 // The skinny kernel split over K (<= 64 tokens, long rows): 4 feature tiles
-// per workgroup, each group's K in P pieces.  Workspace: the groups'
-// counters (rounded up to 256 B), then one slot of TT * 4 tiles of 16x16
-// int32 per (group, piece).
+// per workgroup, each group's K in P pieces.  Workspace: the counter area,
+// then one slot of TT * 4 tiles of 16x16 int32 per (group, piece).
 static int skinny_split_pieces(int N, int K, int n_tok) {
-    if (n_tok > 64 || N % 64 || K < 8192) return 0;
+    if (n_tok > 64 || N % 64 || K < 8192 || N / 64 > kSplitCounters) return 0;
     const int groups = N / 64;
     const int pieces = std::min(device_cus() / groups, K / 1024);
     return pieces >= 2 ? pieces : 0;
@@ -851,7 +857,7 @@ static int skinny_split_pieces(int N, int K, int n_tok) {
 static size_t skinny_split_ws_bytes(int N, int n_tok, int pieces) {
     if (!pieces) return 0;
     const size_t groups = (size_t)N / 64, tt = (n_tok + 15) / 16;
-    return (groups * 4 + 255) / 256 * 256 + groups * pieces * tt * 4 * 64 * 16;
+    return kSplitCounterBytes + groups * pieces * tt * 4 * 64 * 16;
 }
 
 template <int EPI, int TT>
@@ -860,7 +866,7 @@ static int skinny_split_launch(const GemmParams &p, int pieces, void *ws, hipStr
     sp.P = pieces;
     const size_t groups = (size_t)p.N / 64;
     sp.cnt = (int *)ws;
-    sp.part = (int32_t *)((char *)ws + (groups * 4 + 255) / 256 * 256);
+    sp.part = (int32_t *)((char *)ws + kSplitCounterBytes);
     hipLaunchKernelGGL((gemm_skinny_kernel<EPI, TT, 4, true>), dim3((unsigned)groups, pieces),
                        dim3(256), 0, s, p, sp);
     OXB_CHECK_HIP(hipGetLastError());
@@ -885,57 +891,81 @@ static int lds_launch(const GemmParams &p, hipStream_t s) {
     return 0;
 }
 
-// Split-K plan for the 256x128 DMA-staged tile: pieces per tile, 0 for none.
-// It pays where those tiles leave CUs idle and every piece keeps >= 8 stages
-// (a piece's hand-off costs about what 2-3 stages do): each tile in as many
-// equal pieces as the CUs take.  At 512 tokens, 8192 x 28672 (128 tiles in 2
-// pieces) takes 110 us against 128 for the unsplit 128x128 tiles; 2560 x
-// 6912 in 6 pieces of 4.5 stages 35 us against 22 unsplit.
+// Split-K plans: pieces per tile, 0 for none.  Each tile's K stages in P
+// equal pieces, one workgroup each; a piece's hand-off costs about what 2-3
+// stages do.  Measured on 256 CUs (graphs of 30 calls, alternated with the
+// unsplit kernel in one process):
+// - 64x64 tiles (> 64 tokens; tiles * P up to two workgroups per CU, pieces
+//   of >= 9 stages), tried first: 2560 x 6912 at 65 / 128 / 256 / 384
+//   tokens 16.4 / 16.6 / 17.0 / 17.0 -> 11.3 / 11.5 / 12.5 / 15.3 us;
+//   5120 x 8192 at 65 / 128 19.3 / 19.4 -> 13.4 / 13.8; 8192 x 28672 at
+//   65 / 128 60.5 / 60.9 -> 41.2 / 43.8.
+// - 256x128 DMA-staged tiles where they leave CUs idle, the pieces still
+//   fill 5/8 of them and keep >= 14 stages: 8192 x 28672 at 256 / 512
+//   tokens 77.8 / 126.6 -> 72.2 / 107.8 us.  Shallower pieces lost or broke
+//   even: 2560 x 6912 at 768 / 1536 tokens 21.6 / 37.0 unsplit against
+//   31.3 / 38.7 in pieces of 9 / 13.5 stages, 5120 x 8192 at 256 tokens
+//   22.8 against 33.4 in pieces of 8.
+static int split64_pieces(int N, int K, int n_tok) {
+    if (n_tok <= 64 || N % 64) return 0;
+    const int cus = device_cus();
+    const long tiles = (long)(N / 64) * ((n_tok + 63) / 64);
+    if (tiles > kSplitCounters) return 0;
+    const long pieces = std::min<long>(2L * cus / tiles, (K / 256) / 9);
+    return pieces >= 2 ? (int)pieces : 0;
+}
+
 static int split_pieces(int N, int K, int n_tok) {
     if (n_tok <= 64 || N % 256) return 0;
     const int cus = device_cus();
     const long tiles = (long)(N / 256) * ((n_tok + 127) / 128);
-    const long pieces = std::min<long>(cus / tiles, (K / 256) / 8);
+    if (tiles > kSplitCounters) return 0;
+    const long pieces = std::min<long>(cus / tiles, (K / 256) / 14);
     if (pieces < 2 || tiles * pieces < (long)cus * 5 / 8) return 0;
     return (int)pieces;
 }
 
-// workspace: the tiles' counters (rounded up to 256 B), then one 128 KB slot
-// of accumulators per piece
-static size_t split_ws_bytes(int N, int n_tok, int pieces) {
+// workspace: the counter area, then one slot of int32 accumulators (FT x TK)
+// per workgroup
+template <int FT, int TK>
+static size_t tile_split_ws_bytes(int N, int n_tok, int pieces) {
     if (!pieces) return 0;
-    const size_t tiles = (size_t)(N / 256) * ((n_tok + 127) / 128);
-    return (tiles * 4 + 255) / 256 * 256 + tiles * pieces * 256 * 128 * 4;
+    const size_t tiles = (size_t)(N / FT) * ((n_tok + TK - 1) / TK);
+    return kSplitCounterBytes + tiles * pieces * FT * TK * 4;
 }
 
-template <int EPI>
-static int split_launch(const GemmParams &p, int pieces, void *ws, hipStream_t s) {
+template <int EPI, int MF, int MT, int NWF, int NBUF>
+static int tile_split_launch(const GemmParams &p, int pieces, void *ws, hipStream_t s) {
+    constexpr int FT = 32 * MF * NWF, TK = 64 * MT;
     SplitParams sp{};
     sp.P = pieces;
-    sp.tiles_f = p.N / 256;
-    const size_t tiles = (size_t)sp.tiles_f * ((p.n_tok + 127) / 128);
+    sp.tiles_f = p.N / FT;
+    const size_t tiles = (size_t)sp.tiles_f * ((p.n_tok + TK - 1) / TK);
     sp.cnt = (int *)ws;
-    sp.part = (int32_t *)((char *)ws + (tiles * 4 + 255) / 256 * 256);
-    hipLaunchKernelGGL((gemm_split_kernel<EPI, 2, 2, 4, 3>), dim3((unsigned)(tiles * pieces)),
-                       dim3(512), 0, s, p, sp);
+    sp.part = (int32_t *)((char *)ws + kSplitCounterBytes);
+    hipLaunchKernelGGL((gemm_split_kernel<EPI, MF, MT, NWF, NBUF>), dim3((unsigned)(tiles * pieces)),
+                       dim3(128 * NWF), 0, s, p, sp);
     OXB_CHECK_HIP(hipGetLastError());
     return 0;
 }
 
-// With a workspace that holds it, a split over K where it pays (the 256x128
-// tiles above 64 tokens, the skinny kernel's 64-row groups at up to 64).
-// Otherwise n_tok <= 64: skinny kernel (2 feature tiles per workgroup once
-// there are 3+ token tiles and enough rows, to halve the activation
-// re-reads); else the LDS-staged kernel (the 64x64 register-tiled kernel for
-// N % 64 != 0).
+// With a workspace that holds it, a split over K where it pays (the 64x64
+// or 256x128 tiles above 64 tokens, the skinny kernel's 64-row groups at up
+// to 64).  Otherwise n_tok <= 64: skinny kernel (2 feature tiles per
+// workgroup once there are 3+ token tiles and enough rows, to halve the
+// activation re-reads); else the LDS-staged kernel (the 64x64
+// register-tiled kernel for N % 64 != 0).
 template <int EPI>
 static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
                        size_t ws_bytes = 0) {
     hipStream_t s = (hipStream_t)stream;
     if (ws) {
+        const int p64 = split64_pieces(p.N, p.K, p.n_tok);
+        if (p64 && ws_bytes >= tile_split_ws_bytes<64, 64>(p.N, p.n_tok, p64))
+            return tile_split_launch<EPI, 1, 1, 2, 4>(p, p64, ws, s);
         const int pieces = split_pieces(p.N, p.K, p.n_tok);
-        if (pieces && ws_bytes >= split_ws_bytes(p.N, p.n_tok, pieces))
-            return split_launch<EPI>(p, pieces, ws, s);
+        if (pieces && ws_bytes >= tile_split_ws_bytes<256, 128>(p.N, p.n_tok, pieces))
+            return tile_split_launch<EPI, 2, 2, 4, 3>(p, pieces, ws, s);
         const int sk = skinny_split_pieces(p.N, p.K, p.n_tok);
         if (sk && ws_bytes >= skinny_split_ws_bytes(p.N, p.n_tok, sk)) {
             switch ((p.n_tok + 15) >> 4) {
@@ -986,8 +1016,10 @@ static int gemm_launch(const GemmParams &p, void *stream, void *ws = nullptr,
 
 extern "C" size_t oxb_gemm_ws_bytes(int N, int K, int n_tok) {
     if (N <= 0 || N % 32 || K <= 0 || K % 256 || n_tok <= 0) return 0;   // shapes the GEMM rejects
+    const int p64 = split64_pieces(N, K, n_tok);
+    if (p64) return tile_split_ws_bytes<64, 64>(N, n_tok, p64);
     const int pieces = split_pieces(N, K, n_tok);
-    if (pieces) return split_ws_bytes(N, n_tok, pieces);
+    if (pieces) return tile_split_ws_bytes<256, 128>(N, n_tok, pieces);
     return skinny_split_ws_bytes(N, n_tok, skinny_split_pieces(N, K, n_tok));
 }
 

@@ -134,7 +134,8 @@ int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale, const
                 const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,
                 int epilogue, void *stream);
 /* The same GEMM with a workspace, which lets long-K shapes run split over K:
- * more than 64 tokens whose 256 x 128 output tiles leave CUs idle, and up to
+ * more than 64 tokens whose 64 x 64 or 256 x 128 output tiles leave CUs idle
+ * (e.g. a 2560 x 6912 down projection over 65-384 prompt tokens), and up to
  * 64 tokens with K >= 8192, where the split gives each workgroup wider
  * feature groups and so fewer re-reads of the activations.  Each tile's (or
  * feature group's) K stages are cut into equal pieces, one workgroup each;
@@ -142,10 +143,12 @@ int oxb_gemm_i8(const void *W_tiled, const int8_t *X, const float *xscale, const
  * result bits are the same.
  * oxb_gemm_ws_bytes gives the workspace a shape needs (0: the shape runs
  * unsplit, and ws may be NULL); with a smaller or NULL workspace the call runs
- * as oxb_gemm_i8.  The workspace's arrival counters must be zero before its
- * first use (a zero-filled allocation) and every call leaves them zero; calls
- * that share a workspace must not run concurrently.  No counterpart in the
- * reference (nn/bitlinear.rs:207-247 dispatches one workgroup per tile). */
+ * as oxb_gemm_i8.  The workspace starts with a fixed 16 KB area of arrival
+ * counters, which must be zero before its first use (a zero-filled
+ * allocation); every call leaves them zero, so one workspace of the largest
+ * size needed serves calls of any shapes in turn.  Calls that share a
+ * workspace must not run concurrently.  No counterpart in the reference
+ * (nn/bitlinear.rs:207-247 dispatches one workgroup per tile). */
 size_t oxb_gemm_ws_bytes(int N, int K, int n_tok);
 int oxb_gemm_i8_ws(const void *W_tiled, const int8_t *X, const float *xscale, const int *xsum,
                    const float *wscale, int N, int K, int n_tok, float *Y, int32_t *acc_out,

@@ -243,14 +243,26 @@ def test_built_kernels_have_no_private_segment():
 
 def test_gemm_workspace_sizes():
     """oxb_gemm_ws_bytes (a host computation; 256 CUs assumed without a GPU):
-    the split shapes need a workspace (counters, then one int32 slot per
-    piece), every other shape and every shape the GEMM rejects none."""
+    the split shapes need a workspace (the 16 KB counter area, then one int32
+    slot per piece), every other shape and every shape the GEMM rejects none."""
     L = nat.lib()
-    # 8192 x 28672: 128 tiles of 256 x 128 in 2 pieces at 512 tokens; the
-    # skinny kernel's 128 feature groups of 64 rows in 2 pieces at <= 64 tokens
-    assert L.oxb_gemm_ws_bytes(8192, 28672, 512) == 512 + 128 * 2 * 256 * 128 * 4
-    assert L.oxb_gemm_ws_bytes(8192, 28672, 8) == 512 + 128 * 2 * 1 * 4 * 64 * 16
-    assert L.oxb_gemm_ws_bytes(8192, 28672, 64) == 512 + 128 * 2 * 4 * 4 * 64 * 16
-    for shape in [(2560, 6912, 512), (13824, 2560, 512), (28672, 8192, 64), (8192, 28672, 4096),
-                  (2560, 2560, 8), (0, 256, 4), (100, 8192, 4), (64, 8200, 4), (8192, 28672, 0)]:
+    c = 16384
+    # 8192 x 28672: 128 tiles of 256 x 128 in 2 pieces at 512 tokens, 64 in 4
+    # at 256; the skinny kernel's 128 feature groups of 64 rows in 2 pieces at
+    # <= 64 tokens; 256 tiles of 64 x 64 in 2 pieces at 65 tokens
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 512) == c + 128 * 2 * 256 * 128 * 4
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 256) == c + 64 * 4 * 256 * 128 * 4
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 8) == c + 128 * 2 * 1 * 4 * 64 * 16
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 64) == c + 128 * 2 * 4 * 4 * 64 * 16
+    assert L.oxb_gemm_ws_bytes(8192, 28672, 65) == c + 256 * 2 * 64 * 64 * 4
+    # the 2B down projection: 80 tiles of 64 x 64 in 3 pieces (9 stages) at
+    # 65-128 tokens, 160 in 3 at 256, 240 in 2 at 384; none from 448 tokens
+    assert L.oxb_gemm_ws_bytes(2560, 6912, 65) == c + 80 * 3 * 64 * 64 * 4
+    assert L.oxb_gemm_ws_bytes(2560, 6912, 128) == c + 80 * 3 * 64 * 64 * 4
+    assert L.oxb_gemm_ws_bytes(2560, 6912, 256) == c + 160 * 3 * 64 * 64 * 4
+    assert L.oxb_gemm_ws_bytes(2560, 6912, 384) == c + 240 * 2 * 64 * 64 * 4
+    for shape in [(2560, 6912, 448), (2560, 6912, 512), (2560, 6912, 1536), (2560, 2560, 128),
+                  (13824, 2560, 128), (13824, 2560, 512), (28672, 8192, 64), (5120, 8192, 256),
+                  (8192, 28672, 4096), (2560, 2560, 8), (0, 256, 4), (100, 8192, 4),
+                  (64, 8200, 4), (8192, 28672, 0)]:
         assert L.oxb_gemm_ws_bytes(*shape) == 0, shape

@@ -636,6 +636,10 @@ def test_gemm_mfma_bitexact(N, K, n):
     assert np.array_equal(Y, Y_o)
 
 
+# the split GEMMs' arrival counters: a fixed area at the start of a workspace
+CNT_BYTES = 16384
+
+
 def _tiled_rows(q, s, n, K):
     """The oracle's int8 rows on the device in the GEMM's token-tiled layout
     [n/16][K/256][4 planes][4 chunks][16 tokens][16 B], k = stage*256 +
@@ -696,19 +700,19 @@ def test_gemm_sweep_shapes_bitexact(N, K, n):
             ops.sync()
             assert np.array_equal(acc2.download(), acc_o)
             assert np.array_equal(Y2.download(), Y_o)
-            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any()
+            assert not np.frombuffer(work.download()[:CNT_BYTES].tobytes(), np.int32).any()
 
 
-@pytest.mark.parametrize("n", [130, 256, 40, 64])
+@pytest.mark.parametrize("n", [130, 512, 40, 64])
 def test_gemm_split_k_epilogues(n):
     """The split-K kernels on 5120 x 8192 with the store, residual and
-    gate|up epilogues: 130 and 256 tokens on the 256 x 128 tiles (40 or 80
-    tiles, each in 4 or 3 pieces of 8 to 11 K stages), 40 and 64 tokens on
-    the skinny kernel (80 feature groups of 64 rows, each in 3 pieces); ragged
-    token counts (130: a token tile of 2 real rows; 40: of 8) included.  Each
-    equals the oracle bit for bit, on two calls sharing one workspace, and
-    the arrival counters are zero after each call.  Calls with a workspace
-    too small, or none, run unsplit with the same bits."""
+    gate|up epilogues: 130 tokens on 64 x 64 tiles (240 tiles in 2 pieces of
+    16 K stages), 512 on the 256 x 128 tiles (80 tiles in 2 pieces), 40 and
+    64 tokens on the skinny kernel (80 feature groups of 64 rows, each in 3
+    pieces); ragged token counts (130: a token tile of 2 real rows; 40: of 8)
+    included.  Each equals the oracle bit for bit, on two calls sharing one
+    workspace, and the arrival counters are zero after each call.  Calls with
+    a workspace too small, or none, run unsplit with the same bits."""
     rng = np.random.default_rng(5120 + n)
     N, K = 5120, 8192
     L = ops.lib()
@@ -738,13 +742,14 @@ def test_gemm_split_k_epilogues(n):
             ops.sync()
             assert np.array_equal(acc.download(), acc_o), (epi, call)
             assert np.array_equal(Y.download(), want[epi]), (epi, call)
-            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any(), (epi, call)
+            assert not np.frombuffer(work.download()[:CNT_BYTES].tobytes(), np.int32).any(), (epi, call)
 
 
-@pytest.mark.parametrize("n", [512, 8])
+@pytest.mark.parametrize("n", [512, 65, 8])
 def test_gemm_split_k_graph_replays(n):
     """The K splits (8192 x 28672: the 256 x 128 tiles at 512 tokens, the
-    skinny kernel at 8) captured in a graph of three calls on one workspace
+    64 x 64 tiles at 65, the skinny kernel at 8) captured in a graph of three
+    calls on one workspace
     and replayed four times, with eager calls and synchronisations between
     the replays: every replay gives the unsplit kernel's bits (each call's
     last arrival puts its counters back to zero, so no clearing node is
@@ -786,10 +791,43 @@ def test_gemm_split_k_graph_replays(n):
                                        outs[0].ptr, None, 0, work.ptr, wsb, stream), "gemm_i8_ws")
             ops.check(L.oxb_stream_sync(stream), "sync")
             assert np.array_equal(outs[0].download(), want), rep
-            assert not np.frombuffer(work.download()[:256].tobytes(), np.int32).any(), rep
+            assert not np.frombuffer(work.download()[:CNT_BYTES].tobytes(), np.int32).any(), rep
     finally:
         L.oxb_graph_destroy(graph)
         L.oxb_stream_destroy(stream)
+
+
+def test_gemm_split_k_forms_share_a_workspace():
+    """One workspace serving the three split forms in turn (5120 x 8192: 512
+    tokens on 256 x 128 tiles, 130 on 64 x 64 tiles, 40 on the skinny kernel,
+    then again in another order): every form keeps its arrival counters in
+    the same fixed area, so no form reads another's leftover partial sums as
+    counters.  Every call equals the oracle's rows bit for bit."""
+    rng = np.random.default_rng(4242)
+    N, K, n = 5120, 8192, 512
+    L = ops.lib()
+    Wn = synth.i2s_pack(ternary(rng, N, K))
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    wsc = rng.uniform(0.01, 0.02, N).astype(np.float32)
+    q, s = O.quantize(x)
+    acc_o, Y_o = O.gemm(Wn, q, wsc, s, K)
+    Wt = ops.upload_ternary(Wn, K)
+    dws = ops.DeviceArray.from_host(wsc)
+    rows = (512, 130, 40, 130, 512, 40)
+    sizes = [L.oxb_gemm_ws_bytes(N, K, m) for m in rows]
+    assert all(sizes)
+    work = ops.DeviceArray((max(sizes),), np.uint8, zero=True)
+    inputs = {m: _tiled_rows(q[:m], s[:m], m, K) for m in set(rows)}
+    for i, m in enumerate(rows):
+        dX, dsc, dsm = inputs[m]
+        Y = ops.DeviceArray((m, N), np.float32)
+        acc = ops.DeviceArray((m, N), np.int32)
+        ops.check(L.oxb_gemm_i8_ws(Wt.ptr, dX.ptr, dsc.ptr, dsm.ptr, dws.ptr, N, K, m, Y.ptr,
+                                   acc.ptr, 0, work.ptr, max(sizes), None), "gemm_i8_ws")
+        ops.sync()
+        assert np.array_equal(acc.download(), acc_o[:m]), (i, m)
+        assert np.array_equal(Y.download(), Y_o[:m]), (i, m)
+        assert not np.frombuffer(work.download()[:CNT_BYTES].tobytes(), np.int32).any(), (i, m)
 
 
 @pytest.mark.parametrize("n", [40, 41, 130, 600])   # skinny (41: a real and a padding row share a workgroup of the quantizer), 128x64 LDS-staged, 256x128 DMA-staged
