@@ -152,7 +152,8 @@ __device__ inline void load_row_exact(const float *__restrict__ x, const float *
     }
 }
 
-// NREG: strided f32 values per thread in the prologue (ceil(K/256));
+// NREG: strided f32 values per thread in the prologue (ceil(K/256)); for the
+// streamed int8 rows, the activation row's 16-byte groups per thread;
 // PF: 16-byte weight chunks per lane per batch.
 // Waves per SIMD the register budget must allow: 4 (<= 128 VGPRs) for the
 // one-batch shapes, so that e.g. 864 workgroups of a 13824-row GEMV are all
@@ -226,7 +227,24 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     };
     uint4 A[TT][PF];
     [[maybe_unused]] uint4 B[TT][PF];
+    // streamed int8 rows: the activation row's loads go out first, all at
+    // once, then two weight batches; its LDS writes then wait for those
+    // loads only, not for the weights behind them (a copy loop after the
+    // first batch waited for that batch from HBM, then for each further
+    // group in turn, before the second batch went out: 8192 x 28672 /
+    // 28672 x 8192 / 2560 x 6912 took 11.8 / 12.1 / 3.95 us, now 11.4 /
+    // 11.4 / 3.53)
+    constexpr int XU = STREAM && PRO == PRO_INT8 ? NREG : 1;
+    [[maybe_unused]] u32x4_t xr[XU];
+    if constexpr (STREAM && PRO == PRO_INT8) {
+#pragma unroll
+        for (int u = 0; u < XU; ++u)   // clamped: the ragged group re-reads the row's last 16 B
+            xr[u] = ((const u32x4_t *)p.xq)[min(tid + u * 64 * NW, (K >> 4) - 1)];
+    }
     load_batch(A, 0);
+    if constexpr (STREAM && PRO == PRO_INT8) {
+        if (nb > 1) load_batch(B, 1);
+    }
     // RoPE pair of this thread's row at the position (q and k rows), issued
     // as soon as the position is back; clamped so the load stays in the table
     [[maybe_unused]] float2 cs = make_float2(1.0f, 0.0f);
@@ -240,8 +258,16 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     float in_scale;
     int xsum = 0;
     if constexpr (PRO == PRO_INT8) {
-        for (int i = tid; i < (K >> 4); i += 64 * NW)
-            ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
+        if constexpr (STREAM) {
+#pragma unroll
+            for (int u = 0; u < XU; ++u) {
+                const int i = tid + u * 64 * NW;
+                if (i < (K >> 4)) ((u32x4_t *)xq_lds)[i] = xr[u];
+            }
+        } else {
+            for (int i = tid; i < (K >> 4); i += 64 * NW)
+                ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
+        }
         in_scale = p.xscale[0];
         xsum = p.xsum[0];
         lds_barrier();
@@ -317,6 +343,20 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     };
     if constexpr (!STREAM) {   // the launcher picks one batch only when it covers the range
         mac_batch(A, 0);
+    } else if constexpr (PRO == PRO_INT8) {   // B already holds batch 1
+        int b = 0;
+        for (; b + 2 < nb; b += 2) {
+            mac_batch(A, b);
+            load_batch(A, b + 2);
+            mac_batch(B, b + 1);
+            if (b + 3 < nb) load_batch(B, b + 3);
+        }
+        if (b + 1 < nb) {
+            mac_batch(A, b);
+            mac_batch(B, b + 1);
+        } else {
+            mac_batch(A, b);
+        }
     } else {
         int b = 0;
         for (; b + 2 < nb; b += 2) {
@@ -509,7 +549,12 @@ static int launch(const GemvParams &p, hipStream_t s) {
     if constexpr (PRO == PRO_INT8) {
         if (cpl <= 1) return launch_n<PRO, EPI, 1, 1, false>(p, s);
         if (cpl <= 3) return launch_n<PRO, EPI, 1, 3, false>(p, s);
-        return launch_n<PRO, EPI, 1, 1, false, 1, 8, true>(p, s);
+        // NREG: the activation row's 16-byte groups per thread (512 threads)
+        const int xu = ((p.K >> 4) + 511) / 512;
+        if (xu <= 1) return launch_n<PRO, EPI, 1, 1, false, 1, 8, true>(p, s);
+        if (xu <= 2) return launch_n<PRO, EPI, 2, 1, false, 1, 8, true>(p, s);
+        if (xu <= 4) return launch_n<PRO, EPI, 4, 1, false, 1, 8, true>(p, s);
+        return launch_n<PRO, EPI, 8, 1, false, 1, 8, true>(p, s);
     } else {
         if (p.K <= 1024) return launch_n<PRO, EPI, 4, 1, false>(p, s);
         if (p.K == 2560) {
