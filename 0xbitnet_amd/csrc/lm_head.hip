@@ -191,11 +191,47 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p, const float2 *
         __builtin_amdgcn_sched_barrier(0);
     };
     uint4 A[HQ], B[HQ];
+    // One row: its values, pairs and gamma pairs are loaded first, then the
+    // first two weight batches, so the norm waits for the row only (not for
+    // the weights queued behind it) and both batches stay in flight across
+    // the barrier.  D = 512 NJ: 2 NJ strided values and NJ pairs per thread.
+    // (One pass of the 2B head 98.5 -> 98.1 us, decode 1298 -> 1300 tok/s.)
+    constexpr bool EARLY = NV == 1 && !HG;
+    [[maybe_unused]] float xr[EARLY ? 2 * NJ : 1];
+    [[maybe_unused]] float2 xp[EARLY ? NJ : 1], gp[EARLY ? NJ : 1];
+    if constexpr (EARLY) {
+#pragma unroll
+        for (int k = 0; k < 2 * NJ; ++k) xr[k] = p.x[tid + 256 * k];
+#pragma unroll
+        for (int k = 0; k < NJ; ++k) {
+            const int u = tid + 256 * k, i = u / NJ, j = u % NJ;
+            const int t = (bitrev4(i & 15) << 4) | bitrev4(i >> 4);
+            const int d0 = 2 * (t + 256 * j);
+            xp[k] = make_float2(p.x[d0], p.x[d0 + 1]);
+            gp[k] = make_float2(p.gamma[d0], p.gamma[d0 + 1]);
+        }
+    }
     if (nseq > 0) load_hg(A, 0);   // weights do not depend on the norm: start early
+    if constexpr (EARLY) {
+        if (nseq > 0) load_hg(B, 1);
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 2 * NJ; ++k) {
+            const float sq = xr[k] * xr[k];
+            ss = ss + sq;
+        }
+        const float sum = block256_tree_sum_fast(ss, red);
+        const float rms = 1.0f / sqrtf(sum / (float)D + p.eps);
+#pragma unroll
+        for (int k = 0; k < NJ; ++k) {
+            const float a0 = xp[k].x * rms, a1 = xp[k].y * rms;
+            hp[0][tid + 256 * k] = make_float2(a0 * gp[k].x, a1 * gp[k].y);
+        }
+    }
 
     // final RMSNorm (sh/rmsnorm.wgsl order) of each row straight into its pair table
 #pragma unroll 1
-    for (int v = 0; v < (HG ? 0 : NV); ++v) {
+    for (int v = 0; v < (HG || EARLY ? 0 : NV); ++v) {
         const float *x = p.x + (size_t)v * p.x_stride;
         float ss = 0.0f;
         for (int c = tid; c < D; c += 256) {
@@ -256,15 +292,25 @@ __global__ __launch_bounds__(256) void lm_head_kernel(LmParams p, const float2 *
     };
     int s = 0;
     float g0[NV], g1[NV];
-    for (; s < nseq - 2; s += 2) {
-        load_hg(B, s + 1);
-        half_groups(A, 8 * w + (s & 7), g0);
-        load_hg(A, s + 2);
-        half_groups(B, 8 * w + (s & 7) + 1, g1);
-        finish_pair(g0, g1, s);
+    if constexpr (EARLY) {   // B already holds half-group 1 (nseq is a multiple of 8)
+        for (; s < nseq - 2; s += 2) {
+            half_groups(A, 8 * w + (s & 7), g0);
+            load_hg(A, s + 2);
+            half_groups(B, 8 * w + (s & 7) + 1, g1);
+            load_hg(B, s + 3);
+            finish_pair(g0, g1, s);
+        }
+    } else {
+        for (; s < nseq - 2; s += 2) {
+            load_hg(B, s + 1);
+            half_groups(A, 8 * w + (s & 7), g0);
+            load_hg(A, s + 2);
+            half_groups(B, 8 * w + (s & 7) + 1, g1);
+            finish_pair(g0, g1, s);
+        }
     }
     if (nseq > 0) {   // last pair: nothing left to prefetch
-        load_hg(B, s + 1);
+        if constexpr (!EARLY) load_hg(B, s + 1);
         half_groups(A, 8 * w + (s & 7), g0);
         half_groups(B, 8 * w + (s & 7) + 1, g1);
         finish_pair(g0, g1, s);
