@@ -152,8 +152,8 @@ __device__ inline void load_row_exact(const float *__restrict__ x, const float *
     }
 }
 
-// NREG: strided f32 values per thread in the prologue (ceil(K/256)); for the
-// streamed int8 rows, the activation row's 16-byte groups per thread;
+// NREG: strided f32 values per thread in the prologue (ceil(K/256)); for int8
+// rows, the activation row's 16-byte groups per thread;
 // PF: 16-byte weight chunks per lane per batch.
 // Waves per SIMD the register budget must allow: 4 (<= 128 VGPRs) for the
 // one-batch shapes, so that e.g. 864 workgroups of a 13824-row GEMV are all
@@ -227,16 +227,18 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     };
     uint4 A[TT][PF];
     [[maybe_unused]] uint4 B[TT][PF];
-    // streamed int8 rows: the activation row's loads go out first, all at
-    // once, then two weight batches; its LDS writes then wait for those
-    // loads only, not for the weights behind them (a copy loop after the
-    // first batch waited for that batch from HBM, then for each further
-    // group in turn, before the second batch went out: 8192 x 28672 /
-    // 28672 x 8192 / 2560 x 6912 took 11.8 / 12.1 / 3.95 us, now 11.4 /
-    // 11.4 / 3.53)
-    constexpr int XU = STREAM && PRO == PRO_INT8 ? NREG : 1;
+    // int8 rows: the activation row's loads go out first, all at once,
+    // then the weights (two batches when streamed); its LDS writes then wait
+    // for those loads only, not for the weights behind them, and the barrier
+    // passes while the weights are in flight (a copy loop after the first
+    // batch waited for that batch from HBM, then for each further group in
+    // turn, before a second batch went out: 8192 x 28672 / 28672 x 8192 /
+    // 2560 x 6912 took 11.8 / 12.1 / 3.95 us, now 11.4 / 11.4 / 3.53; one
+    // batch, K = 2560: 6912 / 3840 / 13824 rows 3.15 / 2.71 / 4.00 -> 2.96 /
+    // 2.55 / 3.81 us)
+    constexpr int XU = PRO == PRO_INT8 ? NREG : 1;
     [[maybe_unused]] u32x4_t xr[XU];
-    if constexpr (STREAM && PRO == PRO_INT8) {
+    if constexpr (PRO == PRO_INT8) {
 #pragma unroll
         for (int u = 0; u < XU; ++u)   // clamped: the ragged group re-reads the row's last 16 B
             xr[u] = ((const u32x4_t *)p.xq)[min(tid + u * 64 * NW, (K >> 4) - 1)];
@@ -258,15 +260,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 2 : PF * TT <= 3 ? 4 : 2) void g
     float in_scale;
     int xsum = 0;
     if constexpr (PRO == PRO_INT8) {
-        if constexpr (STREAM) {
 #pragma unroll
-            for (int u = 0; u < XU; ++u) {
-                const int i = tid + u * 64 * NW;
-                if (i < (K >> 4)) ((u32x4_t *)xq_lds)[i] = xr[u];
-            }
-        } else {
-            for (int i = tid; i < (K >> 4); i += 64 * NW)
-                ((int4 *)xq_lds)[i] = ((const int4 *)p.xq)[i];
+        for (int u = 0; u < XU; ++u) {
+            const int i = tid + u * 64 * NW;
+            if (i < (K >> 4)) ((u32x4_t *)xq_lds)[i] = xr[u];
         }
         in_scale = p.xscale[0];
         xsum = p.xsum[0];
@@ -547,6 +544,8 @@ static int launch(const GemvParams &p, hipStream_t s) {
     const int KC = p.K >> 6;
     const int cpl = (((((KC + 3) >> 2) + 1) & ~1) + 3) >> 2;
     if constexpr (PRO == PRO_INT8) {
+        // one batch of 1 or 3 chunks per lane: K <= 3072, one activation group
+        // per thread (256 threads)
         if (cpl <= 1) return launch_n<PRO, EPI, 1, 1, false>(p, s);
         if (cpl <= 3) return launch_n<PRO, EPI, 1, 3, false>(p, s);
         // NREG: the activation row's 16-byte groups per thread (512 threads)
