@@ -167,9 +167,19 @@ __global__ __launch_bounds__(kSmpLocal) void sample_local_kernel(SmpArgs a) {
     const int *w;
     const int nw = smp_window(a, c, &w);
     const bool pen = c.penalty != 1.0f && nw > 0;
-    for (int i = tid; i < n; i += kSmpLocal) {
-        vals[i] = a.logits[base + i];
-        cnt[i] = 0;
+    {   // the block's logits: every load out before the first store
+        constexpr int kPer = kSmpChunk / kSmpLocal;
+        float lv[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) lv[q] = a.logits[base + min(tid + q * kSmpLocal, n - 1)];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = tid + q * kSmpLocal;
+            if (i < n) {
+                vals[i] = lv[q];
+                cnt[i] = 0;
+            }
+        }
     }
     if (tid == 0) {
         s_bad = 0;
@@ -264,12 +274,26 @@ __global__ __launch_bounds__(kSmpThreads) void sample_final_kernel(SmpArgs a) {
     atomicMax(&s_lo, lo);
     lds_barrier();
     lo = s_lo;
-    // the largest key is in its block's list whatever k is
+    // the largest key is in its block's list whatever k is.  The keys are
+    // read 8 per thread at a time, all 8 loads out before the first use (one
+    // at a time, the LDS atomics between them kept each a round trip of its
+    // own: 13 for k = 50 over 63 blocks)
     uint32_t mx = 0;
-    for (int i = tid; i < nk; i += kSmpThreads) {
-        const unsigned long long k = a.cand[(size_t)(i / kl) * kSmpKMax + (i % kl)];
-        mx = max(mx, (uint32_t)(k >> 32));
-        if (sparse && (uint32_t)(k >> 32) >= lo) sk[atomicAdd(&s_nl, 1)] = k;
+    constexpr int kB = 8;
+    for (int i0 = tid; i0 < nk; i0 += kB * kSmpThreads) {
+        unsigned long long kv[kB];
+#pragma unroll
+        for (int q = 0; q < kB; ++q) {
+            const int i = min(i0 + q * kSmpThreads, nk - 1);   // clamped; used only below nk
+            kv[q] = a.cand[(size_t)(i / kl) * kSmpKMax + (i % kl)];
+        }
+#pragma unroll
+        for (int q = 0; q < kB; ++q) {
+            if (i0 + q * kSmpThreads >= nk) break;
+            const unsigned long long k = kv[q];
+            mx = max(mx, (uint32_t)(k >> 32));
+            if (sparse && (uint32_t)(k >> 32) >= lo) sk[atomicAdd(&s_nl, 1)] = k;
+        }
     }
     atomicMax(&s_mx, mx);
     lds_barrier();
